@@ -1,0 +1,95 @@
+// arfq_common.h -- device-side layout of the repacked GGUF blocks and the
+// per-format dequant helpers shared by every kernel (GEMV, GEMM, MoE, and the
+// arfq_dequant_f32 parity hook).
+//
+// Device layouts (all lossless permutations of ggml's bytes; each stream is a
+// separate 256-B aligned allocation; blocks are ordered expert-major, then row,
+// then along k):
+//   Q4_K  hdr[nblk] 16 B  = d(f16) | dmin(f16) | scales[12]   (ggml bytes 0..15)
+//         qs [nblk] 128 B = ggml bytes 16..143 verbatim
+//   Q8_0  qs [nblk] 32 B  = the 32 i8 codes;   d[nblk] f16
+//   Q6_K  qb [nblk] 192 B = 4 chunks of 48 B; chunk c (n2 = c/2, l0 = 16*(c%2)):
+//                           ql[64n2+l0 .. +16] | ql[64n2+32+l0 .. +16] | qh[32n2+l0 .. +16]
+//         sc [nblk] 16 B  = the 16 i8 sub-block scales;  d[nblk] f16
+#pragma once
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace arfq {
+
+constexpr int QK_K = 256;
+constexpr int WAVE = 64;
+
+// f16 bits -> f32.  v_cvt_f32_f16 is exact for every f16 value, subnormals
+// included (f16 denormals are not flushed in the default gfx950 FP mode); the
+// exhaustive 65536-pattern test pins this against the reference's
+// f16_to_f32 (crates/arf-ml/src/dtype.rs:41-70).
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xffffu)));
+}
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (non-temporal hint: each weight byte is read once).
+__device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+
+// 6-bit scale / min of Q4_K sub-block j (0..7) from the header dwords
+// s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11]  (ggml
+// get_scale_min_k4; crates/arf-ml/src/weight.rs:1353-1365).
+__device__ __forceinline__ void q4k_scale_min(uint32_t s0, uint32_t s1, uint32_t s2, int j,
+                                              uint32_t &sc, uint32_t &m) {
+    if (j < 4) {
+        sc = byte_of(s0, j) & 63u;
+        m = byte_of(s1, j) & 63u;
+    } else {
+        const int i = j - 4;
+        sc = (byte_of(s2, i) & 0xFu) | ((byte_of(s0, i) >> 6) << 4);
+        m = (byte_of(s2, i) >> 4) | ((byte_of(s1, i) >> 6) << 4);
+    }
+}
+
+// Q4_K weight:  (d*sc)*q - (dmin*m), three separately rounded f32 operations
+// (crates/arf-core/src/model/gguf.rs:2022-2031).  Contraction into an FMA would
+// change the last bit, so it is switched off here.
+__device__ __forceinline__ float q4k_weight(float d1, float m1, uint32_t q) {
+#pragma clang fp contract(off)
+    return d1 * (float)q - m1;
+}
+__device__ __forceinline__ float q4k_d1(float d, uint32_t sc) {
+#pragma clang fp contract(off)
+    return d * (float)sc;
+}
+
+// Q8_0 weight: d * q (crates/arf-core/src/model/gguf.rs:1645).
+__device__ __forceinline__ float q80_weight(float d, int q) {
+#pragma clang fp contract(off)
+    return d * (float)q;
+}
+
+// Q6_K weight: (d * sc) * (q - 32), left to right (gguf.rs:2120-2123).
+__device__ __forceinline__ float q6k_weight(float d, int sc, int q) {
+#pragma clang fp contract(off)
+    return d * (float)sc * (float)(q - 32);
+}
+
+// Extract the 6-bit code q_{t+1} (t = quadrant 0..3) of element i (0..15) of a
+// Q6_K 48-byte chunk, given the chunk as 12 dwords w[0..11]:
+//   t=0: ql_a low nibble | qh bits 0-1;  t=1: ql_b low | qh bits 2-3;
+//   t=2: ql_a high       | qh bits 4-5;  t=3: ql_b high | qh bits 6-7.
+// (crates/arf-core/src/model/gguf.rs:2110-2117)
+__device__ __forceinline__ int q6k_code(const uint32_t *w, int t, int i) {
+    const uint32_t qla = byte_of(w[i >> 2], i & 3);
+    const uint32_t qlb = byte_of(w[4 + (i >> 2)], i & 3);
+    const uint32_t qh = byte_of(w[8 + (i >> 2)], i & 3);
+    const uint32_t lo = (t & 1) ? qlb : qla;
+    const uint32_t nib = (t & 2) ? (lo >> 4) : (lo & 0xFu);
+    return (int)(nib | (((qh >> (2 * t)) & 3u) << 4));
+}
+
+}  // namespace arfq

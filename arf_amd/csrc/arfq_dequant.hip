@@ -1,0 +1,147 @@
+// arfq_dequant.hip -- upload repack (raw ggml blocks -> aligned device streams)
+// and the f32 dequant used by arfq_dequant_f32.  Both are one-time / parity
+// paths, not hot paths: one thread per block (or per sub-unit), byte reads.
+#include "arfq_common.h"
+#include "arfq_internal.h"
+
+namespace arfq {
+
+// ---- repack ------------------------------------------------------------------
+
+__global__ void repack_q4k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr,
+                           uint8_t *__restrict__ qs, int64_t nblk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *src = raw + b * 144;
+    uint8_t *h = hdr + b * 16;
+    uint8_t *q = qs + b * 128;
+    for (int i = 0; i < 16; i++) h[i] = src[i];
+    for (int i = 0; i < 128; i++) q[i] = src[16 + i];
+}
+
+__global__ void repack_q80(const uint8_t *__restrict__ raw, uint8_t *__restrict__ qs,
+                           uint16_t *__restrict__ d, int64_t nblk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *src = raw + b * 34;
+    d[b] = (uint16_t)(src[0] | (src[1] << 8));
+    uint8_t *q = qs + b * 32;
+    for (int i = 0; i < 32; i++) q[i] = src[2 + i];
+}
+
+__global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ qb,
+                           uint8_t *__restrict__ sc, uint16_t *__restrict__ d, int64_t nblk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *src = raw + b * 210;
+    const uint8_t *ql = src, *qh = src + 128;
+    uint8_t *dst = qb + b * 192;
+    for (int c = 0; c < 4; c++) {
+        const int n2 = c >> 1, l0 = 16 * (c & 1);
+        uint8_t *o = dst + 48 * c;
+        for (int i = 0; i < 16; i++) {
+            o[i] = ql[64 * n2 + l0 + i];
+            o[16 + i] = ql[64 * n2 + 32 + l0 + i];
+            o[32 + i] = qh[32 * n2 + l0 + i];
+        }
+    }
+    for (int i = 0; i < 16; i++) sc[b * 16 + i] = src[192 + i];
+    d[b] = (uint16_t)(src[208] | (src[209] << 8));
+}
+
+hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s) {
+    const int tpb = 256;
+    const unsigned grid = (unsigned)((w->nblk + tpb - 1) / tpb);
+    switch (w->qtype) {
+    case ARFQ_Q4_K:
+        repack_q4k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, w->nblk);
+        break;
+    case ARFQ_Q8_0:
+        repack_q80<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint16_t *)w->s1, w->nblk);
+        break;
+    case ARFQ_Q6_K:
+        repack_q6k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1,
+                                        (uint16_t *)w->s2, w->nblk);
+        break;
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---- dequant -----------------------------------------------------------------
+
+// One thread per (block, sub-block j): 32 outputs.
+__global__ void dequant_q4k(const uint4 *__restrict__ hdr, const uint8_t *__restrict__ qs,
+                            float *__restrict__ out, int64_t nblk) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 8) return;
+    const int64_t b = t >> 3;
+    const int j = (int)(t & 7);
+    const uint4 h = hdr[b];
+    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+    uint32_t sc, m;
+    q4k_scale_min(h.y, h.z, h.w, j, sc, m);
+    const float d1 = q4k_d1(d, sc);
+    const float m1 = q4k_d1(dmin, m);
+    const uint8_t *q = qs + b * 128 + (j >> 1) * 32;
+    const int shift = (j & 1) * 4;
+    float *o = out + b * 256 + j * 32;
+    for (int i = 0; i < 32; i++) o[i] = q4k_weight(d1, m1, (q[i] >> shift) & 0xFu);
+}
+
+__global__ void dequant_q80(const int8_t *__restrict__ qs, const uint16_t *__restrict__ d,
+                            float *__restrict__ out, int64_t nblk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const float dv = h2f(d[b]);
+    for (int i = 0; i < 32; i++) out[b * 32 + i] = q80_weight(dv, qs[b * 32 + i]);
+}
+
+// One thread per (block, 48-byte chunk c): 64 outputs.
+__global__ void dequant_q6k(const uint32_t *__restrict__ qb, const int8_t *__restrict__ sc,
+                            const uint16_t *__restrict__ d, float *__restrict__ out,
+                            int64_t nblk) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 4) return;
+    const int64_t b = t >> 2;
+    const int c = (int)(t & 3);
+    uint32_t w[12];
+    for (int i = 0; i < 12; i++) w[i] = qb[b * 48 + c * 12 + i];
+    const float dv = h2f(d[b]);
+    const int n2 = c >> 1, isub = c & 1;
+    float *o = out + b * 256 + 128 * n2 + 16 * isub;
+    for (int tq = 0; tq < 4; tq++) {
+        const int s = sc[b * 16 + 8 * n2 + isub + 2 * tq];
+        for (int i = 0; i < 16; i++) o[32 * tq + i] = q6k_weight(dv, s, q6k_code(w, tq, i));
+    }
+}
+
+hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s) {
+    const int tpb = 256;
+    switch (w->qtype) {
+    case ARFQ_Q4_K: {
+        const unsigned grid = (unsigned)((w->nblk * 8 + tpb - 1) / tpb);
+        dequant_q4k<<<grid, tpb, 0, s>>>((const uint4 *)w->s0, (const uint8_t *)w->s1, out,
+                                         w->nblk);
+        break;
+    }
+    case ARFQ_Q8_0: {
+        const unsigned grid = (unsigned)((w->nblk + tpb - 1) / tpb);
+        dequant_q80<<<grid, tpb, 0, s>>>((const int8_t *)w->s0, (const uint16_t *)w->s1, out,
+                                         w->nblk);
+        break;
+    }
+    case ARFQ_Q6_K: {
+        const unsigned grid = (unsigned)((w->nblk * 4 + tpb - 1) / tpb);
+        dequant_q6k<<<grid, tpb, 0, s>>>((const uint32_t *)w->s0, (const int8_t *)w->s1,
+                                         (const uint16_t *)w->s2, out, w->nblk);
+        break;
+    }
+    default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace arfq

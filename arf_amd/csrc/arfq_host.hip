@@ -1,0 +1,343 @@
+// arfq_host.hip -- the C ABI (include/arfq.h): contexts, weight upload,
+// kernel selection by (qtype, m), MoE orchestration and the memory / timing
+// helpers.  All device work goes to the context's stream.
+#include <stdio.h>
+#include <string.h>
+
+#include <new>
+#include <string>
+
+#include "arfq_internal.h"
+
+namespace {
+
+thread_local std::string g_create_err;
+
+int fail(arfq_ctx *ctx, int code, const std::string &msg) {
+    if (ctx) ctx->err = msg;
+    return code;
+}
+
+int hip_fail(arfq_ctx *ctx, hipError_t e, const char *what) {
+    std::string m = std::string(what) + ": " + hipGetErrorString(e);
+    return fail(ctx, ARFQ_E_DEVICE, m);
+}
+
+#define HIP_TRY(ctx, expr)                                   \
+    do {                                                     \
+        hipError_t _e = (expr);                              \
+        if (_e != hipSuccess) return hip_fail(ctx, _e, #expr); \
+    } while (0)
+
+// Make the context's device current for this thread.
+int use_device(arfq_ctx *ctx) {
+    hipError_t e = hipSetDevice(ctx->device);
+    if (e != hipSuccess) return hip_fail(ctx, e, "hipSetDevice");
+    return ARFQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int arfq_version(void) { return ARFQ_VERSION; }
+
+const char *arfq_status_string(int status) {
+    switch (status) {
+    case ARFQ_OK: return "ok";
+    case ARFQ_E_INVALID: return "invalid argument";
+    case ARFQ_E_SHAPE: return "shape mismatch";
+    case ARFQ_E_DEVICE: return "HIP device error";
+    case ARFQ_E_NOMEM: return "device out of memory";
+    case ARFQ_E_UNSUPPORTED: return "unsupported";
+    default: return "unknown status";
+    }
+}
+
+int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
+    if (!out) {
+        g_create_err = "arfq_ctx_create: out is NULL";
+        return ARFQ_E_INVALID;
+    }
+    *out = nullptr;
+    int ndev = 0;
+    hipError_t e = hipGetDeviceCount(&ndev);
+    if (e != hipSuccess || ndev == 0) {
+        g_create_err = std::string("arfq_ctx_create: no HIP device (") +
+                       (e != hipSuccess ? hipGetErrorString(e) : "count 0") + ")";
+        return ARFQ_E_DEVICE;
+    }
+    if (device < 0 || device >= ndev) {
+        g_create_err = "arfq_ctx_create: device index out of range";
+        return ARFQ_E_INVALID;
+    }
+    arfq_ctx *ctx = new (std::nothrow) arfq_ctx();
+    if (!ctx) return ARFQ_E_NOMEM;
+    ctx->device = device;
+    e = hipSetDevice(device);
+    if (e == hipSuccess) {
+        if (stream) {
+            ctx->stream = (hipStream_t)stream;
+        } else {
+            e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+            ctx->own_stream = (e == hipSuccess);
+        }
+    }
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
+    if (e == hipSuccess) e = hipEventCreate(&ctx->ev_stop);
+    if (e != hipSuccess) {
+        g_create_err = std::string("arfq_ctx_create: ") + hipGetErrorString(e);
+        arfq_ctx_destroy(ctx);
+        return ARFQ_E_DEVICE;
+    }
+    *out = ctx;
+    return ARFQ_OK;
+}
+
+int arfq_ctx_destroy(arfq_ctx *ctx) {
+    if (!ctx) return ARFQ_E_INVALID;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
+    if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
+    if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+    return ARFQ_OK;
+}
+
+void *arfq_ctx_stream(arfq_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+const char *arfq_last_error(const arfq_ctx *ctx) {
+    return ctx ? ctx->err.c_str() : g_create_err.c_str();
+}
+
+int arfq_ctx_sync(arfq_ctx *ctx) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (int rc = use_device(ctx)) return rc;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return ARFQ_OK;
+}
+
+// ---------------------------------------------------------------- weights ----
+
+static int weight_create(arfq_ctx *ctx, int qtype, size_t nbytes, int64_t n_rows, int64_t k_cols,
+                         int n_experts, arfq_weight **out) {
+    if (!ctx || !out) return fail(ctx, ARFQ_E_INVALID, "weight upload: null argument");
+    *out = nullptr;
+    const int bb = arfq::block_bytes_of(qtype);
+    if (bb == 0) return fail(ctx, ARFQ_E_INVALID, "weight upload: unknown qtype");
+    const int qk = arfq::qk_of(qtype);
+    if (n_rows <= 0 || k_cols <= 0 || n_experts <= 0)
+        return fail(ctx, ARFQ_E_SHAPE, "weight upload: non-positive dimension");
+    if (k_cols % qk != 0)
+        return fail(ctx, ARFQ_E_SHAPE,
+                    "weight upload: k_cols must be a multiple of " + std::to_string(qk));
+    if (n_rows > (int64_t)1 << 30 || k_cols > (int64_t)1 << 30)
+        return fail(ctx, ARFQ_E_SHAPE, "weight upload: dimension too large");
+    const int64_t nblk = (int64_t)n_experts * n_rows * (k_cols / qk);
+    if ((size_t)nblk * (size_t)bb != nbytes)
+        return fail(ctx, ARFQ_E_SHAPE,
+                    "weight upload: nbytes " + std::to_string(nbytes) + " != expected " +
+                        std::to_string((size_t)nblk * bb));
+    if (int rc = use_device(ctx)) return rc;
+    arfq_weight *w = new (std::nothrow) arfq_weight();
+    if (!w) return fail(ctx, ARFQ_E_NOMEM, "weight upload: host allocation");
+    w->ctx = ctx;
+    w->qtype = qtype;
+    w->n = n_rows;
+    w->k = k_cols;
+    w->experts = n_experts;
+    w->nblk = nblk;
+    w->bytes = (size_t)n_rows * (size_t)(k_cols / qk) * (size_t)bb;
+    size_t sz[3] = {0, 0, 0};
+    switch (qtype) {
+    case ARFQ_Q4_K: sz[0] = nblk * 16; sz[1] = nblk * 128; break;
+    case ARFQ_Q8_0: sz[0] = nblk * 32; sz[1] = nblk * 2; break;
+    case ARFQ_Q6_K: sz[0] = nblk * 192; sz[1] = nblk * 16; sz[2] = nblk * 2; break;
+    }
+    void **dst[3] = {&w->s0, &w->s1, &w->s2};
+    for (int i = 0; i < 3; i++) {
+        if (!sz[i]) continue;
+        // round up so 16-byte vector loads of the last element stay in bounds
+        hipError_t e = hipMalloc(dst[i], (sz[i] + 255) & ~(size_t)255);
+        if (e != hipSuccess) {
+            arfq_weight_free(w);
+            return fail(ctx, ARFQ_E_NOMEM, std::string("weight upload: hipMalloc: ") +
+                                               hipGetErrorString(e));
+        }
+    }
+    *out = w;
+    return ARFQ_OK;
+}
+
+int arfq_weight_upload_device(arfq_ctx *ctx, int qtype, const void *dev_blocks, size_t nbytes,
+                              int64_t n_rows, int64_t k_cols, int n_experts, arfq_weight **out) {
+    if (!dev_blocks) return fail(ctx, ARFQ_E_INVALID, "weight upload: null blocks");
+    arfq_weight *w = nullptr;
+    if (int rc = weight_create(ctx, qtype, nbytes, n_rows, k_cols, n_experts, &w)) return rc;
+    hipError_t e = arfq::launch_repack(w, (const uint8_t *)dev_blocks, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        arfq_weight_free(w);
+        return hip_fail(ctx, e, "weight upload: repack");
+    }
+    *out = w;
+    return ARFQ_OK;
+}
+
+int arfq_weight_upload(arfq_ctx *ctx, int qtype, const void *host_blocks, size_t nbytes,
+                       int64_t n_rows, int64_t k_cols, int n_experts, arfq_weight **out) {
+    if (!ctx || !host_blocks || !out) return fail(ctx, ARFQ_E_INVALID, "weight upload: null argument");
+    arfq_weight *w = nullptr;
+    if (int rc = weight_create(ctx, qtype, nbytes, n_rows, k_cols, n_experts, &w)) return rc;
+    void *staging = nullptr;
+    hipError_t e = hipMalloc(&staging, nbytes);
+    if (e != hipSuccess) {
+        arfq_weight_free(w);
+        return fail(ctx, ARFQ_E_NOMEM, std::string("weight upload: staging: ") + hipGetErrorString(e));
+    }
+    e = hipMemcpyAsync(staging, host_blocks, nbytes, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = arfq::launch_repack(w, (const uint8_t *)staging, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(staging);
+    if (e != hipSuccess) {
+        arfq_weight_free(w);
+        return hip_fail(ctx, e, "weight upload");
+    }
+    *out = w;
+    return ARFQ_OK;
+}
+
+int arfq_weight_free(arfq_weight *w) {
+    if (!w) return ARFQ_E_INVALID;
+    if (w->ctx) (void)hipSetDevice(w->ctx->device);
+    if (w->s0) (void)hipFree(w->s0);
+    if (w->s1) (void)hipFree(w->s1);
+    if (w->s2) (void)hipFree(w->s2);
+    delete w;
+    return ARFQ_OK;
+}
+
+int arfq_weight_info(const arfq_weight *w, int *qtype, int64_t *n_rows, int64_t *k_cols,
+                     int *n_experts, size_t *device_bytes) {
+    if (!w) return ARFQ_E_INVALID;
+    if (qtype) *qtype = w->qtype;
+    if (n_rows) *n_rows = w->n;
+    if (k_cols) *k_cols = w->k;
+    if (n_experts) *n_experts = w->experts;
+    if (device_bytes) *device_bytes = w->bytes;
+    return ARFQ_OK;
+}
+
+// ----------------------------------------------------------------- matmul ----
+
+static int check_matmul(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m,
+                        const void *x, int x_dtype, const float *y) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (!w || !x || !y) return fail(ctx, ARFQ_E_INVALID, "matmul: null argument");
+    if (x_dtype != ARFQ_F32 && x_dtype != ARFQ_F16)
+        return fail(ctx, ARFQ_E_INVALID, "matmul: unknown x dtype");
+    if (expert < 0 || expert >= w->experts)
+        return fail(ctx, ARFQ_E_SHAPE, "matmul: expert index out of range");
+    if (m <= 0 || m > (int64_t)1 << 24) return fail(ctx, ARFQ_E_SHAPE, "matmul: bad m");
+    return ARFQ_OK;
+}
+
+static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m,
+                          const void *x, int x_dtype, float *y) {
+    hipError_t e;
+    if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
+        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream);
+    } else if (arfq::gemm_supports(w, m)) {
+        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->stream);
+    } else {
+        return fail(ctx, ARFQ_E_UNSUPPORTED,
+                    "matmul: no kernel for qtype " + std::to_string(w->qtype) + " at m=" +
+                        std::to_string(m) + (x_dtype == ARFQ_F16 ? " (f16 x)" : " (f32 x)"));
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "matmul launch");
+    return ARFQ_OK;
+}
+
+int arfq_matmul(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m, const void *x,
+                int x_dtype, float *y) {
+    if (int rc = check_matmul(ctx, w, expert, m, x, x_dtype, y)) return rc;
+    if (int rc = use_device(ctx)) return rc;
+    return matmul_enqueue(ctx, w, expert, m, x, x_dtype, y);
+}
+
+int arfq_matmul_repeat(arfq_ctx *ctx, const arfq_weight *const *ws, int n_ws, int iters,
+                       int64_t m, const void *x, int x_dtype, float *y) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (!ws || n_ws <= 0 || iters < 0) return fail(ctx, ARFQ_E_INVALID, "matmul_repeat: bad args");
+    for (int i = 0; i < n_ws; i++) {
+        if (int rc = check_matmul(ctx, ws[i], 0, m, x, x_dtype, y)) return rc;
+        if (ws[i]->n != ws[0]->n || ws[i]->k != ws[0]->k || ws[i]->qtype != ws[0]->qtype)
+            return fail(ctx, ARFQ_E_SHAPE, "matmul_repeat: weights differ in shape");
+    }
+    if (int rc = use_device(ctx)) return rc;
+    for (int i = 0; i < iters; i++)
+        if (int rc = matmul_enqueue(ctx, ws[i % n_ws], 0, m, x, x_dtype, y)) return rc;
+    return ARFQ_OK;
+}
+
+int arfq_dequant_f32(arfq_ctx *ctx, const arfq_weight *w, float *out) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (!w || !out) return fail(ctx, ARFQ_E_INVALID, "dequant: null argument");
+    if (int rc = use_device(ctx)) return rc;
+    hipError_t e = arfq::launch_dequant(w, out, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "dequant launch");
+    return ARFQ_OK;
+}
+
+// ---------------------------------------------------------------- helpers ----
+
+int arfq_dev_malloc(arfq_ctx *ctx, size_t bytes, void **out) {
+    if (!ctx || !out) return fail(ctx, ARFQ_E_INVALID, "dev_malloc: null argument");
+    if (int rc = use_device(ctx)) return rc;
+    hipError_t e = hipMalloc(out, bytes ? bytes : 1);
+    if (e != hipSuccess) return fail(ctx, ARFQ_E_NOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+    return ARFQ_OK;
+}
+
+int arfq_dev_free(arfq_ctx *ctx, void *p) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (int rc = use_device(ctx)) return rc;
+    HIP_TRY(ctx, hipFree(p));
+    return ARFQ_OK;
+}
+
+int arfq_copy_h2d(arfq_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(ctx, ARFQ_E_INVALID, "copy_h2d: null");
+    if (int rc = use_device(ctx)) return rc;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return ARFQ_OK;
+}
+
+int arfq_copy_d2h(arfq_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(ctx, ARFQ_E_INVALID, "copy_d2h: null");
+    if (int rc = use_device(ctx)) return rc;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    HIP_TRY(ctx, hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return ARFQ_OK;
+}
+
+int arfq_timer_start(arfq_ctx *ctx) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (int rc = use_device(ctx)) return rc;
+    HIP_TRY(ctx, hipEventRecord(ctx->ev_start, ctx->stream));
+    return ARFQ_OK;
+}
+
+int arfq_timer_stop(arfq_ctx *ctx, float *ms) {
+    if (!ctx || !ms) return fail(ctx, ARFQ_E_INVALID, "timer_stop: null");
+    if (int rc = use_device(ctx)) return rc;
+    HIP_TRY(ctx, hipEventRecord(ctx->ev_stop, ctx->stream));
+    HIP_TRY(ctx, hipEventSynchronize(ctx->ev_stop));
+    HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->ev_start, ctx->ev_stop));
+    return ARFQ_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,188 @@
+"""Benchmark of the GGUF quantized-matmul hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
+
+Headline (the JSON `value`): Q4_K decode GEMV, m=1, k=5120, n=17408 -- one step
+is one GEMV launch over one activation vector.  Weights are 8 distinct seeded
+copies (8 x 50 MB, above the 256 MB MALL) used round-robin so the timed loop
+streams from HBM.  Timing: HIP events recorded on the library's stream around
+exactly K back-to-back launches, after W warm-up launches and a stream sync.
+Secondary configs are measured the same way and reported under "configs".
+
+The CPU baseline runs the oracle (a C restatement of Arf's CPU matmul) on the
+host on a bounded sample; it is a reported baseline, not the target.
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0         # MI355X HBM3E
+FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(qtype, m, n, k, x_bytes=4):
+    from arf_amd import synth
+    wb = n * (k // synth.QK[qtype]) * synth.BLOCK_BYTES[qtype]
+    return wb + m * k * x_bytes + m * n * 4
+
+
+def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.float32):
+    """Average ms per launch of arfq_matmul over `steps` launches rotating `copies` weights."""
+    from arf_amd import QType, synth
+    qt = {"q4_k": QType.Q4_K, "q6_k": QType.Q6_K, "q8_0": QType.Q8_0}[qtype]
+    raw = synth.weight(qtype, n, k, seed=seed)
+    ws = [ctx.upload(qt, raw, n, k) for _ in range(copies)]
+    x = ctx.to_device(synth.activations(m, k, seed=seed + 1).astype(x_dtype))
+    y = ctx.empty((m, n), np.float32)
+    ctx.matmul_repeat(ws, warmup, m, x, y)
+    ctx.sync()
+    ctx.timer_start()
+    ctx.matmul_repeat(ws, steps, m, x, y)
+    ms = ctx.timer_stop()
+    ctx.sync()
+    for w in ws:
+        w.free()
+    return ms / steps, ms
+
+
+def cpu_baseline_c2(budget_s):
+    """Oracle matmul_nt_q4ks at m=1 (serial, as the reference's par_rows runs m<2) on
+    the full C2 weight, repeated for about `budget_s` seconds."""
+    from arf_amd import synth
+    from oracle import oracle
+    n, k = 17408, 5120
+    raw = synth.weight("q4_k", n, k, seed=0xA7F00002)
+    x = synth.activations(1, k, seed=0xA7F00003)
+    q4ks = oracle.q4ks_from_ggml(raw, n, k)  # load-time transcode, not timed
+    oracle.set_threads(1)
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oracle.matmul_q4ks(x, q4ks, n)
+        reps += 1
+        if time.perf_counter() - t0 >= budget_s:
+            break
+    dt = (time.perf_counter() - t0) / reps
+    oracle.set_threads(0)
+    gbs = algorithmic_bytes("q4_k", 1, n, k) / dt / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} full C2 GEMVs (m=1, k=5120, n=17408) in {dt * reps:.1f} s, "
+                      f"{dt * 1e3:.1f} ms each, oracle matmul_nt_q4ks serial (reference "
+                      f"par_rows is serial at m<2); host {platform.processor() or platform.machine()}"}
+
+
+def load_traffic(name):
+    p = os.path.join(ROOT, "profiles", name)
+    if os.path.exists(p):
+        with open(p) as f:
+            return json.load(f).get("traffic_bytes_per_launch")
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=200)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--quick", action="store_true", help="headline config only")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked --gpus {args.gpus}); "
+              "the multi-GPU sharding is design-only", file=sys.stderr)
+        sys.exit(2)
+
+    import arf_amd
+    ctx = arf_amd.Context(0)
+
+    # ---- headline: C2 Q4_K GEMV ----
+    n, k, m = 17408, 5120, 1
+    log(f"[bench] C2 q4_k gemv m={m} k={k} n={n}: warmup {args.warmup}, steps {args.steps}")
+    ms, total_ms = time_matmul(ctx, "q4_k", m, n, k, args.steps, args.warmup, args.copies,
+                               seed=0xA7F00002)
+    nbytes = algorithmic_bytes("q4_k", m, n, k)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] C2: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+
+    configs = {}
+    if not args.quick:
+        steps2 = max(50, args.steps // 4)
+        # C1 Q8_0 GEMV
+        ms1, _ = time_matmul(ctx, "q8_0", 1, 2048, 2048, steps2, 50, 64, seed=0xA7F00001)
+        b1 = algorithmic_bytes("q8_0", 1, 2048, 2048)
+        configs["c1_q8_0_gemv_m1_k2048_n2048"] = {
+            "us_per_launch": round(ms1 * 1e3, 3), "GB/s": round(b1 / ms1 / 1e6, 1),
+            "hbm_frac": round(b1 / ms1 / 1e6 / HBM_PEAK_GBS, 4), "weight_copies": 64}
+        log(f"[bench] C1: {ms1 * 1e3:.2f} us/launch")
+        # C3 Q6_K GEMV / skinny GEMM
+        for mm in (1, 8, 32, 64):
+            try:
+                ms3, _ = time_matmul(ctx, "q6_k", mm, 5120, 17408, steps2, 20, 6, seed=0xA7F00003)
+            except arf_amd.ArfqError as e:
+                configs[f"c3_q6_k_m{mm}_k17408_n5120"] = {"error": str(e)}
+                continue
+            b3 = algorithmic_bytes("q6_k", mm, 5120, 17408)
+            configs[f"c3_q6_k_m{mm}_k17408_n5120"] = {
+                "us_per_launch": round(ms3 * 1e3, 3), "GB/s": round(b3 / ms3 / 1e6, 1),
+                "hbm_frac": round(b3 / ms3 / 1e6 / HBM_PEAK_GBS, 4)}
+            log(f"[bench] C3 m={mm}: {ms3 * 1e3:.2f} us/launch")
+        # C4 Q4_K prefill GEMM
+        try:
+            ms4, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, 20, 3, 2, seed=0xA7F00004,
+                                 x_dtype=np.float16)
+            fl = 2.0 * 2048 * 17408 * 5120
+            tf = fl / (ms4 * 1e-3) / 1e12
+            configs["c4_q4_k_gemm_m2048_k5120_n17408"] = {
+                "us_per_launch": round(ms4 * 1e3, 1), "TFLOP/s": round(tf, 1),
+                "mfma_frac": round(tf / FP16_MFMA_PEAK_TFLOPS, 4)}
+            log(f"[bench] C4: {ms4 * 1e3:.1f} us/launch, {tf:.1f} TFLOP/s")
+        except arf_amd.ArfqError as e:
+            configs["c4_q4_k_gemm_m2048_k5120_n17408"] = {"error": str(e)}
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s)")
+        cpu = cpu_baseline_c2(args.cpu_seconds)
+        log(f"[bench] cpu: {cpu['value']} GB/s")
+
+    ctx.close()
+    out = {
+        "metric": "Q4_K GEMV weight GB/s (% of HBM peak); prefill GEMM TFLOP/s (% MFMA)",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded Q4_K superblocks per BASELINE config 2, x ~ N(0,1) f32)",
+        "config": {"workload": "c2_q4_k_gemv_m1_k5120_n17408", "m": m, "k": k, "n": n,
+                   "weight_copies": args.copies, "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": load_traffic("q4k_gemv_c2_traffic.json")},
+        "cpu_baseline": cpu,
+        "configs": configs,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,171 @@
+/*
+ * arfq.h -- C ABI of the MI355X (gfx950) GGUF quantized-matmul library.
+ *
+ * The library replaces the GPU side of Arf's quantized matmul path: the weight
+ * upload for GGUF Q8_0 / Q4_K / Q6_K tensors, the matmul entry point that picks
+ * a GEMV or a tiled GEMM by the activation row count, and the expert-grouped
+ * MoE block.  Each declaration cites the reference interface it replaces
+ * (paths relative to the joydle/Arf source tree).
+ *
+ * Conventions (shared by every entry point):
+ *   - Every call returns an int status: ARFQ_OK (0) or a negative ARFQ_E_*
+ *     code; arfq_last_error(ctx) holds a message for the last failure.  No C++
+ *     exception crosses this boundary.  (The reference panics on shape
+ *     mismatches, crates/arf-ml/src/matmul.rs:180-183,374-386; here the same
+ *     checks return ARFQ_E_SHAPE.)
+ *   - A weight matrix is [n rows = outputs, k cols = inputs], row-major, ggml
+ *     blocks running along k; y[m, n] = sum_k x[m, k] * W[n, k]
+ *     (crates/arf-ml/src/matmul.rs:84-99, crates/arf-core/src/model/gguf.rs:780-782).
+ *   - x, y, ids and other activations are DEVICE pointers owned by the caller.
+ *     Weights are owned by their arfq_weight handle.
+ *   - Work is enqueued asynchronously on the context's HIP stream; one context
+ *     is used by one thread at a time (the reference's single-owner model,
+ *     crates/arf-gpu/src/gpu/metal/island.rs:968-971).
+ *   - Accumulation is fp32.  Dequantized weights are bit-identical to the
+ *     reference's CPU dequant (arfq_dequant_f32 is the hook that proves it).
+ */
+#ifndef ARFQ_H
+#define ARFQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ARFQ_VERSION 100 /* 1.0.0 */
+
+/* status codes */
+#define ARFQ_OK 0
+#define ARFQ_E_INVALID -1   /* null handle / pointer, unknown enum */
+#define ARFQ_E_SHAPE -2     /* dimension or byte-count mismatch */
+#define ARFQ_E_DEVICE -3    /* HIP runtime error */
+#define ARFQ_E_NOMEM -4     /* device allocation failed */
+#define ARFQ_E_UNSUPPORTED -5 /* valid request this build does not implement */
+
+/* ggml type ids, crates/arf-core/src/model/gguf.rs:36-90 (GgmlType). */
+typedef enum {
+    ARFQ_Q8_0 = 8,  /* 34 B per 32 weights: f16 d, 32 x i8 */
+    ARFQ_Q4_K = 12, /* 144 B per 256 weights: f16 d, f16 dmin, 12 B 6-bit scales/mins, 128 B nibbles */
+    ARFQ_Q6_K = 14  /* 210 B per 256 weights: ql[128], qh[64], i8 scales[16], f16 d */
+} arfq_qtype;
+
+/* activation element type */
+typedef enum { ARFQ_F32 = 0, ARFQ_F16 = 1 } arfq_dtype;
+
+typedef struct arfq_ctx arfq_ctx;
+typedef struct arfq_weight arfq_weight;
+
+/* Library version (ARFQ_VERSION). */
+int arfq_version(void);
+
+/* Static text for a status code. */
+const char *arfq_status_string(int status);
+
+/* Create a context on HIP device `device`.  `stream` is a hipStream_t to enqueue
+ * on, or NULL for a stream the context creates (default priority) and owns.
+ * Replaces the reference's GpuContext/CommandPass pair as the owner of the
+ * queue (crates/arf-gpu/src/gpu/context.rs:28-120, command.rs:169-243). */
+int arfq_ctx_create(int device, void *stream, arfq_ctx **out);
+int arfq_ctx_destroy(arfq_ctx *ctx);
+/* The hipStream_t the context enqueues on. */
+void *arfq_ctx_stream(arfq_ctx *ctx);
+/* Message for the last failed call on this context ("" if none).  A NULL ctx
+ * returns the message of the last failed arfq_ctx_create on this thread. */
+const char *arfq_last_error(const arfq_ctx *ctx);
+/* Block until all work enqueued on the context's stream has finished. */
+int arfq_ctx_sync(arfq_ctx *ctx);
+
+/* Upload `n_experts` stacked [n_rows, k_cols] matrices of raw ggml blocks from
+ * HOST memory.  `nbytes` must equal n_experts * n_rows * k_cols / QK *
+ * block_bytes (QK = 32 / 256; block_bytes = 34 / 144 / 210).  Experts are
+ * concatenated in expert-major order, the PackedExperts layout
+ * (crates/arf-gpu/src/gpu/types.rs:89-112).  The upload is a lossless repack
+ * into 16-byte-aligned device streams.  Replaces the Q4KS/Q8_0 upload in
+ * crates/arf-gpu/src/weights.rs:1140-1236 and crates/arf-gpu/src/gpu/flux/t5.rs:106-140
+ * (which transcode first; here the GPU reads ggml's own bit layout).
+ * Synchronous: returns after the data is on the device. */
+int arfq_weight_upload(arfq_ctx *ctx, int qtype, const void *host_blocks, size_t nbytes,
+                       int64_t n_rows, int64_t k_cols, int n_experts, arfq_weight **out);
+/* Same, from raw ggml blocks already in DEVICE memory (e.g. a GGUF tensor
+ * copied as-is); the source is only read, and may be freed after the call. */
+int arfq_weight_upload_device(arfq_ctx *ctx, int qtype, const void *dev_blocks, size_t nbytes,
+                              int64_t n_rows, int64_t k_cols, int n_experts, arfq_weight **out);
+int arfq_weight_free(arfq_weight *w);
+/* Shape and type of an uploaded weight; any out-pointer may be NULL.
+ * `device_bytes` is the bytes one full matmul streams (GpuMatWeight::bytes_num,
+ * crates/arf-gpu/src/gpu/types.rs:69-82). */
+int arfq_weight_info(const arfq_weight *w, int *qtype, int64_t *n_rows, int64_t *k_cols,
+                     int *n_experts, size_t *device_bytes);
+
+/* y[m, n_rows] (f32) = x[m, k_cols] . W^T for expert `expert` of `w` (0 for a
+ * plain matrix).  x is f32 or f16 per `x_dtype`.  The library picks the kernel
+ * by (qtype, m): wave-per-rows GEMV for small m, dequant-into-LDS MFMA GEMM
+ * otherwise.  Replaces add_matmul_m / add_matmul
+ * (crates/arf-gpu/src/gpu/dispatch.rs:169-202, Q4KS arms :517-630) and the
+ * island's gemv_q4ks / gemv_q4ks_batch / matmul_mm_q4ks selection
+ * (crates/arf-gpu/src/gpu/metal/island.rs:4289-4333). */
+int arfq_matmul(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m, const void *x,
+                int x_dtype, float *y);
+
+/* Dequantize every expert of `w` into out[n_experts * n_rows * k_cols] (device,
+ * f32) with the same device dequant code the matmuls use.  Bit-identical to
+ * dequant_q8_0 / dequant_q4_k / dequant_q6_k
+ * (crates/arf-core/src/model/gguf.rs:1633-1649,2004-2035,2092-2131) and to
+ * Q4KSMatrix::to_f32 (crates/arf-ml/src/weight.rs:1110-1136). */
+int arfq_dequant_f32(arfq_ctx *ctx, const arfq_weight *w, float *out);
+
+/* Top-k routing for `tokens` rows of router logits [tokens, n_experts] (device
+ * f32): full softmax, the top_k largest probabilities (ties -> lower index),
+ * renormalised to sum 1 when norm_topk != 0.  Writes ids[tokens, top_k] (i32)
+ * and weights[tokens, top_k] (f32), both device.  Replaces the moe_route(_b)
+ * kernels (crates/arf-gpu/src/shaders/metal/moe_route_msl.metal:18-98,
+ * moe_batch_msl.metal:371-449); oracle top_k_softmax
+ * (crates/arf-core/src/model/moe.rs:89-121). */
+int arfq_moe_route(arfq_ctx *ctx, const float *logits, int64_t tokens, int n_experts, int top_k,
+                   int norm_topk, int32_t *ids, float *weights);
+
+/* The MoE feed-forward block on `tokens` rows of x [tokens, hidden]:
+ * route (as arfq_moe_route), group (token, slot) pairs by expert, run each
+ * expert's SwiGLU  down(silu(gate . x) * (up . x)), and scatter-add the results
+ * weighted by the router weights into y[tokens, hidden] (f32, overwritten).
+ * gate/up hold n_experts x [inter, hidden]; down holds n_experts x [hidden,
+ * inter]; all Q4_K.  Replaces add_moe_block_batched
+ * (crates/arf-gpu/src/gpu/batch.rs:355-460) and the island's sorted mm_id chain
+ * (crates/arf-gpu/src/gpu/metal/island.rs:4033-4134); oracle MoeMlp::forward
+ * (crates/arf-core/src/model/moe.rs:53-86).  Scratch memory is owned by the
+ * context and grows on demand. */
+int arfq_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+             const arfq_weight *down, const float *router_logits, int64_t tokens, int top_k,
+             int norm_topk, const void *x, int x_dtype, float *y);
+
+/* As arfq_moe, with routing already done: ids/weights [tokens, top_k] (device). */
+int arfq_moe_ids(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                 const arfq_weight *down, const int32_t *ids, const float *weights,
+                 int64_t tokens, int top_k, const void *x, int x_dtype, float *y);
+
+/* ---- device-memory and timing helpers -------------------------------------
+ * For callers without their own HIP allocator (the FFI host, tests, the bench).
+ * The reference's equivalents are GpuContext buffer init / readback
+ * (crates/arf-gpu/src/gpu/context.rs:505-611) and its per-kernel timestamp
+ * queries (crates/arf-gpu/src/gpu/command.rs:186-243). */
+int arfq_dev_malloc(arfq_ctx *ctx, size_t bytes, void **out);
+int arfq_dev_free(arfq_ctx *ctx, void *p);
+/* Synchronous copies (they wait for the context's stream first). */
+int arfq_copy_h2d(arfq_ctx *ctx, void *dst, const void *src, size_t bytes);
+int arfq_copy_d2h(arfq_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Record a start event / a stop event on the context's stream; elapsed time in
+ * ms between the last start and stop (waits for the stop event). */
+int arfq_timer_start(arfq_ctx *ctx);
+int arfq_timer_stop(arfq_ctx *ctx, float *ms);
+/* Enqueue `iters` arfq_matmul calls back to back, call i using ws[i % n_ws]
+ * (distinct weight copies, so a timing loop streams from HBM rather than from
+ * a cache), all with the same x and y.  For timing loops only. */
+int arfq_matmul_repeat(arfq_ctx *ctx, const arfq_weight *const *ws, int n_ws, int iters,
+                       int64_t m, const void *x, int x_dtype, float *y);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* ARFQ_H */

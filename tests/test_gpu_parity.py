@@ -1,0 +1,138 @@
+"""GPU parity: the HIP path (through the C ABI) against the CPU oracle.
+
+Dequant: bit-exact (memcmp of the f32 arrays), including f16-subnormal scales.
+Matmul: max_i |g_i - c_i| / max(|c_i|, rms(c)) <= 2e-3 (fp32 accumulation).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from formats import make_q80_block
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# ------------------------------------------------------------- dequant ----
+def test_f16_conversion_exhaustive_via_q8_0(gpu_ctx, oracle):
+    # q = 1 everywhere, d = every f16 pattern: dequant = f16_to_f32(d) * 1
+    _say("case: f16 exhaustive")
+    from arf_amd import QType
+    d = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    blocks = np.zeros((65536, 34), np.uint8)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:34] = 1
+    w = gpu_ctx.upload(QType.Q8_0, blocks, 2048, 1024)
+    got = gpu_ctx.dequant(w).numpy().reshape(65536, 32)[:, 0]
+    want = oracle.dequant("q8_0", blocks, 65536 * 32).reshape(65536, 32)[:, 0]
+    finite = np.isfinite(want)
+    assert np.array_equal(got[finite].view(np.uint32), want[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isinf(got), np.isinf(want))
+
+
+@pytest.mark.parametrize("qtype", ["q4_k", "q6_k", "q8_0"])
+def test_dequant_bit_exact(gpu_ctx, oracle, qtype):
+    _say("case: dequant", qtype)
+    from arf_amd import QType, synth
+    n, k, E = 40, 1024, 3
+    raw = synth.weight(qtype, n, k, seed=101, experts=E)
+    bb = synth.BLOCK_BYTES[qtype]
+    blk = raw.reshape(-1, bb)
+    # f16-subnormal and zero scales in some blocks
+    dofs = {"q4_k": 0, "q8_0": 0, "q6_k": 208}[qtype]
+    blk[::5, dofs:dofs + 2] = np.array([3, 0], np.uint8)
+    blk[1::9, dofs:dofs + 2] = 0
+    w = gpu_ctx.upload({"q4_k": QType.Q4_K, "q6_k": QType.Q6_K, "q8_0": QType.Q8_0}[qtype],
+                       raw, n, k, E)
+    got = gpu_ctx.dequant(w).numpy()
+    want = oracle.dequant(qtype, raw, E * n * k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_dequant_q80_known_closed_form(gpu_ctx):
+    from arf_amd import QType
+    qs = np.arange(-128, 128).reshape(8, 32)
+    blocks = np.concatenate([make_q80_block(0.5, q) for q in qs])
+    w = gpu_ctx.upload(QType.Q8_0, blocks, 1, 256)
+    got = gpu_ctx.dequant(w).numpy()
+    assert np.array_equal(got, 0.5 * np.arange(-128, 128, dtype=np.float32))
+
+
+# ---------------------------------------------------------------- GEMV ----
+def _matmul(ctx, qtype, n, k, m, seed, x_dtype=np.float32, experts=1, expert=0):
+    from arf_amd import QType, synth
+    raw = synth.weight(qtype, n, k, seed=seed, experts=experts)
+    x = synth.activations(m, k, seed=seed + 1).astype(x_dtype)
+    w = ctx.upload({"q4_k": QType.Q4_K, "q6_k": QType.Q6_K, "q8_0": QType.Q8_0}[qtype],
+                   raw, n, k, experts)
+    xd = ctx.to_device(x)
+    y = ctx.empty((m, n), np.float32)
+    ctx.matmul(w, xd, m, y, expert)
+    got = y.numpy()
+    per = raw.size // experts
+    return got, raw[expert * per:(expert + 1) * per], x
+
+
+@pytest.mark.parametrize("qtype,n,k", [
+    ("q4_k", 64, 256), ("q4_k", 37, 1024), ("q4_k", 130, 5120), ("q4_k", 33, 768),
+    ("q8_0", 64, 2048), ("q8_0", 31, 96), ("q8_0", 100, 512),
+    ("q6_k", 64, 4352), ("q6_k", 21, 256), ("q6_k", 50, 17408),
+])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+def test_gemv_small_shapes(gpu_ctx, oracle, qtype, n, k, m):
+    _say("case: gemv", qtype, n, k, m)
+    got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=7 * n + k + m)
+    want = oracle.matmul_q(qtype, x, raw, n)
+    assert rel_err(got, want) <= TOL
+
+
+def test_gemv_expert_offset(gpu_ctx, oracle):
+    _say("case: gemv expert offset")
+    got, raw, x = _matmul(gpu_ctx, "q4_k", 48, 512, 1, seed=5, experts=4, expert=3)
+    assert rel_err(got, oracle.matmul_q("q4_k", x, raw, 48)) <= TOL
+
+
+def test_c1_q8_0_gemv_full(gpu_ctx, oracle):
+    _say("case: C1 full")
+    got, raw, x = _matmul(gpu_ctx, "q8_0", 2048, 2048, 1, seed=0xA7F00001)
+    assert rel_err(got, oracle.matmul_q("q8_0", x, raw, 2048)) <= TOL
+
+
+def test_c2_q4_k_gemv_full(gpu_ctx, oracle):
+    _say("case: C2 full")
+    got, raw, x = _matmul(gpu_ctx, "q4_k", 17408, 5120, 1, seed=0xA7F00002)
+    want = oracle.matmul_q("q4_k", x, raw, 17408)
+    e = rel_err(got, want)
+    _say("C2 rel err", e)
+    assert e <= TOL
+
+
+def test_c3_q6_k_gemv_m1_full(gpu_ctx, oracle):
+    _say("case: C3 m=1 full")
+    got, raw, x = _matmul(gpu_ctx, "q6_k", 5120, 17408, 1, seed=0xA7F00003)
+    e = rel_err(got, oracle.matmul_q("q6_k", x, raw, 5120))
+    _say("C3 m=1 rel err", e)
+    assert e <= TOL
+
+
+def test_shape_errors_raise(gpu_ctx):
+    from arf_amd import QType, synth
+    raw = synth.weight("q4_k", 4, 256, seed=1)
+    with pytest.raises(ValueError):
+        gpu_ctx.upload(QType.Q4_K, raw[:-1], 4, 256)
+    with pytest.raises(ValueError):
+        gpu_ctx.upload(QType.Q4_K, raw, 4, 255)
+    w = gpu_ctx.upload(QType.Q4_K, raw, 4, 256)
+    x = gpu_ctx.to_device(np.zeros((1, 256), np.float32))
+    y = gpu_ctx.empty((1, 4), np.float32)
+    with pytest.raises(ValueError):
+        gpu_ctx.matmul(w, x, 1, y, expert=1)

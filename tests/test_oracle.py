@@ -1,0 +1,296 @@
+"""CPU tests that pin the oracle (oracle/arfq_oracle.c) before it is trusted.
+
+Sources of truth, in order: the reference's own known-answer tests and golden
+gates (quoted with file:line), then closed forms built independently of the
+oracle's code (forward packing + exact rational arithmetic, IEEE conversions,
+float64 matmuls).  A plausible decoder mistake (wrong nibble, quadrant, qh bit
+pair, scale index, sign fold) fails at least one of these exactly.
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from formats import (lcg_q4k_blocks, make_q4k_block, make_q6k_block, make_q80_block,
+                     moe_route_lcg_logits, pack_q4k_scales, q4k_exact, q6k_exact,
+                     ref_make_q4k_block)
+
+
+# ---------------------------------------------------------------- f16 ----
+def test_f16_known_values(oracle):
+    # crates/arf-core/src/model/gguf.rs:2485-2491
+    assert oracle.f16_to_f32(0x3C00) == 1.0
+    assert oracle.f16_to_f32(0x4000) == 2.0
+    assert oracle.f16_to_f32(0xC000) == -2.0
+    assert oracle.f16_to_f32(0x0000) == 0.0
+    assert abs(oracle.f16_to_f32(0x3555) - 0.333) < 1e-3
+
+
+def test_f16_all_patterns_match_ieee(oracle):
+    # all 65536 patterns vs numpy's IEEE binary16 -> binary32 (exact, NaN payload kept)
+    import ctypes
+    L = oracle.lib()
+    bits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = bits.view(np.float16).astype(np.float32).view(np.uint32)
+    got = np.array([L.arfo_f16_to_f32(int(h)) for h in bits], np.float32).view(np.uint32)
+    nan = np.isnan(bits.view(np.float16))
+    assert np.array_equal(got[~nan], want[~nan])
+    # NaNs: ctypes float round trip may quiet a signalling NaN; the class must match
+    assert np.all(np.isnan(got[nan].view(np.float32)))
+
+
+# ------------------------------------------------------- Q4_K scale/min ----
+def test_q4k_scale_min_known(oracle):
+    # gguf.rs:2494-2505
+    assert all(oracle.q4k_get_scale_min([0] * 12, j) == (0, 0) for j in range(8))
+    s = [0] * 12
+    s[0], s[4] = 0b0010_1010, 0b0001_0101
+    assert oracle.q4k_get_scale_min(s, 0) == (42, 21)
+    # gguf.rs:2963-2980 (j>=4 branch): sc = 51, m = 26
+    s = [0] * 12
+    s[0], s[4], s[8] = 0b1100_0101, 0b0100_0111, 0b1010_0011
+    assert oracle.q4k_get_scale_min(s, 4) == (51, 26)
+
+
+def test_q4k_scale_min_roundtrip_random(oracle):
+    rng = np.random.default_rng(7)
+    for _ in range(300):
+        sc = rng.integers(0, 64, 8).tolist()
+        m = rng.integers(0, 64, 8).tolist()
+        packed = pack_q4k_scales(sc, m)
+        for j in range(8):
+            assert oracle.q4k_get_scale_min(packed, j) == (sc[j], m[j])
+
+
+# ------------------------------------------------------------ Q4_K dequant ----
+def test_dequant_q4k_known_block(oracle):
+    # gguf.rs:2522-2538: d=2, dmin=1, sc0=3, m0=5, q=4 -> 19.0; next weight -> -5.0
+    b = np.zeros(144, np.uint8)
+    b[0:2] = np.array([0x4000], np.uint16).view(np.uint8)
+    b[2:4] = np.array([0x3C00], np.uint16).view(np.uint8)
+    b[4], b[8], b[16] = 3, 5, 0x04
+    out = oracle.dequant("q4_k", b, 256)
+    assert out[0] == 19.0 and out[1] == -5.0
+
+
+def test_dequant_q4k_exact_forward_packing(oracle):
+    rng = np.random.default_rng(11)
+    for trial in range(40):
+        d = 2.0 ** int(rng.integers(-8, 2))
+        dmin = 2.0 ** int(rng.integers(-8, 2))
+        sc = rng.integers(0, 64, 8).tolist()
+        m = rng.integers(0, 64, 8).tolist()
+        q = rng.integers(0, 16, 256).tolist()
+        blk = make_q4k_block(d, dmin, sc, m, q)
+        got = oracle.dequant("q4_k", blk, 256)
+        want = np.array([float(v) for v in q4k_exact(d, dmin, sc, m, q)], np.float64)
+        assert np.array_equal(got.astype(np.float64), want), trial
+
+
+def _q4ks_bit_exact(oracle, raw, rows, cols, label):
+    ggml = oracle.dequant("q4_k", raw, rows * cols)
+    q4ks = oracle.q4ks_to_f32(oracle.q4ks_from_ggml(raw, rows, cols), rows, cols)
+    assert np.array_equal(ggml.view(np.uint32), q4ks.view(np.uint32)), label
+    return ggml
+
+
+def test_from_ggml_q4k_is_bit_exact_gate(oracle):
+    # crates/arf-core/src/model/gguf.rs:2862-2982, cases (a)-(e)
+    sc = np.zeros(12, np.uint8); sc[0], sc[4] = 3, 5
+    qs = np.zeros(128, np.uint8); qs[0] = 0x04
+    out = _q4ks_bit_exact(oracle, ref_make_q4k_block(2.0, 1.0, sc, qs), 1, 256, "known_block")
+    assert out[0] == 19.0
+    sc = np.zeros(12, np.uint8); sc[1], sc[5] = 10, 63
+    qs = np.zeros(128, np.uint8); qs[0] = 0x70
+    out = _q4ks_bit_exact(oracle, ref_make_q4k_block(1.0, 0.5, sc, qs), 1, 256, "sign_fold_m63")
+    assert out[32] == np.float32(10.0 * 7 - 31.5)  # sub-block 1, weight 0: 1*10*7 - 0.5*63
+    raw = lcg_q4k_blocks(0x12345678, 3, 1.0, 64.0, 0.5, 128.0)
+    _q4ks_bit_exact(oracle, raw, 1, 768, "pseudo_random_1row_3blocks")
+    raw = lcg_q4k_blocks(0xDEADBEEF, 2, 2.0, 128.0, 1.0, 256.0)
+    _q4ks_bit_exact(oracle, raw, 2, 256, "multi_row_2x256")
+    sc = np.zeros(12, np.uint8)
+    sc[0], sc[4], sc[8] = 0b1100_0101, 0b0100_0111, 0b1010_0011
+    qs = np.zeros(128, np.uint8); qs[64] = 0x0F
+    out = _q4ks_bit_exact(oracle, ref_make_q4k_block(0.25, 0.125, sc, qs), 1, 256,
+                          "high_scale_path_j4")
+    assert out[128] == np.float32(0.25 * 51 * 15 - 0.125 * 26)
+
+
+def test_q4ks_transcode_bit_exact_random_with_subnormals(oracle):
+    from arf_amd import synth
+    raw = synth.weight("q4_k", 8, 1024, seed=5).reshape(-1, 144)
+    raw[::7, 0:2] = np.array([1, 0], np.uint8)  # smallest f16 subnormal d
+    raw[3::11, 2:4] = np.array([0x17, 0x02], np.uint8)  # subnormal dmin
+    _q4ks_bit_exact(oracle, raw.reshape(-1), 8, 1024, "random_subnormal")
+
+
+# ------------------------------------------------------------ Q6_K dequant ----
+def test_dequant_q6k_known_block(oracle):
+    # gguf.rs:2564-2575: d=0.5, sc0=4, ql0=10 -> -44.0
+    b = np.zeros(210, np.uint8)
+    b[192], b[0] = 4, 10
+    b[208:210] = np.array([0x3800], np.uint16).view(np.uint8)
+    assert oracle.dequant("q6_k", b, 256)[0] == -44.0
+
+
+def test_dequant_q6k_exact_forward_packing(oracle):
+    rng = np.random.default_rng(13)
+    for trial in range(40):
+        d = 2.0 ** int(rng.integers(-10, 1))
+        sc = rng.integers(-32, 32, 16).tolist()
+        q = rng.integers(0, 64, 256).tolist()
+        got = oracle.dequant("q6_k", make_q6k_block(d, sc, q), 256)
+        want = np.array([float(v) for v in q6k_exact(d, sc, q)], np.float64)
+        assert np.array_equal(got.astype(np.float64), want), trial
+
+
+def test_dequant_q6k_each_quadrant_and_qh_pair(oracle):
+    # one nonzero code at a time: every (half, quadrant, qh pair, scale slot)
+    for e in range(0, 256, 5):
+        for hi in range(4):
+            q = [32] * 256
+            q[e] = (hi << 4) | (e % 16)
+            sc = list(range(1, 17))
+            got = oracle.dequant("q6_k", make_q6k_block(1.0, sc, q), 256)
+            want = np.zeros(256)
+            want[e] = sc[e // 16] * (q[e] - 32)
+            assert np.array_equal(got, want), (e, hi)
+
+
+# ------------------------------------------------------------ Q8_0 dequant ----
+def test_dequant_q80_closed_form(oracle):
+    qs = np.arange(-128, 128, dtype=np.int32)
+    for d in (1.0, 0.5, 0.001, 6.0e-8, 65504.0):
+        blocks = np.concatenate([make_q80_block(d, qs[i:i + 32]) for i in range(0, 256, 32)])
+        got = oracle.dequant("q8_0", blocks, 256)
+        want = np.float32(np.float16(d)) * qs.astype(np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), d
+
+
+# --------------------------------------------------------------- matmuls ----
+def test_matmul_nt_matches_float64(oracle):
+    # crates/arf-ml/src/matmul.rs:516-531 (nt vs standard, k not a multiple of 8)
+    for (m, k, n) in [(3, 13, 5), (64, 40, 64), (4, 300, 33)]:
+        a = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+        b = np.random.default_rng(n).standard_normal((n, k)).astype(np.float32)
+        got = oracle.matmul_nt(a, b)
+        want = a.astype(np.float64) @ b.astype(np.float64).T
+        assert np.max(np.abs(got - want)) < 1e-4
+
+
+def test_matmul_nt_integer_exact(oracle):
+    # crates/arf-ml/src/matmul.rs:551-566 (parallel path == serial), integer data -> exact
+    a = (np.arange(64 * 40) % 7).astype(np.float32).reshape(64, 40)
+    b = (np.arange(64 * 40) % 5).astype(np.float32).reshape(64, 40)
+    assert np.array_equal(oracle.matmul_nt(a, b), (a.astype(np.int64) @ b.astype(np.int64).T))
+
+
+@pytest.mark.parametrize("qtype,k", [("q4_k", 512), ("q6_k", 512), ("q8_0", 256)])
+def test_quantized_linear_equals_dequant_matmul(oracle, qtype, k):
+    # weight.rs:1693-1709: quantized linear == dequant + f32 matmul
+    from arf_amd import synth
+    n, m = 24, 3
+    blocks = synth.weight(qtype, n, k, seed=17)
+    x = synth.activations(m, k, seed=18)
+    w = oracle.dequant(qtype, blocks, n * k).reshape(n, k).astype(np.float64)
+    want = x.astype(np.float64) @ w.T
+    got = oracle.matmul_q(qtype, x, blocks, n)
+    assert rel_err(got, want) < 1e-5
+
+
+def test_quantized_matmul_exact_on_integer_inputs(oracle):
+    # power-of-two scales + integer activations: every f32 op is exact
+    rng = np.random.default_rng(3)
+    n, k = 4, 512
+    blocks, wexact = [], []
+    for r in range(n):
+        for sb in range(k // 256):
+            sc = rng.integers(0, 64, 8).tolist(); m = rng.integers(0, 64, 8).tolist()
+            q = rng.integers(0, 16, 256).tolist()
+            blocks.append(make_q4k_block(0.25, 0.5, sc, m, q))
+            wexact += [float(v) for v in q4k_exact(0.25, 0.5, sc, m, q)]
+    W = np.array(wexact).reshape(n, k)
+    x = rng.integers(-3, 4, (2, k)).astype(np.float32)
+    got = oracle.matmul_q("q4_k", x, np.concatenate(blocks), n)
+    assert np.array_equal(got.astype(np.float64), x.astype(np.float64) @ W.T)
+
+
+def test_par_rows_threads_do_not_change_result(oracle):
+    from arf_amd import synth
+    blocks = synth.weight("q4_k", 64, 512, seed=1)
+    x = synth.activations(16, 512, seed=2)
+    oracle.set_threads(1)
+    serial = oracle.matmul_q("q4_k", x, blocks, 64)
+    oracle.set_threads(0)
+    par = oracle.matmul_q("q4_k", x, blocks, 64)
+    assert np.array_equal(serial, par)
+
+
+# ------------------------------------------------------------ routing ----
+def test_top_k_softmax_reference_cases(oracle):
+    # crates/arf-core/src/model/moe.rs:134-159
+    ids, w = oracle.top_k_softmax([2.0, -1.0, 3.0, 0.0], 2, True)
+    assert ids.tolist() == [2, 0] and abs(w.sum() - 1.0) < 1e-6 and w[0] > w[1]
+    ids, w = oracle.top_k_softmax([2.0, -1.0, 3.0, 0.0], 2, False)
+    assert 0.5 < w.sum() < 1.0
+    ids, _ = oracle.top_k_softmax([1.0, 1.0, 1.0, 1.0], 2, True)
+    assert ids.tolist() == [0, 1]
+
+
+def test_top_k_softmax_128_expert_lcg_cases(oracle):
+    # crates/arf-gpu/tests/moe_gpu.rs:84-93: two 128-expert top-8 cases, seed 99
+    state = 99
+    for norm in (True, False):
+        logits, state = moe_route_lcg_logits(128, state)
+        ids, w = oracle.top_k_softmax(logits, 8, norm)
+        p = np.exp(logits.astype(np.float64) - logits.max())
+        p /= p.sum()
+        order = sorted(range(128), key=lambda i: (-p[i], i))[:8]
+        assert ids.tolist() == order
+        want = p[order] / (p[order].sum() if norm else 1.0)
+        assert np.max(np.abs(w - want)) < 1e-6
+
+
+# ---------------------------------------------------------------- MoE ----
+def _silu64(v):
+    return v / (1.0 + np.exp(-v))
+
+
+def test_moe_forward_matches_float64_composition(oracle):
+    from arf_amd import synth
+    E, hidden, inter, T, top_k = 4, 256, 256, 3, 2
+    gate = synth.weight("q4_k", inter, hidden, seed=31, experts=E)
+    up = synth.weight("q4_k", inter, hidden, seed=32, experts=E)
+    down = synth.weight("q4_k", hidden, inter, seed=33, experts=E)
+    x = synth.activations(T, hidden, seed=34)
+    logits = synth.router_logits(T, E, seed=35)
+    got = oracle.moe_forward(x, gate, up, down, E, inter, logits, top_k, True)
+    G = oracle.dequant("q4_k", gate, E * inter * hidden).reshape(E, inter, hidden).astype(np.float64)
+    U = oracle.dequant("q4_k", up, E * inter * hidden).reshape(E, inter, hidden).astype(np.float64)
+    D = oracle.dequant("q4_k", down, E * hidden * inter).reshape(E, hidden, inter).astype(np.float64)
+    want = np.zeros((T, hidden))
+    for t in range(T):
+        p = np.exp(logits[t].astype(np.float64) - logits[t].max()); p /= p.sum()
+        ids = sorted(range(E), key=lambda i: (-p[i], i))[:top_k]
+        wts = p[ids] / p[ids].sum()
+        xt = x[t].astype(np.float64)
+        for e, wt in zip(ids, wts):
+            h = _silu64(G[e] @ xt) * (U[e] @ xt)
+            want[t] += wt * (D[e] @ h)
+    assert rel_err(got, want) < 1e-4
+
+
+def test_moe_one_hot_router_is_the_expert(oracle):
+    from arf_amd import synth
+    E, hidden, inter = 3, 256, 256
+    gate = synth.weight("q4_k", inter, hidden, seed=41, experts=E)
+    up = synth.weight("q4_k", inter, hidden, seed=42, experts=E)
+    down = synth.weight("q4_k", hidden, inter, seed=43, experts=E)
+    x = synth.activations(1, hidden, seed=44)
+    logits = np.array([[-1e4, 30.0, -1e4]], np.float32)  # all mass on expert 1
+    got = oracle.moe_forward(x, gate, up, down, E, inter, logits, 1, True)
+    gb = gate.reshape(E, -1)[1]; ub = up.reshape(E, -1)[1]; db = down.reshape(E, -1)[1]
+    g = oracle.matmul_q("q4_k", x, gb, inter)
+    u = oracle.matmul_q("q4_k", x, ub, inter)
+    h = (g / (1 + np.exp(-g))) * u
+    y = oracle.matmul_q("q4_k", h.astype(np.float32), db, hidden)
+    assert rel_err(got, y) < 1e-6
