@@ -6,7 +6,14 @@
 // separate 256-B aligned allocation; blocks are ordered expert-major, then row,
 // then along k):
 //   Q4_K  hdr[nblk] 16 B  = d(f16) | dmin(f16) | scales[12]   (ggml bytes 0..15)
-//         qs [nblk] 128 B = ggml bytes 16..143 verbatim
+//         qs [nblk] 128 B = the 256 nibbles regrouped per sub-block: dword 4j+w
+//                           holds elements 32j+8w .. 32j+8w+7 of sub-block j; its
+//                           byte i (0..3) holds element 32j+8w+i in the low nibble
+//                           and element 32j+8w+4+i in the high nibble (nibble
+//                           position p <-> element 8w + q4k_sigma(p)).  The order
+//                           matches how the GEMV packs x digits with v_perm.
+//                           ggml stores element 32j+i in byte 32*(j/2)+i, low
+//                           nibble for even j, high for odd j.
 //   Q8_0  qs [nblk] 32 B  = the 32 i8 codes;   d[nblk] f16
 //   Q6_K  qb [nblk] 192 B = 4 chunks of 48 B; chunk c (n2 = c/2, l0 = 16*(c%2)):
 //                           ql[64n2+l0 .. +16] | ql[64n2+32+l0 .. +16] | qh[32n2+l0 .. +16]
@@ -36,6 +43,11 @@ __device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
     const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
     return make_uint4(v.x, v.y, v.z, v.w);
 }
+
+// nibble position p (0..7) of a Q4_K code dword -> element offset within its
+// 8-element group; and the inverse
+__host__ __device__ constexpr int q4k_sigma(int p) { return (p & 1) ? 4 + (p >> 1) : (p >> 1); }
+__host__ __device__ constexpr int q4k_sigma_inv(int t) { return t < 4 ? 2 * t : 2 * (t - 4) + 1; }
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 

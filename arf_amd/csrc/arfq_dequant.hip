@@ -14,9 +14,21 @@ __global__ void repack_q4k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
     if (b >= nblk) return;
     const uint8_t *src = raw + b * 144;
     uint8_t *h = hdr + b * 16;
-    uint8_t *q = qs + b * 128;
     for (int i = 0; i < 16; i++) h[i] = src[i];
-    for (int i = 0; i < 128; i++) q[i] = src[16 + i];
+    // regroup nibbles per sub-block: element 32j+i lives in ggml byte
+    // 32*(j/2)+i, low nibble for even j, high nibble for odd j; it goes to
+    // dword 4j + i/8, nibble position q4k_sigma_inv(i%8)
+    uint32_t *q = reinterpret_cast<uint32_t *>(qs + b * 128);
+    for (int j = 0; j < 8; j++) {
+        const uint8_t *g = src + 16 + 32 * (j >> 1);
+        const int sh = (j & 1) * 4;
+        for (int w = 0; w < 4; w++) {
+            uint32_t v = 0;
+            for (int t = 0; t < 8; t++)
+                v |= (uint32_t)((g[8 * w + t] >> sh) & 0xF) << (4 * q4k_sigma_inv(t));
+            q[4 * j + w] = v;
+        }
+    }
 }
 
 __global__ void repack_q80(const uint8_t *__restrict__ raw, uint8_t *__restrict__ qs,
@@ -72,7 +84,7 @@ hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s
 // ---- dequant -----------------------------------------------------------------
 
 // One thread per (block, sub-block j): 32 outputs.
-__global__ void dequant_q4k(const uint4 *__restrict__ hdr, const uint8_t *__restrict__ qs,
+__global__ void dequant_q4k(const uint4 *__restrict__ hdr, const uint32_t *__restrict__ qs,
                             float *__restrict__ out, int64_t nblk) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= nblk * 8) return;
@@ -84,10 +96,10 @@ __global__ void dequant_q4k(const uint4 *__restrict__ hdr, const uint8_t *__rest
     q4k_scale_min(h.y, h.z, h.w, j, sc, m);
     const float d1 = q4k_d1(d, sc);
     const float m1 = q4k_d1(dmin, m);
-    const uint8_t *q = qs + b * 128 + (j >> 1) * 32;
-    const int shift = (j & 1) * 4;
+    const uint32_t *q = qs + b * 32 + j * 4;
     float *o = out + b * 256 + j * 32;
-    for (int i = 0; i < 32; i++) o[i] = q4k_weight(d1, m1, (q[i] >> shift) & 0xFu);
+    for (int i = 0; i < 32; i++)
+        o[i] = q4k_weight(d1, m1, (q[i >> 3] >> (4 * q4k_sigma_inv(i & 7))) & 0xFu);
 }
 
 __global__ void dequant_q80(const int8_t *__restrict__ qs, const uint16_t *__restrict__ d,
@@ -122,7 +134,7 @@ hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s) {
     switch (w->qtype) {
     case ARFQ_Q4_K: {
         const unsigned grid = (unsigned)((w->nblk * 8 + tpb - 1) / tpb);
-        dequant_q4k<<<grid, tpb, 0, s>>>((const uint4 *)w->s0, (const uint8_t *)w->s1, out,
+        dequant_q4k<<<grid, tpb, 0, s>>>((const uint4 *)w->s0, (const uint32_t *)w->s1, out,
                                          w->nblk);
         break;
     }

@@ -83,6 +83,7 @@ int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
             ctx->own_stream = (e == hipSuccess);
         }
     }
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, device);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_stop);
     if (e != hipSuccess) {

@@ -11,6 +11,7 @@
 
 struct arfq_ctx {
     int device = 0;
+    int cus = 0;  // compute units of the device
     hipStream_t stream = nullptr;
     bool own_stream = false;
     std::string err;
