@@ -23,6 +23,9 @@ FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # no packed-FP32 VALU ops in device code (v_pk_{add,mul,fma}_f32)
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # atomics here are issued by one chosen lane on purpose; the wave-level
+    # aggregation the optimizer adds (a lane-scan loop) only costs time
+    "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
     "-Wall", "-Wno-unused-function", "-Wno-unused-command-line-argument",
     "-I", os.path.join(HERE, "..", "include"),
 ]

@@ -201,20 +201,39 @@ __device__ __forceinline__ void xq_process(const XqRound &r, int items, int base
 }
 
 // (d*sc_j, dmin*m_j) of sub-block j from a Q4_K header (ggml get_scale_min_k4,
-// crates/arf-ml/src/weight.rs:1353-1365), branch-free for a lane-dependent j.
+// crates/arf-ml/src/weight.rs:1353-1365), branch-free for a lane-dependent j:
+// two v_perm gather byte j%4 of scales[0..3], scales[4..7], scales[8..11] into
+// D = [A, B, C, 0]; then
+//   j < 4:  sc = A & 63,                 m = B & 63
+//   j >= 4: sc = (C & 15) | (A>>6)<<4,   m = (C >> 4) | (B>>6)<<4
+// are each two bit-field extracts (width 0 yields 0) and a shift-or.
 struct Q4kLane {
-    uint32_t sh;  // 8*(j%4)
-    bool hi;      // j >= 4
+    uint32_t sel1, sel2;          // v_perm selectors
+    uint32_t o1, w1, o2, w2;      // sc = bfe(D,o1,w1) | bfe(D,o2,w2) << 4
+    uint32_t o3, w3, o4, w4;      // m  = bfe(D,o3,w3) | bfe(D,o4,w4) << 4
 };
 
-__device__ __forceinline__ void q4k_sub_scales(const uint4 h, const Q4kLane L, float &d1,
+__device__ __forceinline__ Q4kLane q4k_lane(int j) {
+    const uint32_t i = (uint32_t)(j & 3);
+    Q4kLane L;
+    L.sel1 = i | ((4u + i) << 8) | (0x0Cu << 16) | (0x0Cu << 24);
+    L.sel2 = 0u | (1u << 8) | ((4u + i) << 16) | (0x0Cu << 24);
+    if (j < 4) {
+        L.o1 = 0; L.w1 = 6; L.o2 = 0; L.w2 = 0;
+        L.o3 = 8; L.w3 = 6; L.o4 = 0; L.w4 = 0;
+    } else {
+        L.o1 = 16; L.w1 = 4; L.o2 = 6; L.w2 = 2;
+        L.o3 = 20; L.w3 = 4; L.o4 = 14; L.w4 = 2;
+    }
+    return L;
+}
+
+__device__ __forceinline__ void q4k_sub_scales(const uint4 h, const Q4kLane &L, float &d1,
                                                float &m1) {
-    const uint32_t A = h.y >> L.sh, B = h.z >> L.sh, C = h.w >> L.sh;
-    const uint32_t sc_lo = A & 63u, m_lo = B & 63u;
-    const uint32_t sc_hi = (C & 15u) | ((A >> 2) & 48u);
-    const uint32_t m_hi = ((C >> 4) & 15u) | ((B >> 2) & 48u);
-    const uint32_t sc = L.hi ? sc_hi : sc_lo;
-    const uint32_t mm = L.hi ? m_hi : m_lo;
+    const uint32_t T = __builtin_amdgcn_perm(h.z, h.y, L.sel1);
+    const uint32_t D = __builtin_amdgcn_perm(h.w, T, L.sel2);
+    const uint32_t sc = __builtin_amdgcn_ubfe(D, L.o1, L.w1) | (__builtin_amdgcn_ubfe(D, L.o2, L.w2) << 4);
+    const uint32_t mm = __builtin_amdgcn_ubfe(D, L.o3, L.w3) | (__builtin_amdgcn_ubfe(D, L.o4, L.w4) << 4);
     d1 = h2f(h.x) * (float)sc;
     m1 = h2f(h.x >> 16) * (float)mm;
 }
@@ -286,7 +305,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     const int ll = tid & 31;
     const int g = tid >> 5;
     const int j = ll & 7, bq = ll >> 3;
-    const Q4kLane L{(uint32_t)(8 * (j & 3)), j >= 4};
+    const Q4kLane L = q4k_lane(j);
     const uint32_t *hdr32 = reinterpret_cast<const uint32_t *>(hdr);
 
     const int G = gridDim.x;
