@@ -245,12 +245,36 @@ static int check_matmul(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t
     return ARFQ_OK;
 }
 
+// Grow the context scratch to at least `bytes` (synchronises the stream first
+// when it has to reallocate, since enqueued work may still use the old block).
+static int ensure_scratch(arfq_ctx *ctx, size_t bytes) {
+    if (ctx->scratch_bytes >= bytes) return ARFQ_OK;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+    const size_t sz = (bytes + 0xFFFFF) & ~(size_t)0xFFFFF;
+    hipError_t e = hipMalloc(&ctx->scratch, sz);
+    if (e != hipSuccess) return fail(ctx, ARFQ_E_NOMEM, std::string("scratch: ") + hipGetErrorString(e));
+    ctx->scratch_bytes = sz;
+    return ARFQ_OK;
+}
+
 static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m,
                           const void *x, int x_dtype, float *y) {
     hipError_t e;
     if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
         e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream);
     } else if (arfq::gemm_supports(w, m)) {
+        if (x_dtype == ARFQ_F32) {
+            // the MFMA path reads f16 activations: round x once into scratch
+            const int64_t cnt = m * w->k;
+            if (int rc = ensure_scratch(ctx, (size_t)cnt * 2)) return rc;
+            e = arfq::launch_f32_to_f16((const float *)x, (__half *)ctx->scratch, cnt, ctx->stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "f32->f16 launch");
+            x = ctx->scratch;
+            x_dtype = ARFQ_F16;
+        }
         e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->stream);
     } else {
         return fail(ctx, ARFQ_E_UNSUPPORTED,

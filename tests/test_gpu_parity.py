@@ -136,3 +136,38 @@ def test_shape_errors_raise(gpu_ctx):
     y = gpu_ctx.empty((1, 4), np.float32)
     with pytest.raises(ValueError):
         gpu_ctx.matmul(w, x, 1, y, expert=1)
+
+
+# ---------------------------------------------------------------- GEMM ----
+@pytest.mark.parametrize("m,n,k", [(8, 64, 256), (130, 200, 512), (300, 128, 1024),
+                                   (64, 17, 768), (257, 129, 5120)])
+def test_gemm_q4k_f16_small(gpu_ctx, oracle, m, n, k):
+    _say("case: gemm q4k f16", m, n, k)
+    got, raw, x = _matmul(gpu_ctx, "q4_k", n, k, m, seed=3 * m + n + k, x_dtype=np.float16)
+    want = oracle.matmul_q("q4_k", x.astype(np.float32), raw, n)
+    e = rel_err(got, want)
+    _say("rel err", e)
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("m", [5, 16, 64])
+def test_gemm_q4k_f32_x(gpu_ctx, oracle, m):
+    # m > 4 with f32 x goes through the MFMA path (x rounded to f16 once)
+    _say("case: gemm q4k f32 x", m)
+    got, raw, x = _matmul(gpu_ctx, "q4_k", 96, 2048, m, seed=91 + m)
+    e = rel_err(got, oracle.matmul_q("q4_k", x, raw, 96))
+    _say("rel err", e)
+    assert e <= TOL
+
+
+def test_c4_q4_k_gemm_full(gpu_ctx, oracle):
+    # full C4 shape on the GPU; the oracle checks a sample of 48 x rows
+    _say("case: C4 full")
+    m, n, k = 2048, 17408, 5120
+    got, raw, x = _matmul(gpu_ctx, "q4_k", n, k, m, seed=0xA7F00004, x_dtype=np.float16)
+    rows = np.r_[0:16, 1016:1032, 2032:2048]
+    want = oracle.matmul_q("q4_k", x[rows].astype(np.float32), raw, n)
+    e = rel_err(got[rows], want)
+    _say("C4 rel err (48 sampled rows)", e)
+    assert e <= TOL
+    assert np.all(np.isfinite(got))
