@@ -266,16 +266,31 @@ static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64
     if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
         e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream);
     } else if (arfq::gemm_supports(w, m)) {
+        // MFMA path.  f16 x is used as given; f32 x is rounded to f16 once for
+        // prefill shapes (m > 64, as the reference's half tiles do) and split
+        // into an f16 hi + lo pair for batched decode (m <= 64), where the
+        // path is bound by weight bytes and the second MFMA is free.
+        const bool xsplit = x_dtype == ARFQ_F32 && m <= 64;
+        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, xsplit);
+        const int64_t cnt = m * w->k;
+        const size_t xbytes = x_dtype == ARFQ_F32 ? (size_t)cnt * 2 * (xsplit ? 2 : 1) : 0;
+        const size_t xoff = (xbytes + 255) & ~(size_t)255;
+        const size_t pbytes = plan.splits > 1 ? (size_t)plan.splits * m * w->n * sizeof(float) : 0;
+        if (int rc = ensure_scratch(ctx, xoff + pbytes)) return rc;
+        const _Float16 *xh = (const _Float16 *)x, *xl = nullptr;
         if (x_dtype == ARFQ_F32) {
-            // the MFMA path reads f16 activations: round x once into scratch
-            const int64_t cnt = m * w->k;
-            if (int rc = ensure_scratch(ctx, (size_t)cnt * 2)) return rc;
-            e = arfq::launch_f32_to_f16((const float *)x, (__half *)ctx->scratch, cnt, ctx->stream);
-            if (e != hipSuccess) return hip_fail(ctx, e, "f32->f16 launch");
-            x = ctx->scratch;
-            x_dtype = ARFQ_F16;
+            __half *hh = (__half *)ctx->scratch;
+            if (xsplit) {
+                e = arfq::launch_split_f32((const float *)x, hh, hh + cnt, cnt, ctx->stream);
+                xl = (const _Float16 *)(hh + cnt);
+            } else {
+                e = arfq::launch_f32_to_f16((const float *)x, hh, cnt, ctx->stream);
+            }
+            if (e != hipSuccess) return hip_fail(ctx, e, "x conversion launch");
+            xh = (const _Float16 *)hh;
         }
-        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->stream);
+        float *partials = pbytes ? (float *)((char *)ctx->scratch + xoff) : nullptr;
+        e = arfq::launch_gemm(w, expert, m, xh, xl, y, partials, plan, ctx->stream);
     } else {
         return fail(ctx, ARFQ_E_UNSUPPORTED,
                     "matmul: no kernel for qtype " + std::to_string(w->qtype) + " at m=" +

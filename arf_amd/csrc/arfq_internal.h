@@ -56,11 +56,21 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
 bool gemv_supports(const arfq_weight *w, int64_t m);
 
 // ---- arfq_gemm.hip ----
-// Dequant-into-LDS MFMA GEMM for expert `e`, x f32 or f16 (row-major [m, k]).
-hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
-                       float *y, hipStream_t s);
+// Launch shape of the dequant-into-LDS MFMA GEMM.
+struct GemmPlan {
+    int bm = 128;         // x rows per workgroup tile (64 or 128)
+    int splits = 1;       // split-K factor (partials [splits][m][n] then a reduce)
+    bool xsplit = false;  // x given as f16 hi + lo (an f32 x split in two)
+};
+GemmPlan gemm_plan(const arfq_weight *w, int64_t m, bool xsplit);
 bool gemm_supports(const arfq_weight *w, int64_t m);
-// Convert x f32 -> f16 (used when a GEMM path needs half activations).
+// y[m, n] = x[m, k] . W_e^T with x = xh (+ xl when plan.xsplit), row-major f16.
+// `partials` holds splits * m * n floats when plan.splits > 1.
+hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const _Float16 *xh,
+                       const _Float16 *xl, float *y, float *partials, const GemmPlan &p,
+                       hipStream_t s);
+// x f32 -> f16 (round to nearest), and x f32 -> hi + lo f16 pair.
 hipError_t launch_f32_to_f16(const float *x, __half *y, int64_t n, hipStream_t s);
+hipError_t launch_split_f32(const float *x, __half *hi, __half *lo, int64_t n, hipStream_t s);
 
 }  // namespace arfq

@@ -150,13 +150,51 @@ def test_gemm_q4k_f16_small(gpu_ctx, oracle, m, n, k):
     assert e <= TOL
 
 
-@pytest.mark.parametrize("m", [5, 16, 64])
-def test_gemm_q4k_f32_x(gpu_ctx, oracle, m):
-    # m > 4 with f32 x goes through the MFMA path (x rounded to f16 once)
-    _say("case: gemm q4k f32 x", m)
-    got, raw, x = _matmul(gpu_ctx, "q4_k", 96, 2048, m, seed=91 + m)
-    e = rel_err(got, oracle.matmul_q("q4_k", x, raw, 96))
+@pytest.mark.parametrize("m", [5, 16, 64, 65, 200])
+@pytest.mark.parametrize("qtype,n,k", [("q4_k", 96, 2048), ("q6_k", 130, 1792), ("q8_0", 77, 1216)])
+def test_gemm_f32_x(gpu_ctx, oracle, qtype, n, k, m):
+    # m > 4 goes through the MFMA path: f32 x split into an f16 hi + lo pair
+    # for m <= 64, rounded to f16 above
+    _say("case: gemm f32 x", qtype, n, k, m)
+    got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=91 + m + n)
+    e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
     _say("rel err", e)
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("qtype,m,n,k", [("q6_k", 33, 64, 4096), ("q8_0", 129, 300, 640),
+                                         ("q6_k", 256, 136, 512)])
+def test_gemm_f16_x_other_formats(gpu_ctx, oracle, qtype, m, n, k):
+    _say("case: gemm f16 x", qtype, m, n, k)
+    got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=5 * m + n, x_dtype=np.float16)
+    e = rel_err(got, oracle.matmul_q(qtype, x.astype(np.float32), raw, n))
+    _say("rel err", e)
+    assert e <= TOL
+
+
+def test_gemm_split_k_is_deterministic(gpu_ctx):
+    # a skinny shape runs split-K; the ordered reduction gives the same bits twice
+    from arf_amd import QType, synth
+    n, k, m = 256, 8192, 8
+    raw = synth.weight("q4_k", n, k, seed=17)
+    w = gpu_ctx.upload(QType.Q4_K, raw, n, k)
+    x = gpu_ctx.to_device(synth.activations(m, k, seed=18))
+    y1 = gpu_ctx.empty((m, n), np.float32)
+    y2 = gpu_ctx.empty((m, n), np.float32)
+    gpu_ctx.matmul(w, x, m, y1)
+    gpu_ctx.matmul(w, x, m, y2)
+    assert np.array_equal(y1.numpy().view(np.uint32), y2.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("m", [8, 32, 64])
+def test_c3_q6_k_batched_decode_full(gpu_ctx, oracle, m):
+    # C3: Q6_K K=17408 N=5120 at decode batch m; the oracle checks 4 x rows
+    _say("case: C3 full m =", m)
+    n, k = 5120, 17408
+    got, raw, x = _matmul(gpu_ctx, "q6_k", n, k, m, seed=0xA7F00003 + m)
+    rows = np.array([0, 1, m // 2, m - 1])
+    e = rel_err(got[rows], oracle.matmul_q("q6_k", x[rows], raw, n))
+    _say("C3 rel err", e)
     assert e <= TOL
 
 
