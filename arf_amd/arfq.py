@@ -77,6 +77,7 @@ _SIGS = {
     "arfq_dev_free": (_int, [_vp, _vp]),
     "arfq_copy_h2d": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
     "arfq_copy_d2h": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "arfq_copy_d2d": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
     "arfq_timer_start": (_int, [_vp]),
     "arfq_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
     "arfq_matmul_repeat": (_int, [_vp, ctypes.POINTER(_vp), _int, _int, _i64, _vp, _int, _vp]),
@@ -266,6 +267,13 @@ class Context:
         _check(self.handle, load_library().arfq_moe_ids(
             self.handle, gate.handle, up.handle, down.handle, ids.ptr, weights.ptr, int(tokens),
             int(top_k), x.ptr, int(xd), y.ptr))
+
+    def copy_d2d(self, dst, src, nbytes=None):
+        """Enqueue dst <- src (device arrays) on the context's stream."""
+        nb = src.nbytes if nbytes is None else int(nbytes)
+        if nb > dst.nbytes or nb > src.nbytes:
+            raise ValueError("copy_d2d: size")
+        _check(self.handle, load_library().arfq_copy_d2d(self.handle, dst.ptr, src.ptr, nb))
 
     # -- timing --
     def timer_start(self):

@@ -9,6 +9,8 @@
 
 #include "arfq_internal.h"
 
+#include <algorithm>
+
 namespace {
 
 thread_local std::string g_create_err;
@@ -361,6 +363,29 @@ int arfq_copy_d2h(arfq_ctx *ctx, void *dst, const void *src, size_t bytes) {
     if (int rc = use_device(ctx)) return rc;
     HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
     HIP_TRY(ctx, hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return ARFQ_OK;
+}
+
+// One 16-byte load and store per lane, grid-stride.
+__global__ void copy16_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = src[i];
+}
+
+int arfq_copy_d2d(arfq_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (!ctx || (!dst && bytes) || (!src && bytes)) return fail(ctx, ARFQ_E_INVALID, "copy_d2d: null");
+    if (int rc = use_device(ctx)) return rc;
+    if (bytes == 0) return ARFQ_OK;
+    if ((((uintptr_t)dst | (uintptr_t)src | bytes) & 15) == 0) {
+        const int64_t n = (int64_t)(bytes / 16);
+        const int64_t want = (n + 255) / 256;
+        const unsigned grid = (unsigned)std::min<int64_t>(want, (int64_t)std::max(ctx->cus, 1) * 16);
+        copy16_kernel<<<grid, 256, 0, ctx->stream>>>((const uint4 *)src, (uint4 *)dst, n);
+        HIP_TRY(ctx, hipGetLastError());
+    } else {
+        HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    }
     return ARFQ_OK;
 }
 

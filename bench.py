@@ -91,6 +91,34 @@ def load_traffic(name):
     return None
 
 
+COPY_PROBE_BYTES = 256 << 20
+COPY_PROBE_LAUNCHES = 4
+TRAFFIC_PROBE_LAUNCHES = 16
+
+
+def traffic_probe(ctx, copies):
+    """Kernels for the HBM byte counters (FETCH_SIZE / WRITE_SIZE, one rocprofv3
+    --pmc pass each): COPY_PROBE_LAUNCHES copies of COPY_PROBE_BYTES (the known
+    size that calibrates the counters: a copy reads and writes exactly that many
+    bytes), then TRAFFIC_PROBE_LAUNCHES C2 GEMVs rotating `copies` weights, as
+    in the timed loop."""
+    from arf_amd import QType, synth
+    a = ctx.empty((COPY_PROBE_BYTES,), np.uint8)
+    b = ctx.empty((COPY_PROBE_BYTES,), np.uint8)
+    for _ in range(COPY_PROBE_LAUNCHES):
+        ctx.copy_d2d(b, a)
+    ctx.sync()
+    n, k = 17408, 5120
+    raw = synth.weight("q4_k", n, k, seed=0xA7F00002)
+    ws = [ctx.upload(QType.Q4_K, raw, n, k) for _ in range(copies)]
+    x = ctx.to_device(synth.activations(1, k, seed=0xA7F00003))
+    y = ctx.empty((1, n), np.float32)
+    ctx.matmul_repeat(ws, TRAFFIC_PROBE_LAUNCHES, 1, x, y)
+    ctx.sync()
+    log(f"[probe] {COPY_PROBE_LAUNCHES} copies of {COPY_PROBE_BYTES} B, "
+        f"{TRAFFIC_PROBE_LAUNCHES} C2 GEMVs over {copies} weight copies")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -100,6 +128,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
+                         "calibration), then TRAFFIC_PROBE_LAUNCHES C2 GEMVs; prints no JSON")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked --gpus {args.gpus}); "
@@ -108,6 +139,10 @@ def main():
 
     import arf_amd
     ctx = arf_amd.Context(0)
+    if args.traffic_probe:
+        traffic_probe(ctx, args.copies)
+        ctx.close()
+        return
 
     # ---- headline: C2 Q4_K GEMV ----
     n, k, m = 17408, 5120, 1
@@ -171,10 +206,12 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32",
+        "dtype": "u4xi16->i32,f32",
         "data": "synthetic (seeded Q4_K superblocks per BASELINE config 2, x ~ N(0,1) f32)",
         "config": {"workload": "c2_q4_k_gemv_m1_k5120_n17408", "m": m, "k": k, "n": n,
-                   "weight_copies": args.copies, "parallelism": "single-gpu"},
+                   "weight_copies": args.copies, "parallelism": "single-gpu",
+                   "compute": "4-bit codes x 16-bit fixed-point activation digits on v_dot8 "
+                              "(exact int32 per sub-block), f32 scale and accumulate"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic("q4k_gemv_c2_traffic.json")},

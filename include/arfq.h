@@ -155,6 +155,12 @@ int arfq_dev_free(arfq_ctx *ctx, void *p);
 /* Synchronous copies (they wait for the context's stream first). */
 int arfq_copy_h2d(arfq_ctx *ctx, void *dst, const void *src, size_t bytes);
 int arfq_copy_d2h(arfq_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Enqueue a device-to-device copy on the context's stream (asynchronous).  It
+ * runs a plain 16-byte-per-lane copy kernel when both pointers and `bytes` are
+ * 16-byte aligned (hipMemcpyAsync otherwise); the kernel doubles as the
+ * known-size reference for HBM byte counters.  No counterpart in the
+ * reference (its buffers are copied by the wgpu/Metal runtime). */
+int arfq_copy_d2d(arfq_ctx *ctx, void *dst, const void *src, size_t bytes);
 /* Record a start event / a stop event on the context's stream; elapsed time in
  * ms between the last start and stop (waits for the stop event). */
 int arfq_timer_start(arfq_ctx *ctx);
