@@ -268,31 +268,9 @@ static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64
     if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
         e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream);
     } else if (arfq::gemm_supports(w, m)) {
-        // MFMA path.  f16 x is used as given; f32 x is rounded to f16 once for
-        // prefill shapes (m > 64, as the reference's half tiles do) and split
-        // into an f16 hi + lo pair for batched decode (m <= 64), where the
-        // path is bound by weight bytes and the second MFMA is free.
-        const bool xsplit = x_dtype == ARFQ_F32 && m <= 64;
-        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, xsplit);
-        const int64_t cnt = m * w->k;
-        const size_t xbytes = x_dtype == ARFQ_F32 ? (size_t)cnt * 2 * (xsplit ? 2 : 1) : 0;
-        const size_t xoff = (xbytes + 255) & ~(size_t)255;
-        const size_t pbytes = plan.splits > 1 ? (size_t)plan.splits * m * w->n * sizeof(float) : 0;
-        if (int rc = ensure_scratch(ctx, xoff + pbytes)) return rc;
-        const _Float16 *xh = (const _Float16 *)x, *xl = nullptr;
-        if (x_dtype == ARFQ_F32) {
-            __half *hh = (__half *)ctx->scratch;
-            if (xsplit) {
-                e = arfq::launch_split_f32((const float *)x, hh, hh + cnt, cnt, ctx->stream);
-                xl = (const _Float16 *)(hh + cnt);
-            } else {
-                e = arfq::launch_f32_to_f16((const float *)x, hh, cnt, ctx->stream);
-            }
-            if (e != hipSuccess) return hip_fail(ctx, e, "x conversion launch");
-            xh = (const _Float16 *)hh;
-        }
-        float *partials = pbytes ? (float *)((char *)ctx->scratch + xoff) : nullptr;
-        e = arfq::launch_gemm(w, expert, m, xh, xl, y, partials, plan, ctx->stream);
+        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
+        if (int rc = ensure_scratch(ctx, plan.scratch_bytes)) return rc;
+        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->scratch, plan, ctx->stream);
     } else {
         return fail(ctx, ARFQ_E_UNSUPPORTED,
                     "matmul: no kernel for qtype " + std::to_string(w->qtype) + " at m=" +
@@ -322,6 +300,139 @@ int arfq_matmul_repeat(arfq_ctx *ctx, const arfq_weight *const *ws, int n_ws, in
     for (int i = 0; i < iters; i++)
         if (int rc = matmul_enqueue(ctx, ws[i % n_ws], 0, m, x, x_dtype, y)) return rc;
     return ARFQ_OK;
+}
+
+// -------------------------------------------------------------------- MoE ----
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int arfq_moe_route(arfq_ctx *ctx, const float *logits, int64_t tokens, int n_experts, int top_k,
+                   int norm_topk, int32_t *ids, float *weights) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (tokens < 0) return fail(ctx, ARFQ_E_SHAPE, "moe_route: tokens < 0");
+    if (tokens > 0 && (!logits || !ids || !weights))
+        return fail(ctx, ARFQ_E_INVALID, "moe_route: null argument");
+    if (n_experts < 1 || n_experts > arfq::MOE_ROUTE_EXPERTS_MAX)
+        return fail(ctx, ARFQ_E_SHAPE, "moe_route: n_experts must be in [1, 1024]");
+    if (top_k < 1 || top_k > n_experts || top_k > arfq::MOE_TOPK_MAX)
+        return fail(ctx, ARFQ_E_SHAPE, "moe_route: top_k must be in [1, min(n_experts, 64)]");
+    if (int rc = use_device(ctx)) return rc;
+    hipError_t e = arfq::launch_moe_route(logits, tokens, n_experts, top_k, norm_topk ? 1 : 0, ids,
+                                          weights, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "moe_route launch");
+    return ARFQ_OK;
+}
+
+// Shapes: gate/up n_experts x [inter, hidden]; down n_experts x [hidden, inter].
+static int check_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                     const arfq_weight *down, int64_t tokens, int top_k, const void *x,
+                     int x_dtype, const float *y) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (!gate || !up || !down) return fail(ctx, ARFQ_E_INVALID, "moe: null weight");
+    if (tokens < 0) return fail(ctx, ARFQ_E_SHAPE, "moe: tokens < 0");
+    if (tokens > 0 && (!x || !y)) return fail(ctx, ARFQ_E_INVALID, "moe: null x or y");
+    if (x_dtype != ARFQ_F32 && x_dtype != ARFQ_F16)
+        return fail(ctx, ARFQ_E_INVALID, "moe: unknown x dtype");
+    const int E = gate->experts;
+    if (up->experts != E || down->experts != E)
+        return fail(ctx, ARFQ_E_SHAPE, "moe: gate/up/down expert counts differ");
+    if (E > arfq::MOE_EXPERTS_MAX) return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: more than 512 experts");
+    if (up->qtype != gate->qtype) return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: gate and up differ in qtype");
+    if (up->n != gate->n || up->k != gate->k || down->n != gate->k || down->k != gate->n)
+        return fail(ctx, ARFQ_E_SHAPE,
+                    "moe: want gate/up [inter, hidden] and down [hidden, inter]");
+    if (gate->k % 64 != 0 || down->k % 64 != 0)
+        return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: hidden and inter must be multiples of 64");
+    if (top_k < 1 || top_k > E || top_k > arfq::MOE_TOPK_MAX)
+        return fail(ctx, ARFQ_E_SHAPE, "moe: top_k must be in [1, min(n_experts, 64)]");
+    if (tokens * top_k > (int64_t)1 << 24) return fail(ctx, ARFQ_E_SHAPE, "moe: too many tokens");
+    return ARFQ_OK;
+}
+
+// Route (when ids == NULL) + group + grouped GEMMs + combine, all on the stream.
+// Scratch layout: [x f16] [ids] [weights] [off] [sorted] [tiles] [ntiles] [h f16] [o f32].
+static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                       const arfq_weight *down, const float *logits, const int32_t *ids_in,
+                       const float *wts_in, int64_t tokens, int top_k, int norm_topk,
+                       const void *x, int x_dtype, float *y) {
+    if (tokens == 0) return ARFQ_OK;
+    const int E = gate->experts;
+    const int64_t hidden = gate->k, inter = gate->n, P = tokens * top_k;
+    const int64_t max_tiles = arfq::moe_max_tiles(P, E);
+    const bool gsums = gate->qtype == ARFQ_Q4_K, dsums = down->qtype == ARFQ_Q4_K;
+    size_t o = 0;
+    const size_t o_x = o;     o += x_dtype == ARFQ_F32 ? align256((size_t)tokens * hidden * 2) : 0;
+    const size_t o_xs = o;    o += gsums ? align256((size_t)tokens * (hidden / 16) * 2) : 0;
+    const size_t o_ids = o;   o += ids_in ? 0 : align256((size_t)P * 4);
+    const size_t o_w = o;     o += ids_in ? 0 : align256((size_t)P * 4);
+    const size_t o_off = o;   o += align256((size_t)(E + 1) * 4);
+    const size_t o_srt = o;   o += align256((size_t)P * 4);
+    const size_t o_tl = o;    o += align256((size_t)max_tiles * 8);
+    const size_t o_nt = o;    o += 256;
+    const size_t o_h = o;     o += align256((size_t)P * inter * 4);
+    const size_t o_h16 = o;   o += align256((size_t)P * inter * 2);
+    const size_t o_rs = o;    o += align256((size_t)P * 4);
+    const size_t o_hs = o;    o += dsums ? align256((size_t)P * (inter / 16) * 2) : 0;
+    const size_t o_o = o;     o += align256((size_t)P * hidden * 4);
+    if (int rc = ensure_scratch(ctx, o)) return rc;
+    char *sc = (char *)ctx->scratch;
+    hipError_t e;
+    // the grouped GEMMs read f16 activation tiles (as the reference's half mm_id
+    // tiles) and, for Q4_K, the x sub-block sums
+    const _Float16 *xh = x_dtype == ARFQ_F32 ? (const _Float16 *)(sc + o_x) : (const _Float16 *)x;
+    uint16_t *xs = gsums ? (uint16_t *)(sc + o_xs) : nullptr;
+    e = arfq::launch_xprep(x, x_dtype, tokens, hidden,
+                           x_dtype == ARFQ_F32 ? (_Float16 *)(sc + o_x) : nullptr, nullptr, xs,
+                           ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "moe: x preparation launch");
+    const int32_t *ids = ids_in;
+    const float *wts = wts_in;
+    if (!ids_in) {
+        e = arfq::launch_moe_route(logits, tokens, E, top_k, norm_topk ? 1 : 0,
+                                   (int32_t *)(sc + o_ids), (float *)(sc + o_w), ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "moe: route launch");
+        ids = (const int32_t *)(sc + o_ids);
+        wts = (const float *)(sc + o_w);
+    }
+    int32_t *off = (int32_t *)(sc + o_off), *srt = (int32_t *)(sc + o_srt);
+    int32_t *nt = (int32_t *)(sc + o_nt);
+    void *tiles = sc + o_tl;
+    float *h = (float *)(sc + o_h);
+    _Float16 *h16 = (_Float16 *)(sc + o_h16);
+    float *rs = (float *)(sc + o_rs);
+    uint16_t *hs = dsums ? (uint16_t *)(sc + o_hs) : nullptr;
+    float *ob = (float *)(sc + o_o);
+    e = arfq::launch_moe_group(ids, P, E, off, srt, tiles, nt, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "moe: group launch");
+    e = arfq::launch_moe_gateup(gate, up, xh, xs, top_k, off, srt, tiles, nt, max_tiles, h,
+                                ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "moe: gate/up launch");
+    e = arfq::launch_moe_hprep(h, P, (int)inter, h16, hs, rs, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "moe: h preparation launch");
+    e = arfq::launch_moe_down(down, h16, hs, rs, off, srt, tiles, nt, max_tiles, ob, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "moe: down launch");
+    e = arfq::launch_moe_combine(ob, ids, wts, tokens, top_k, E, hidden, y, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "moe: combine launch");
+    return ARFQ_OK;
+}
+
+int arfq_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+             const arfq_weight *down, const float *router_logits, int64_t tokens, int top_k,
+             int norm_topk, const void *x, int x_dtype, float *y) {
+    if (int rc = check_moe(ctx, gate, up, down, tokens, top_k, x, x_dtype, y)) return rc;
+    if (tokens > 0 && !router_logits) return fail(ctx, ARFQ_E_INVALID, "moe: null router logits");
+    if (int rc = use_device(ctx)) return rc;
+    return moe_enqueue(ctx, gate, up, down, router_logits, nullptr, nullptr, tokens, top_k,
+                       norm_topk, x, x_dtype, y);
+}
+
+int arfq_moe_ids(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                 const arfq_weight *down, const int32_t *ids, const float *weights,
+                 int64_t tokens, int top_k, const void *x, int x_dtype, float *y) {
+    if (int rc = check_moe(ctx, gate, up, down, tokens, top_k, x, x_dtype, y)) return rc;
+    if (tokens > 0 && (!ids || !weights)) return fail(ctx, ARFQ_E_INVALID, "moe_ids: null ids or weights");
+    if (int rc = use_device(ctx)) return rc;
+    return moe_enqueue(ctx, gate, up, down, nullptr, ids, weights, tokens, top_k, 0, x, x_dtype, y);
 }
 
 int arfq_dequant_f32(arfq_ctx *ctx, const arfq_weight *w, float *out) {

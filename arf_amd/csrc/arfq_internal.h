@@ -56,21 +56,54 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
 bool gemv_supports(const arfq_weight *w, int64_t m);
 
 // ---- arfq_gemm.hip ----
-// Launch shape of the dequant-into-LDS MFMA GEMM.
+// Launch shape and scratch layout of the dequant-into-LDS MFMA GEMM.
 struct GemmPlan {
-    int bm = 128;         // x rows per workgroup tile (64 or 128)
-    int splits = 1;       // split-K factor (partials [splits][m][n] then a reduce)
-    bool xsplit = false;  // x given as f16 hi + lo (an f32 x split in two)
+    int bm = 128;          // x rows per workgroup tile (64 or 128)
+    int splits = 1;        // split-K factor (partials [splits][m][n] then a reduce)
+    bool xsplit = false;   // x as f16 hi + lo (an f32 x split in two)
+    bool convert = false;  // x arrives as f32 and is converted into scratch
+    bool sums = false;     // the format needs x sub-block sums (Q4_K)
+    size_t off_xh = 0, off_xl = 0, off_xs = 0, off_part = 0, scratch_bytes = 0;
 };
-GemmPlan gemm_plan(const arfq_weight *w, int64_t m, bool xsplit);
+GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype);
 bool gemm_supports(const arfq_weight *w, int64_t m);
-// y[m, n] = x[m, k] . W_e^T with x = xh (+ xl when plan.xsplit), row-major f16.
-// `partials` holds splits * m * n floats when plan.splits > 1.
-hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const _Float16 *xh,
-                       const _Float16 *xl, float *y, float *partials, const GemmPlan &p,
-                       hipStream_t s);
-// x f32 -> f16 (round to nearest), and x f32 -> hi + lo f16 pair.
-hipError_t launch_f32_to_f16(const float *x, __half *y, int64_t n, hipStream_t s);
-hipError_t launch_split_f32(const float *x, __half *hi, __half *lo, int64_t n, hipStream_t s);
+// y[m, n] = x[m, k] . W_e^T; `scratch` holds plan.scratch_bytes.
+hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
+                       float *y, void *scratch, const GemmPlan &p, hipStream_t s);
+// Activation preparation: x (f32 or f16, [m, k]) -> f16 copy (xh), f16
+// remainder (xl), bf16 sub-block sums (xs, [m][k / 256][16]); null outputs are skipped.
+hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
+                        _Float16 *xl, uint16_t *xs, hipStream_t s);
+
+// ---- arfq_moe.hip ----
+// Routing: ids/weights [tokens, top_k] from logits [tokens, E] (E <= 1024, top_k <= 64).
+hipError_t launch_moe_route(const float *logits, int64_t tokens, int E, int top_k, int norm,
+                            int32_t *ids, float *wts, hipStream_t s);
+// Grouping of P = tokens * top_k pairs by expert (E <= MOE_MAX_EXPERTS): off[E + 1],
+// sorted[P] (pair indices), tiles[moe_max_tiles] (int2 expert, first row), *ntiles.
+hipError_t launch_moe_group(const int32_t *ids, int64_t P, int E, int32_t *off, int32_t *sorted,
+                            void *tiles, int32_t *ntiles, hipStream_t s);
+int64_t moe_max_tiles(int64_t P, int E);
+// h[P, inter] (f32, sorted order) = silu(x . gate^T) * (x . up^T) per pair;
+// xs: x sub-block sums (Q4_K weights only, else null).
+hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, const _Float16 *x,
+                             const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
+                             const void *tiles, const int32_t *ntiles, int64_t max_tiles,
+                             float *h, hipStream_t s);
+// h (f32) -> h16 = h / rs[row] (rs a power of two keeping h16 in f16 range)
+// and, when hs is set, the bf16 sub-block sums of h16.
+hipError_t launch_moe_hprep(const float *h, int64_t P, int inter, _Float16 *h16, uint16_t *hs,
+                            float *rs, hipStream_t s);
+// o[pair, hidden] (f32) = rs[row] * (h16[sorted row] . down^T).
+hipError_t launch_moe_down(const arfq_weight *down, const _Float16 *h, const uint16_t *hs,
+                           const float *rs, const int32_t *off,
+                           const int32_t *sorted, const void *tiles, const int32_t *ntiles,
+                           int64_t max_tiles, float *o, hipStream_t s);
+// y[t] = sum_j w[t, j] * o[t * top_k + j] in slot order.
+hipError_t launch_moe_combine(const float *o, const int32_t *ids, const float *wts, int64_t tokens,
+                              int top_k, int E, int64_t hidden, float *y, hipStream_t s);
+constexpr int MOE_EXPERTS_MAX = 512;
+constexpr int MOE_ROUTE_EXPERTS_MAX = 1024;
+constexpr int MOE_TOPK_MAX = 64;
 
 }  // namespace arfq

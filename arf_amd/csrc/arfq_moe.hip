@@ -1,26 +1,491 @@
-// arfq_moe.hip -- top-k routing, expert grouping and the grouped SwiGLU MoE.
-#include "arfq_common.h"
+// arfq_moe.hip -- the expert-grouped MoE block on device:
+//   route   -> ids[t, j], weights[t, j]       (top-k of the softmax per token)
+//   group   -> (token, slot) pairs sorted by expert, stable in t*top_k + slot,
+//              plus a list of BM-row tiles per expert
+//   gate|up -> h[pair] = silu(x_t . gate_e^T) * (x_t . up_e^T)   (f16, sorted order)
+//   down    -> o[t*top_k + j] = h[pair] . down_e^T               (f32)
+//   combine -> y[t] = sum_j w[t, j] * o[t*top_k + j] in slot order
+// The grouped GEMMs reuse the dense GEMM's tile loop (arfq_gemm_tile.h).
+//
+// Reference behaviour: moe_route_msl.metal:18-98 / moe_batch_msl.metal:371-563
+// (route, CSR by expert, swiglu, slot-ordered reduce), moe_mm_id_q4ks.metal:103-700
+// (grouped mm_id over an expert tile list); oracle MoeMlp::forward
+// (crates/arf-core/src/model/moe.rs:53-86), top_k_softmax (moe.rs:89-121),
+// Mlp::forward (crates/arf-core/src/model/mlp.rs:20-24), silu
+// (crates/arf-ml/src/lib.rs:160-162).
+#include "arfq_gemm_tile.h"
 #include "arfq_internal.h"
 
-extern "C" {
+namespace arfq {
 
-int arfq_moe_route(arfq_ctx *ctx, const float *, int64_t, int, int, int, int32_t *, float *) {
-    if (!ctx) return ARFQ_E_INVALID;
-    ctx->err = "moe_route: not implemented";
-    return ARFQ_E_UNSUPPORTED;
+// ---- route -------------------------------------------------------------------
+// One wave per token; lane l holds logits l, l+64, ... (E <= 64 * MOE_ROUTE_PL).
+// softmax exactly as the reference: max, exp(l - max), sum in index order,
+// divide; then top_k rounds of a wave argmax on (prob desc, index asc), which is
+// the reference's stable sort + truncate; renormalise by the selected sum
+// (summed in selection order) when norm != 0.
+constexpr int MOE_ROUTE_PL = 16;
+
+__global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits,
+                                                        int64_t tokens, int E, int top_k,
+                                                        int norm, int32_t *__restrict__ ids,
+                                                        float *__restrict__ wts) {
+    const int lane = threadIdx.x & 63;
+    const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= tokens) return;
+    const float *lg = logits + t * E;
+    float v[MOE_ROUTE_PL];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < MOE_ROUTE_PL; j++) {
+        const int i = j * 64 + lane;
+        v[j] = i < E ? lg[i] : -INFINITY;
+        mx = fmaxf(mx, v[j]);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+#pragma unroll
+    for (int j = 0; j < MOE_ROUTE_PL; j++) v[j] = (j * 64 + lane < E) ? expf(v[j] - mx) : 0.f;
+    // sum in index order (the reference's sequential iterator sum)
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < MOE_ROUTE_PL; j++) {
+        if (j * 64 >= E) break;
+        const int cnt = min(64, E - j * 64);
+        for (int l = 0; l < cnt; l++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
+    }
+#pragma unroll
+    for (int j = 0; j < MOE_ROUTE_PL; j++) v[j] = (j * 64 + lane < E) ? v[j] / s : -INFINITY;
+
+    uint32_t taken = 0;
+    float myw = 0.f;
+    int myid = 0;
+    float wsum = 0.f;
+    for (int r = 0; r < top_k; r++) {
+        float bp = -INFINITY;
+        int bi = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < MOE_ROUTE_PL; j++) {
+            const int i = j * 64 + lane;
+            if (i < E && !((taken >> j) & 1u) && (v[j] > bp || bi == 0x7fffffff)) {
+                bp = v[j];
+                bi = i;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float op = __shfl_xor(bp, o);
+            const int oi = __shfl_xor(bi, o);
+            if (op > bp || (op == bp && oi < bi) || (bi == 0x7fffffff && oi != 0x7fffffff)) {
+                bp = op;
+                bi = oi;
+            }
+        }
+        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        if (lane == r) {
+            myw = bp;
+            myid = bi;
+        }
+        wsum += bp;
+    }
+    if (lane < top_k) {
+        ids[t * top_k + lane] = myid;
+        wts[t * top_k + lane] = (norm && wsum > 0.f) ? myw / wsum : myw;
+    }
 }
 
-int arfq_moe(arfq_ctx *ctx, const arfq_weight *, const arfq_weight *, const arfq_weight *,
-             const float *, int64_t, int, int, const void *, int, float *) {
-    if (!ctx) return ARFQ_E_INVALID;
-    ctx->err = "moe: not implemented";
-    return ARFQ_E_UNSUPPORTED;
+// ---- group -------------------------------------------------------------------
+// One 1024-thread workgroup.  Pass 1 counts pairs per expert; a scan gives the
+// expert row offsets and the tile list (ceil(count / bm) tiles per expert).
+// Pass 2 walks the pairs in chunks of 1024 in index order; inside a chunk each
+// wave ranks its lanes among equal experts (ballot per distinct expert), a
+// per-wave histogram gives the rank of the wave, and a running per-expert base
+// carries the chunks: position = offset[e] + base[e] + wave prefix + rank, which
+// is the stable order.  Pairs whose expert id is out of range are dropped.
+constexpr int MOE_MAX_EXPERTS = 512;
+
+__device__ __forceinline__ int block_excl_scan_1024(int v, int *tmp, int &total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(inc, o);
+        if (lane >= o) inc += u;
+    }
+    if (lane == 63) tmp[w] = inc;
+    __syncthreads();
+    int wbase = 0, tot = 0;
+    for (int i = 0; i < 16; i++) {
+        const int x = tmp[i];
+        if (i < w) wbase += x;
+        tot += x;
+    }
+    __syncthreads();
+    total = tot;
+    return wbase + inc - v;
 }
 
-int arfq_moe_ids(arfq_ctx *ctx, const arfq_weight *, const arfq_weight *, const arfq_weight *,
-                 const int32_t *, const float *, int64_t, int, const void *, int, float *) {
-    if (!ctx) return ARFQ_E_INVALID;
-    ctx->err = "moe_ids: not implemented";
-    return ARFQ_E_UNSUPPORTED;
+__global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restrict__ ids,
+                                                         int64_t P, int E, int bm,
+                                                         int32_t *__restrict__ off,
+                                                         int32_t *__restrict__ sorted,
+                                                         int2 *__restrict__ tiles,
+                                                         int32_t *__restrict__ ntiles) {
+    __shared__ int cnt[MOE_MAX_EXPERTS];   // pass 1 counts, then row offsets
+    __shared__ int base[MOE_MAX_EXPERTS];  // rows already placed per expert
+    __shared__ int ctot[MOE_MAX_EXPERTS];  // this chunk's rows per expert
+    __shared__ int whist[16][MOE_MAX_EXPERTS];
+    __shared__ int tmp[32];
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    for (int e = tid; e < E; e += 1024) {
+        cnt[e] = 0;
+        base[e] = 0;
+    }
+    __syncthreads();
+    for (int64_t p = tid; p < P; p += 1024) {
+        const int e = ids[p];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    const int c = tid < E ? cnt[tid] : 0;
+    const int tc = (c + bm - 1) / bm;
+    int rows_total, tiles_total;
+    const int ex_c = block_excl_scan_1024(c, tmp, rows_total);
+    const int ex_t = block_excl_scan_1024(tc, tmp + 16, tiles_total);
+    if (tid < E) {
+        off[tid] = ex_c;
+        for (int i = 0; i < tc; i++) tiles[ex_t + i] = make_int2(tid, ex_c + i * bm);
+        cnt[tid] = ex_c;
+    }
+    if (tid == 0) {
+        off[E] = rows_total;
+        *ntiles = tiles_total;
+    }
+    __syncthreads();
+
+    const uint64_t lt = (1ull << lane) - 1ull;
+    for (int64_t cb = 0; cb < P; cb += 1024) {
+        const int64_t p = cb + tid;
+        const int e = p < P ? ids[p] : -1;
+        const bool valid = e >= 0 && e < E;
+        for (int i = lane; i < E; i += 64) whist[w][i] = 0;
+        __syncthreads();
+        int rank = 0;
+        uint64_t active = __ballot(valid);
+        while (active) {
+            const int leader = __ffsll((long long)active) - 1;
+            const int le = __shfl(e, leader);
+            const uint64_t m = __ballot(valid && e == le);
+            if (valid && e == le) rank = __popcll(m & lt);
+            if (lane == leader) whist[w][le] = __popcll(m);
+            active &= ~m;
+        }
+        __syncthreads();
+        if (tid < E) {
+            int run = 0;
+            for (int i = 0; i < 16; i++) {
+                const int x = whist[i][tid];
+                whist[i][tid] = run;
+                run += x;
+            }
+            ctot[tid] = run;
+        }
+        __syncthreads();
+        if (valid) sorted[cnt[e] + base[e] + whist[w][e] + rank] = (int32_t)p;
+        __syncthreads();
+        if (tid < E) base[tid] += ctot[tid];
+        __syncthreads();
+    }
 }
+
+// ---- grouped GEMMs -------------------------------------------------------------
+constexpr int MOE_BM = 64;
+
+// gate|up: output tile = 64 rows (pairs of one expert) x 64 columns of inter.
+// The 128 weight rows of the tile are gate rows n0..n0+63 (waves wn = 0) and up
+// rows n0..n0+63 (waves wn = 1), so both projections share one x tile; the up
+// accumulators go through LDS to the gate waves, which write
+// h = silu(g) * u in f32 (its range can exceed f16's; moe_hprep scales it).
+template <class F>
+__global__ __launch_bounds__(GM_THREADS) void moe_gateup_kernel(
+    F gate, F up, int64_t expert_blocks, const _Float16 *__restrict__ x,
+    const uint16_t *__restrict__ xs, int K, int inter, int top_k, const int32_t *__restrict__ off,
+    const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, float *__restrict__ h) {
+    extern __shared__ _Float16 lds[];
+    if ((int)blockIdx.x >= *ntiles) return;  // uniform over the workgroup
+    const int tid = threadIdx.x;
+    const int2 tile = tiles[blockIdx.x];
+    const int e = tile.x, row0 = tile.y;
+    const int rows = min(MOE_BM, off[e + 1] - row0);
+    const int n0 = blockIdx.y * 64;
+
+    int64_t xrow[MOE_BM / 32], xsrow[MOE_BM / 32];
+#pragma unroll
+    for (int i = 0; i < MOE_BM / 32; i++) {
+        const int r = min((tid >> 3) + 32 * i, rows - 1);
+        const int64_t tok = sorted[row0 + r] / top_k;
+        xrow[i] = tok * K;
+        xsrow[i] = tok * (K / 16);
+    }
+    const int wr = tid >> 1;
+    const F fe = (wr < 64 ? gate : up).shifted((int64_t)e * expert_blocks);
+    const int64_t wrow = min(n0 + (wr & 63), inter - 1);
+
+    floatx16 acc[1][2];
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[0][b][i] = 0.f;
+    gemm_tile_run<F, MOE_BM, false>(fe, wrow, xrow, xsrow, x, nullptr, xs, 0, K / GM_BK, acc, lds);
+
+    // the loop ended with a barrier: LDS is free.  up waves -> LDS [64][65] f32
+    float *ex = reinterpret_cast<float *>(lds);
+    const int wn = tid >> 7;
+    if (wn == 1) {
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++)
+                ex[tile_out_row<MOE_BM>(0, i) * 65 + tile_out_col(b) - 64] = acc[0][b][i];
+    }
+    __syncthreads();
+    if (wn == 0) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            const int col = tile_out_col(b);
+            const int n = n0 + col;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int r = tile_out_row<MOE_BM>(0, i);
+                if (r < rows && n < inter) {
+                    const float g = acc[0][b][i];
+                    const float u = ex[r * 65 + col];
+                    const float sg = g / (1.0f + expf(-g));
+                    h[(int64_t)(row0 + r) * inter + n] = sg * u;
+                }
+            }
+        }
+    }
 }
+
+// h rows (f32) -> f16 copies scaled by a power of two per row, so that the
+// largest |h| of the row is below 2^15: h16 = h / rs (exact scaling), the
+// down GEMM multiplies its output row by rs.  For Q4_K down weights also the
+// sub-block sums of h16 (bf16 hi + lo, the xs layout).  One wave per row.
+__global__ __launch_bounds__(256) void moe_hprep_kernel(const float *__restrict__ h, int64_t P,
+                                                        int inter, _Float16 *__restrict__ h16,
+                                                        uint16_t *__restrict__ hs,
+                                                        float *__restrict__ rs) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= P) return;
+    const float *src = h + row * inter;
+    float amax = 0.f;
+    for (int i = lane; i < inter; i += 64) amax = fmaxf(amax, fabsf(src[i]));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+    const int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;  // amax < 2^ex
+    const int sh = ex > 15 ? ex - 15 : 0;
+    const float inv = ldexpf(1.f, -sh);
+    if (lane == 0) rs[row] = ldexpf(1.f, sh);
+    const int nsub = inter / 32;
+    for (int sub = lane; sub < nsub; sub += 64) {
+        float sum = 0.f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            half8 hv;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                hv[i] = (_Float16)(src[sub * 32 + 8 * c + i] * inv);
+                sum += (float)hv[i];
+            }
+            reinterpret_cast<half8 *>(h16 + row * inter + sub * 32)[c] = hv;
+        }
+        if (hs) {
+            const uint32_t hi = bf16_bits(sum);
+            const uint32_t lo = bf16_bits(sum - bf16_to_f32(hi));
+            uint16_t *d = hs + row * (inter / 16) + (sub >> 3) * 16 + (sub & 7);
+            d[0] = (uint16_t)hi;
+            d[8] = (uint16_t)lo;
+        }
+    }
+}
+
+// down: output tile = 64 pair rows x 128 columns of hidden; rows are stored to
+// o[pair index] so the combine can read each token's slots in order.
+template <class F>
+__global__ __launch_bounds__(GM_THREADS) void moe_down_kernel(
+    F down, int64_t expert_blocks, const _Float16 *__restrict__ h, const uint16_t *__restrict__ hs,
+    const float *__restrict__ rs, int K, int hidden, const int32_t *__restrict__ off,
+    const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
+    const int32_t *__restrict__ ntiles, float *__restrict__ o) {
+    extern __shared__ _Float16 lds[];
+    if ((int)blockIdx.x >= *ntiles) return;
+    const int tid = threadIdx.x;
+    const int2 tile = tiles[blockIdx.x];
+    const int e = tile.x, row0 = tile.y;
+    const int rows = min(MOE_BM, off[e + 1] - row0);
+    const int n0 = blockIdx.y * GM_BN;
+
+    int64_t xrow[MOE_BM / 32], xsrow[MOE_BM / 32];
+#pragma unroll
+    for (int i = 0; i < MOE_BM / 32; i++) {
+        const int64_t r = row0 + min((tid >> 3) + 32 * i, rows - 1);
+        xrow[i] = r * K;
+        xsrow[i] = r * (K / 16);
+    }
+    const F fe = down.shifted((int64_t)e * expert_blocks);
+    const int64_t wrow = min(n0 + (tid >> 1), hidden - 1);
+
+    floatx16 acc[1][2];
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[0][b][i] = 0.f;
+    gemm_tile_run<F, MOE_BM, false>(fe, wrow, xrow, xsrow, h, nullptr, hs, 0, K / GM_BK, acc, lds);
+
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const int n = n0 + tile_out_col(b);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int r = tile_out_row<MOE_BM>(0, i);
+            if (r < rows && n < hidden)
+                o[(int64_t)sorted[row0 + r] * hidden + n] = acc[0][b][i] * rs[row0 + r];
+        }
+    }
+}
+
+// ---- combine -------------------------------------------------------------------
+// y[t, c] = ((0 + w0*o0) + w1*o1) + ... over the token's slots in order, each
+// product and sum rounded separately (the reference's out[t] += w_j * y_j).
+__global__ void moe_combine_kernel(const float *__restrict__ o, const int32_t *__restrict__ ids,
+                                   const float *__restrict__ wts, int64_t tokens, int top_k, int E,
+                                   int hidden, float *__restrict__ y) {
+#pragma clang fp contract(off)
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= tokens * hidden) return;
+    const int64_t t = i / hidden;
+    const int c = (int)(i - t * hidden);
+    float acc = 0.f;
+    for (int j = 0; j < top_k; j++) {
+        const int e = ids[t * top_k + j];
+        if (e < 0 || e >= E) continue;  // dropped pair: contributes nothing
+        const float p = wts[t * top_k + j] * o[(t * top_k + j) * hidden + c];
+        acc = acc + p;
+    }
+    y[i] = acc;
+}
+
+// ---- launchers -----------------------------------------------------------------
+
+hipError_t launch_moe_route(const float *logits, int64_t tokens, int E, int top_k, int norm,
+                            int32_t *ids, float *wts, hipStream_t s) {
+    if (tokens == 0) return hipSuccess;
+    moe_route_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, top_k, norm,
+                                                                  ids, wts);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_group(const int32_t *ids, int64_t P, int E, int32_t *off, int32_t *sorted,
+                            void *tiles, int32_t *ntiles, hipStream_t s) {
+    moe_group_kernel<<<1, 1024, 0, s>>>(ids, P, E, MOE_BM, off, sorted, (int2 *)tiles, ntiles);
+    return hipGetLastError();
+}
+
+int64_t moe_max_tiles(int64_t P, int E) { return (P + MOE_BM - 1) / MOE_BM + E; }
+
+template <class F>
+static hipError_t set_lds_once(const void *fn, size_t bytes, bool &done) {
+    if (done) return hipSuccess;
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess) done = true;
+    return e;
+}
+
+template <class F>
+static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const _Float16 *x,
+                           const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted, const void *tiles,
+                           const int32_t *ntiles, int64_t max_tiles, float *h, hipStream_t s) {
+    static bool attr = false;
+    constexpr size_t lds = gm_lds(MOE_BM, false);
+    static_assert(lds >= 64 * 65 * sizeof(float), "epilogue exchange must fit the tile LDS");
+    if (hipError_t e = set_lds_once<F>((const void *)moe_gateup_kernel<F>, lds, attr)) return e;
+    const int64_t eb = gw->n * g.nblk;
+    const dim3 grid((unsigned)max_tiles, (unsigned)((gw->n + 63) / 64));
+    moe_gateup_kernel<F><<<grid, GM_THREADS, lds, s>>>(g, u, eb, x, xs, (int)gw->k, (int)gw->n,
+                                                       top_k, off, sorted, (const int2 *)tiles,
+                                                       ntiles, h);
+    return hipGetLastError();
+}
+
+template <class F>
+static hipError_t down_t(const F &d, const arfq_weight *dw, const _Float16 *h, const uint16_t *hs,
+                         const float *rs, const int32_t *off,
+                         const int32_t *sorted, const void *tiles, const int32_t *ntiles,
+                         int64_t max_tiles, float *o, hipStream_t s) {
+    static bool attr = false;
+    constexpr size_t lds = gm_lds(MOE_BM, false);
+    if (hipError_t e = set_lds_once<F>((const void *)moe_down_kernel<F>, lds, attr)) return e;
+    const int64_t eb = dw->n * d.nblk;
+    const dim3 grid((unsigned)max_tiles, (unsigned)((dw->n + GM_BN - 1) / GM_BN));
+    moe_down_kernel<F><<<grid, GM_THREADS, lds, s>>>(d, eb, h, hs, rs, (int)dw->k, (int)dw->n, off,
+                                                     sorted, (const int2 *)tiles, ntiles, o);
+    return hipGetLastError();
+}
+
+FmtQ4K fmt_q4k(const arfq_weight *w);  // arfq_gemm.hip
+FmtQ6K fmt_q6k(const arfq_weight *w);
+FmtQ80 fmt_q80(const arfq_weight *w);
+
+hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, const _Float16 *x,
+                             const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
+                             const void *tiles, const int32_t *ntiles, int64_t max_tiles,
+                             float *h, hipStream_t s) {
+    switch (gate->qtype) {
+    case ARFQ_Q4_K:
+        return gateup_t(fmt_q4k(gate), fmt_q4k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+                        max_tiles, h, s);
+    case ARFQ_Q6_K:
+        return gateup_t(fmt_q6k(gate), fmt_q6k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+                        max_tiles, h, s);
+    case ARFQ_Q8_0:
+        return gateup_t(fmt_q80(gate), fmt_q80(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+                        max_tiles, h, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_moe_down(const arfq_weight *down, const _Float16 *h, const uint16_t *hs,
+                           const float *rs, const int32_t *off,
+                           const int32_t *sorted, const void *tiles, const int32_t *ntiles,
+                           int64_t max_tiles, float *o, hipStream_t s) {
+    switch (down->qtype) {
+    case ARFQ_Q4_K:
+        return down_t(fmt_q4k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+    case ARFQ_Q6_K:
+        return down_t(fmt_q6k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+    case ARFQ_Q8_0:
+        return down_t(fmt_q80(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_moe_hprep(const float *h, int64_t P, int inter, _Float16 *h16, uint16_t *hs,
+                            float *rs, hipStream_t s) {
+    if (P == 0) return hipSuccess;
+    moe_hprep_kernel<<<(unsigned)((P + 3) / 4), 256, 0, s>>>(h, P, inter, h16, hs, rs);
+    return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const float *o, const int32_t *ids, const float *wts, int64_t tokens,
+                              int top_k, int E, int64_t hidden, float *y, hipStream_t s) {
+    const int64_t n = tokens * hidden;
+    if (n == 0) return hipSuccess;
+    moe_combine_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(o, ids, wts, tokens, top_k, E,
+                                                                   (int)hidden, y);
+    return hipGetLastError();
+}
+
+}  // namespace arfq

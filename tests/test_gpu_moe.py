@@ -1,0 +1,238 @@
+"""GPU parity of the MoE path (routing, grouping, grouped SwiGLU GEMMs, combine)
+against the CPU oracle, through the C ABI.
+
+Routing: expert ids identical to the oracle's top_k_softmax (crates/arf-core/src/
+model/moe.rs:89-121); weights within 1e-6 (only the exp's last bit may differ).
+MoE block: max|g - c| / max(|c|, rms(c)) <= 2e-3 against MoeMlp::forward
+(moe.rs:53-86) on the same f16-valued x.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import rel_err
+from formats import moe_route_lcg_logits
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def _say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def _route(ctx, logits, top_k, norm):
+    T, E = logits.shape
+    lg = ctx.to_device(logits)
+    ids = ctx.empty((T, top_k), np.int32)
+    w = ctx.empty((T, top_k), np.float32)
+    ctx.moe_route(lg, T, E, top_k, norm, ids, w)
+    return ids.numpy(), w.numpy()
+
+
+def _check_route(oracle, logits, top_k, norm, got_ids, got_w):
+    for t in range(logits.shape[0]):
+        ids, w = oracle.top_k_softmax(logits[t], top_k, norm)
+        assert got_ids[t].tolist() == ids.tolist(), f"token {t}"
+        assert np.max(np.abs(got_w[t] - w)) <= 1e-6, f"token {t}"
+
+
+# ------------------------------------------------------------- routing ----
+def test_route_reference_cases(gpu_ctx, oracle):
+    # crates/arf-core/src/model/moe.rs:134-159 (incl. the tie case -> lower index)
+    _say("case: route reference cases")
+    lg = np.array([[2.0, -1.0, 3.0, 0.0], [1.0, 1.0, 1.0, 1.0]], np.float32)
+    for norm in (True, False):
+        ids, w = _route(gpu_ctx, lg, 2, norm)
+        assert ids[0].tolist() == [2, 0] and ids[1].tolist() == [0, 1]
+        _check_route(oracle, lg, 2, norm, ids, w)
+        if norm:
+            assert abs(float(w[0].sum()) - 1.0) < 1e-6
+
+
+def test_route_128_expert_lcg_cases(gpu_ctx, oracle):
+    # crates/arf-gpu/tests/moe_gpu.rs:84-93: 128 experts, top-8, LCG seed 99
+    _say("case: route 128-expert LCG")
+    state = 99
+    rows = []
+    for _ in range(2):
+        lg, state = moe_route_lcg_logits(128, state)
+        rows.append(lg)
+    lg = np.stack(rows)
+    for norm in (True, False):
+        ids, w = _route(gpu_ctx, lg, 8, norm)
+        _check_route(oracle, lg, 8, norm, ids, w)
+
+
+@pytest.mark.parametrize("T,E,k", [(512, 128, 8), (37, 8, 2), (5, 1000, 64), (3, 64, 1),
+                                   (1, 200, 7)])
+def test_route_random(gpu_ctx, oracle, T, E, k):
+    from arf_amd import synth
+    _say("case: route random", T, E, k)
+    lg = synth.router_logits(T, E, seed=T * 1000 + E + k)
+    ids, w = _route(gpu_ctx, lg, k, True)
+    _check_route(oracle, lg, k, True, ids, w)
+
+
+def test_route_shape_errors(gpu_ctx):
+    lg = gpu_ctx.to_device(np.zeros((2, 8), np.float32))
+    ids = gpu_ctx.empty((2, 9), np.int32)
+    w = gpu_ctx.empty((2, 9), np.float32)
+    with pytest.raises(ValueError):
+        gpu_ctx.moe_route(lg, 2, 8, 9, True, ids, w)  # top_k > n_experts
+    with pytest.raises(ValueError):
+        gpu_ctx.moe_route(lg, 2, 8, 0, True, ids, w)
+
+
+# ---------------------------------------------------------------- block ----
+def _weights(ctx, E, hidden, inter, seed, qd="q4_k"):
+    from arf_amd import QType, synth
+    qt = {"q4_k": QType.Q4_K, "q6_k": QType.Q6_K, "q8_0": QType.Q8_0}
+    gate = synth.weight("q4_k", inter, hidden, seed=seed, experts=E)
+    up = synth.weight("q4_k", inter, hidden, seed=seed + 1, experts=E)
+    down = synth.weight(qd, hidden, inter, seed=seed + 2, experts=E)
+    wg = ctx.upload(QType.Q4_K, gate, inter, hidden, E)
+    wu = ctx.upload(QType.Q4_K, up, inter, hidden, E)
+    wd = ctx.upload(qt[qd], down, hidden, inter, E)
+    return (gate, up, down), (wg, wu, wd)
+
+
+def _moe_gpu(ctx, ws, x, logits, top_k, norm):
+    T, hidden = x.shape
+    y = ctx.empty((T, hidden), np.float32)
+    ctx.moe(ws[0], ws[1], ws[2], ctx.to_device(logits), T, top_k, norm, ctx.to_device(x), y)
+    return y.numpy()
+
+
+@pytest.mark.parametrize("T,E,k,hidden,inter", [(5, 8, 2, 256, 256), (70, 16, 4, 512, 768),
+                                                (1, 4, 4, 256, 512), (129, 6, 2, 768, 256),
+                                                (70, 16, 4, 512, 256)])
+def test_moe_block_small(gpu_ctx, oracle, T, E, k, hidden, inter):
+    # synthetic Q4_K experts give |silu(g) * u| up to ~1e5 at hidden >= 512: the
+    # intermediate must not overflow f16 on the way to the down projection
+    from arf_amd import synth
+    _say("case: moe block", T, E, k, hidden, inter)
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=T + E + k)
+    x = synth.activations(T, hidden, seed=T + 7, dtype=np.float16)
+    logits = synth.router_logits(T, E, seed=T + 8)
+    got = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    want = oracle.moe_forward(x.astype(np.float32), raw[0], raw[1], raw[2], E, inter, logits, k,
+                              True)
+    e = rel_err(got, want)
+    _say("rel err", e)
+    assert e <= TOL
+
+
+def test_moe_f32_x_and_no_renorm(gpu_ctx, oracle):
+    # f32 x is rounded to f16 for the grouped GEMM tiles; the oracle sees that x
+    from arf_amd import synth
+    _say("case: moe f32 x")
+    T, E, k, hidden, inter = 33, 8, 3, 512, 256
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=300)
+    x = synth.activations(T, hidden, seed=301)
+    logits = synth.router_logits(T, E, seed=302)
+    got = _moe_gpu(gpu_ctx, ws, x, logits, k, False)
+    x16 = x.astype(np.float16).astype(np.float32)
+    want = oracle.moe_forward(x16, raw[0], raw[1], raw[2], E, inter, logits, k, False)
+    assert rel_err(got, want) <= TOL
+
+
+def test_moe_down_q6_k(gpu_ctx, oracle):
+    # down projection in Q6_K (as Q4_K_M GGUFs ship ffn_down_exps); composed from oracle parts
+    from arf_amd import synth
+    _say("case: moe q6_k down")
+    T, E, k, hidden, inter = 9, 4, 2, 256, 512
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=400, qd="q6_k")
+    x = synth.activations(T, hidden, seed=401, dtype=np.float16)
+    logits = synth.router_logits(T, E, seed=402)
+    got = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    g_e = raw[0].reshape(E, -1)
+    u_e = raw[1].reshape(E, -1)
+    d_e = raw[2].reshape(E, -1)
+    want = np.zeros((T, hidden), np.float32)
+    xf = x.astype(np.float32)
+    for t in range(T):
+        ids, w = oracle.top_k_softmax(logits[t], k, True)
+        for e, wt in zip(ids, w):
+            g = oracle.matmul_q("q4_k", xf[t:t + 1], g_e[e], inter)
+            u = oracle.matmul_q("q4_k", xf[t:t + 1], u_e[e], inter)
+            h = (g / (1.0 + np.exp(-g))) * u
+            want[t] += wt * oracle.matmul_q("q6_k", h.astype(np.float32), d_e[e], hidden)[0]
+    assert rel_err(got, want) <= TOL
+
+
+def test_moe_ids_matches_moe_and_drops_invalid(gpu_ctx, oracle):
+    from arf_amd import synth
+    _say("case: moe_ids")
+    T, E, k, hidden, inter = 20, 8, 2, 256, 256
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=500)
+    x = synth.activations(T, hidden, seed=501, dtype=np.float16)
+    logits = synth.router_logits(T, E, seed=502)
+    ref = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    ids = np.zeros((T, k), np.int32)
+    w = np.zeros((T, k), np.float32)
+    for t in range(T):
+        ids[t], w[t] = oracle.top_k_softmax(logits[t], k, True)
+    y = gpu_ctx.empty((T, hidden), np.float32)
+    gpu_ctx.moe_ids(ws[0], ws[1], ws[2], gpu_ctx.to_device(ids), gpu_ctx.to_device(w), T, k,
+                    gpu_ctx.to_device(x), y)
+    assert rel_err(y.numpy(), ref) <= 1e-6
+    # an out-of-range id drops that (token, slot) pair; the others are unchanged
+    bad = ids.copy()
+    bad[3, 1] = E + 5
+    bad[7, 0] = -1
+    gpu_ctx.moe_ids(ws[0], ws[1], ws[2], gpu_ctx.to_device(bad), gpu_ctx.to_device(w), T, k,
+                    gpu_ctx.to_device(x), y)
+    got = y.numpy()
+    keep = np.ones(T, bool)
+    keep[[3, 7]] = False
+    assert rel_err(got[keep], ref[keep]) <= 1e-6
+    assert np.all(np.isfinite(got))
+
+
+def test_moe_deterministic(gpu_ctx):
+    from arf_amd import synth
+    T, E, k, hidden, inter = 300, 16, 4, 256, 256
+    _, ws = _weights(gpu_ctx, E, hidden, inter, seed=600)
+    x = synth.activations(T, hidden, seed=601, dtype=np.float16)
+    logits = synth.router_logits(T, E, seed=602)
+    a = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    b = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    assert np.all(np.isfinite(a))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+def test_moe_shape_errors(gpu_ctx):
+    from arf_amd import QType, synth
+    _, ws = _weights(gpu_ctx, 4, 256, 256, seed=700)
+    x = gpu_ctx.to_device(np.zeros((2, 256), np.float16))
+    lg = gpu_ctx.to_device(np.zeros((2, 4), np.float32))
+    y = gpu_ctx.empty((2, 256), np.float32)
+    with pytest.raises(ValueError):
+        gpu_ctx.moe(ws[0], ws[1], ws[2], lg, 2, 5, True, x, y)  # top_k > experts
+    down_bad = gpu_ctx.upload(QType.Q4_K, synth.weight("q4_k", 512, 256, seed=1, experts=4),
+                              512, 256, 4)
+    with pytest.raises(ValueError):
+        gpu_ctx.moe(ws[0], ws[1], down_bad, lg, 2, 2, True, x, y)
+
+
+def test_c5_moe_full(gpu_ctx, oracle):
+    # C5: 128 experts, top-8, T=512, hidden 2048, inter 768; oracle on 24 sampled tokens
+    from arf_amd import synth
+    _say("case: C5 full")
+    cfg = synth.CONFIGS["c5_moe"]
+    T, E, k, hidden, inter = cfg["tokens"], cfg["experts"], cfg["top_k"], cfg["hidden"], cfg["inter"]
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=0xA7F00005)
+    x = synth.activations(T, hidden, seed=0xA7F00008, dtype=np.float16)
+    logits = synth.router_logits(T, E, seed=0xA7F00009)
+    got = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    rows = np.r_[0:8, 252:260, 504:512]
+    want = oracle.moe_forward(x[rows].astype(np.float32), raw[0], raw[1], raw[2], E, inter,
+                              logits[rows], k, True)
+    e = rel_err(got[rows], want)
+    _say("C5 rel err (24 sampled tokens)", e)
+    assert e <= TOL
+    assert np.all(np.isfinite(got))
