@@ -14,6 +14,7 @@
 // dequant_q6_k + matmul_nt for Q6_K.
 #include "arfq_gemm_tile.h"
 #include "arfq_internal.h"
+#include "arfq_skinny.h"
 
 #include <algorithm>
 
@@ -42,7 +43,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q(
     // split-K: this workgroup's range of steps (whole 256-element blocks for
     // the exact formats)
     const int S = gridDim.y, sp = blockIdx.y;
-    const int unit = F::KIND == 0 ? 1 : 4;
+    const int unit = F::PHASED ? 4 : 1;  // steps whose decode depends on st % 4 start blocks
     const int nu = K / GM_BK / unit;
     const int st0 = unit * (int)((int64_t)sp * nu / S);
     const int st1 = unit * (int)((int64_t)(sp + 1) * nu / S);
@@ -81,6 +82,37 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q(
     }
 }
 
+// Skinny products (m <= 64): workgroup = 128 weight rows x all m rows, over the
+// 256-element blocks of split blockIdx.y (arfq_skinny.h).
+template <class F, int TA>
+__global__ __launch_bounds__(SK_THREADS) void gemm_sk(F fmt, const _Float16 *__restrict__ x,
+                                                      const uint16_t *__restrict__ xs,
+                                                      float *__restrict__ y, int M, int N, int K) {
+    extern __shared__ _Float16 lds[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * 128;
+    const int nb = K / 256, S = gridDim.y, sp = blockIdx.y;
+    const int b0 = (int)((int64_t)sp * nb / S), b1 = (int)((int64_t)(sp + 1) * nb / S);
+    const SkRows<TA> rows = sk_rows<TA>(M, K, [](int r) { return r; });
+    const int n = n0 + 32 * wave + (lane & 31);
+    const F fm[1] = {fmt};
+    const int64_t wrow0[1] = {n0 + 32 * wave};
+    floatx16 acc[1][TA];
+#pragma unroll
+    for (int t = 0; t < TA; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
+    skinny_run<F, TA, 1>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds);
+    float *out = y + (int64_t)sp * M * N;
+#pragma unroll
+    for (int t = 0; t < TA; t++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int m = sk_out_row(t, i);
+            if (m < M && n < N) out[(int64_t)m * N + n] = acc[0][t][i];
+        }
+}
+
 // y[i] = part[0][i] + part[1][i] + ... in split order
 __global__ void splitk_reduce(const float *__restrict__ part, float *__restrict__ y, int64_t n,
                               int S) {
@@ -117,21 +149,29 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     GemmPlan p;
-    p.bm = m > 64 ? 128 : 64;
-    // f32 x: rounded to f16 for prefill shapes (m > 64, as the reference's half
-    // tiles), split into f16 hi + lo for batched decode (m <= 64), where the
-    // path is bound by weight bytes and the second MFMA is free
-    p.xsplit = x_dtype == ARFQ_F32 && m <= 64;
-    p.convert = x_dtype == ARFQ_F32;
-    p.sums = w->qtype == ARFQ_Q4_K;
-    const int64_t mt = (m + p.bm - 1) / p.bm, nt = (w->n + GM_BN - 1) / GM_BN;
-    const int unit = w->qtype == ARFQ_Q8_0 ? 1 : 4;
-    const int64_t nu = w->k / GM_BK / unit;
     const int cus = w->ctx && w->ctx->cus > 0 ? w->ctx->cus : 256;
-    // split K until ~2 workgroups per CU are in flight, keeping >= 8 steps a split
-    int64_t S = std::max<int64_t>(1, (2 * (int64_t)cus) / std::max<int64_t>(1, mt * nt));
-    S = std::min<int64_t>(S, std::max<int64_t>(1, nu * unit / 8));
-    S = std::min<int64_t>(S, nu);
+    p.skinny = m <= 64 && w->k % 256 == 0;
+    p.bm = m > 64 ? 128 : 64;
+    // f32 x: rounded to f16 for the skinny kernel and for prefill shapes (m > 64,
+    // as the reference's half tiles), split into f16 hi + lo otherwise
+    p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && m <= 64;
+    p.convert = x_dtype == ARFQ_F32;
+    p.sums = p.skinny && w->qtype == ARFQ_Q4_K;  // only the exact skinny path reads x sums
+    int64_t S;
+    if (p.skinny) {
+        // split K (whole blocks, >= 2 per split) until ~2 workgroups per CU
+        const int64_t nt = (w->n + 127) / 128, nb = w->k / 256;
+        S = std::max<int64_t>(1, (2 * (int64_t)cus) / nt);
+        S = std::min<int64_t>(S, std::max<int64_t>(1, nb / 2));
+    } else {
+        const int64_t mt = (m + p.bm - 1) / p.bm, nt = (w->n + GM_BN - 1) / GM_BN;
+        const int unit = w->qtype == ARFQ_Q8_0 ? 1 : 4;
+        const int64_t nu = w->k / GM_BK / unit;
+        // split K until ~2 workgroups per CU are in flight, keeping >= 8 steps a split
+        S = std::max<int64_t>(1, (2 * (int64_t)cus) / std::max<int64_t>(1, mt * nt));
+        S = std::min<int64_t>(S, std::max<int64_t>(1, nu * unit / 8));
+        S = std::min<int64_t>(S, nu);
+    }
     p.splits = (int)std::min<int64_t>(S, 16);
     size_t o = 0;
     p.off_xh = o;
@@ -144,6 +184,39 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     o += p.splits > 1 ? al256((size_t)p.splits * m * w->n * 4) : 0;
     p.scratch_bytes = o;
     return p;
+}
+
+template <class F, int TA>
+static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
+                              const uint16_t *xs, float *out, int S, hipStream_t s) {
+    static bool attr_set = false;
+    constexpr size_t lds = sk_lds<F, TA, 1>();
+    if (!attr_set) {
+        hipError_t err = hipFuncSetAttribute((const void *)gemm_sk<F, TA>,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (err != hipSuccess) return err;
+        attr_set = true;
+    }
+    const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
+    gemm_sk<F, TA><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, out, (int)m, (int)w->n, (int)w->k);
+    return hipGetLastError();
+}
+
+template <class F>
+static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
+                            const uint16_t *xs, float *out, int S, hipStream_t s) {
+    return m <= 32 ? launch_sk_t<F, 1>(fmt, w, m, x, xs, out, S, s)
+                   : launch_sk_t<F, 2>(fmt, w, m, x, xs, out, S, s);
+}
+
+SkQ4K sk_q4k(const arfq_weight *w) {
+    return {(const uint4 *)w->s0, (const uint4 *)w->s1, (int)(w->k / 256)};
+}
+SkQ6K sk_q6k(const arfq_weight *w) {
+    return {(const uint2 *)w->s0, (const uint4 *)w->s1, (const uint16_t *)w->s2, (int)(w->k / 256)};
+}
+SkQ80 sk_q80(const arfq_weight *w) {
+    return {(const uint4 *)w->s0, (const uint16_t *)w->s1, (int)(w->k / 32)};
 }
 
 template <class F, int BM, bool XS>
@@ -200,14 +273,31 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     }
     float *out = p.splits > 1 ? (float *)(sc + p.off_part) : y;
     hipError_t err;
-    switch (w->qtype) {
+    if (p.skinny) {
+        switch (w->qtype) {
+        case ARFQ_Q4_K:
+            err = launch_sk(sk_q4k(w).shifted((int64_t)e * w->n * (w->k / 256)), w, m, xh, xs, out,
+                            p.splits, s);
+            break;
+        case ARFQ_Q6_K:
+            err = launch_sk(sk_q6k(w).shifted((int64_t)e * w->n * (w->k / 256)), w, m, xh, xs, out,
+                            p.splits, s);
+            break;
+        case ARFQ_Q8_0:
+            err = launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xh, xs, out,
+                            p.splits, s);
+            break;
+        default:
+            return hipErrorInvalidValue;
+        }
+    } else switch (w->qtype) {
     case ARFQ_Q4_K: {
-        const FmtQ4K f = fmt_q4k(w).shifted((int64_t)e * w->n * (w->k / 256));
+        const FmtQ4KR f{fmt_q4k(w).shifted((int64_t)e * w->n * (w->k / 256))};
         err = launch_fmt(f, w, m, xh, xl, xs, out, p, s);
         break;
     }
     case ARFQ_Q6_K: {
-        const FmtQ6K f = fmt_q6k(w).shifted((int64_t)e * w->n * (w->k / 256));
+        const FmtQ6KR f{fmt_q6k(w).shifted((int64_t)e * w->n * (w->k / 256))};
         err = launch_fmt(f, w, m, xh, xl, xs, out, p, s);
         break;
     }

@@ -90,13 +90,15 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_floa
 // xk(st, q): k index of slot 8q of step st (slots 8q..8q+7 are 8 consecutive
 // k);  load(): the raw data of half `ws` of weight row `row` for step st;
 // deq(): its 32 values as f16 pairs, o[4r..4r+3] = the 8 halves at slot
-// run_off(ws, r);  scale(): (d, dmin) of the raw's block;  mins(): the block's
+// run_off(ws, r), given the step's phase ph = st % 4 (a compile-time constant
+// in the unrolled tile loop, so no branch on it survives);  scale(): (d, dmin) of the raw's block;  mins(): the block's
 // 8 sub-block mins as 4 bf16 pairs.
 
 // Q4_K: step st = sub-blocks 2p, 2p+1 (p = st % 4) of block st / 4; half ws =
 // sub-block 2p + ws, slots 32ws + e = element 64p + 32ws + e.
 struct FmtQ4K {
     static constexpr int KIND = 2;
+    static constexpr bool PHASED = true;  // deq depends on st % 4
     struct Raw {
         u32x4 c, h;
     };
@@ -106,19 +108,32 @@ struct FmtQ4K {
     __host__ __device__ FmtQ4K shifted(int64_t nb) const { return {hdr + nb, qs + nb * 8, nblk}; }
     __device__ static int xk(int st, int q) { return (st >> 2) * 256 + 64 * (st & 3) + 8 * q; }
     __device__ static int run_off(int ws, int r) { return 32 * ws + 8 * r; }
-    __device__ Raw load(int64_t row, int st, int ws) const {
+    // ph = st % 4 (a compile-time constant at the call site): only the header
+    // dwords the step uses are loaded -- d|dmin and the mins (dwords 0, 2) only
+    // for phase 1, whose raw also feeds the block's scale and min-term
+    // operands.  A wide load whose lanes die early lets the register allocator
+    // reuse them while the load is in flight, which costs a full wait.
+    __device__ Raw load(int64_t row, int st, int ws, int ph) const {
         const int64_t blk = row * nblk + (st >> 2);
         Raw r;
         r.c = ldv(qs + blk * 8 + 2 * (st & 3) + ws);
-        r.h = ldv(hdr + blk);
+        const uint32_t *hp = reinterpret_cast<const uint32_t *>(hdr + blk);
+        if (ph == 1) {
+            r.h = ldv(hdr + blk);
+        } else {
+            r.h.x = 0u;
+            r.h.y = hp[1];
+            r.h.z = 0u;
+            r.h.w = ph >= 2 ? hp[3] : 0u;
+        }
         return r;
     }
     // sc_j * q as f16.  Low nibbles become 1024 + q (0x6400 | q) and
     // (1024 + q) * sc - 1024 * sc = sc * q; high nibbles, left in place, become
     // 1024 + 16 q and (1024 + 16 q) * (sc / 16) - 64 * sc = sc * q.  Each FMA is
     // exact (the result is an integer <= 945).
-    __device__ static void deq(const Raw &r, int st, int ws, uint32_t o[16]) {
-        const int j = 2 * (st & 3) + ws;
+    __device__ static void deq(const Raw &r, int ph, int ws, uint32_t o[16]) {
+        const int j = 2 * ph + ws;
         uint32_t sc, mm;
         q4k_scale_min(r.h.y, r.h.z, r.h.w, j, sc, mm);
         const float scf = (float)sc;
@@ -155,6 +170,7 @@ struct FmtQ4K {
 // position i).  Half ws holds positions 8ws..8ws+7 of all four quadrants.
 struct FmtQ6K {
     static constexpr int KIND = 1;
+    static constexpr bool PHASED = true;
     struct Raw {
         u32x2 qa, qb, qh, sc;
         uint32_t d;
@@ -171,7 +187,7 @@ struct FmtQ6K {
         return (st >> 2) * 256 + 128 * (c >> 1) + 16 * (c & 1) + 32 * (q >> 1) + 8 * (q & 1);
     }
     __device__ static int run_off(int ws, int r) { return 16 * r + 8 * ws; }
-    __device__ Raw load(int64_t row, int st, int ws) const {
+    __device__ Raw load(int64_t row, int st, int ws, int) const {
         const int64_t blk = row * nblk + (st >> 2);
         const int c = st & 3;
         const uint2 *ch = qb8 + blk * 24 + c * 6;  // ql_a[16] | ql_b[16] | qh[16]
@@ -184,8 +200,8 @@ struct FmtQ6K {
         return r;
     }
     // sc * (q - 32) as f16: q as 1024 + q (0x6400 | q), minus 1056, times sc.
-    __device__ static void deq(const Raw &r, int st, int, uint32_t o[16]) {
-        const int isub = st & 1;
+    __device__ static void deq(const Raw &r, int ph, int, uint32_t o[16]) {
+        const int isub = ph & 1;
         const uint32_t scw[2] = {r.sc.x, r.sc.y};
         const half2v m1056 = h2splat(-1056.f);
 #pragma unroll
@@ -215,10 +231,69 @@ struct FmtQ6K {
     __device__ static void mins(const Raw &, uint32_t m[4]) { m[0] = m[1] = m[2] = m[3] = 0; }
 };
 
+// Q4_K and Q6_K with the weights rounded to f16 (KIND 0): the prefill tiles
+// (m > 64), where MFMA throughput, not bytes, is the bound and the register
+// file holds no room for per-block accumulators.  One rounding per weight,
+// as the reference's half tiles (matmul_mm_q4ks.metal:166).
+struct FmtQ4KR : FmtQ4K {
+    static constexpr int KIND = 0;
+    __host__ __device__ FmtQ4KR shifted(int64_t nb) const { return {FmtQ4K::shifted(nb)}; }
+    __device__ Raw load(int64_t row, int st, int ws, int) const {
+        const int64_t blk = row * nblk + (st >> 2);
+        Raw r;
+        r.c = ldv(qs + blk * 8 + 2 * (st & 3) + ws);
+        r.h = ldv(hdr + blk);
+        return r;
+    }
+    __device__ static void deq(const Raw &r, int ph, int ws, uint32_t o[16]) {
+        const int j = 2 * ph + ws;
+        uint32_t sc, mm;
+        q4k_scale_min(r.h.y, r.h.z, r.h.w, j, sc, mm);
+        const float d1 = h2f(r.h.x) * (float)sc;
+        const float m1 = h2f(r.h.x >> 16) * (float)mm;
+        const uint32_t cw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            const uint32_t lo = cw[w] & 0x0F0F0F0Fu, hi = (cw[w] >> 4) & 0x0F0F0F0Fu;
+            o[4 * w + 0] = pack2h(fmaf(d1, (float)(lo & 0xffu), -m1), fmaf(d1, (float)((lo >> 8) & 0xffu), -m1));
+            o[4 * w + 1] = pack2h(fmaf(d1, (float)((lo >> 16) & 0xffu), -m1), fmaf(d1, (float)(lo >> 24), -m1));
+            o[4 * w + 2] = pack2h(fmaf(d1, (float)(hi & 0xffu), -m1), fmaf(d1, (float)((hi >> 8) & 0xffu), -m1));
+            o[4 * w + 3] = pack2h(fmaf(d1, (float)((hi >> 16) & 0xffu), -m1), fmaf(d1, (float)(hi >> 24), -m1));
+        }
+    }
+};
+
+struct FmtQ6KR : FmtQ6K {
+    static constexpr int KIND = 0;
+    __host__ __device__ FmtQ6KR shifted(int64_t nb) const { return {FmtQ6K::shifted(nb)}; }
+    // s*q - 32s with one rounding == (d*sc)*(q-32) in f32, then f16
+    __device__ static void deq(const Raw &r, int ph, int, uint32_t o[16]) {
+        const int isub = ph & 1;
+        const float d = h2f(r.d);
+        const uint32_t scw[2] = {r.sc.x, r.sc.y};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int si = isub + 2 * t;
+            const float sf = d * (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
+            const float m32 = -32.f * sf;
+            const u32x2 ql = (t & 1) ? r.qb : r.qa;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const uint32_t l = h ? ql.y : ql.x, hh = h ? r.qh.y : r.qh.x;
+                const uint32_t nib = (t & 2) ? ((l >> 4) & 0x0F0F0F0Fu) : (l & 0x0F0F0F0Fu);
+                const uint32_t q = nib | (((hh >> (2 * t)) & 0x03030303u) << 4);
+                o[4 * t + 2 * h] = pack2h(fmaf((float)(q & 0xffu), sf, m32), fmaf((float)((q >> 8) & 0xffu), sf, m32));
+                o[4 * t + 2 * h + 1] = pack2h(fmaf((float)((q >> 16) & 0xffu), sf, m32), fmaf((float)(q >> 24), sf, m32));
+            }
+        }
+    }
+};
+
 // Q8_0: step st = blocks 2st, 2st+1; half ws = block 2st + ws.  Weights d*q
 // rounded to f16.
 struct FmtQ80 {
     static constexpr int KIND = 0;
+    static constexpr bool PHASED = false;
     struct Raw {
         u32x4 a, b;
         uint32_t d;
@@ -229,7 +304,7 @@ struct FmtQ80 {
     __host__ __device__ FmtQ80 shifted(int64_t nb) const { return {qs + nb * 2, dd + nb, nblk}; }
     __device__ static int xk(int st, int q) { return st * 64 + 8 * q; }
     __device__ static int run_off(int ws, int r) { return 32 * ws + 8 * r; }
-    __device__ Raw load(int64_t row, int st, int ws) const {
+    __device__ Raw load(int64_t row, int st, int ws, int) const {
         const int64_t blk = row * nblk + 2 * st + ws;
         Raw r;
         r.a = ldv(qs + blk * 2);
@@ -268,7 +343,12 @@ struct TileShape {
 //   xsrow[i] element offset (row * K / 16) into xs of the same rows: the x
 //            sub-block sums, 16 bf16 per 256-element block (8 hi, then 8 lo);
 //            read only for KIND 2 formats
-// For KIND >= 1, st0 and st1 are multiples of 4 (whole 256-element blocks).
+// For formats whose decode depends on st % 4 (PHASED: Q4_K, Q6_K) st0 and st1
+// are multiples of 4 (whole 256-element blocks); Q8_0 ranges are arbitrary.
+// Global loads run D steps ahead of the MFMAs in a register ring (D = 4 for
+// 64-row tiles, which stream weights, 2 when x comes as hi + lo; 1 for
+// 128-row tiles, whose registers are spent on accumulators); a load past st1 re-reads step st1 - 1 (a cache
+// hit), which keeps the ring free of branches.
 // The caller zeroes acc and owns `lds` (gm_lds(BM, XSPLIT) bytes).
 template <class F, int BM, bool XSPLIT>
 __device__ __forceinline__ void gemm_tile_run(const F &fmt, int64_t wrow,
@@ -281,6 +361,7 @@ __device__ __forceinline__ void gemm_tile_run(const F &fmt, int64_t wrow,
     using S = TileShape<BM, XSPLIT>;
     constexpr int TA = S::TA, XI = S::XI, NA = S::NA, ATILE = S::ATILE, STAGE = S::STAGE;
     constexpr int KIND = F::KIND;
+    constexpr int D = BM == 64 ? (XSPLIT ? 2 : 4) : 1;  // prefetch depth (steps), divides 4
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
@@ -289,51 +370,53 @@ __device__ __forceinline__ void gemm_tile_run(const F &fmt, int64_t wrow,
     float *sdv_lds = reinterpret_cast<float *>(lds + 2 * STAGE);        // d per weight row
     uint16_t *bv_lds = reinterpret_cast<uint16_t *>(sdv_lds + GM_BN);  // -dmin*m hi[8] lo[8]
 
-    // x hi (or x) and x lo; native vector types: arrays of the HIP uint4 struct
-    // were left in scratch memory by the compiler
-    u32x4 xa[XI], xb[XSPLIT ? XI : 1], xsv[KIND == 2 ? XI : 1];
-    typename F::Raw wv;
-    auto gload = [&](int st) {
+    // the ring: x hi (or x), x lo and the raw weight data of D steps.  Native
+    // vector types: arrays of the HIP uint4 struct were left in scratch memory
+    // by the compiler.
+    u32x4 xa[D][XI], xb[D][XSPLIT ? XI : 1];
+    typename F::Raw wv[D];
+    u32x4 xsv[KIND == 2 ? XI : 1];  // x sub-block sums of the next block to stage
+    auto gload = [&](int slot, int st, int ph) {
         const int kx = F::xk(st, xq);
 #pragma unroll
         for (int i = 0; i < XI; i++) {
-            xa[i] = *reinterpret_cast<const u32x4 *>(xh + xrow[i] + kx);
-            if constexpr (XSPLIT) xb[i] = *reinterpret_cast<const u32x4 *>(xl + xrow[i] + kx);
+            xa[slot][i] = *reinterpret_cast<const u32x4 *>(xh + xrow[i] + kx);
+            if constexpr (XSPLIT) xb[slot][i] = *reinterpret_cast<const u32x4 *>(xl + xrow[i] + kx);
         }
-        wv = fmt.load(wrow, st, ws);
+        wv[slot] = fmt.load(wrow, st, ws, ph);
     };
     // the x sub-block sums of block blk: thread xq & 1 takes the hi or lo half
-    auto xsload = [&](int blk) {
+    auto xsload = [&](u32x4 (&dst)[KIND == 2 ? XI : 1], int blk) {
         if constexpr (KIND == 2) {
 #pragma unroll
             for (int i = 0; i < XI; i++)
-                xsv[i] = *reinterpret_cast<const u32x4 *>(xs + xsrow[i] + blk * 16 + 8 * (xq & 1));
+                dst[i] = *reinterpret_cast<const u32x4 *>(xs + xsrow[i] + blk * 16 + 8 * (xq & 1));
         }
     };
-    auto lstore = [&](int buf, int st) {
+    auto lstore = [&](int buf, int slot, int ph) {
         _Float16 *As = lds + buf * STAGE;
         _Float16 *Bs = As + NA * ATILE;
 #pragma unroll
         for (int i = 0; i < XI; i++) {
-            *reinterpret_cast<u32x4 *>(As + (xr + 32 * i) * GM_LD + 8 * xq) = xa[i];
+            *reinterpret_cast<u32x4 *>(As + (xr + 32 * i) * GM_LD + 8 * xq) = xa[slot][i];
             if constexpr (XSPLIT)
-                *reinterpret_cast<u32x4 *>(As + ATILE + (xr + 32 * i) * GM_LD + 8 * xq) = xb[i];
+                *reinterpret_cast<u32x4 *>(As + ATILE + (xr + 32 * i) * GM_LD + 8 * xq) = xb[slot][i];
         }
         uint32_t o[16];
-        F::deq(wv, st, ws, o);
+        F::deq(wv[slot], ph, ws, o);
 #pragma unroll
         for (int r = 0; r < 4; r++)
             *reinterpret_cast<uint4 *>(Bs + wr * GM_LD + F::run_off(ws, r)) =
                 make_uint4(o[4 * r], o[4 * r + 1], o[4 * r + 2], o[4 * r + 3]);
     };
     // a block's scale and min-term operands (from the raw of one of its steps)
-    auto bstore = [&]() {
+    auto bstore = [&](int slot) {
         if (ws == 0) {
-            const float2 dd = F::scale(wv);
+            const float2 dd = F::scale(wv[slot]);
             sdv_lds[wr] = dd.x;
             if constexpr (KIND == 2) {
                 uint32_t m[4];
-                F::mins(wv, m);
+                F::mins(wv[slot], m);
                 uint32_t hi[4], lo[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -385,77 +468,81 @@ __device__ __forceinline__ void gemm_tile_run(const F &fmt, int64_t wrow,
                         c[t][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a][t], bf[b], c[t][b], 0, 0, 0);
         }
     };
-
-    if constexpr (KIND == 0) {
-        gload(st0);
-        lstore(0, st0);
-        __syncthreads();
-        for (int st = st0; st < st1; st++) {
-            const int buf = (st - st0) & 1;
-            const int nx = min(st + 1, st1 - 1);  // the last step reloads itself (unused)
-            gload(nx);
-            mfma_step(buf, acc);
-            lstore(buf ^ 1, nx);
-            __syncthreads();
+    // block end (exact formats): acc += d * C_block (+ the Q4_K min term, two
+    // bf16 MFMAs into a zeroed temporary).  acc is only touched by VALU ops and
+    // the block sums only by MFMAs, which keeps each in one register file.
+    auto block_end = [&](floatx16 (&cb)[TA][2]) {
+        const float d0 = sdv_lds[wn * 64 + lr], d1 = sdv_lds[wn * 64 + 32 + lr];
+        floatx16 cm[TA][2];
+        if constexpr (KIND == 2) {
+            // A: stage h pad = X hi (h = 0) / X lo (h = 1); B: (-dmin m) hi, then lo
+            const int h = lane >> 5;
+            bf16x8 am[TA], bh[2], bl[2];
+#pragma unroll
+            for (int t = 0; t < TA; t++)
+                am[t] = *reinterpret_cast<const bf16x8 *>(
+                    lds + h * STAGE + (wm * (BM / 2) + 32 * t + lr) * GM_LD + GM_BK);
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const uint16_t *bvr = bv_lds + (wn * 64 + 32 * b + lr) * 16;
+                bh[b] = *reinterpret_cast<const bf16x8 *>(bvr);
+                bl[b] = *reinterpret_cast<const bf16x8 *>(bvr + 8);
+            }
+#pragma unroll
+            for (int t = 0; t < TA; t++)
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    floatx16 z;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) z[i] = 0.f;
+                    cm[t][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[t], bh[b], z, 0, 0, 0);
+                    cm[t][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[t], bl[b], cm[t][b], 0, 0, 0);
+                }
         }
-    } else {
-        floatx16 cb[TA][2];
 #pragma unroll
         for (int t = 0; t < TA; t++)
 #pragma unroll
             for (int b = 0; b < 2; b++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) cb[t][b][i] = 0.f;
-        gload(st0);
-        lstore(0, st0);
-        __syncthreads();
-        for (int blk = st0 >> 2; blk < (st1 >> 2); blk++) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int st = 4 * blk + j;
-                const int nx = min(st + 1, st1 - 1);
-                gload(nx);
-                if (j == 0) xsload(blk);
-                mfma_step(j & 1, cb);
-                if (j == 3) {
-                    // block end: acc += d * C_block, then (Q4_K) the min term
-                    const float d0 = sdv_lds[wn * 64 + lr], d1 = sdv_lds[wn * 64 + 32 + lr];
-#pragma unroll
-                    for (int t = 0; t < TA; t++)
-#pragma unroll
-                        for (int b = 0; b < 2; b++)
-#pragma unroll
-                            for (int i = 0; i < 16; i++) {
-                                acc[t][b][i] = fmaf(b ? d1 : d0, cb[t][b][i], acc[t][b][i]);
-                                cb[t][b][i] = 0.f;
-                            }
-                    if constexpr (KIND == 2) {
-                        // A: stage h pad = X hi (h = 0) / X lo (h = 1); B: (-dmin m) hi, then lo
-                        const int h = lane >> 5;
-                        bf16x8 am[TA], bh[2], bl[2];
-#pragma unroll
-                        for (int t = 0; t < TA; t++)
-                            am[t] = *reinterpret_cast<const bf16x8 *>(
-                                lds + h * STAGE + (wm * (BM / 2) + 32 * t + lr) * GM_LD + GM_BK);
-#pragma unroll
-                        for (int b = 0; b < 2; b++) {
-                            const uint16_t *bvr = bv_lds + (wn * 64 + 32 * b + lr) * 16;
-                            bh[b] = *reinterpret_cast<const bf16x8 *>(bvr);
-                            bl[b] = *reinterpret_cast<const bf16x8 *>(bvr + 8);
-                        }
-#pragma unroll
-                        for (int t = 0; t < TA; t++)
-#pragma unroll
-                            for (int b = 0; b < 2; b++) {
-                                acc[t][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[t], bh[b], acc[t][b], 0, 0, 0);
-                                acc[t][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[t], bl[b], acc[t][b], 0, 0, 0);
-                            }
-                    }
+                for (int i = 0; i < 16; i++) {
+                    float a = fmaf(b ? d1 : d0, cb[t][b][i], acc[t][b][i]);
+                    if constexpr (KIND == 2) a += cm[t][b][i];
+                    acc[t][b][i] = a;
+                    cb[t][b][i] = 0.f;
                 }
-                lstore((j & 1) ^ 1, nx);
-                if (j == 0) bstore();  // block blk's scales / mins (raw of step 4 blk + 1)
-                __syncthreads();
+    };
+
+    floatx16 cb[TA][2];
+#pragma unroll
+    for (int t = 0; t < TA; t++)
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) cb[t][b][i] = 0.f;
+    // prologue: D steps in flight, the first one staged
+#pragma unroll
+    for (int d = 0; d < D; d++) gload(d, min(st0 + d, st1 - 1), d & 3);
+    xsload(xsv, st0 >> 2);
+    lstore(0, 0, 0);
+    __syncthreads();
+    for (int g = st0; g < st1; g += 4) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int st = g + j;
+            if (KIND == 0 && st >= st1) break;  // Q8_0 ranges need not be whole groups of 4
+            // slot j % D was staged (step st) last iteration: refill it D ahead
+            gload(j % D, min(st + D, st1 - 1), (j + D) & 3);
+            // the next block's sums, after this block's were staged (j == 0)
+            if (KIND == 2 && j == (D == 4 ? 1 : 3)) xsload(xsv, min((st >> 2) + 1, (st1 >> 2) - 1));
+            if constexpr (KIND == 0) {
+                mfma_step(j & 1, acc);
+            } else {
+                mfma_step(j & 1, cb);
+                if (j == 3) block_end(cb);
             }
+            lstore((j & 1) ^ 1, (j + 1) % D, (j + 1) & 3);  // step st + 1 (stale past st1)
+            if (KIND != 0 && j == 0) bstore((j + 1) % D);  // block st / 4: raw of step st + 1, sums xsv
+            __syncthreads();
         }
     }
 }

@@ -341,8 +341,8 @@ static int check_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *
     if (up->n != gate->n || up->k != gate->k || down->n != gate->k || down->k != gate->n)
         return fail(ctx, ARFQ_E_SHAPE,
                     "moe: want gate/up [inter, hidden] and down [hidden, inter]");
-    if (gate->k % 64 != 0 || down->k % 64 != 0)
-        return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: hidden and inter must be multiples of 64");
+    if (gate->k % 256 != 0 || down->k % 256 != 0)
+        return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: hidden and inter must be multiples of 256");
     if (top_k < 1 || top_k > E || top_k > arfq::MOE_TOPK_MAX)
         return fail(ctx, ARFQ_E_SHAPE, "moe: top_k must be in [1, min(n_experts, 64)]");
     if (tokens * top_k > (int64_t)1 << 24) return fail(ctx, ARFQ_E_SHAPE, "moe: too many tokens");

@@ -63,6 +63,7 @@ struct GemmPlan {
     bool xsplit = false;   // x as f16 hi + lo (an f32 x split in two)
     bool convert = false;  // x arrives as f32 and is converted into scratch
     bool sums = false;     // the format needs x sub-block sums (Q4_K)
+    bool skinny = false;   // m <= 64: the weight-streaming kernel (arfq_skinny.h)
     size_t off_xh = 0, off_xl = 0, off_xs = 0, off_part = 0, scratch_bytes = 0;
 };
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype);

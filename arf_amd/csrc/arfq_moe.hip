@@ -15,6 +15,7 @@
 // (crates/arf-ml/src/lib.rs:160-162).
 #include "arfq_gemm_tile.h"
 #include "arfq_internal.h"
+#include "arfq_skinny.h"
 
 namespace arfq {
 
@@ -198,75 +199,51 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restri
     }
 }
 
-// ---- grouped GEMMs -------------------------------------------------------------
+// ---- grouped GEMMs ----------------------------------------------------------------
+// Both run the skinny weight-streaming loop (arfq_skinny.h) over one expert
+// tile of up to MOE_BM = 64 (token, slot) rows.
 constexpr int MOE_BM = 64;
 
-// gate|up: output tile = 64 rows (pairs of one expert) x 64 columns of inter.
-// The 128 weight rows of the tile are gate rows n0..n0+63 (waves wn = 0) and up
-// rows n0..n0+63 (waves wn = 1), so both projections share one x tile; the up
-// accumulators go through LDS to the gate waves, which write
-// h = silu(g) * u in f32 (its range can exceed f16's; moe_hprep scales it).
+// gate|up: workgroup = one tile x 128 columns of inter; wave w streams the
+// same 32 rows of gate and of up (NW = 2), so each lane ends with g and u of
+// the same outputs and writes h = silu(g) * u in f32 (its range can exceed
+// f16's; moe_hprep scales it).
 template <class F>
-__global__ __launch_bounds__(GM_THREADS) void moe_gateup_kernel(
+__global__ __launch_bounds__(SK_THREADS) void moe_gateup_kernel(
     F gate, F up, int64_t expert_blocks, const _Float16 *__restrict__ x,
     const uint16_t *__restrict__ xs, int K, int inter, int top_k, const int32_t *__restrict__ off,
     const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ h) {
     extern __shared__ _Float16 lds[];
     if ((int)blockIdx.x >= *ntiles) return;  // uniform over the workgroup
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int2 tile = tiles[blockIdx.x];
     const int e = tile.x, row0 = tile.y;
     const int rows = min(MOE_BM, off[e + 1] - row0);
-    const int n0 = blockIdx.y * 64;
-
-    int64_t xrow[MOE_BM / 32], xsrow[MOE_BM / 32];
+    const int n0 = blockIdx.y * 128 + 32 * wave;
+    const SkRows<2> xr = sk_rows<2>(rows, K, [&](int r) { return sorted[row0 + r] / top_k; });
+    const F fm[2] = {gate.shifted((int64_t)e * expert_blocks), up.shifted((int64_t)e * expert_blocks)};
+    const int64_t wrow0[2] = {n0, n0};
+    floatx16 acc[2][2];
 #pragma unroll
-    for (int i = 0; i < MOE_BM / 32; i++) {
-        const int r = min((tid >> 3) + 32 * i, rows - 1);
-        const int64_t tok = sorted[row0 + r] / top_k;
-        xrow[i] = tok * K;
-        xsrow[i] = tok * (K / 16);
-    }
-    const int wr = tid >> 1;
-    const F fe = (wr < 64 ? gate : up).shifted((int64_t)e * expert_blocks);
-    const int64_t wrow = min(n0 + (wr & 63), inter - 1);
-
-    floatx16 acc[1][2];
+    for (int w = 0; w < 2; w++)
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+        for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[0][b][i] = 0.f;
-    gemm_tile_run<F, MOE_BM, false>(fe, wrow, xrow, xsrow, x, nullptr, xs, 0, K / GM_BK, acc, lds);
-
-    // the loop ended with a barrier: LDS is free.  up waves -> LDS [64][65] f32
-    float *ex = reinterpret_cast<float *>(lds);
-    const int wn = tid >> 7;
-    if (wn == 1) {
+            for (int i = 0; i < 16; i++) acc[w][t][i] = 0.f;
+    skinny_run<F, 2, 2>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc, lds);
+    const int n = n0 + (lane & 31);
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++)
-                ex[tile_out_row<MOE_BM>(0, i) * 65 + tile_out_col(b) - 64] = acc[0][b][i];
-    }
-    __syncthreads();
-    if (wn == 0) {
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int col = tile_out_col(b);
-            const int n = n0 + col;
-#pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int r = tile_out_row<MOE_BM>(0, i);
-                if (r < rows && n < inter) {
-                    const float g = acc[0][b][i];
-                    const float u = ex[r * 65 + col];
-                    const float sg = g / (1.0f + expf(-g));
-                    h[(int64_t)(row0 + r) * inter + n] = sg * u;
-                }
+        for (int i = 0; i < 16; i++) {
+            const int r = sk_out_row(t, i);
+            if (r < rows && n < inter) {
+                const float g = acc[0][t][i], u = acc[1][t][i];
+                const float sg = g / (1.0f + expf(-g));
+                h[(int64_t)(row0 + r) * inter + n] = sg * u;
             }
         }
-    }
 }
 
 // h rows (f32) -> f16 copies scaled by a power of two per row, so that the
@@ -312,49 +289,40 @@ __global__ __launch_bounds__(256) void moe_hprep_kernel(const float *__restrict_
     }
 }
 
-// down: output tile = 64 pair rows x 128 columns of hidden; rows are stored to
-// o[pair index] so the combine can read each token's slots in order.
+// down: workgroup = one tile x 128 columns of hidden; rows are stored to
+// o[pair index], scaled back by the row's h scale, so the combine can read
+// each token's slots in order.
 template <class F>
-__global__ __launch_bounds__(GM_THREADS) void moe_down_kernel(
+__global__ __launch_bounds__(SK_THREADS) void moe_down_kernel(
     F down, int64_t expert_blocks, const _Float16 *__restrict__ h, const uint16_t *__restrict__ hs,
     const float *__restrict__ rs, int K, int hidden, const int32_t *__restrict__ off,
     const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ o) {
     extern __shared__ _Float16 lds[];
     if ((int)blockIdx.x >= *ntiles) return;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int2 tile = tiles[blockIdx.x];
     const int e = tile.x, row0 = tile.y;
     const int rows = min(MOE_BM, off[e + 1] - row0);
-    const int n0 = blockIdx.y * GM_BN;
-
-    int64_t xrow[MOE_BM / 32], xsrow[MOE_BM / 32];
-#pragma unroll
-    for (int i = 0; i < MOE_BM / 32; i++) {
-        const int64_t r = row0 + min((tid >> 3) + 32 * i, rows - 1);
-        xrow[i] = r * K;
-        xsrow[i] = r * (K / 16);
-    }
-    const F fe = down.shifted((int64_t)e * expert_blocks);
-    const int64_t wrow = min(n0 + (tid >> 1), hidden - 1);
-
+    const int n0 = blockIdx.y * 128 + 32 * wave;
+    const SkRows<2> xr = sk_rows<2>(rows, K, [&](int r) { return row0 + r; });
+    const F fm[1] = {down.shifted((int64_t)e * expert_blocks)};
+    const int64_t wrow0[1] = {n0};
     floatx16 acc[1][2];
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[0][b][i] = 0.f;
-    gemm_tile_run<F, MOE_BM, false>(fe, wrow, xrow, xsrow, h, nullptr, hs, 0, K / GM_BK, acc, lds);
-
+        for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
+    skinny_run<F, 2, 1>(fm, wrow0, hidden, xr, h, hs, 0, K / 256, acc, lds);
+    const int n = n0 + (lane & 31);
 #pragma unroll
-    for (int b = 0; b < 2; b++) {
-        const int n = n0 + tile_out_col(b);
+    for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
-            const int r = tile_out_row<MOE_BM>(0, i);
+            const int r = sk_out_row(t, i);
             if (r < rows && n < hidden)
-                o[(int64_t)sorted[row0 + r] * hidden + n] = acc[0][b][i] * rs[row0 + r];
+                o[(int64_t)sorted[row0 + r] * hidden + n] = acc[0][t][i] * rs[row0 + r];
         }
-    }
 }
 
 // ---- combine -------------------------------------------------------------------
@@ -397,24 +365,21 @@ hipError_t launch_moe_group(const int32_t *ids, int64_t P, int E, int32_t *off, 
 int64_t moe_max_tiles(int64_t P, int E) { return (P + MOE_BM - 1) / MOE_BM + E; }
 
 template <class F>
-static hipError_t set_lds_once(const void *fn, size_t bytes, bool &done) {
-    if (done) return hipSuccess;
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-    if (e == hipSuccess) done = true;
-    return e;
-}
-
-template <class F>
 static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const _Float16 *x,
-                           const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted, const void *tiles,
-                           const int32_t *ntiles, int64_t max_tiles, float *h, hipStream_t s) {
+                           const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
+                           const void *tiles, const int32_t *ntiles, int64_t max_tiles, float *h,
+                           hipStream_t s) {
     static bool attr = false;
-    constexpr size_t lds = gm_lds(MOE_BM, false);
-    static_assert(lds >= 64 * 65 * sizeof(float), "epilogue exchange must fit the tile LDS");
-    if (hipError_t e = set_lds_once<F>((const void *)moe_gateup_kernel<F>, lds, attr)) return e;
+    constexpr size_t lds = sk_lds<F, 2, 2>();
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)moe_gateup_kernel<F>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
     const int64_t eb = gw->n * g.nblk;
-    const dim3 grid((unsigned)max_tiles, (unsigned)((gw->n + 63) / 64));
-    moe_gateup_kernel<F><<<grid, GM_THREADS, lds, s>>>(g, u, eb, x, xs, (int)gw->k, (int)gw->n,
+    const dim3 grid((unsigned)max_tiles, (unsigned)((gw->n + 127) / 128));
+    moe_gateup_kernel<F><<<grid, SK_THREADS, lds, s>>>(g, u, eb, x, xs, (int)gw->k, (int)gw->n,
                                                        top_k, off, sorted, (const int2 *)tiles,
                                                        ntiles, h);
     return hipGetLastError();
@@ -422,22 +387,27 @@ static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const 
 
 template <class F>
 static hipError_t down_t(const F &d, const arfq_weight *dw, const _Float16 *h, const uint16_t *hs,
-                         const float *rs, const int32_t *off,
-                         const int32_t *sorted, const void *tiles, const int32_t *ntiles,
-                         int64_t max_tiles, float *o, hipStream_t s) {
+                         const float *rs, const int32_t *off, const int32_t *sorted,
+                         const void *tiles, const int32_t *ntiles, int64_t max_tiles, float *o,
+                         hipStream_t s) {
     static bool attr = false;
-    constexpr size_t lds = gm_lds(MOE_BM, false);
-    if (hipError_t e = set_lds_once<F>((const void *)moe_down_kernel<F>, lds, attr)) return e;
+    constexpr size_t lds = sk_lds<F, 2, 1>();
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute((const void *)moe_down_kernel<F>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
     const int64_t eb = dw->n * d.nblk;
-    const dim3 grid((unsigned)max_tiles, (unsigned)((dw->n + GM_BN - 1) / GM_BN));
-    moe_down_kernel<F><<<grid, GM_THREADS, lds, s>>>(d, eb, h, hs, rs, (int)dw->k, (int)dw->n, off,
+    const dim3 grid((unsigned)max_tiles, (unsigned)((dw->n + 127) / 128));
+    moe_down_kernel<F><<<grid, SK_THREADS, lds, s>>>(d, eb, h, hs, rs, (int)dw->k, (int)dw->n, off,
                                                      sorted, (const int2 *)tiles, ntiles, o);
     return hipGetLastError();
 }
 
-FmtQ4K fmt_q4k(const arfq_weight *w);  // arfq_gemm.hip
-FmtQ6K fmt_q6k(const arfq_weight *w);
-FmtQ80 fmt_q80(const arfq_weight *w);
+SkQ4K sk_q4k(const arfq_weight *w);  // arfq_gemm.hip
+SkQ6K sk_q6k(const arfq_weight *w);
+SkQ80 sk_q80(const arfq_weight *w);
 
 hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, const _Float16 *x,
                              const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
@@ -445,13 +415,13 @@ hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, con
                              float *h, hipStream_t s) {
     switch (gate->qtype) {
     case ARFQ_Q4_K:
-        return gateup_t(fmt_q4k(gate), fmt_q4k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+        return gateup_t(sk_q4k(gate), sk_q4k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
     case ARFQ_Q6_K:
-        return gateup_t(fmt_q6k(gate), fmt_q6k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+        return gateup_t(sk_q6k(gate), sk_q6k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
     case ARFQ_Q8_0:
-        return gateup_t(fmt_q80(gate), fmt_q80(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+        return gateup_t(sk_q80(gate), sk_q80(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
     default: return hipErrorInvalidValue;
     }
@@ -463,11 +433,11 @@ hipError_t launch_moe_down(const arfq_weight *down, const _Float16 *h, const uin
                            int64_t max_tiles, float *o, hipStream_t s) {
     switch (down->qtype) {
     case ARFQ_Q4_K:
-        return down_t(fmt_q4k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+        return down_t(sk_q4k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
     case ARFQ_Q6_K:
-        return down_t(fmt_q6k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+        return down_t(sk_q6k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
     case ARFQ_Q8_0:
-        return down_t(fmt_q80(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+        return down_t(sk_q80(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
     default: return hipErrorInvalidValue;
     }
 }

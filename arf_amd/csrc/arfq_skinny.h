@@ -1,0 +1,419 @@
+// arfq_skinny.h -- weight-streaming MFMA tile loop for skinny products
+// (m <= 64 activation rows): batched decode and the MoE expert tiles.
+//
+// A workgroup is 4 waves; wave w owns 32 weight rows and all (up to 64) x
+// rows of the tile.  Per 256-element block each wave loads its 32 rows'
+// weight bytes with fully coalesced 16-byte loads (whole cache lines: a load
+// that touched 32 rows at once would leave the L1 miss queue, not HBM, as the
+// limit), one block ahead of use, and parks them in a wave-private LDS slab.
+// From the slab each lane reads, per step, the bytes of the
+// v_mfma_f32_32x32x16_f16 B operand it owns -- lane l holds weight row l % 32
+// and, per MFMA, 8 consecutive k of its half (l / 32) -- so no barrier guards
+// the weights.  x is staged in LDS one block at a time and shared by the 4
+// waves (two barriers per block).
+//
+// The weight operand is exact: Q4_K lanes hold sc_j * q and Q6_K lanes
+// sc * (q - 32) as f16 integers; each block accumulates separately and is
+// scaled by the lane's own d at the block end (lane l's C column is its weight
+// row, so d is a register, not a broadcast).  Q4_K's min term
+// -dmin * sum_j m_j * X_j enters as two bf16 MFMAs against the x sub-block
+// sums X_j.  Q8_0 lanes hold d * q rounded to f16.
+//
+// K-slot map of step p (64 elements) of block b: lane half h and MFMA kk use
+// elements a_off(p, kk, h) + 0..7 of the block; the x operand is read from LDS
+// with the same map, so the contraction is unchanged.
+//
+// Reference behaviour: matmul_vec_q4ks_batch_msl.metal:104-288 (B <= 64 rows
+// share each unpacked weight) with the arithmetic of matmul_nt_q4ks /
+// matmul_nt_q8_0 (crates/arf-ml/src/matmul.rs:174-204,322-400) and
+// dequant_q6_k (crates/arf-core/src/model/gguf.rs:2092-2131).
+#pragma once
+#include "arfq_gemm_tile.h"
+
+namespace arfq {
+
+constexpr int SK_THREADS = 256;
+constexpr int SK_XLD = 256 + 8;  // halves per x row in LDS (16 bytes of padding)
+
+
+__device__ __forceinline__ half8 u4_to_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(half8, u32x4{a, b, c, d});
+}
+
+// ---- formats ------------------------------------------------------------------
+// RB: bytes of one weight row's 256-element block in the main stream, loaded
+// coalesced by the wave (RB / 16 lanes per row, whole cache lines) into its
+// LDS slab [32 rows][RB + 16].  frag(): the lane's B operands of step p from
+// its slab row (LDS) and its block data.  load_blk(): the lane's own-row block
+// data (scales), one small load per block.
+
+// Q4_K: step p = sub-blocks 2p (h = 0), 2p + 1 (h = 1); MFMA kk = dword kk of
+// the lane's sub-block (elements 8kk .. 8kk + 7, sigma nibble order).
+struct SkQ4K {
+    static constexpr int KIND = 2, RB = 128;
+    struct Blk {
+        u32x4 h;
+    };
+    const uint4 *hdr, *qs;
+    int nblk;
+    __host__ __device__ SkQ4K shifted(int64_t nb) const { return {hdr + nb, qs + nb * 8, nblk}; }
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    __device__ const uint8_t *raw(int64_t row, int b) const {
+        return reinterpret_cast<const uint8_t *>(qs + (row * nblk + b) * 8);
+    }
+    __device__ Blk load_blk(int64_t row, int b) const { return {ldv(hdr + row * nblk + b)}; }
+    __device__ static float2 scale(const Blk &k) { return make_float2(h2f(k.h.x), h2f(k.h.x >> 16)); }
+    // B operands of step p: sc_j * q, j = 2p + h.  v_perm puts two code bytes
+    // in the low bytes of two halves with 0x64 above them; masking keeps
+    // 0x64 and the low nibble (the f16 1024 + q) or the high nibble
+    // (1024 + 16 q); then (1024 + q) * sc - 1024 sc and
+    // (1024 + 16 q) * (sc / 16) - 64 sc are exact packed f16 FMAs.
+    __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
+        const u32x4 c = *reinterpret_cast<const u32x4 *>(srow + 32 * p + 16 * h);
+        uint32_t sc, mm;
+        q4k_scale_min(k.h.y, k.h.z, k.h.w, 2 * p + h, sc, mm);
+        const float scf = (float)sc;
+        const half2v s1 = h2splat(scf), c1 = h2splat(-1024.f * scf);
+        const half2v s16 = h2splat(scf * 0.0625f), c16 = h2splat(-64.f * scf);
+        const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+            // dword w: byte i low nibble = element 8w+i, high nibble = element 8w+4+i
+            const uint32_t t01 = __builtin_amdgcn_perm(0x64646464u, cw[w], 0x04010400u);  // b0 64 b1 64
+            const uint32_t t23 = __builtin_amdgcn_perm(0x64646464u, cw[w], 0x04030402u);  // b2 64 b3 64
+            f[w] = u4_to_h8(pk_fma(t01 & 0x640F640Fu, s1, c1), pk_fma(t23 & 0x640F640Fu, s1, c1),
+                            pk_fma(t01 & 0x64F064F0u, s16, c16), pk_fma(t23 & 0x64F064F0u, s16, c16));
+        }
+    }
+    // min-term B operands: (-dmin * m_j) as bf16 hi and lo, j = 0..7
+    __device__ static void minsb(const Blk &k, bf16x8 &hi, bf16x8 &lo) {
+        const float dmin = h2f(k.h.x >> 16);
+        uint32_t hv[4], lv[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t h2[2], l2[2];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                uint32_t sc, mm;
+                q4k_scale_min(k.h.y, k.h.z, k.h.w, 2 * i + u, sc, mm);
+                const float v = -dmin * (float)mm;
+                h2[u] = bf16_bits(v);
+                l2[u] = bf16_bits(v - bf16_to_f32(h2[u]));
+            }
+            hv[i] = h2[0] | (h2[1] << 16);
+            lv[i] = l2[0] | (l2[1] << 16);
+        }
+        hi = __builtin_bit_cast(bf16x8, u32x4{hv[0], hv[1], hv[2], hv[3]});
+        lo = __builtin_bit_cast(bf16x8, u32x4{lv[0], lv[1], lv[2], lv[3]});
+    }
+};
+
+// Q6_K: step p = 48-byte chunk p (n2 = p/2, isub = p%2); lane half h takes
+// positions 8h .. 8h + 7 of the 4 quadrants; MFMA kk = quadrant kk:
+// element 128 n2 + 16 isub + 32 kk + 8 h + i.
+struct SkQ6K {
+    static constexpr int KIND = 1, RB = 192;
+    struct Blk {
+        u32x4 sc;  // the 16 i8 scales
+        uint32_t d;
+    };
+    const uint2 *qb8;  // 192-byte chunk streams as 8-byte units
+    const uint4 *sc16;
+    const uint16_t *dd;
+    int nblk;
+    __host__ __device__ SkQ6K shifted(int64_t nb) const {
+        return {qb8 + nb * 24, sc16 + nb, dd + nb, nblk};
+    }
+    __device__ static int a_off(int p, int kk, int h) {
+        return 128 * (p >> 1) + 16 * (p & 1) + 32 * kk + 8 * h;
+    }
+    __device__ const uint8_t *raw(int64_t row, int b) const {
+        return reinterpret_cast<const uint8_t *>(qb8 + (row * nblk + b) * 24);
+    }
+    __device__ Blk load_blk(int64_t row, int b) const {
+        return {ldv(sc16 + row * nblk + b), dd[row * nblk + b]};
+    }
+    __device__ static float2 scale(const Blk &k) { return make_float2(h2f(k.d), 0.f); }
+    // sc * (q - 32): q as the f16 1024 + q (v_perm inserts 0x64 above each code
+    // byte; the 2 qh bits go to bits 4-5), minus 1056, times sc.
+    __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
+        const uint8_t *ch = srow + 48 * p;  // ql_a[16] | ql_b[16] | qh[16]
+        const u32x2 qa = *reinterpret_cast<const u32x2 *>(ch + 8 * h);
+        const u32x2 qb = *reinterpret_cast<const u32x2 *>(ch + 16 + 8 * h);
+        const u32x2 qh = *reinterpret_cast<const u32x2 *>(ch + 32 + 8 * h);
+        const uint32_t scw[4] = {k.sc.x, k.sc.y, k.sc.z, k.sc.w};
+        const half2v m1056 = h2splat(-1056.f);
+        // qh bytes of positions (4hh + 2pr, +1) spread into the two halves
+        uint32_t hp[2][2];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+            for (int pr = 0; pr < 2; pr++)
+                hp[hh][pr] = __builtin_amdgcn_perm(0u, hh ? qh.y : qh.x, pr ? 0x0c030c02u : 0x0c010c00u);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int si = 8 * (p >> 1) + (p & 1) + 2 * t;  // scale index
+            const half2v sv = h2splat((float)(int8_t)(scw[si >> 2] >> (8 * (si & 3))));
+            const u32x2 ql = (t & 1) ? qb : qa;
+            uint32_t o[4];
+#pragma unroll
+            for (int hh = 0; hh < 2; hh++) {
+                const uint32_t l = (t & 2) ? ((hh ? ql.y : ql.x) >> 4) : (hh ? ql.y : ql.x);
+#pragma unroll
+                for (int pr = 0; pr < 2; pr++) {
+                    const uint32_t lp = __builtin_amdgcn_perm(0x64646464u, l, pr ? 0x04030402u : 0x04010400u);
+                    const uint32_t top = 2 * t <= 4 ? (hp[hh][pr] << (4 - 2 * t)) : (hp[hh][pr] >> (2 * t - 4));
+                    const uint32_t q = (lp & 0x640F640Fu) | (top & 0x00300030u);
+                    o[2 * hh + pr] = as_u((as_h2(q) + m1056) * sv);
+                }
+            }
+            f[t] = u4_to_h8(o[0], o[1], o[2], o[3]);
+        }
+    }
+    __device__ static void minsb(const Blk &, bf16x8 &hi, bf16x8 &lo) {
+        hi = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+        lo = hi;
+    }
+};
+
+// Q8_0: step p of 256-element block b = Q8_0 blocks 8b + 2p (h = 0) and
+// 8b + 2p + 1 (h = 1); MFMA kk = bytes 8kk .. 8kk + 7 of the lane's block.
+// Weights d * q rounded to f16 (the format's scale is per 32 weights).
+struct SkQ80 {
+    static constexpr int KIND = 0, RB = 256;
+    struct Blk {
+        u32x4 d;  // the 8 f16 scales of the 8 Q8_0 blocks
+    };
+    const uint4 *qs;
+    const uint16_t *dd;
+    int nblk;  // Q8_0 blocks per row
+    __host__ __device__ SkQ80 shifted(int64_t nb) const { return {qs + nb * 2, dd + nb, nblk}; }
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    __device__ const uint8_t *raw(int64_t row, int b) const {
+        return reinterpret_cast<const uint8_t *>(qs + (row * nblk + 8 * b) * 2);
+    }
+    __device__ Blk load_blk(int64_t row, int b) const {
+        return {*reinterpret_cast<const u32x4 *>(dd + row * nblk + 8 * b)};
+    }
+    __device__ static float2 scale(const Blk &) { return make_float2(1.f, 0.f); }
+    __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(srow + 64 * p + 32 * h);
+        const u32x4 bq = *reinterpret_cast<const u32x4 *>(srow + 64 * p + 32 * h + 16);
+        const int bi = 2 * p + h;
+        const uint32_t dw[4] = {k.d.x, k.d.y, k.d.z, k.d.w};
+        const float d = h2f(dw[bi >> 1] >> (16 * (bi & 1)));
+        const uint32_t cw[8] = {a.x, a.y, a.z, a.w, bq.x, bq.y, bq.z, bq.w};
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            uint32_t o[4];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                const uint32_t v = cw[2 * kk + u];
+                o[2 * u] = pack2h(d * (float)(int8_t)(v & 0xffu), d * (float)(int8_t)((v >> 8) & 0xffu));
+                o[2 * u + 1] = pack2h(d * (float)(int8_t)((v >> 16) & 0xffu), d * (float)(int8_t)(v >> 24));
+            }
+            f[kk] = u4_to_h8(o[0], o[1], o[2], o[3]);
+        }
+    }
+    __device__ static void minsb(const Blk &, bf16x8 &hi, bf16x8 &lo) {
+        hi = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+        lo = hi;
+    }
+};
+
+// ---- the loop -------------------------------------------------------------------
+// x staging: XR = 32 TA rows x 256 k per block = XR * 32 chunks of 16 B over
+// the 256 threads; thread tid stages chunks c = tid + 256 i (row c / 32 =
+// (tid >> 5) + 8 i, k 8 * (tid & 31)) and, for KIND 2, 16 B of the sums of row
+// min(tid >> 1, XR - 1).
+template <int TA>
+struct SkRows {
+    static constexpr int XC = 32 * TA * 32 / SK_THREADS;  // chunks per thread (4 or 8)
+    int64_t x[XC];  // element offset (row * K) of row (tid >> 5) + 8 i
+    int64_t s;      // element offset (row * K / 16) of row min(tid >> 1, XR - 1)
+};
+
+// LDS of the loop: the x block of XR rows (+ its sub-block sums) and one weight
+// slab [32][RB + 16] per wave and weight.
+template <class F, int TA, int NW>
+constexpr size_t sk_lds() {
+    return (size_t)32 * TA * SK_XLD * 2 + (size_t)32 * TA * 32 + (size_t)4 * NW * 32 * (F::RB + 16);
+}
+
+// Accumulates acc[w][t] (w < NW weights, t < TA 32-row x tiles) over the
+// 256-element blocks [b0, b1) for the wave's 32 weight rows wrow0[w] ..
+// wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
+// `rows` gives the x rows this thread stages.  All 256 threads of the
+// workgroup call it with the same block range.
+template <class F, int TA, int NW>
+__device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
+                                           int64_t nrows, const SkRows<TA> &rows,
+                                           const _Float16 *__restrict__ x,
+                                           const uint16_t *__restrict__ xs, int b0, int b1,
+                                           floatx16 (&acc)[NW][TA], _Float16 *lds) {
+    constexpr int KIND = F::KIND;
+    constexpr int XR = 32 * TA;  // x rows staged
+    constexpr int XC = SkRows<TA>::XC;
+    constexpr int RL = F::RB / 16;          // lanes per weight row in a coalesced load
+    constexpr int NI = 32 * F::RB / 1024;   // 16-byte loads per lane per block
+    constexpr int SL = F::RB + 16;          // slab row stride (bytes)
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = lane >> 5, lr = lane & 31;
+    _Float16 *xl = lds;                                              // [XR][SK_XLD]
+    uint16_t *sl = reinterpret_cast<uint16_t *>(lds + XR * SK_XLD);  // [XR][16]
+    uint8_t *slab = reinterpret_cast<uint8_t *>(sl + XR * 16) + (size_t)wave * NW * 32 * SL;
+
+    u32x4 xv[XC], sv;
+    auto xload = [&](int b) {
+#pragma unroll
+        for (int i = 0; i < XC; i++)
+            xv[i] = *reinterpret_cast<const u32x4 *>(x + rows.x[i] + 256 * b + 8 * (tid & 31));
+        if constexpr (KIND == 2)
+            sv = *reinterpret_cast<const u32x4 *>(xs + rows.s + 16 * b + 8 * (tid & 1));
+    };
+    auto xstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < XC; i++)
+            *reinterpret_cast<u32x4 *>(xl + ((tid >> 5) + 8 * i) * SK_XLD + 8 * (tid & 31)) = xv[i];
+        if constexpr (KIND == 2) {
+            if (tid < 2 * XR) *reinterpret_cast<u32x4 *>(sl + (tid >> 1) * 16 + 8 * (tid & 1)) = sv;
+        }
+    };
+
+    // weights: each wave loads its 32 rows x RB bytes of a block with NI
+    // coalesced 16-byte loads per lane (flat chunk c = 64 i + lane: row c / RL,
+    // bytes 16 (c % RL)), one block ahead of use
+    u32x4 rv[NW][NI];
+    typename F::Blk wb[NW], wbn[NW];
+    auto wload = [&](int b) {
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int c = 64 * i + lane;
+                const int64_t row = min(wrow0[w] + c / RL, nrows - 1);
+                rv[w][i] = *reinterpret_cast<const u32x4 *>(fmt[w].raw(row, b) + 16 * (c % RL));
+            }
+    };
+    auto wstore = [&]() {
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+#pragma unroll
+            for (int i = 0; i < NI; i++) {
+                const int c = 64 * i + lane;
+                *reinterpret_cast<u32x4 *>(slab + (w * 32 + c / RL) * SL + 16 * (c % RL)) = rv[w][i];
+            }
+    };
+    int64_t myrow[NW];
+#pragma unroll
+    for (int w = 0; w < NW; w++) myrow[w] = min(wrow0[w] + lr, nrows - 1);
+
+#pragma unroll
+    for (int w = 0; w < NW; w++) wb[w] = fmt[w].load_blk(myrow[w], b0);
+    wload(b0);
+    xload(b0);
+    xstore();
+    __syncthreads();
+
+    floatx16 cb[NW][TA], cmin[NW][KIND == 2 ? TA : 1];
+    if constexpr (KIND == 2) {
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+#pragma unroll
+            for (int t = 0; t < TA; t++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) cmin[w][t][i] = 0.f;
+    }
+    for (int b = b0; b < b1; b++) {
+        const int bn = min(b + 1, b1 - 1);  // past the end: a re-read of the last block
+        wstore();                            // block b's weights (loaded one block ago)
+        wload(bn);
+        xload(bn);
+#pragma unroll
+        for (int w = 0; w < NW; w++) wbn[w] = fmt[w].load_blk(myrow[w], bn);
+        // keep the scheduler from sinking the loads: they must be in flight
+        // during this block, not issued at its end
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                half8 bf[4];
+                F::frag(slab + (w * 32 + lr) * SL, wb[w], p, h, bf);
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+#pragma unroll
+                    for (int t = 0; t < TA; t++) {
+                        const half8 af = *reinterpret_cast<const half8 *>(
+                            xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
+                        if (KIND != 0 && p == 0 && kk == 0) {
+                            floatx16 z;
+#pragma unroll
+                            for (int i = 0; i < 16; i++) z[i] = 0.f;
+                            cb[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], z, 0, 0, 0);
+                        } else if (KIND != 0) {
+                            cb[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], cb[w][t], 0, 0, 0);
+                        } else {
+                            acc[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], acc[w][t], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        }
+        if constexpr (KIND != 0) {
+            // block end: acc += d * C_block; the min term (two bf16 MFMAs)
+            // accumulates across blocks in its own registers
+#pragma unroll
+            for (int w = 0; w < NW; w++) {
+                const float2 dd = F::scale(wb[w]);
+                if constexpr (KIND == 2) {
+                    bf16x8 bh, bl;
+                    F::minsb(wb[w], bh, bl);
+#pragma unroll
+                    for (int t = 0; t < TA; t++) {
+                        const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sl + (32 * t + lr) * 16 + 8 * h);
+                        cmin[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][t], 0, 0, 0);
+                        cmin[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][t], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int t = 0; t < TA; t++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) acc[w][t][i] = fmaf(dd.x, cb[w][t][i], acc[w][t][i]);
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < NW; w++) wb[w] = wbn[w];
+        __syncthreads();  // every wave is done with this block's x
+        xstore();
+        __syncthreads();
+    }
+    if constexpr (KIND == 2) {
+#pragma unroll
+        for (int w = 0; w < NW; w++)
+#pragma unroll
+            for (int t = 0; t < TA; t++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[w][t][i] += cmin[w][t][i];
+    }
+}
+
+// The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
+// [*, K] matrix.
+template <int TA, class RowOf>
+__device__ __forceinline__ SkRows<TA> sk_rows(int n, int K, RowOf row_of) {
+    SkRows<TA> r;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < SkRows<TA>::XC; i++) r.x[i] = (int64_t)row_of(min((tid >> 5) + 8 * i, n - 1)) * K;
+    r.s = (int64_t)row_of(min(tid >> 1, min(32 * TA, n) - 1)) * (K / 16);
+    return r;
+}
+
+// Row of accumulator element i of x tile t for this lane (column = lane % 32).
+__device__ __forceinline__ int sk_out_row(int t, int i) {
+    const int lane = threadIdx.x & 63;
+    return 32 * t + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+}
+
+}  // namespace arfq
