@@ -25,8 +25,9 @@ namespace arfq {
 // divide; then top_k rounds of a wave argmax on (prob desc, index asc), which is
 // the reference's stable sort + truncate; renormalise by the selected sum
 // (summed in selection order) when norm != 0.
-constexpr int MOE_ROUTE_PL = 16;
+constexpr int MOE_ROUTE_PL = 16;  // up to 1024 experts
 
+template <int PL>
 __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits,
                                                         int64_t tokens, int E, int top_k,
                                                         int norm, int32_t *__restrict__ ids,
@@ -35,10 +36,10 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;
     const float *lg = logits + t * E;
-    float v[MOE_ROUTE_PL];
+    float v[PL];
     float mx = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < MOE_ROUTE_PL; j++) {
+    for (int j = 0; j < PL; j++) {
         const int i = j * 64 + lane;
         v[j] = i < E ? lg[i] : -INFINITY;
         mx = fmaxf(mx, v[j]);
@@ -46,17 +47,17 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
 #pragma unroll
-    for (int j = 0; j < MOE_ROUTE_PL; j++) v[j] = (j * 64 + lane < E) ? expf(v[j] - mx) : 0.f;
+    for (int j = 0; j < PL; j++) v[j] = (j * 64 + lane < E) ? expf(v[j] - mx) : 0.f;
     // sum in index order (the reference's sequential iterator sum)
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < MOE_ROUTE_PL; j++) {
+    for (int j = 0; j < PL; j++) {
         if (j * 64 >= E) break;
         const int cnt = min(64, E - j * 64);
         for (int l = 0; l < cnt; l++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
     }
 #pragma unroll
-    for (int j = 0; j < MOE_ROUTE_PL; j++) v[j] = (j * 64 + lane < E) ? v[j] / s : -INFINITY;
+    for (int j = 0; j < PL; j++) v[j] = (j * 64 + lane < E) ? v[j] / s : -INFINITY;
 
     uint32_t taken = 0;
     float myw = 0.f;
@@ -66,7 +67,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
         float bp = -INFINITY;
         int bi = 0x7fffffff;
 #pragma unroll
-        for (int j = 0; j < MOE_ROUTE_PL; j++) {
+        for (int j = 0; j < PL; j++) {
             const int i = j * 64 + lane;
             if (i < E && !((taken >> j) & 1u) && (v[j] > bp || bi == 0x7fffffff)) {
                 bp = v[j];
@@ -95,14 +96,14 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
     }
 }
 
-// ---- group -------------------------------------------------------------------
-// One 1024-thread workgroup.  Pass 1 counts pairs per expert; a scan gives the
-// expert row offsets and the tile list (ceil(count / bm) tiles per expert).
-// Pass 2 walks the pairs in chunks of 1024 in index order; inside a chunk each
-// wave ranks its lanes among equal experts (ballot per distinct expert), a
-// per-wave histogram gives the rank of the wave, and a running per-expert base
-// carries the chunks: position = offset[e] + base[e] + wave prefix + rank, which
-// is the stable order.  Pairs whose expert id is out of range are dropped.
+// ---- group ---------------------------------------------------------------------
+// One 1024-thread workgroup: count the (token, slot) pairs per expert, scan the
+// counts into row offsets and a tile list (ceil(count / bm) tiles per expert),
+// then place each pair at offset[e] + an LDS atomic cursor.  The order of the
+// pairs inside an expert's rows is whatever the atomics give: every row is
+// computed on its own and the combine sums each token's slots in slot order,
+// so the output does not depend on it.  Pairs whose expert id is out of range
+// are dropped.
 constexpr int MOE_MAX_EXPERTS = 512;
 
 __device__ __forceinline__ int block_excl_scan_1024(int v, int *tmp, int &total) {
@@ -132,16 +133,10 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restri
                                                          int32_t *__restrict__ sorted,
                                                          int2 *__restrict__ tiles,
                                                          int32_t *__restrict__ ntiles) {
-    __shared__ int cnt[MOE_MAX_EXPERTS];   // pass 1 counts, then row offsets
-    __shared__ int base[MOE_MAX_EXPERTS];  // rows already placed per expert
-    __shared__ int ctot[MOE_MAX_EXPERTS];  // this chunk's rows per expert
-    __shared__ int whist[16][MOE_MAX_EXPERTS];
+    __shared__ int cnt[MOE_MAX_EXPERTS];  // counts, then the placement cursors
     __shared__ int tmp[32];
-    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    for (int e = tid; e < E; e += 1024) {
-        cnt[e] = 0;
-        base[e] = 0;
-    }
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 1024) cnt[e] = 0;
     __syncthreads();
     for (int64_t p = tid; p < P; p += 1024) {
         const int e = ids[p];
@@ -163,39 +158,9 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restri
         *ntiles = tiles_total;
     }
     __syncthreads();
-
-    const uint64_t lt = (1ull << lane) - 1ull;
-    for (int64_t cb = 0; cb < P; cb += 1024) {
-        const int64_t p = cb + tid;
-        const int e = p < P ? ids[p] : -1;
-        const bool valid = e >= 0 && e < E;
-        for (int i = lane; i < E; i += 64) whist[w][i] = 0;
-        __syncthreads();
-        int rank = 0;
-        uint64_t active = __ballot(valid);
-        while (active) {
-            const int leader = __ffsll((long long)active) - 1;
-            const int le = __shfl(e, leader);
-            const uint64_t m = __ballot(valid && e == le);
-            if (valid && e == le) rank = __popcll(m & lt);
-            if (lane == leader) whist[w][le] = __popcll(m);
-            active &= ~m;
-        }
-        __syncthreads();
-        if (tid < E) {
-            int run = 0;
-            for (int i = 0; i < 16; i++) {
-                const int x = whist[i][tid];
-                whist[i][tid] = run;
-                run += x;
-            }
-            ctot[tid] = run;
-        }
-        __syncthreads();
-        if (valid) sorted[cnt[e] + base[e] + whist[w][e] + rank] = (int32_t)p;
-        __syncthreads();
-        if (tid < E) base[tid] += ctot[tid];
-        __syncthreads();
+    for (int64_t p = tid; p < P; p += 1024) {
+        const int e = ids[p];
+        if (e >= 0 && e < E) sorted[atomicAdd(&cnt[e], 1)] = (int32_t)p;
     }
 }
 
@@ -328,22 +293,26 @@ __global__ __launch_bounds__(SK_THREADS) void moe_down_kernel(
 // ---- combine -------------------------------------------------------------------
 // y[t, c] = ((0 + w0*o0) + w1*o1) + ... over the token's slots in order, each
 // product and sum rounded separately (the reference's out[t] += w_j * y_j).
+// Grid: (hidden / 4 / 256 column blocks, tokens); 4 columns per thread.
 __global__ void moe_combine_kernel(const float *__restrict__ o, const int32_t *__restrict__ ids,
-                                   const float *__restrict__ wts, int64_t tokens, int top_k, int E,
-                                   int hidden, float *__restrict__ y) {
+                                   const float *__restrict__ wts, int top_k, int E, int hidden,
+                                   float *__restrict__ y) {
 #pragma clang fp contract(off)
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= tokens * hidden) return;
-    const int64_t t = i / hidden;
-    const int c = (int)(i - t * hidden);
-    float acc = 0.f;
+    const int64_t t = blockIdx.y;
+    const int c4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (4 * c4 >= hidden) return;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j = 0; j < top_k; j++) {
         const int e = ids[t * top_k + j];
         if (e < 0 || e >= E) continue;  // dropped pair: contributes nothing
-        const float p = wts[t * top_k + j] * o[(t * top_k + j) * hidden + c];
-        acc = acc + p;
+        const float w = wts[t * top_k + j];
+        const float4 v = reinterpret_cast<const float4 *>(o + (t * top_k + j) * hidden)[c4];
+        acc.x = acc.x + w * v.x;
+        acc.y = acc.y + w * v.y;
+        acc.z = acc.z + w * v.z;
+        acc.w = acc.w + w * v.w;
     }
-    y[i] = acc;
+    reinterpret_cast<float4 *>(y + t * hidden)[c4] = acc;
 }
 
 // ---- launchers -----------------------------------------------------------------
@@ -351,8 +320,15 @@ __global__ void moe_combine_kernel(const float *__restrict__ o, const int32_t *_
 hipError_t launch_moe_route(const float *logits, int64_t tokens, int E, int top_k, int norm,
                             int32_t *ids, float *wts, hipStream_t s) {
     if (tokens == 0) return hipSuccess;
-    moe_route_kernel<<<(unsigned)((tokens + 3) / 4), 256, 0, s>>>(logits, tokens, E, top_k, norm,
-                                                                  ids, wts);
+    const unsigned grid = (unsigned)((tokens + 3) / 4);
+    if (E <= 64)
+        moe_route_kernel<1><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
+    else if (E <= 128)
+        moe_route_kernel<2><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
+    else if (E <= 256)
+        moe_route_kernel<4><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
+    else
+        moe_route_kernel<MOE_ROUTE_PL><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
     return hipGetLastError();
 }
 
@@ -451,10 +427,9 @@ hipError_t launch_moe_hprep(const float *h, int64_t P, int inter, _Float16 *h16,
 
 hipError_t launch_moe_combine(const float *o, const int32_t *ids, const float *wts, int64_t tokens,
                               int top_k, int E, int64_t hidden, float *y, hipStream_t s) {
-    const int64_t n = tokens * hidden;
-    if (n == 0) return hipSuccess;
-    moe_combine_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(o, ids, wts, tokens, top_k, E,
-                                                                   (int)hidden, y);
+    if (tokens == 0) return hipSuccess;
+    const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
+    moe_combine_kernel<<<grid, 256, 0, s>>>(o, ids, wts, top_k, E, (int)hidden, y);
     return hipGetLastError();
 }
 

@@ -57,6 +57,39 @@ def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.flo
     return ms / steps, ms
 
 
+def time_moe(ctx, steps, copies):
+    """Average ms per arfq_moe call (C5) rotating `copies` weight sets."""
+    from arf_amd import QType, synth
+    cfg = synth.CONFIGS["c5_moe"]
+    E, T, k, hdim, inter = cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"], cfg["inter"]
+    sets = []
+    for c in range(copies):
+        g = ctx.upload(QType.Q4_K, synth.weight("q4_k", inter, hdim, seed=0xA7F00005 + 3 * c, experts=E),
+                       inter, hdim, E)
+        u = ctx.upload(QType.Q4_K, synth.weight("q4_k", inter, hdim, seed=0xA7F00006 + 3 * c, experts=E),
+                       inter, hdim, E)
+        d = ctx.upload(QType.Q4_K, synth.weight("q4_k", hdim, inter, seed=0xA7F00007 + 3 * c, experts=E),
+                       hdim, inter, E)
+        sets.append((g, u, d))
+    x = ctx.to_device(synth.activations(T, hdim, seed=0xA7F00008, dtype=np.float16))
+    lg = ctx.to_device(synth.router_logits(T, E, seed=0xA7F00009))
+    y = ctx.empty((T, hdim), np.float32)
+    for i in range(3):
+        g, u, d = sets[i % copies]
+        ctx.moe(g, u, d, lg, T, k, True, x, y)
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(steps):
+        g, u, d = sets[i % copies]
+        ctx.moe(g, u, d, lg, T, k, True, x, y)
+    ms = ctx.timer_stop()
+    ctx.sync()
+    for ws in sets:
+        for w in ws:
+            w.free()
+    return ms / steps
+
+
 def cpu_baseline_c2(budget_s):
     """Oracle matmul_nt_q4ks at m=1 (serial, as the reference's par_rows runs m<2) on
     the full C2 weight, repeated for about `budget_s` seconds."""
@@ -138,6 +171,7 @@ def main():
         sys.exit(2)
 
     import arf_amd
+    from arf_amd import synth
     ctx = arf_amd.Context(0)
     if args.traffic_probe:
         traffic_probe(ctx, args.copies)
@@ -187,6 +221,21 @@ def main():
             log(f"[bench] C4: {ms4 * 1e3:.1f} us/launch, {tf:.1f} TFLOP/s")
         except arf_amd.ArfqError as e:
             configs["c4_q4_k_gemm_m2048_k5120_n17408"] = {"error": str(e)}
+        # C5 MoE block
+        try:
+            ms5 = time_moe(ctx, max(10, args.steps // 100), 3)
+            cfg = synth.CONFIGS["c5_moe"]
+            E, T, k, hdim, inter = cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"], cfg["inter"]
+            wbytes = 3 * E * inter * hdim // 256 * 144
+            b5 = wbytes + T * hdim * 2 + T * E * 4 + T * hdim * 4
+            fl5 = 2.0 * T * k * 3 * inter * hdim
+            configs["c5_moe_q4_k_e128_top8_t512_h2048_i768"] = {
+                "us_per_launch": round(ms5 * 1e3, 1), "GB/s": round(b5 / ms5 / 1e6, 1),
+                "hbm_frac": round(b5 / ms5 / 1e6 / HBM_PEAK_GBS, 4),
+                "TFLOP/s": round(fl5 / (ms5 * 1e-3) / 1e12, 1), "weight_copies": 3}
+            log(f"[bench] C5: {ms5 * 1e3:.1f} us/launch")
+        except arf_amd.ArfqError as e:
+            configs["c5_moe_q4_k_e128_top8_t512_h2048_i768"] = {"error": str(e)}
 
     cpu = None
     if not args.no_cpu:
