@@ -147,16 +147,14 @@ struct XqRound {
     float4 v0, v1;
 };
 
+// Branch-free: threads past the end re-read the last item (their results are
+// not stored), so the number of loads in flight never depends on the data.
 __device__ __forceinline__ XqRound xq_load(const float *__restrict__ x, int items, int base) {
-    const int it = base + (int)threadIdx.x;
+    const int it = min(base + (int)threadIdx.x, items - 1);
+    const float4 *src = reinterpret_cast<const float4 *>(x) + (int64_t)it * 2;
     XqRound r;
-    r.v0 = make_float4(0.f, 0.f, 0.f, 0.f);
-    r.v1 = r.v0;
-    if (it < items) {
-        const float4 *src = reinterpret_cast<const float4 *>(x) + (int64_t)it * 2;
-        r.v0 = src[0];
-        r.v1 = src[1];
-    }
+    r.v0 = src[0];
+    r.v1 = src[1];
     return r;
 }
 
@@ -200,42 +198,43 @@ __device__ __forceinline__ void xq_process(const XqRound &r, int items, int base
     }
 }
 
-// (d*sc_j, dmin*m_j) of sub-block j from a Q4_K header (ggml get_scale_min_k4,
-// crates/arf-ml/src/weight.rs:1353-1365), branch-free for a lane-dependent j:
-// two v_perm gather byte j%4 of scales[0..3], scales[4..7], scales[8..11] into
-// D = [A, B, C, 0]; then
-//   j < 4:  sc = A & 63,                 m = B & 63
-//   j >= 4: sc = (C & 15) | (A>>6)<<4,   m = (C >> 4) | (B>>6)<<4
-// are each two bit-field extracts (width 0 yields 0) and a shift-or.
-struct Q4kLane {
-    uint32_t sel1, sel2;          // v_perm selectors
-    uint32_t o1, w1, o2, w2;      // sc = bfe(D,o1,w1) | bfe(D,o2,w2) << 4
-    uint32_t o3, w3, o4, w4;      // m  = bfe(D,o3,w3) | bfe(D,o4,w4) << 4
+// (d*sc, dmin*m) of sub-blocks jj and jj+4 (jj = 0..3) of a Q4_K block from
+// its header dwords h0 = d|dmin, h1 = scales[0..3], h2 = scales[4..7],
+// h3 = scales[8..11] (ggml get_scale_min_k4, crates/arf-ml/src/weight.rs:
+// 1353-1365): with A, B, C = byte jj of h1, h2, h3,
+//   sub-block jj:    sc = A & 63,                 m = B & 63
+//   sub-block jj+4:  sc = (C & 15) | (A>>6)<<4,   m = (C >> 4) | (B>>6)<<4
+struct PairScales {
+    float d_lo, m_lo, d_hi, m_hi;
 };
 
-__device__ __forceinline__ Q4kLane q4k_lane(int j) {
-    const uint32_t i = (uint32_t)(j & 3);
-    Q4kLane L;
-    L.sel1 = i | ((4u + i) << 8) | (0x0Cu << 16) | (0x0Cu << 24);
-    L.sel2 = 0u | (1u << 8) | ((4u + i) << 16) | (0x0Cu << 24);
-    if (j < 4) {
-        L.o1 = 0; L.w1 = 6; L.o2 = 0; L.w2 = 0;
-        L.o3 = 8; L.w3 = 6; L.o4 = 0; L.w4 = 0;
-    } else {
-        L.o1 = 16; L.w1 = 4; L.o2 = 6; L.w2 = 2;
-        L.o3 = 20; L.w3 = 4; L.o4 = 14; L.w4 = 2;
-    }
-    return L;
+__device__ __forceinline__ PairScales q4k_pair_scales(uint32_t h0, uint32_t h1, uint32_t h2,
+                                                      uint32_t h3, uint32_t sh) {
+    const uint32_t A = __builtin_amdgcn_ubfe(h1, sh, 8);
+    const uint32_t B = __builtin_amdgcn_ubfe(h2, sh, 8);
+    const uint32_t C = __builtin_amdgcn_ubfe(h3, sh, 8);
+    const float d = h2f(h0), dmin = h2f(h0 >> 16);
+    PairScales p;
+    p.d_lo = d * (float)(A & 63u);
+    p.m_lo = dmin * (float)(B & 63u);
+    p.d_hi = d * (float)((C & 15u) | ((A >> 6) << 4));
+    p.m_hi = dmin * (float)((C >> 4) | ((B >> 6) << 4));
+    return p;
 }
 
-__device__ __forceinline__ void q4k_sub_scales(const uint4 h, const Q4kLane &L, float &d1,
-                                               float &m1) {
-    const uint32_t T = __builtin_amdgcn_perm(h.z, h.y, L.sel1);
-    const uint32_t D = __builtin_amdgcn_perm(h.w, T, L.sel2);
-    const uint32_t sc = __builtin_amdgcn_ubfe(D, L.o1, L.w1) | (__builtin_amdgcn_ubfe(D, L.o2, L.w2) << 4);
-    const uint32_t mm = __builtin_amdgcn_ubfe(D, L.o3, L.w3) | (__builtin_amdgcn_ubfe(D, L.o4, L.w4) << 4);
-    d1 = h2f(h.x) * (float)sc;
-    m1 = h2f(h.x >> 16) * (float)mm;
+// DPP broadcast of lane k of each quad (quad_perm [k,k,k,k]).
+template <int K>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, K * 0x55, 0xf, 0xf, true);
+}
+
+// Sum over a 16-lane DPP row, result in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<QP_XOR1>(v);
+    v += dpp<QP_XOR2>(v);
+    v += dpp<0x141>(v);  // row_half_mirror
+    v += dpp<0x140>(v);  // row_mirror
+    return v;
 }
 
 // sum(q * x) / 2^(e-15) for one 32-weight sub-block: codes c (4 dwords), digits D0..D3.
@@ -266,132 +265,197 @@ __device__ __forceinline__ int q4k_subdot(const uint4 c, const uint4 D0, const u
     return (int)(a0 + (a1 << 4) + (a2 << 8) + (a3 << 12)) - (int)(sq << 15);
 }
 
-// header dwords 0..3 of the lane's block from the 8-lane block group
-// (ds_swizzle bitmask mode: source lane = (lane & 0x18) | k within 32 lanes)
-__device__ __forceinline__ uint4 q4k_gather_header(uint32_t v) {
-    return make_uint4((uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x18 | (0 << 5)),
-                      (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x18 | (1 << 5)),
-                      (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x18 | (2 << 5)),
-                      (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x18 | (3 << 5)));
-}
-
 }  // namespace
 
 constexpr int Q4K_GEMV_THREADS = 1024;
-constexpr int Q4K_GEMV_GROUPS = Q4K_GEMV_THREADS / 32;
-constexpr int Q4K_GEMV_PF = 4;  // steps of loads in flight per lane
+constexpr int Q4K_GEMV_GROUPS = Q4K_GEMV_THREADS / 16;  // 16-lane groups
+constexpr int Q4K_GEMV_PF = 2;                          // steps of loads in flight
+constexpr int Q4K_GEMV_CHUNK = 2;                       // rows per claimed chunk (divides PF)
+constexpr uint32_t Q4K_OOB = 0x80000000u;               // buffer offset past any stream
 
 // Work split: one 1024-thread workgroup per CU (x is quantized once per CU);
-// workgroup w owns rows [w*n/G, (w+1)*n/G).  Inside it, rows are handed out
-// dynamically: each of the 32 half-wave groups claims whole rows from an LDS
-// counter (so waves that the hardware serves faster take more rows and the
-// workgroup's tail is at most one row).  A group streams a row as spr = nblk/4
-// "steps" of 4 blocks; lane ll owns sub-block j = ll%8 of block 4s + ll/8, and
-// the group keeps PF steps of code/header loads in flight across row
-// boundaries (the next row is claimed when the load ring reaches it).  Each
-// lane loads one dword of the block header (dword j%4) and gets the other
-// three from its 8-lane block group with ds_swizzle.
+// workgroup w owns rows [r0, r1) = [w*n/G, (w+1)*n/G).  Each row is cut into
+// spr = ceil(nblk/4) "columns" of 4 blocks; a "step" is one (row, column)
+// pair.  The steps are handed out in chunks of CHUNK consecutive rows of one
+// column: group g starts with chunk g and then claims chunks from an LDS
+// counter, so the waves the memory system serves first take more chunks (on
+// this hardware the older waves of a CU are served first).  Lane l of a
+// 16-lane group serves block 4*column + l/4 of the row and its sub-blocks
+// jj = l%4 and jj+4: two 16-B code loads and one header dword (jj), the other
+// three header dwords coming from its quad by DPP.  For one x row the x digits
+// of the group's current column are held in registers (reloaded from LDS when
+// the column changes); for more x rows they are read from LDS.  Each step's
+// 16-lane sum is the complete contribution of that (row, column) pair; it goes
+// to LDS part[mi][row][column], and at the end every row adds its columns in
+// order, so the result does not depend on which group computed what.
+//
+// Loads are raw buffer loads with 32-bit offsets; an offset past the stream
+// (blocks past the row's end, steps past the end of the work) returns zeros
+// without touching memory, which contributes exactly 0 (d = 0, q = 0).  Each
+// lane keeps PF steps in flight: a slot is consumed and then refilled with the
+// next claimed step, in a loop unrolled by PF, so every load lands in the
+// registers it is consumed from and the waits are counted ones.
+//
+// Start-up order matters for the first microseconds: every wave issues its x
+// loads, then all waves pass a barrier before any weight load is issued (the
+// CU serves requests in issue order, and x gates all compute), then x is
+// quantized into LDS and the weight ring starts.
 template <int MX, int PF = Q4K_GEMV_PF>
 __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
-    const uint4 *__restrict__ hdr, const uint4 *__restrict__ qs, const float *__restrict__ x,
-    float *__restrict__ y, int n, int nblk, int m) {
+    const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
+    uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk,
+    int m) {
+    constexpr bool XREG = MX == 1;
+    constexpr int C = Q4K_GEMV_CHUNK;
+    static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
     extern __shared__ uint4 smem4[];
+    __shared__ int next_chunk;
     const int nsub = nblk * 8;
     uint4 *dg = smem4;
     float2 *xs = reinterpret_cast<float2 *>(smem4 + (size_t)MX * 4 * nsub);
-    __shared__ int next_row;
+    float *part = reinterpret_cast<float *>(xs + (size_t)MX * nsub);  // [MX][R][spr]
+
+    const __amdgpu_buffer_rsrc_t hrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)hdr_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t qrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)qs, (short)0, (int)qs_bytes, 0x00020000);
 
     const int tid = threadIdx.x;
-    const int ll = tid & 31;
-    const int g = tid >> 5;
-    const int j = ll & 7, bq = ll >> 3;
-    const Q4kLane L = q4k_lane(j);
-    const uint32_t *hdr32 = reinterpret_cast<const uint32_t *>(hdr);
+    const int l16 = tid & 15, grp = tid >> 4;
+    const int bq = l16 >> 2, jj = l16 & 3;
 
     const int G = gridDim.x;
     const int r0 = (int)((int64_t)blockIdx.x * n / G);
     const int r1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
-    const int spr = (nblk + 3) >> 2;  // steps per row
+    const int R = r1 - r0;
+    const int spr = (nblk + 3) >> 2;
+    const int cpc = (R + C - 1) / C;  // chunks per column
+    const int nchunks = cpc * spr;
 
-    if (tid == 0) next_row = r0 + Q4K_GEMV_GROUPS;
-    __syncthreads();
-    // claim the next row of this workgroup (-1 when none is left); lane 0 of
-    // the half-wave does the LDS atomic, a swizzle broadcasts it
-    auto claim = [&]() -> int {
-        int r = 0;
-        if (ll == 0) r = atomicAdd(&next_row, 1);
-        r = __builtin_amdgcn_ds_swizzle(r, 0x00);  // source lane = lane & ~31
-        return r < r1 ? r : -1;
+    // issue state: the current step's column and row.  Chunks are exactly C
+    // rows (rows past the column's end are empty steps), so a new chunk starts
+    // at every C-th issue and the claims sit at fixed places in the unrolled
+    // loop instead of behind data-dependent branches.
+    int icol = 0, irow = 0;
+    auto start_chunk = [&](int k) {
+        icol = k < nchunks ? k / cpc : spr;  // spr = no more work
+        irow = (k - icol * cpc) * C;
     };
-
-    // issue pointer: row irow (absolute, -1 = done), step is.  Loads are
-    // issued unconditionally (clamped addresses once the rows run out) so the
-    // compiler keeps PF steps in flight with counted waits.
-    int irow = r0 + g < r1 ? r0 + g : -1, is = 0;
-    uint4 cbuf[PF];
+    u32x4 clo[PF], chi[PF];
     uint32_t hbuf[PF];
-    int srow[PF], sstep[PF];
-    auto issue = [&](int u) {
-        const int b = min(4 * is + bq, nblk - 1);
-        const int row = irow >= 0 ? irow : r0;
-        const int64_t blk = (int64_t)row * nblk + b;
-        cbuf[u] = ld_nt(qs + blk * 8 + j);
-        hbuf[u] = hdr32[blk * 4 + (j & 3)];
-        srow[u] = irow;
-        sstep[u] = is;
-        if (irow >= 0 && ++is == spr) {
-            is = 0;
-            irow = claim();
+    int srow[PF], scol[PF];  // step held by each slot
+    auto issue = [&](int u, bool first) {
+        if (u % C == 0) {
+            int k = grp;
+            if (!first) {
+                if (l16 == 0) k = atomicAdd(&next_chunk, 1);
+                k = __builtin_amdgcn_ds_swizzle(k, 0x10);  // lane 0 of each 16-lane group
+            }
+            start_chunk(k);
+        } else {
+            irow++;
         }
+        const int b = 4 * icol + bq;
+        const bool live = icol < spr && irow < R && b < nblk;
+        const uint32_t blk = (uint32_t)(r0 + irow) * (uint32_t)nblk + (uint32_t)b;
+        const uint32_t oc = live ? blk * 128u + (uint32_t)jj * 16u : Q4K_OOB;
+        const uint32_t oh = live ? blk * 16u + (uint32_t)jj * 4u : Q4K_OOB;
+        clo[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oc, 0, 2);
+        chi[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oc + 64u, 0, 2);
+        hbuf[u] = __builtin_amdgcn_raw_buffer_load_b32(hrs, oh, 0, 0);
+        srow[u] = irow;
+        scol[u] = icol;
     };
 
-    // x first (it gates the compute), then the weight ring, then quantize
+    if (tid == 0) next_chunk = Q4K_GEMV_GROUPS;
+    // x loads of every wave, then a barrier, then the first weight loads
     const int xitems = m * nsub * 4;
     const XqRound xr0 = xq_load(x, xitems, 0);
-#pragma unroll
-    for (int u = 0; u < PF; u++) issue(u);
+    __builtin_amdgcn_s_barrier();
+    issue(0, true);
+    __builtin_amdgcn_sched_barrier(0);
     xq_process(xr0, xitems, 0, nsub, dg, xs);
     for (int base = Q4K_GEMV_THREADS; base < xitems; base += Q4K_GEMV_THREADS)
         xq_process(xq_load(x, xitems, base), xitems, base, nsub, dg, xs);
-    __syncthreads();
-
-    float acc[MX];
+    __syncthreads();  // x digits and next_chunk are visible from here on
 #pragma unroll
-    for (int mi = 0; mi < MX; mi++) acc[mi] = 0.f;
-    bool more = srow[0] >= 0;
-    while (more) {
+    for (int u = 1; u < PF; u++) {
+        issue(u, u < C);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // x digits of the column being consumed (sub-blocks jj, jj+4)
+    int xcol = -1, ub_lo = 0;
+    uint4 X[2][4];
+    float2 XS[2];
+    auto load_x = [&](int col) {
+        xcol = col;
+        ub_lo = min(4 * col + bq, nblk - 1) * 8 + jj;
+        if (XREG) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+#pragma unroll
+                for (int d = 0; d < 4; d++) X[h][d] = dg[(size_t)d * nsub + ub_lo + 4 * h];
+                XS[h] = xs[ub_lo + 4 * h];
+            }
+        }
+    };
+    const uint32_t sh = 8u * (uint32_t)jj;
+
+    auto consume = [&](int u) {
+        const int col = scol[u], row = srow[u];
+        const bool live = col < spr && row < R;
+        if (live && col != xcol) load_x(col);
+        const uint32_t hw = hbuf[u];
+        const PairScales ps = q4k_pair_scales(quad_bcast<0>(hw), quad_bcast<1>(hw),
+                                              quad_bcast<2>(hw), quad_bcast<3>(hw), sh);
+        const uint4 cl = make_uint4(clo[u].x, clo[u].y, clo[u].z, clo[u].w);
+        const uint4 ch = make_uint4(chi[u].x, chi[u].y, chi[u].z, chi[u].w);
+#pragma unroll
+        for (int mi = 0; mi < MX; mi++) {
+            if (MX == 1 || mi < m) {
+                int s_lo, s_hi;
+                float2 x_lo, x_hi;
+                if (XREG) {
+                    s_lo = q4k_subdot(cl, X[0][0], X[0][1], X[0][2], X[0][3]);
+                    s_hi = q4k_subdot(ch, X[1][0], X[1][1], X[1][2], X[1][3]);
+                    x_lo = XS[0];
+                    x_hi = XS[1];
+                } else {
+                    const uint4 *dp = dg + (size_t)mi * 4 * nsub + ub_lo;
+                    s_lo = q4k_subdot(cl, dp[0], dp[nsub], dp[2 * nsub], dp[3 * nsub]);
+                    s_hi = q4k_subdot(ch, dp[4], dp[nsub + 4], dp[2 * nsub + 4], dp[3 * nsub + 4]);
+                    x_lo = xs[mi * nsub + ub_lo];
+                    x_hi = xs[mi * nsub + ub_lo + 4];
+                }
+                float v = ps.d_lo * (x_lo.x * (float)s_lo) - ps.m_lo * x_lo.y;
+                v += ps.d_hi * (x_hi.x * (float)s_hi) - ps.m_hi * x_hi.y;
+                v = row16_sum(v);
+                if (l16 == 0 && live) part[((size_t)mi * R + row) * spr + col] = v;
+            }
+        }
+    };
+
+    // consume a slot, then refill it (after its codes are used, so the new
+    // load lands in the same registers); claims are monotonic, so once slot 0
+    // holds no work, neither does any later slot
+    while (scol[0] < spr) {
 #pragma unroll
         for (int u = 0; u < PF; u++) {
-            const int row = srow[u], st = sstep[u];
-            if (row < 0) {
-                more = false;  // uniform within the group; later slots are empty too
-                break;
-            }
-            const uint4 c = cbuf[u];
-            const uint4 h = q4k_gather_header(hbuf[u]);
-            issue(u);
-            const int b = 4 * st + bq;
-            float d1, m1;
-            q4k_sub_scales(h, L, d1, m1);
-            const int ub = min(b, nblk - 1) * 8 + j;
-#pragma unroll
-            for (int mi = 0; mi < MX; mi++) {
-                if (mi < m) {
-                    const uint4 *dp = dg + (size_t)mi * 4 * nsub + ub;
-                    const float2 sx = xs[mi * nsub + ub];
-                    const int S = q4k_subdot(c, dp[0], dp[nsub], dp[2 * nsub], dp[3 * nsub]);
-                    const float part = d1 * (sx.x * (float)S) - m1 * sx.y;
-                    acc[mi] += b < nblk ? part : 0.f;
-                }
-            }
-            if (st == spr - 1) {
-#pragma unroll
-                for (int mi = 0; mi < MX; mi++) {
-                    const float v = half_wave_sum_dpp(acc[mi]);
-                    acc[mi] = 0.f;
-                    if (ll == 0 && mi < m) y[(int64_t)mi * n + row] = v;
-                }
-            }
+            consume(u);
+            issue(u, false);
+        }
+    }
+    __syncthreads();
+
+    // each row adds its columns in order
+    for (int t = tid; t < MX * R; t += Q4K_GEMV_THREADS) {
+        const int mi = t / R, r = t - mi * R;
+        if (mi < m) {
+            const float *pr = part + (size_t)t * spr;
+            float v = 0.f;
+            for (int c = 0; c < spr; c++) v += pr[c];
+            y[(int64_t)mi * n + r0 + r] = v;
         }
     }
 }
@@ -531,12 +595,14 @@ __global__ __launch_bounds__(64) void gemv_q6k(const uint4 *__restrict__ qb,
 // ---------------------------------------------------------------- launch ----
 constexpr int GEMV_MAX_M = 4;
 
-// LDS the Q4_K GEMV needs for the quantized x of m rows (digits + scale/sum).
-static size_t q4k_gemv_lds(int64_t m, int64_t k) { return (size_t)m * (k / 32) * (16 * 4 + 8); }
+static size_t q4k_gemv_lds(const arfq_weight *w, int mx);
 
 bool gemv_supports(const arfq_weight *w, int64_t m) {
     if (m < 1 || m > GEMV_MAX_M) return false;
-    if (w->qtype == ARFQ_Q4_K) return q4k_gemv_lds(m <= 2 ? m : 4, w->k) <= 60 * 1024;
+    // the buffer loads address one expert's code stream with 32-bit offsets
+    if (w->qtype == ARFQ_Q4_K)
+        return q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
+               w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
     return w->qtype == ARFQ_Q8_0 || w->qtype == ARFQ_Q6_K;
 }
 
@@ -566,19 +632,36 @@ static hipError_t launch_gemv_t(const arfq_weight *w, int e, int m, const float 
     return hipGetLastError();
 }
 
+static int64_t q4k_gemv_grid(const arfq_weight *w) {
+    const int nblk = (int)(w->k / 256);
+    const int64_t steps = w->n * ((nblk + 3) / 4);
+    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
+    // one workgroup per CU; small problems get fewer (>= 2 steps per group)
+    int64_t grid = std::min<int64_t>(cus, (steps + 2 * Q4K_GEMV_GROUPS - 1) / (2 * Q4K_GEMV_GROUPS));
+    grid = std::min<int64_t>(grid, w->n);  // every workgroup owns at least one row
+    return grid < 1 ? 1 : grid;
+}
+
+// LDS of the Q4_K GEMV: quantized x of mx rows (digits + scale/sum) and the
+// per-(row, column) sums of the workgroup's rows.
+static size_t q4k_gemv_lds(const arfq_weight *w, int mx) {
+    const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
+    const int64_t grid = q4k_gemv_grid(w);
+    const int64_t rows = (w->n + grid - 1) / grid;
+    return (size_t)mx * (w->k / 32) * (16 * 4 + 8) + (size_t)mx * rows * spr * 4;
+}
+
 template <int MX>
 static hipError_t launch_gemv_q4k(const arfq_weight *w, int e, int m, const float *x, float *y,
                                   hipStream_t s) {
     const int n = (int)w->n, nblk = (int)(w->k / 256);
-    const int64_t eb = (int64_t)e * w->n * nblk;
-    const int64_t steps = (int64_t)n * ((nblk + 3) / 4);
-    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
-    // one workgroup per CU; small problems get fewer (>= 4 steps per group)
-    int64_t grid = std::min<int64_t>(cus, (steps + 4 * Q4K_GEMV_GROUPS - 1) / (4 * Q4K_GEMV_GROUPS));
-    if (grid < 1) grid = 1;
-    const size_t lds = q4k_gemv_lds(MX, w->k);
+    const int64_t nb = w->n * nblk;  // blocks of one expert
+    const int64_t eb = (int64_t)e * nb;
+    const int64_t grid = q4k_gemv_grid(w);
+    const size_t lds = q4k_gemv_lds(w, MX);
     gemv_q4k<MX><<<(unsigned)grid, Q4K_GEMV_THREADS, lds, s>>>(
-        (const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8, x, y, n, nblk, m);
+        (const uint8_t *)w->s0 + eb * 16, (uint32_t)(nb * 16), (const uint8_t *)w->s1 + eb * 128,
+        (uint32_t)(nb * 128), x, y, n, nblk, m);
     return hipGetLastError();
 }
 
