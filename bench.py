@@ -225,10 +225,11 @@ def main():
         try:
             ms5 = time_moe(ctx, max(10, args.steps // 100), 3)
             cfg = synth.CONFIGS["c5_moe"]
-            E, T, k, hdim, inter = cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"], cfg["inter"]
+            E, T, topk, hdim, inter = (cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"],
+                                       cfg["inter"])
             wbytes = 3 * E * inter * hdim // 256 * 144
             b5 = wbytes + T * hdim * 2 + T * E * 4 + T * hdim * 4
-            fl5 = 2.0 * T * k * 3 * inter * hdim
+            fl5 = 2.0 * T * topk * 3 * inter * hdim
             configs["c5_moe_q4_k_e128_top8_t512_h2048_i768"] = {
                 "us_per_launch": round(ms5 * 1e3, 1), "GB/s": round(b5 / ms5 / 1e6, 1),
                 "hbm_frac": round(b5 / ms5 / 1e6 / HBM_PEAK_GBS, 4),
