@@ -1,11 +1,13 @@
 // arfq_moe.hip -- the expert-grouped MoE block on device:
 //   route   -> ids[t, j], weights[t, j]       (top-k of the softmax per token)
-//   group   -> (token, slot) pairs sorted by expert, stable in t*top_k + slot,
-//              plus a list of BM-row tiles per expert
-//   gate|up -> h[pair] = silu(x_t . gate_e^T) * (x_t . up_e^T)   (f16, sorted order)
-//   down    -> o[t*top_k + j] = h[pair] . down_e^T               (f32)
+//   group   -> (token, slot) pairs grouped by expert (row offsets per expert)
+//              plus a list of up to MOE_BM-row tiles per expert
+//   gate|up -> h[pair] = silu(x_t . gate_e^T) * (x_t . up_e^T)   (f32, grouped order)
+//   hprep   -> h16 = h / rs (rs a power of two per row), sub-block sums of h16
+//   down    -> o[t*top_k + j] = rs * (h16[pair] . down_e^T)     (f32)
 //   combine -> y[t] = sum_j w[t, j] * o[t*top_k + j] in slot order
-// The grouped GEMMs reuse the dense GEMM's tile loop (arfq_gemm_tile.h).
+// The grouped GEMMs run the skinny weight-streaming MFMA loop
+// (arfq_skinny.h) with exact integer weight operands.
 //
 // Reference behaviour: moe_route_msl.metal:18-98 / moe_batch_msl.metal:371-563
 // (route, CSR by expert, swiglu, slot-ordered reduce), moe_mm_id_q4ks.metal:103-700
