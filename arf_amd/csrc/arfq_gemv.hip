@@ -267,14 +267,16 @@ __device__ __forceinline__ int q4k_subdot(const uint4 c, const uint4 D0, const u
 
 }  // namespace
 
-constexpr int Q4K_GEMV_THREADS = 1024;
+constexpr int Q4K_GEMV_THREADS = 512;
+constexpr int Q4K_GEMV_WG_PER_CU = 2;
 constexpr int Q4K_GEMV_GROUPS = Q4K_GEMV_THREADS / 16;  // 16-lane groups
 constexpr int Q4K_GEMV_PF = 2;                          // steps of loads in flight
 constexpr int Q4K_GEMV_CHUNK = 2;                       // rows per claimed chunk (divides PF)
 constexpr uint32_t Q4K_OOB = 0x80000000u;               // buffer offset past any stream
 
-// Work split: one 1024-thread workgroup per CU (x is quantized once per CU);
-// workgroup w owns rows [r0, r1) = [w*n/G, (w+1)*n/G).  Each row is cut into
+// Work split: two 512-thread workgroups per CU (x is quantized once per
+// workgroup; two independent workgroups per CU measured faster than one of
+// 1024 threads); workgroup w owns rows [r0, r1) = [w*n/G, (w+1)*n/G).  Each row is cut into
 // spr = ceil(nblk/4) "columns" of 4 blocks; a "step" is one (row, column)
 // pair.  The steps are handed out in chunks of CHUNK consecutive rows of one
 // column: group g starts with chunk g and then claims chunks from an LDS
@@ -297,10 +299,11 @@ constexpr uint32_t Q4K_OOB = 0x80000000u;               // buffer offset past an
 // registers it is consumed from and the waits are counted ones.
 //
 // Start-up order matters for the first microseconds: every wave issues its x
-// loads, then all waves pass a barrier before any weight load is issued (the
-// CU serves requests in issue order, and x gates all compute), then x is
-// quantized into LDS and the weight ring starts.
-template <int MX, int PF = Q4K_GEMV_PF>
+// loads (XR rounds of the workgroup, all of them for the shapes the launcher
+// sizes XR for), then all waves pass a barrier before any weight load is
+// issued (the CU serves requests in issue order, and x gates all compute),
+// then x is quantized into LDS and the weight ring starts.
+template <int MX, int XR, int PF = Q4K_GEMV_PF>
 __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk,
@@ -370,12 +373,16 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     if (tid == 0) next_chunk = Q4K_GEMV_GROUPS;
     // x loads of every wave, then a barrier, then the first weight loads
     const int xitems = m * nsub * 4;
-    const XqRound xr0 = xq_load(x, xitems, 0);
+    XqRound xr[XR];
+#pragma unroll
+    for (int r = 0; r < XR; r++) xr[r] = xq_load(x, xitems, r * Q4K_GEMV_THREADS);
     __builtin_amdgcn_s_barrier();
     issue(0, true);
     __builtin_amdgcn_sched_barrier(0);
-    xq_process(xr0, xitems, 0, nsub, dg, xs);
-    for (int base = Q4K_GEMV_THREADS; base < xitems; base += Q4K_GEMV_THREADS)
+#pragma unroll
+    for (int r = 0; r < XR; r++)
+        if (r * Q4K_GEMV_THREADS < xitems) xq_process(xr[r], xitems, r * Q4K_GEMV_THREADS, nsub, dg, xs);
+    for (int base = XR * Q4K_GEMV_THREADS; base < xitems; base += Q4K_GEMV_THREADS)
         xq_process(xq_load(x, xitems, base), xitems, base, nsub, dg, xs);
     __syncthreads();  // x digits and next_chunk are visible from here on
 #pragma unroll
@@ -636,8 +643,9 @@ static int64_t q4k_gemv_grid(const arfq_weight *w) {
     const int nblk = (int)(w->k / 256);
     const int64_t steps = w->n * ((nblk + 3) / 4);
     const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
-    // one workgroup per CU; small problems get fewer (>= 2 steps per group)
-    int64_t grid = std::min<int64_t>(cus, (steps + 2 * Q4K_GEMV_GROUPS - 1) / (2 * Q4K_GEMV_GROUPS));
+    // two workgroups per CU; small problems get fewer (>= 2 steps per group)
+    int64_t grid = std::min<int64_t>((int64_t)Q4K_GEMV_WG_PER_CU * cus,
+                                     (steps + 2 * Q4K_GEMV_GROUPS - 1) / (2 * Q4K_GEMV_GROUPS));
     grid = std::min<int64_t>(grid, w->n);  // every workgroup owns at least one row
     return grid < 1 ? 1 : grid;
 }
@@ -651,18 +659,29 @@ static size_t q4k_gemv_lds(const arfq_weight *w, int mx) {
     return (size_t)mx * (w->k / 32) * (16 * 4 + 8) + (size_t)mx * rows * spr * 4;
 }
 
-template <int MX>
-static hipError_t launch_gemv_q4k(const arfq_weight *w, int e, int m, const float *x, float *y,
-                                  hipStream_t s) {
+template <int MX, int XR>
+static hipError_t launch_gemv_q4k_t(const arfq_weight *w, int e, int m, const float *x, float *y,
+                                    hipStream_t s) {
     const int n = (int)w->n, nblk = (int)(w->k / 256);
     const int64_t nb = w->n * nblk;  // blocks of one expert
     const int64_t eb = (int64_t)e * nb;
     const int64_t grid = q4k_gemv_grid(w);
     const size_t lds = q4k_gemv_lds(w, MX);
-    gemv_q4k<MX><<<(unsigned)grid, Q4K_GEMV_THREADS, lds, s>>>(
+    gemv_q4k<MX, XR><<<(unsigned)grid, Q4K_GEMV_THREADS, lds, s>>>(
         (const uint8_t *)w->s0 + eb * 16, (uint32_t)(nb * 16), (const uint8_t *)w->s1 + eb * 128,
         (uint32_t)(nb * 128), x, y, n, nblk, m);
     return hipGetLastError();
+}
+
+// XR: rounds of x loads issued ahead of the weight ring (the rest, if any,
+// are loaded after it)
+template <int MX>
+static hipError_t launch_gemv_q4k(const arfq_weight *w, int e, int m, const float *x, float *y,
+                                  hipStream_t s) {
+    const int64_t rounds = ((int64_t)m * (w->k / 8) + Q4K_GEMV_THREADS - 1) / Q4K_GEMV_THREADS;
+    if (rounds <= 1) return launch_gemv_q4k_t<MX, 1>(w, e, m, x, y, s);
+    if (rounds <= 2) return launch_gemv_q4k_t<MX, 2>(w, e, m, x, y, s);
+    return launch_gemv_q4k_t<MX, 4>(w, e, m, x, y, s);
 }
 
 hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, float *y,
