@@ -15,6 +15,7 @@
 #include "arfq_gemm_tile.h"
 #include "arfq_internal.h"
 #include "arfq_skinny.h"
+#include "arfq_gemm_bd.h"
 
 #include <algorithm>
 
@@ -156,9 +157,30 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     // as the reference's half tiles), split into f16 hi + lo otherwise
     p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && m <= 64;
     p.convert = x_dtype == ARFQ_F32;
-    p.sums = p.skinny && w->qtype == ARFQ_Q4_K;  // only the exact skinny path reads x sums
+    // Q4_K prefill: the direct-operand kernel (one launch, no split-K)
+    p.bd = !p.skinny && w->qtype == ARFQ_Q4_K && m > 64;
+    // the exact Q4_K paths read x sub-block sums (min term)
+    p.sums = (p.skinny || p.bd) && w->qtype == ARFQ_Q4_K;
     int64_t S;
-    if (p.skinny) {
+    size_t bd_part = 0;
+    if (p.bd) {
+        S = 1;
+        // the tiles past the last whole round of workgroups (one per CU) are
+        // split into K ranges that fill that round; with XCD order the whole
+        // tiles stay a multiple of the M tiles
+        const int64_t mt = (m + BD_BM - 1) / BD_BM, nt = (w->n + BD_BN - 1) / BD_BN;
+        const int64_t tiles = mt * nt, nb = w->k / 256;
+        int64_t r = tiles % cus;
+        if (mt % 8 == 0 && r % mt) r = std::min(tiles, (r / mt + 1) * mt);
+        const int64_t chunks = r ? std::min<int64_t>({(int64_t)cus / r, nb, 16}) : 1;
+        if (r && chunks >= 2) {
+            p.bd_full = (int)(tiles - r);
+            p.bd_chunks = (int)chunks;
+            bd_part = (size_t)r * chunks * BD_BM * BD_BN * 4;
+        } else {
+            p.bd_full = (int)tiles;
+        }
+    } else if (p.skinny) {
         // split K (whole blocks, >= 2 per split) until ~2 workgroups per CU
         const int64_t nt = (w->n + 127) / 128, nb = w->k / 256;
         S = std::max<int64_t>(1, (2 * (int64_t)cus) / nt);
@@ -181,7 +203,7 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     p.off_xs = o;
     o += p.sums ? al256((size_t)m * (w->k / 16) * 2) : 0;
     p.off_part = o;
-    o += p.splits > 1 ? al256((size_t)p.splits * m * w->n * 4) : 0;
+    o += p.splits > 1 ? al256((size_t)p.splits * m * w->n * 4) : al256(bd_part);
     p.scratch_bytes = o;
     return p;
 }
@@ -260,6 +282,34 @@ FmtQ80 fmt_q80(const arfq_weight *w) {
     return {(const uint4 *)w->s0, (const uint16_t *)w->s1, (int)(w->k / 32)};
 }
 
+// Q4_K prefill: weights straight into the MFMA operands (arfq_gemm_bd.h)
+static hipError_t launch_bd_q4k(const arfq_weight *w, int e, int64_t m, const _Float16 *x,
+                                const uint16_t *xs, float *y, float *part, const GemmPlan &p,
+                                hipStream_t s) {
+    const int64_t nblk = w->k / 256;
+    const int64_t eb = (int64_t)e * w->n * nblk;
+    const int mt = (int)((m + BD_BM - 1) / BD_BM), nt = (int)((w->n + BD_BN - 1) / BD_BN);
+    const int tiles = mt * nt, nsplit = tiles - p.bd_full;
+    const int xcd = (mt % 8 == 0 && p.bd_full % mt == 0) ? 1 : 0;
+    if (nsplit && !part) return hipErrorInvalidValue;
+    static bool attr_set = false;  // the attribute belongs to the kernel: set once per process
+    if (!attr_set) {
+        hipError_t err = hipFuncSetAttribute((const void *)gemm_bd_q4k,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bd_lds());
+        if (err != hipSuccess) return err;
+        attr_set = true;
+    }
+    const unsigned items = (unsigned)(p.bd_full + nsplit * p.bd_chunks);
+    gemm_bd_q4k<<<items, BD_THREADS, bd_lds(), s>>>(
+        (const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8, x, xs, y, part, (int)m,
+        (int)w->n, (int)w->k, mt, xcd, p.bd_full, p.bd_chunks);
+    hipError_t err = hipGetLastError();
+    if (err != hipSuccess || !nsplit) return err;
+    bd_reduce_kernel<<<dim3(BD_BM * BD_BN / 256, (unsigned)nsplit), 256, 0, s>>>(
+        part, y, (int)m, (int)w->n, mt, p.bd_full, p.bd_chunks);
+    return hipGetLastError();
+}
+
 hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
                        float *y, void *scratch, const GemmPlan &p, hipStream_t s) {
     char *sc = (char *)scratch;
@@ -292,6 +342,10 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         }
     } else switch (w->qtype) {
     case ARFQ_Q4_K: {
+        if (p.bd) {
+            err = launch_bd_q4k(w, e, m, xh, xs, out, (float *)(sc + p.off_part), p, s);
+            break;
+        }
         const FmtQ4KR f{fmt_q4k(w).shifted((int64_t)e * w->n * (w->k / 256))};
         err = launch_fmt(f, w, m, xh, xl, xs, out, p, s);
         break;

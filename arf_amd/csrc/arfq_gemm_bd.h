@@ -1,0 +1,371 @@
+// arfq_gemm_bd.h -- prefill GEMM for Q4_K weights with the weights going
+// straight from memory into the MFMA B operands (no LDS for weights).
+//
+// A workgroup of 8 waves computes 128 x rows by 512 weight rows; wave w owns
+// the 64 weight rows [n0 + 64 w, n0 + 64 w + 64) for all 128 x rows, as 4 x 2
+// tiles of v_mfma_f32_32x32x16_f16 with f32 accumulators.  Only the f16 x tile
+// (and its sub-block sums) goes through LDS: one whole block (128 x 256
+// halves, 16-byte row padding), double buffered, so the waves meet at one
+// barrier per block and can drift apart within it; all eight waves read it,
+// so each x tile is fetched once per 512 weight rows.  A step is 64 k (a
+// quarter block).  In step p of block b, lane l serves weight row (l % 32) of
+// each of its two 32-row groups and Q4_K sub-block j = 2 p + l / 32: one
+// 16-byte load of that sub-block's codes per group gives the B operands of
+// the step's 4 MFMA groups (group kk uses dword kk: block elements
+// 64 p + 32 (l/32) + 8 kk .. + 7), and the A operands read the x tile with
+// the same element map.  Code loads run two steps ahead; the operand
+// registers of the next MFMA group are refilled while the current group's
+// MFMAs issue (the schedule is pinned with sched_barrier).
+//
+// The B operands are exact: sc_j * q (<= 63 * 15) as f16 integers, made from
+// the code bits with v_perm (each nibble under the f16 bit pattern of 1024)
+// and one packed f16 FMA per two weights (ggml get_scale_min_k4 for sc_j, m_j:
+// crates/arf-ml/src/weight.rs:1353-1365).  The block scale d multiplies the
+// whole block, so instead of a second set of accumulators the accumulators run
+// in units of the current block's d: before block b they are multiplied by
+// d_{b-1} / d_b, and after the last block by d_last (a block with d = 0 uses
+// scale 1 and zero weights).  The min term -dmin_b * sum_j m_j * X_j (X_j:
+// the x sub-block sums, bf16 hi + lo from xprep) goes in at the start of each
+// block with two bf16 MFMAs per tile, its coefficients -dmin * m_j / d_b split
+// into bf16 hi + lo.  So y = sum_b (d_b * sum sc*q*x - dmin_b * sum m*X), as
+// the reference factorises it (crates/arf-ml/src/matmul.rs:327-358).
+//
+// Reference behaviour: matmul_mm_q4ks.metal:65-290 (dequantized Q4_K tiles,
+// simdgroup MMA with f32 accumulation, half x tiles) and the arithmetic of
+// matmul_nt_q4ks (crates/arf-ml/src/matmul.rs:322-400).
+#pragma once
+#include "arfq_gemm_tile.h"
+
+namespace arfq {
+
+constexpr int BD_BM = 128;         // x rows per workgroup (all waves)
+constexpr int BD_WN = 64;          // weight rows per wave
+constexpr int BD_NW = 8;           // waves per workgroup
+constexpr int BD_BN = BD_NW * BD_WN;  // weight rows per workgroup
+constexpr int BD_THREADS = 64 * BD_NW;
+constexpr int BD_LD = 256 + 8;     // halves per LDS x row: one block, 16-byte pad
+
+// LDS: x tiles [2][BD_BM][BD_LD] halves, then the x sub-block sums [2][BD_BM][16] bf16
+__host__ __device__ constexpr size_t bd_lds() {
+    return (size_t)2 * BD_BM * BD_LD * sizeof(_Float16) + (size_t)2 * BD_BM * 16 * sizeof(uint16_t);
+}
+
+// workgroup barrier for the x tile: this wave's LDS writes are complete, no
+// wait on the (prefetching) global loads
+__device__ __forceinline__ void bd_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__device__ __forceinline__ half8 bd_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return __builtin_bit_cast(half8, u32x4{a, b, c, d});
+}
+
+// sc * q of one code dword (8 nibbles of one sub-block, sigma order: byte i
+// low nibble = element i, high nibble = element 4 + i), in element order:
+// (1024 + q) * sc - 1024 sc and (1024 + 16 q) * (sc / 16) - 64 sc, exact
+struct BdScale {
+    half2v s1, c1, s16, c16;
+};
+
+__device__ __forceinline__ BdScale bd_scale(uint32_t sc) {
+    const half2v s1 = h2splat((float)sc);  // sc <= 63: every product below is exact
+    return {s1, s1 * (half2v){-1024.f, -1024.f}, s1 * (half2v){0.0625f, 0.0625f},
+            s1 * (half2v){-64.f, -64.f}};
+}
+
+__device__ __forceinline__ half8 bd_dequant(uint32_t c, const BdScale &k) {
+    const uint32_t t01 = __builtin_amdgcn_perm(0x64646464u, c, 0x04010400u);  // b0 64 b1 64
+    const uint32_t t23 = __builtin_amdgcn_perm(0x64646464u, c, 0x04030402u);  // b2 64 b3 64
+    return bd_h8(pk_fma(t01 & 0x640F640Fu, k.s1, k.c1), pk_fma(t23 & 0x640F640Fu, k.s1, k.c1),
+                 pk_fma(t01 & 0x64F064F0u, k.s16, k.c16), pk_fma(t23 & 0x64F064F0u, k.s16, k.c16));
+}
+
+// The min-term B operands of one block: (-dmin * m_j / su) for j = 0..7 as
+// bf16 hi and lo (every lane all 8, in j order).  Lane half h works out
+// j = 4h .. 4h + 3 and v_permlane32_swap hands each half the other's four.
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void bd_mins(const u32x4 hd, float inv_su, int h, bf16x8 &hi, bf16x8 &lo) {
+    const float f = -h2f(hd.x >> 16) * inv_su;
+    // m_j bytes (ggml get_scale_min_k4): j < 4: scales[4 + j] & 63;
+    // j >= 4: (scales[4 + j] >> 4) | ((scales[j] >> 6) << 4)
+    const uint32_t mb = h ? (((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u)) : (hd.z & 0x3F3F3F3Fu);
+    float c[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) c[i] = f * (float)((mb >> (8 * i)) & 0xffu);
+    uint32_t hv[2], lv[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const bf16x2v hb = {(__bf16)c[2 * i], (__bf16)c[2 * i + 1]};
+        const bf16x2v lb = {(__bf16)(c[2 * i] - (float)hb[0]), (__bf16)(c[2 * i + 1] - (float)hb[1])};
+        hv[i] = __builtin_bit_cast(uint32_t, hb);
+        lv[i] = __builtin_bit_cast(uint32_t, lb);
+    }
+    // after the swap, .x of every lane holds lane half 0's dword and .y half 1's
+    const auto h0 = __builtin_amdgcn_permlane32_swap(hv[0], hv[0], false, false);
+    const auto h1 = __builtin_amdgcn_permlane32_swap(hv[1], hv[1], false, false);
+    const auto l0 = __builtin_amdgcn_permlane32_swap(lv[0], lv[0], false, false);
+    const auto l1 = __builtin_amdgcn_permlane32_swap(lv[1], lv[1], false, false);
+    hi = __builtin_bit_cast(bf16x8, u32x4{h0[0], h1[0], h0[1], h1[1]});
+    lo = __builtin_bit_cast(bf16x8, u32x4{l0[0], l1[0], l0[1], l1[1]});
+}
+
+// Work items: the first `full` items are whole tiles (in XCD order when
+// xcd_order); the remaining tiles are each split into `chunks` K ranges of
+// whole blocks, one item per range, whose partial tiles go to part[item -
+// full][BD_BM][BD_BN] and are added in chunk order by bd_reduce_kernel.  This
+// fills the last round of workgroups when the tiles do not divide the CUs.
+__global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
+    const uint4 *__restrict__ hdr, const uint4 *__restrict__ qs, const _Float16 *__restrict__ x,
+    const uint16_t *__restrict__ xs, float *__restrict__ y, float *__restrict__ part, int m, int n,
+    int k, int mt, int xcd_order, int full, int chunks) {
+    extern __shared__ _Float16 sx[];  // [2][BD_BM][BD_LD]
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int nblk = k / 256;
+
+    // tile and block range of this work item (XCD x keeps a fixed set of x
+    // tiles when the M tiles divide by 8; the dispatcher places workgroup b on
+    // XCD b % 8)
+    const int item = blockIdx.x;
+    int tile, kb0 = 0, kb1 = nblk;
+    const bool split = item >= full;
+    if (!split) {
+        if (xcd_order) {
+            const int xcd = item & 7, q = item >> 3, per = mt >> 3;
+            tile = (q / per) * mt + xcd * per + q % per;
+        } else {
+            tile = item;
+        }
+    } else {
+        const int li = item - full, ch = li % chunks;
+        tile = full + li / chunks;
+        kb0 = (int)((int64_t)ch * nblk / chunks);
+        kb1 = (int)((int64_t)(ch + 1) * nblk / chunks);
+    }
+    const int tm = tile % mt, tn = tile / mt;
+    const int m0 = tm * BD_BM, n0 = tn * BD_BN + wave * BD_WN;
+    const int st0 = 4 * kb0, st1 = 4 * kb1;  // this item's steps
+
+    const int col = lane & 31, h = lane >> 5;
+    const int64_t wr0 = min(n0 + col, n - 1), wr1 = min(n0 + 32 + col, n - 1);
+
+    // x tile staging: thread t copies row t / 4.  The next block's x moves in
+    // two halves (halves 0..127 of the row, then 128..255), each loaded at
+    // the start of one half of the current block and stored into the other
+    // buffer near its end: thread (t % 4) takes 2 x 16 bytes per 64 halves.
+    const int xr = tid >> 2, xo = (tid & 3) * 16;
+    const _Float16 *xsrc = x + (int64_t)min(m0 + xr, m - 1) * k + xo;
+    u32x4 xa[4];
+    auto xload = [&](int blk, int half) {
+        const uint4 *src = reinterpret_cast<const uint4 *>(xsrc + (int64_t)blk * 256 + 128 * half);
+        xa[0] = ldv(src);
+        xa[1] = ldv(src + 1);
+        xa[2] = ldv(src + 8);  // + 64 halves
+        xa[3] = ldv(src + 9);
+    };
+    // x sub-block sums of the next block: thread t moves 4 of row t / 4's 16
+    const uint16_t *xssrc = xs + (int64_t)min(m0 + xr, m - 1) * (k / 16) + (tid & 3) * 4;
+    uint16_t *sxs = reinterpret_cast<uint16_t *>(sx + 2 * BD_BM * BD_LD);  // [2][BD_BM][16]
+    u32x2 xsa;
+    auto xsload = [&](int blk) { xsa = *reinterpret_cast<const u32x2 *>(xssrc + (int64_t)blk * 16); };
+    auto xsstore = [&](int buf) {
+        *reinterpret_cast<u32x2 *>(sxs + ((size_t)buf * BD_BM + xr) * 16 + (tid & 3) * 4) = xsa;
+    };
+    auto xstore = [&](int buf, int half) {
+        u32x4 *dst = reinterpret_cast<u32x4 *>(sx + ((size_t)buf * BD_BM + xr) * BD_LD + 128 * half + xo);
+        dst[0] = xa[0];
+        dst[1] = xa[1];
+        dst[8] = xa[2];
+        dst[9] = xa[3];
+    };
+
+    // code ring: slot s % 2 holds step s (the two groups' 16-byte sub-block
+    // loads); it is refilled with step s + 2 as soon as its last dword is
+    // dequantized
+    u32x4 cq[2][2];
+    auto cload = [&](int u, int st) {
+        st = min(st, st1 - 1);  // past the end: reload the last step (unused)
+        const int blk = st >> 2, j = 2 * (st & 3) + h;
+        cq[u][0] = ldv(qs + (wr0 * nblk + blk) * 8 + j);
+        cq[u][1] = ldv(qs + (wr1 * nblk + blk) * 8 + j);
+    };
+    // block headers of the two rows, one block ahead
+    u32x4 hdn[2];
+    auto hload = [&](int blk) {
+        blk = min(blk, kb1 - 1);
+        hdn[0] = ldv(hdr + wr0 * nblk + blk);
+        hdn[1] = ldv(hdr + wr1 * nblk + blk);
+    };
+
+    floatx16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int g = 0; g < 2; g++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[i][g][e] = 0.f;
+
+    // prologue: the first block's x tile, the first headers and code steps
+#pragma unroll
+    for (int hf = 0; hf < 2; hf++) {
+        xload(kb0, hf);
+        xstore(0, hf);
+    }
+    xsload(kb0);
+    xsstore(0);
+    hload(kb0);
+#pragma unroll
+    for (int u = 0; u < 2; u++) cload(u, st0 + u);
+    bd_barrier();
+
+    float sprev[2] = {1.f, 1.f};  // accumulator unit (block scale) per group
+    for (int blk = kb0; blk < kb1; blk++) {
+        // this block's integer scales (sub-blocks j = 2p + h, byte p) and unit d
+        uint32_t scd[2];
+        float inv[2];
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const u32x4 hd = hdn[g];
+            const float d = h2f(hd.x);
+            const bool live = d != 0.f;
+            const float su = live ? d : 1.f;
+            uint32_t packed = 0;
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                uint32_t sc, mm;
+                q4k_scale_min(hd.y, hd.z, hd.w, 2 * p + h, sc, mm);
+                packed |= sc << (8 * p);
+            }
+            scd[g] = live ? packed : 0u;
+            // move the accumulators into units of this block's d
+            inv[g] = __builtin_amdgcn_rcpf(su);
+            const float ratio = sprev[g] * inv[g];
+            sprev[g] = su;
+#pragma unroll
+            for (int mg = 0; mg < 4; mg++)
+#pragma unroll
+                for (int e = 0; e < 16; e++) acc[mg][g][e] *= ratio;
+        }
+        const int buf = (blk - kb0) & 1;
+        // the min term of this block, -dmin * sum_j m_j X_j in units of d: one
+        // bf16 MFMA pair per tile against the x sub-block sums (lane half h
+        // reads the hi / lo half of row (32 mg + l % 32)'s 16)
+        {
+            bf16x8 bh[2], bl[2];
+#pragma unroll
+            for (int g = 0; g < 2; g++) bd_mins(hdn[g], inv[g], h, bh[g], bl[g]);
+#pragma unroll
+            for (int mg = 0; mg < 4; mg++) {
+                const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sxs + ((size_t)buf * BD_BM + 32 * mg + col) * 16 + 8 * h);
+#pragma unroll
+                for (int g = 0; g < 2; g++) {
+                    acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh[g], acc[mg][g], 0, 0, 0);
+                    acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl[g], acc[mg][g], 0, 0, 0);
+                }
+            }
+        }
+        hload(blk + 1);
+        const int nb = min(blk + 1, kb1 - 1);  // next block (past the end: unused copy)
+        const _Float16 *xt0 = sx + ((size_t)buf * BD_BM + col) * BD_LD + 32 * h;
+
+        // 16 MFMA groups per block: group i = (step p = i / 4, dword kk = i % 4)
+        // of 8 MFMAs, g-major.  The operand registers of group i + 1 are
+        // refilled as soon as group i's last use of them has issued: b[0]
+        // (dequantized codes) after the four g = 0 MFMAs, a[mg] (x from LDS)
+        // after MFMA (mg, g = 1), b[1] after the last MFMA.
+        half8 a[4], b[2];
+        BdScale ks[2];
+        auto xread = [&](int i, int mg) {
+            a[mg] = *reinterpret_cast<const half8 *>(xt0 + (size_t)mg * 32 * BD_LD + 64 * (i >> 2) + 8 * (i & 3));
+        };
+        auto deq = [&](int i, int g) {
+            const int p = i >> 2, kk = i & 3;
+            if (kk == 0) ks[g] = bd_scale((scd[g] >> (8 * p)) & 0xffu);
+            const uint32_t cw = kk == 0 ? cq[p & 1][g].x : kk == 1 ? cq[p & 1][g].y : kk == 2 ? cq[p & 1][g].z : cq[p & 1][g].w;
+            b[g] = bd_dequant(cw, ks[g]);
+        };
+#pragma unroll
+        for (int mg = 0; mg < 4; mg++) xread(0, mg);
+        deq(0, 0);
+        deq(0, 1);
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            const int p = i >> 2, kk = i & 3;
+            const bool more = i < 15;
+            __builtin_amdgcn_sched_barrier(0);
+            if (i == 0) {
+                xload(nb, 0);
+                xsload(nb);
+            }
+            if (i == 8) xload(nb, 1);
+#pragma unroll
+            for (int mg = 0; mg < 4; mg++) {
+                acc[mg][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[0], acc[mg][0], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (more) deq(i + 1, 0);
+#pragma unroll
+            for (int mg = 0; mg < 4; mg++) {
+                acc[mg][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[1], acc[mg][1], 0, 0, 0);
+                if (more) xread(i + 1, mg);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (kk == 3) cload(p & 1, 4 * blk + p + 2);  // the slot is free: step + 2
+            if (more) deq(i + 1, 1);
+            if (i == 6) {
+                xstore(buf ^ 1, 0);
+                xsstore(buf ^ 1);
+            }
+            if (i == 14) xstore(buf ^ 1, 1);
+        }
+        bd_barrier();
+    }
+    // back to true units
+#pragma unroll
+    for (int g = 0; g < 2; g++)
+#pragma unroll
+        for (int mg = 0; mg < 4; mg++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[mg][g][e] *= sprev[g];
+
+    // C layout of a 32x32 tile: lane l, value i -> row 8 (i/4) + 4 (l/32) + i%4, column l % 32
+    float *pt = split ? part + (size_t)(item - full) * BD_BM * BD_BN : nullptr;
+#pragma unroll
+    for (int mg = 0; mg < 4; mg++) {
+#pragma unroll
+        for (int g = 0; g < 2; g++) {
+            const int cl = wave * BD_WN + 32 * g + col;  // column within the tile
+            const int cn = n0 + 32 * g + col;
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int rl = 32 * mg + 8 * (i >> 2) + 4 * h + (i & 3);
+                if (split) {
+                    pt[(size_t)rl * BD_BN + cl] = acc[mg][g][i];
+                } else if (cn < n && m0 + rl < m) {
+                    y[(int64_t)(m0 + rl) * n + cn] = acc[mg][g][i];
+                }
+            }
+        }
+    }
+}
+
+// y of the split tiles: the chunks' partial tiles added in chunk order.
+// One thread per output; grid (BD_BM * BD_BN / 256, split tiles).
+__global__ __launch_bounds__(256) void bd_reduce_kernel(const float *__restrict__ part,
+                                                        float *__restrict__ y, int m, int n,
+                                                        int mt, int full, int chunks) {
+    const int lt = blockIdx.y;
+    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int rl = e / BD_BN, cl = e - rl * BD_BN;
+    const int tile = full + lt;
+    const int r = (tile % mt) * BD_BM + rl, c = (tile / mt) * BD_BN + cl;
+    if (r >= m || c >= n) return;
+    const float *pp = part + (size_t)lt * chunks * BD_BM * BD_BN + e;
+    float v = 0.f;
+    for (int j = 0; j < chunks; j++) v += pp[(size_t)j * BD_BM * BD_BN];
+    y[(int64_t)r * n + c] = v;
+}
+
+}  // namespace arfq

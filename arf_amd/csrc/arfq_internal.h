@@ -64,6 +64,9 @@ struct GemmPlan {
     bool convert = false;  // x arrives as f32 and is converted into scratch
     bool sums = false;     // the format needs x sub-block sums (Q4_K)
     bool skinny = false;   // m <= 64: the weight-streaming kernel (arfq_skinny.h)
+    bool bd = false;       // Q4_K prefill: weights straight into MFMA operands (arfq_gemm_bd.h)
+    int bd_full = 0;       // bd: whole tiles; the rest are split into bd_chunks K ranges
+    int bd_chunks = 1;
     size_t off_xh = 0, off_xl = 0, off_xs = 0, off_part = 0, scratch_bytes = 0;
 };
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype);

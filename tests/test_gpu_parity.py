@@ -172,10 +172,11 @@ def test_gemm_f16_x_other_formats(gpu_ctx, oracle, qtype, m, n, k):
     assert e <= TOL
 
 
-def test_gemm_split_k_is_deterministic(gpu_ctx):
-    # a skinny shape runs split-K; the ordered reduction gives the same bits twice
+@pytest.mark.parametrize("n,k,m", [(256, 8192, 8), (200, 5120, 130)])
+def test_gemm_split_k_is_deterministic(gpu_ctx, n, k, m):
+    # both shapes run split-K (the skinny kernel at m = 8, the prefill kernel's
+    # split tail at m = 130); the ordered reduction gives the same bits twice
     from arf_amd import QType, synth
-    n, k, m = 256, 8192, 8
     raw = synth.weight("q4_k", n, k, seed=17)
     w = gpu_ctx.upload(QType.Q4_K, raw, n, k)
     x = gpu_ctx.to_device(synth.activations(m, k, seed=18))
