@@ -158,7 +158,8 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && m <= 64;
     p.convert = x_dtype == ARFQ_F32;
     // Q4_K prefill: the direct-operand kernel (one launch, no split-K)
-    p.bd = !p.skinny && w->qtype == ARFQ_Q4_K && m > 64;
+    p.bd = !p.skinny && w->qtype == ARFQ_Q4_K && m > 64 &&
+           w->n * (w->k / 2) < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
     // the exact Q4_K paths read x sub-block sums (min term)
     p.sums = (p.skinny || p.bd) && w->qtype == ARFQ_Q4_K;
     int64_t S;

@@ -91,7 +91,9 @@ __device__ __forceinline__ void bd_mins(const u32x4 hd, float inv_su, int h, bf1
     const float f = -h2f(hd.x >> 16) * inv_su;
     // m_j bytes (ggml get_scale_min_k4): j < 4: scales[4 + j] & 63;
     // j >= 4: (scales[4 + j] >> 4) | ((scales[j] >> 6) << 4)
-    const uint32_t mb = h ? (((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u)) : (hd.z & 0x3F3F3F3Fu);
+    const uint32_t mlo = hd.z & 0x3F3F3F3Fu;
+    const uint32_t mhi = ((hd.w >> 4) & 0x0F0F0F0Fu) | ((hd.z >> 2) & 0x30303030u);
+    const uint32_t mb = mlo ^ ((mlo ^ mhi) & (0u - (uint32_t)h));  // branch-free select
     float c[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) c[i] = f * (float)((mb >> (8 * i)) & 0xffu);
@@ -149,27 +151,38 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
     const int st0 = 4 * kb0, st1 = 4 * kb1;  // this item's steps
 
     const int col = lane & 31, h = lane >> 5;
-    const int64_t wr0 = min(n0 + col, n - 1), wr1 = min(n0 + 32 + col, n - 1);
+    const uint32_t wr0 = min(n0 + col, n - 1), wr1 = min(n0 + 32 + col, n - 1);
+    // buffer loads: a per-lane 32-bit offset fixed for the whole item plus a
+    // uniform (SGPR) offset per block and step, so no per-load address math
+    // (the launcher keeps every stream below 2 GiB)
+    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)qs, (short)0, (int)((uint32_t)n * nblk * 128), 0x00020000);
+    const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)hdr, (short)0, (int)((uint32_t)n * nblk * 16), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)x, (short)0, (int)((uint32_t)m * k * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)xs, (short)0, (int)((uint32_t)m * (k / 16) * 2), 0x00020000);
 
     // x tile staging: thread t copies row t / 4.  The next block's x moves in
     // two halves (halves 0..127 of the row, then 128..255), each loaded at
     // the start of one half of the current block and stored into the other
     // buffer near its end: thread (t % 4) takes 2 x 16 bytes per 64 halves.
     const int xr = tid >> 2, xo = (tid & 3) * 16;
-    const _Float16 *xsrc = x + (int64_t)min(m0 + xr, m - 1) * k + xo;
+    const uint32_t xv = (uint32_t)min(m0 + xr, m - 1) * k * 2 + xo * 2;  // bytes
     u32x4 xa[4];
     auto xload = [&](int blk, int half) {
-        const uint4 *src = reinterpret_cast<const uint4 *>(xsrc + (int64_t)blk * 256 + 128 * half);
-        xa[0] = ldv(src);
-        xa[1] = ldv(src + 1);
-        xa[2] = ldv(src + 8);  // + 64 halves
-        xa[3] = ldv(src + 9);
+        const int so = blk * 512 + 256 * half;
+        xa[0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv, so, 0);
+        xa[1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 16, so, 0);
+        xa[2] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 128, so, 0);  // + 64 halves
+        xa[3] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 144, so, 0);
     };
     // x sub-block sums of the next block: thread t moves 4 of row t / 4's 16
-    const uint16_t *xssrc = xs + (int64_t)min(m0 + xr, m - 1) * (k / 16) + (tid & 3) * 4;
+    const uint32_t sv = (uint32_t)min(m0 + xr, m - 1) * (k / 16) * 2 + (tid & 3) * 8;  // bytes
     uint16_t *sxs = reinterpret_cast<uint16_t *>(sx + 2 * BD_BM * BD_LD);  // [2][BD_BM][16]
     u32x2 xsa;
-    auto xsload = [&](int blk) { xsa = *reinterpret_cast<const u32x2 *>(xssrc + (int64_t)blk * 16); };
+    auto xsload = [&](int blk) { xsa = __builtin_amdgcn_raw_buffer_load_b64(srs, sv, blk * 32, 0); };
     auto xsstore = [&](int buf) {
         *reinterpret_cast<u32x2 *>(sxs + ((size_t)buf * BD_BM + xr) * 16 + (tid & 3) * 4) = xsa;
     };
@@ -181,22 +194,25 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
         dst[9] = xa[3];
     };
 
+    const uint32_t qv0 = wr0 * nblk * 128 + 16 * h, qv1 = wr1 * nblk * 128 + 16 * h;
+    const uint32_t hv0 = wr0 * nblk * 16, hv1 = wr1 * nblk * 16;
     // code ring: slot s % 2 holds step s (the two groups' 16-byte sub-block
     // loads); it is refilled with step s + 2 as soon as its last dword is
     // dequantized
     u32x4 cq[2][2];
     auto cload = [&](int u, int st) {
         st = min(st, st1 - 1);  // past the end: reload the last step (unused)
-        const int blk = st >> 2, j = 2 * (st & 3) + h;
-        cq[u][0] = ldv(qs + (wr0 * nblk + blk) * 8 + j);
-        cq[u][1] = ldv(qs + (wr1 * nblk + blk) * 8 + j);
+        const int blk = st >> 2;
+        const int so = blk * 128 + 32 * (st & 3);  // + 16 h in the lane offsets
+        cq[u][0] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qv0, so, 0);
+        cq[u][1] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qv1, so, 0);
     };
     // block headers of the two rows, one block ahead
     u32x4 hdn[2];
     auto hload = [&](int blk) {
         blk = min(blk, kb1 - 1);
-        hdn[0] = ldv(hdr + wr0 * nblk + blk);
-        hdn[1] = ldv(hdr + wr1 * nblk + blk);
+        hdn[0] = __builtin_amdgcn_raw_buffer_load_b128(hrs, hv0, blk * 16, 0);
+        hdn[1] = __builtin_amdgcn_raw_buffer_load_b128(hrs, hv1, blk * 16, 0);
     };
 
     floatx16 acc[4][2];
@@ -220,14 +236,18 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
     for (int u = 0; u < 2; u++) cload(u, st0 + u);
     bd_barrier();
 
-    float sprev[2] = {1.f, 1.f};  // accumulator unit (block scale) per group
-    for (int blk = kb0; blk < kb1; blk++) {
-        // this block's integer scales (sub-blocks j = 2p + h, byte p) and unit d
-        uint32_t scd[2];
-        float inv[2];
+    // block scale state of the current block: scd (integer scales of the
+    // sub-blocks 2p + h, byte p), inv = 1 / su and ratio = su_prev / su, the
+    // factor that moves the accumulators into this block's unit su (= d, or 1
+    // when d = 0); hdc holds the block's headers for the min term
+    uint32_t scd[2];
+    float inv[2], ratio[2], sprev[2] = {1.f, 1.f};
+    u32x4 hdc[2];
+    auto block_scales = [&]() {
 #pragma unroll
         for (int g = 0; g < 2; g++) {
-            const u32x4 hd = hdn[g];
+            hdc[g] = hdn[g];
+            const u32x4 hd = hdc[g];
             const float d = h2f(hd.x);
             const bool live = d != 0.f;
             const float su = live ? d : 1.f;
@@ -239,34 +259,16 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
                 packed |= sc << (8 * p);
             }
             scd[g] = live ? packed : 0u;
-            // move the accumulators into units of this block's d
             inv[g] = __builtin_amdgcn_rcpf(su);
-            const float ratio = sprev[g] * inv[g];
+            ratio[g] = sprev[g] * inv[g];
             sprev[g] = su;
-#pragma unroll
-            for (int mg = 0; mg < 4; mg++)
-#pragma unroll
-                for (int e = 0; e < 16; e++) acc[mg][g][e] *= ratio;
         }
+    };
+    block_scales();
+    hload(kb0 + 1);
+
+    for (int blk = kb0; blk < kb1; blk++) {
         const int buf = (blk - kb0) & 1;
-        // the min term of this block, -dmin * sum_j m_j X_j in units of d: one
-        // bf16 MFMA pair per tile against the x sub-block sums (lane half h
-        // reads the hi / lo half of row (32 mg + l % 32)'s 16)
-        {
-            bf16x8 bh[2], bl[2];
-#pragma unroll
-            for (int g = 0; g < 2; g++) bd_mins(hdn[g], inv[g], h, bh[g], bl[g]);
-#pragma unroll
-            for (int mg = 0; mg < 4; mg++) {
-                const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sxs + ((size_t)buf * BD_BM + 32 * mg + col) * 16 + 8 * h);
-#pragma unroll
-                for (int g = 0; g < 2; g++) {
-                    acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh[g], acc[mg][g], 0, 0, 0);
-                    acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl[g], acc[mg][g], 0, 0, 0);
-                }
-            }
-        }
-        hload(blk + 1);
         const int nb = min(blk + 1, kb1 - 1);  // next block (past the end: unused copy)
         const _Float16 *xt0 = sx + ((size_t)buf * BD_BM + col) * BD_LD + 32 * h;
 
@@ -274,9 +276,18 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
         // of 8 MFMAs, g-major.  The operand registers of group i + 1 are
         // refilled as soon as group i's last use of them has issued: b[0]
         // (dequantized codes) after the four g = 0 MFMAs, a[mg] (x from LDS)
-        // after MFMA (mg, g = 1), b[1] after the last MFMA.
+        // after MFMA (mg, g = 1), b[1] after the last MFMA.  Around them:
+        //  - the accumulators move into this block's unit: g = 1 here, g = 0
+        //    at the end of the previous block (behind its last MFMAs);
+        //  - groups 0, 1 work out the min-term operands and group 2 adds the
+        //    min term -dmin * sum_j m_j X_j (units of d: two bf16 MFMAs per
+        //    tile against the x sub-block sums, lane half h reading the hi /
+        //    lo half of row (32 mg + l % 32)'s 16);
+        //  - group 12 takes the next block's headers (scales, ratio) and
+        //    issues the loads of the one after.
         half8 a[4], b[2];
         BdScale ks[2];
+        bf16x8 bh[2], bl[2], am[4];
         auto xread = [&](int i, int mg) {
             a[mg] = *reinterpret_cast<const half8 *>(xt0 + (size_t)mg * 32 * BD_LD + 64 * (i >> 2) + 8 * (i & 3));
         };
@@ -291,21 +302,51 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
         deq(0, 0);
         deq(0, 1);
 #pragma unroll
+        for (int mg = 0; mg < 4; mg++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) acc[mg][1][e] *= ratio[1];
+#pragma unroll
         for (int i = 0; i < 16; i++) {
             const int p = i >> 2, kk = i & 3;
             const bool more = i < 15;
             __builtin_amdgcn_sched_barrier(0);
-            if (i == 0) {
+            if (i == 3) {
                 xload(nb, 0);
                 xsload(nb);
             }
-            if (i == 8) xload(nb, 1);
+            if (i == 9) xload(nb, 1);
+            if (i == 12) {
+                block_scales();  // the next block's (scd of this one is used up)
+                hload(blk + 2);
+            }
+            if (i < 2) bd_mins(hdc[i], inv[i], h, bh[i], bl[i]);
+            if (i == 1) {
+#pragma unroll
+                for (int mg = 0; mg < 4; mg++)
+                    am[mg] = *reinterpret_cast<const bf16x8 *>(sxs + ((size_t)buf * BD_BM + 32 * mg + col) * 16 + 8 * h);
+            }
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
                 acc[mg][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[0], acc[mg][0], 0, 0, 0);
+                if (i == 2) {
+#pragma unroll
+                    for (int g = 0; g < 2; g++) {
+                        acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bh[g], acc[mg][g], 0, 0, 0);
+                        acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bl[g], acc[mg][g], 0, 0, 0);
+                    }
+                }
                 __builtin_amdgcn_sched_barrier(0);
             }
             if (more) deq(i + 1, 0);
+            if (i == 15) {
+                // group 0's accumulators into the next block's unit (the last
+                // block keeps its unit)
+                const float r0 = blk + 1 < kb1 ? ratio[0] : 1.f;
+#pragma unroll
+                for (int mg = 0; mg < 4; mg++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++) acc[mg][0][e] *= r0;
+            }
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
                 acc[mg][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[1], acc[mg][1], 0, 0, 0);
@@ -314,11 +355,11 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
             }
             if (kk == 3) cload(p & 1, 4 * blk + p + 2);  // the slot is free: step + 2
             if (more) deq(i + 1, 1);
-            if (i == 6) {
+            if (i == 8) {
                 xstore(buf ^ 1, 0);
                 xsstore(buf ^ 1);
             }
-            if (i == 14) xstore(buf ^ 1, 1);
+            if (i == 15) xstore(buf ^ 1, 1);
         }
         bd_barrier();
     }

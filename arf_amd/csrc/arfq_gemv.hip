@@ -96,17 +96,7 @@ __device__ __forceinline__ float dot16_i8(const float *x, uint4 q) {
 // and the sub-block contributes  (d*sc) * that - (dmin*m) * sum(x)  as in the
 // oracle's dot_q4ks (crates/arf-ml/src/matmul.rs:327-358).  The quantization
 // error is at most 2^-15 of the block's max |x| per element (~1e-5 of the
-// output's rms).
-//
-// Work split (persistent, balanced): one 1024-thread workgroup per CU, so x is
-// quantized once per CU.  Workgroup w owns rows [w*n/G, (w+1)*n/G).  A "step"
-// is one row x 4 consecutive blocks; the workgroup's 32 half-wave groups take
-// equal contiguous ranges of its steps (a row may be split between adjacent
-// groups; those partials are added in LDS in group order, so the result is
-// deterministic).  Lane ll of a group owns sub-block j = ll%8 of block
-// 4s + ll/8 of step s and keeps PF steps of code/header loads in flight,
-// across row boundaries.  Each lane loads one dword of the block header (dword
-// j%4) and gets the other three from its 8-lane block group with ds_swizzle.
+// output's rms).  The work split is described at gemv_q4k below.
 
 namespace {
 
