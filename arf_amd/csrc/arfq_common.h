@@ -37,6 +37,7 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 }
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // 16-byte streaming load (non-temporal hint: each weight byte is read once).
 __device__ __forceinline__ uint4 ld_nt(const uint4 *p) {

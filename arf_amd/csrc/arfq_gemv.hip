@@ -457,6 +457,252 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     }
 }
 
+// ------------------------------------------------------------ Q6_K (dot) ----
+// Integer-dot GEMV for one or two x rows.  x is quantized per 32-element
+// block to 16-bit fixed point X = rint(x * 2^(15-e)) (as for Q4_K) and held in
+// LDS as a low-byte plane (u8) and a high-byte plane (i8, X >> 8), both in
+// element order, with the sum of every 16 elements and 2^(e-15) per 32.  A
+// 16-element Q6_K sub-block then gives
+//     sum(q * X) = 256 * sdot4(q, hi) + udot4(q, lo)    (4 + 4 dots, exact int32)
+// and contributes (d*sc) * (2^(e-15) * sum(q*X) - 32 * sum(x)): the oracle's
+// (d*sc)*(q-32) per weight (gguf.rs:2120-2123), factorised.
+// Work split as gemv_q4k: two 512-thread workgroups per CU, steps = (row,
+// column of 4 blocks) claimed in chunks of 2 rows of one column.  Lane l of a
+// 16-lane group serves block 4*column + l/4 and its 48-byte chunk c = l%4
+// (64 codes: 4 quadrant sub-blocks of 16), one scale dword (c) whose
+// neighbours come from its quad by DPP, and the block's d.
+constexpr int Q6K_GEMV_THREADS = 512;
+constexpr int Q6K_GEMV_GROUPS = Q6K_GEMV_THREADS / 16;
+constexpr int Q6K_GEMV_PF = 2;
+constexpr int Q6K_GEMV_CHUNK = 2;
+
+namespace {
+
+// Quantize one round of x items (8 elements each, 4 per 32-element block) into
+// the byte planes: lo/hi [row*k + e], s16 [row*k/16 + e/16], xe [row*k/32 + e/32].
+__device__ __forceinline__ void xq6_process(const XqRound &r, int items, int base, int k,
+                                            uint8_t *lo, uint8_t *hi, float *s16, float *xe) {
+    const int it = base + (int)threadIdx.x;
+    const float4 v0 = r.v0, v1 = r.v1;
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                       fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+    float sum = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+    amax = fmaxf(amax, quad_perm<QP_XOR1>(amax));
+    sum += quad_perm<QP_XOR1>(sum);  // 16 elements (items 2i, 2i+1)
+    amax = fmaxf(amax, quad_perm<QP_XOR2>(amax));
+    const int ex = (amax > 0.f) ? __builtin_amdgcn_frexp_expf(amax) : 0;
+    const float vv[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    uint32_t L[2] = {0u, 0u}, H[2] = {0u, 0u};
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        float q = rintf(ldexpf(vv[t], 15 - ex));
+        q = fminf(fmaxf(q, -32767.f), 32767.f);
+        const uint32_t xi = (uint32_t)(int)q;
+        L[t >> 2] |= (xi & 0xFFu) << (8 * (t & 3));
+        H[t >> 2] |= ((xi >> 8) & 0xFFu) << (8 * (t & 3));
+    }
+    if (it < items) {
+        const int e = it * 8;  // element of the flattened [m][k] x
+        *reinterpret_cast<u32x2 *>(lo + e) = u32x2{L[0], L[1]};
+        *reinterpret_cast<u32x2 *>(hi + e) = u32x2{H[0], H[1]};
+        if ((it & 1) == 0) s16[e >> 4] = sum;
+        if ((it & 3) == 0) xe[e >> 5] = ldexpf(1.f, ex - 15);
+    }
+}
+
+// sum(q * X) of one 16-code quadrant: codes cw[4] (one byte each), planes lo/hi.
+__device__ __forceinline__ int q6k_subdot(const uint32_t *cw, const u32x4 lo, const u32x4 hi) {
+    uint32_t a = __builtin_amdgcn_udot4(cw[0], lo.x, 0u, false);
+    int b = __builtin_amdgcn_sdot4((int)cw[0], (int)hi.x, 0, false);
+    a = __builtin_amdgcn_udot4(cw[1], lo.y, a, false);
+    b = __builtin_amdgcn_sdot4((int)cw[1], (int)hi.y, b, false);
+    a = __builtin_amdgcn_udot4(cw[2], lo.z, a, false);
+    b = __builtin_amdgcn_sdot4((int)cw[2], (int)hi.z, b, false);
+    a = __builtin_amdgcn_udot4(cw[3], lo.w, a, false);
+    b = __builtin_amdgcn_sdot4((int)cw[3], (int)hi.w, b, false);
+    // |256 b + a| <= 16 * 63 * 32767 < 2^25: exact in int32 and in f32
+    return b * 256 + (int)a;
+}
+
+}  // namespace
+
+template <int MX, int XR>
+__global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
+    const uint8_t *__restrict__ qb, uint32_t qb_bytes, const uint8_t *__restrict__ scb,
+    uint32_t sc_bytes, const uint8_t *__restrict__ db, uint32_t d_bytes,
+    const float *__restrict__ x, float *__restrict__ y, int n, int nblk, int m) {
+    constexpr bool XREG = MX == 1;
+    constexpr int C = Q6K_GEMV_CHUNK, PF = Q6K_GEMV_PF;
+    static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
+    extern __shared__ uint4 smem4[];
+    __shared__ int next_chunk;
+    const int k = nblk * 256;
+    uint8_t *xlo = reinterpret_cast<uint8_t *>(smem4);
+    uint8_t *xhi = xlo + (size_t)MX * k;
+    float *s16 = reinterpret_cast<float *>(xhi + (size_t)MX * k);
+    float *xe = s16 + (size_t)MX * (k / 16);
+    float *part = xe + (size_t)MX * (k / 32);  // [MX][R][spr]
+
+    const __amdgpu_buffer_rsrc_t qrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)qb, (short)0, (int)qb_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t srs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)scb, (short)0, (int)sc_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t drs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)db, (short)0, (int)d_bytes, 0x00020000);
+
+    const int tid = threadIdx.x;
+    const int l16 = tid & 15, grp = tid >> 4;
+    const int bq = l16 >> 2, c = l16 & 3, n2 = c >> 1, isub = c & 1;
+
+    const int G = gridDim.x;
+    const int r0 = (int)((int64_t)blockIdx.x * n / G);
+    const int r1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
+    const int R = r1 - r0;
+    const int spr = (nblk + 3) >> 2;
+    const int cpc = (R + C - 1) / C;
+    const int nchunks = cpc * spr;
+
+    int icol = 0, irow = 0;
+    auto start_chunk = [&](int kc) {
+        icol = kc < nchunks ? kc / cpc : spr;
+        irow = (kc - icol * cpc) * C;
+    };
+    u32x4 q0[PF], q1[PF], q2[PF];
+    uint32_t sw[PF], dw[PF];
+    int srow[PF], scol[PF];
+    auto issue = [&](int u, bool first) {
+        if (u % C == 0) {
+            int kc = grp;
+            if (!first) {
+                if (l16 == 0) kc = atomicAdd(&next_chunk, 1);
+                kc = __builtin_amdgcn_ds_swizzle(kc, 0x10);  // lane 0 of each 16-lane group
+            }
+            start_chunk(kc);
+        } else {
+            irow++;
+        }
+        const int b = 4 * icol + bq;
+        const bool live = icol < spr && irow < R && b < nblk;
+        const uint32_t blk = (uint32_t)(r0 + irow) * (uint32_t)nblk + (uint32_t)b;
+        const uint32_t oq = live ? blk * 192u + (uint32_t)c * 48u : Q4K_OOB;
+        q0[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oq, 0, 2);
+        q1[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oq + 16u, 0, 2);
+        q2[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oq + 32u, 0, 2);
+        sw[u] = __builtin_amdgcn_raw_buffer_load_b32(srs, live ? blk * 16u + (uint32_t)c * 4u : Q4K_OOB, 0, 0);
+        dw[u] = __builtin_amdgcn_raw_buffer_load_b16(drs, live ? blk * 2u : Q4K_OOB, 0, 0);
+        srow[u] = irow;
+        scol[u] = icol;
+    };
+
+    if (tid == 0) next_chunk = Q6K_GEMV_GROUPS;
+    const int xitems = m * k / 8;
+    XqRound xr[XR];
+#pragma unroll
+    for (int r = 0; r < XR; r++) xr[r] = xq_load(x, xitems, r * Q6K_GEMV_THREADS);
+    __builtin_amdgcn_s_barrier();
+    issue(0, true);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < XR; r++)
+        if (r * Q6K_GEMV_THREADS < xitems) xq6_process(xr[r], xitems, r * Q6K_GEMV_THREADS, k, xlo, xhi, s16, xe);
+    for (int base = XR * Q6K_GEMV_THREADS; base < xitems; base += Q6K_GEMV_THREADS)
+        xq6_process(xq_load(x, xitems, base), xitems, base, k, xlo, xhi, s16, xe);
+    __syncthreads();
+#pragma unroll
+    for (int u = 1; u < PF; u++) {
+        issue(u, u < C);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // x of the column being consumed: the lane's 4 quadrants (elements
+    // 256 b + 128 n2 + 16 isub + 32 t .. + 15)
+    int xcol = -1, xbase = 0;
+    u32x4 XL[4], XH[4];
+    float XS[4], XE[4];
+    auto load_x = [&](int col) {
+        xcol = col;
+        xbase = min(4 * col + bq, nblk - 1) * 256 + 128 * n2 + 16 * isub;
+        if (XREG) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                XL[t] = *reinterpret_cast<const u32x4 *>(xlo + xbase + 32 * t);
+                XH[t] = *reinterpret_cast<const u32x4 *>(xhi + xbase + 32 * t);
+                XS[t] = s16[(xbase >> 4) + 2 * t];
+                XE[t] = xe[(xbase >> 5) + t];
+            }
+        }
+    };
+
+    auto consume = [&](int u) {
+        const int col = scol[u], row = srow[u];
+        const bool live = col < spr && row < R;
+        if (live && col != xcol) load_x(col);
+        // scales 8 n2 + isub + 2t: bytes isub, isub + 2 of dwords 2 n2 and 2 n2 + 1
+        const uint32_t s0 = quad_bcast<0>(sw[u]), s1 = quad_bcast<1>(sw[u]);
+        const uint32_t s2 = quad_bcast<2>(sw[u]), s3 = quad_bcast<3>(sw[u]);
+        const uint32_t sa = n2 ? s2 : s0, sb = n2 ? s3 : s1;
+        const float d = h2f(dw[u]);
+        const uint32_t sh = 8u * (uint32_t)isub;
+        float dsc[4];
+        dsc[0] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh, 8);
+        dsc[1] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh + 16u, 8);
+        dsc[2] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh, 8);
+        dsc[3] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh + 16u, 8);
+        const uint32_t w[12] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y,
+                                q1[u].z, q1[u].w, q2[u].x, q2[u].y, q2[u].z, q2[u].w};
+#pragma unroll
+        for (int mi = 0; mi < MX; mi++) {
+            if (MX == 1 || mi < m) {
+                float v = 0.f;
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    // quadrant t: ql_a / ql_b (t odd), low / high nibble (t >= 2), qh bits 2t..2t+1
+                    uint32_t cw[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        cw[j] = ((w[4 * (t & 1) + j] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) |
+                                (((w[8 + j] >> (2 * t)) << 4) & 0x30303030u);
+                    int sdot;
+                    float xsum, xsc;
+                    if (XREG) {
+                        sdot = q6k_subdot(cw, XL[t], XH[t]);
+                        xsum = XS[t];
+                        xsc = XE[t];
+                    } else {
+                        const size_t eo = (size_t)mi * k + xbase + 32 * t;
+                        sdot = q6k_subdot(cw, *reinterpret_cast<const u32x4 *>(xlo + eo),
+                                          *reinterpret_cast<const u32x4 *>(xhi + eo));
+                        xsum = s16[eo >> 4];
+                        xsc = xe[eo >> 5];
+                    }
+                    v += dsc[t] * (xsc * (float)sdot - 32.f * xsum);
+                }
+                v = row16_sum(v);
+                if (l16 == 0 && live) part[((size_t)mi * R + row) * spr + col] = v;
+            }
+        }
+    };
+
+    while (scol[0] < spr) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            consume(u);
+            issue(u, false);
+        }
+    }
+    __syncthreads();
+
+    for (int t = tid; t < MX * R; t += Q6K_GEMV_THREADS) {
+        const int mi = t / R, r = t - mi * R;
+        if (mi < m) {
+            const float *pr = part + (size_t)t * spr;
+            float v = 0.f;
+            for (int cc = 0; cc < spr; cc++) v += pr[cc];
+            y[(int64_t)mi * n + r0 + r] = v;
+        }
+    }
+}
+
 // ------------------------------------------------------------------ Q8_0 ----
 // Lane chunk c (0..1) = codes [16c, 16c+16) of a 32-weight block.
 template <int R, int MX>
@@ -593,6 +839,11 @@ __global__ __launch_bounds__(64) void gemv_q6k(const uint4 *__restrict__ qb,
 constexpr int GEMV_MAX_M = 4;
 
 static size_t q4k_gemv_lds(const arfq_weight *w, int mx);
+static size_t q6k_dot_lds(const arfq_weight *w, int mx);
+static bool q6k_dot_ok(const arfq_weight *w, int64_t m) {
+    return m <= 2 && q6k_dot_lds(w, (int)m) <= 64 * 1024 &&
+           w->n * (w->k / 256) * 192 < (int64_t)Q4K_OOB;
+}
 
 bool gemv_supports(const arfq_weight *w, int64_t m) {
     if (m < 1 || m > GEMV_MAX_M) return false;
@@ -642,6 +893,42 @@ static int64_t q4k_gemv_grid(const arfq_weight *w) {
 
 // LDS of the Q4_K GEMV: quantized x of mx rows (digits + scale/sum) and the
 // per-(row, column) sums of the workgroup's rows.
+// steps = (row, column of 4 blocks); two workgroups per CU, >= 2 steps per group
+static int64_t gemv_grid(const arfq_weight *w, int groups) {
+    const int nblk = (int)(w->k / 256);
+    const int64_t steps = w->n * ((nblk + 3) / 4);
+    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
+    int64_t grid = std::min<int64_t>(2 * (int64_t)cus, (steps + 2 * groups - 1) / (2 * groups));
+    grid = std::min<int64_t>(grid, w->n);
+    return grid < 1 ? 1 : grid;
+}
+static size_t q6k_dot_lds(const arfq_weight *w, int mx) {
+    const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
+    const int64_t grid = gemv_grid(w, Q6K_GEMV_GROUPS);
+    const int64_t rows = (w->n + grid - 1) / grid;
+    return (size_t)mx * w->k * 2 + (size_t)mx * (w->k / 16) * 4 + (size_t)mx * (w->k / 32) * 4 +
+           (size_t)mx * rows * spr * 4;
+}
+template <int MX, int XR>
+static hipError_t launch_q6k_dot_t(const arfq_weight *w, int e, int m, const float *x, float *y,
+                                   hipStream_t s) {
+    const int n = (int)w->n, nblk = (int)(w->k / 256);
+    const int64_t nb = w->n * nblk;
+    const int64_t eb = (int64_t)e * nb;
+    const int64_t grid = gemv_grid(w, Q6K_GEMV_GROUPS);
+    gemv_q6k_dot<MX, XR><<<(unsigned)grid, Q6K_GEMV_THREADS, q6k_dot_lds(w, MX), s>>>(
+        (const uint8_t *)w->s0 + eb * 192, (uint32_t)(nb * 192), (const uint8_t *)w->s1 + eb * 16,
+        (uint32_t)(nb * 16), (const uint8_t *)w->s2 + eb * 2, (uint32_t)(nb * 2), x, y, n, nblk, m);
+    return hipGetLastError();
+}
+template <int MX>
+static hipError_t launch_q6k_dot(const arfq_weight *w, int e, int m, const float *x, float *y,
+                                 hipStream_t s) {
+    const int64_t rounds = ((int64_t)m * (w->k / 8) + Q6K_GEMV_THREADS - 1) / Q6K_GEMV_THREADS;
+    if (rounds <= 1) return launch_q6k_dot_t<MX, 1>(w, e, m, x, y, s);
+    if (rounds <= 2) return launch_q6k_dot_t<MX, 2>(w, e, m, x, y, s);
+    return launch_q6k_dot_t<MX, 4>(w, e, m, x, y, s);
+}
 static size_t q4k_gemv_lds(const arfq_weight *w, int mx) {
     const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
     const int64_t grid = q4k_gemv_grid(w);
@@ -682,6 +969,8 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
         if (m == 2) return launch_gemv_q4k<2>(w, e, 2, x, y, s);
         return launch_gemv_q4k<4>(w, e, (int)m, x, y, s);
     }
+    if (w->qtype == ARFQ_Q6_K && q6k_dot_ok(w, m))
+        return m == 1 ? launch_q6k_dot<1>(w, e, 1, x, y, s) : launch_q6k_dot<2>(w, e, 2, x, y, s);
     if (m == 1) return launch_gemv_t<4, 1>(w, e, 1, x, y, s);
     if (m == 2) return launch_gemv_t<4, 2>(w, e, 2, x, y, s);
     return launch_gemv_t<2, 4>(w, e, (int)m, x, y, s);

@@ -95,10 +95,11 @@ def test_gemv_small_shapes(gpu_ctx, oracle, qtype, n, k, m):
     assert rel_err(got, want) <= TOL
 
 
-def test_gemv_expert_offset(gpu_ctx, oracle):
-    _say("case: gemv expert offset")
-    got, raw, x = _matmul(gpu_ctx, "q4_k", 48, 512, 1, seed=5, experts=4, expert=3)
-    assert rel_err(got, oracle.matmul_q("q4_k", x, raw, 48)) <= TOL
+@pytest.mark.parametrize("qtype,m", [("q4_k", 1), ("q6_k", 1), ("q6_k", 2)])
+def test_gemv_expert_offset(gpu_ctx, oracle, qtype, m):
+    _say("case: gemv expert offset", qtype, m)
+    got, raw, x = _matmul(gpu_ctx, qtype, 48, 512, m, seed=5, experts=4, expert=3)
+    assert rel_err(got, oracle.matmul_q(qtype, x, raw, 48)) <= TOL
 
 
 def test_c1_q8_0_gemv_full(gpu_ctx, oracle):
