@@ -893,12 +893,15 @@ static int64_t q4k_gemv_grid(const arfq_weight *w) {
 
 // LDS of the Q4_K GEMV: quantized x of mx rows (digits + scale/sum) and the
 // per-(row, column) sums of the workgroup's rows.
-// steps = (row, column of 4 blocks); two workgroups per CU, >= 2 steps per group
+// steps = (row, column of 4 blocks); two workgroups per CU (one when x is
+// long: every workgroup quantizes all of x, and at C3's k = 17408 one per CU
+// measured 3 % faster), >= 2 steps per group
 static int64_t gemv_grid(const arfq_weight *w, int groups) {
     const int nblk = (int)(w->k / 256);
     const int64_t steps = w->n * ((nblk + 3) / 4);
     const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
-    int64_t grid = std::min<int64_t>(2 * (int64_t)cus, (steps + 2 * groups - 1) / (2 * groups));
+    const int per_cu = w->k > 8192 ? 1 : 2;
+    int64_t grid = std::min<int64_t>(per_cu * (int64_t)cus, (steps + 2 * groups - 1) / (2 * groups));
     grid = std::min<int64_t>(grid, w->n);
     return grid < 1 ? 1 : grid;
 }
