@@ -171,46 +171,61 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restri
 // tile of up to MOE_BM = 64 (token, slot) rows.
 constexpr int MOE_BM = 64;
 
-// gate|up: workgroup = one tile x 128 columns of inter; wave w streams the
-// same 32 rows of gate and of up (NW = 2), so each lane ends with g and u of
-// the same outputs and writes h = silu(g) * u in f32 (its range can exceed
-// f16's; moe_hprep scales it).
+// gate|up: workgroup = one tile x 128 columns of inter, 8 waves: wave w < 4
+// streams gate rows n0 + 32 w, wave w + 4 the same rows of up (one weight per
+// wave keeps two waves per SIMD).  After the loop the up waves hand their
+// accumulators to the gate waves through LDS, and the gate waves write
+// h = silu(g) * u in f32 (its range can exceed f16's; moe_hprep scales it).
+constexpr int MOE_GU_THREADS = 512;
 template <class F>
-__global__ __launch_bounds__(SK_THREADS) void moe_gateup_kernel(
+__global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     F gate, F up, int64_t expert_blocks, const _Float16 *__restrict__ x,
     const uint16_t *__restrict__ xs, int K, int inter, int top_k, const int32_t *__restrict__ off,
     const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ h) {
     extern __shared__ _Float16 lds[];
     if ((int)blockIdx.x >= *ntiles) return;  // uniform over the workgroup
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
+    const int wq = wave & 3;
+    const bool is_up = wave >= 4;
     const int2 tile = tiles[blockIdx.x];
     const int e = tile.x, row0 = tile.y;
     const int rows = min(MOE_BM, off[e + 1] - row0);
-    const int n0 = blockIdx.y * 128 + 32 * wave;
-    const SkRows<2> xr = sk_rows<2>(rows, K, [&](int r) { return sorted[row0 + r] / top_k; });
-    const F fm[2] = {gate.shifted((int64_t)e * expert_blocks), up.shifted((int64_t)e * expert_blocks)};
-    const int64_t wrow0[2] = {n0, n0};
-    floatx16 acc[2][2];
-#pragma unroll
-    for (int w = 0; w < 2; w++)
-#pragma unroll
-        for (int t = 0; t < 2; t++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) acc[w][t][i] = 0.f;
-    skinny_run<F, 2, 2>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc, lds);
-    const int n = n0 + (lane & 31);
+    const int n0 = blockIdx.y * 128 + 32 * wq;
+    const SkRows<2, MOE_GU_THREADS> xr =
+        sk_rows<2, MOE_GU_THREADS>(rows, K, [&](int r) { return sorted[row0 + r] / top_k; });
+    const F fm[1] = {(is_up ? up : gate).shifted((int64_t)e * expert_blocks)};
+    const int64_t wrow0[1] = {n0};
+    floatx16 acc[1][2];
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int r = sk_out_row(t, i);
-            if (r < rows && n < inter) {
-                const float g = acc[0][t][i], u = acc[1][t][i];
-                const float sg = g / (1.0f + expf(-g));
-                h[(int64_t)(row0 + r) * inter + n] = sg * u;
+        for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
+    skinny_run<F, 2, 1, MOE_GU_THREADS>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc, lds);
+    // the loop ends with a barrier after its last LDS use: hand up to gate
+    float *ex = reinterpret_cast<float *>(lds);  // [4 waves][2 tiles][16][64 lanes]
+    if (is_up) {
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) ex[((wq * 2 + t) * 16 + i) * 64 + lane] = acc[0][t][i];
+    }
+    __syncthreads();
+    if (!is_up) {
+        const int n = n0 + (lane & 31);
+#pragma unroll
+        for (int t = 0; t < 2; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int r = sk_out_row(t, i);
+                if (r < rows && n < inter) {
+                    const float g = acc[0][t][i], u = ex[((wq * 2 + t) * 16 + i) * 64 + lane];
+                    const float sg = g / (1.0f + expf(-g));
+                    h[(int64_t)(row0 + r) * inter + n] = sg * u;
+                }
             }
-        }
+    }
 }
 
 // h rows (f32) -> f16 copies scaled by a power of two per row, so that the
@@ -348,7 +363,8 @@ static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const 
                            const void *tiles, const int32_t *ntiles, int64_t max_tiles, float *h,
                            hipStream_t s) {
     static bool attr = false;
-    constexpr size_t lds = sk_lds<F, 2, 2>();
+    constexpr size_t lds = sk_lds<F, 2, 1, MOE_GU_THREADS>();
+    static_assert(lds >= (size_t)4 * 2 * 16 * 64 * 4, "room for the up -> gate hand-off");
     if (!attr) {
         hipError_t e = hipFuncSetAttribute((const void *)moe_gateup_kernel<F>,
                                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -357,7 +373,7 @@ static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const 
     }
     const int64_t eb = gw->n * g.nblk;
     const dim3 grid((unsigned)max_tiles, (unsigned)((gw->n + 127) / 128));
-    moe_gateup_kernel<F><<<grid, SK_THREADS, lds, s>>>(g, u, eb, x, xs, (int)gw->k, (int)gw->n,
+    moe_gateup_kernel<F><<<grid, MOE_GU_THREADS, lds, s>>>(g, u, eb, x, xs, (int)gw->k, (int)gw->n,
                                                        top_k, off, sorted, (const int2 *)tiles,
                                                        ntiles, h);
     return hipGetLastError();

@@ -223,21 +223,21 @@ struct SkQ80 {
 
 // ---- the loop -------------------------------------------------------------------
 // x staging: XR = 32 TA rows x 256 k per block = XR * 32 chunks of 16 B over
-// the 256 threads; thread tid stages chunks c = tid + 256 i (row c / 32 =
-// (tid >> 5) + 8 i, k 8 * (tid & 31)) and, for KIND 2, 16 B of the sums of row
-// min(tid >> 1, XR - 1).
-template <int TA>
+// the NT threads; thread tid stages chunks c = tid + NT i (row c / 32 =
+// (tid >> 5) + (NT / 32) i, k 8 * (tid & 31)) and, for KIND 2, 16 B of the
+// sums of row min(tid >> 1, XR - 1).
+template <int TA, int NT = SK_THREADS>
 struct SkRows {
-    static constexpr int XC = 32 * TA * 32 / SK_THREADS;  // chunks per thread (4 or 8)
-    int64_t x[XC];  // element offset (row * K) of row (tid >> 5) + 8 i
+    static constexpr int XC = 32 * TA * 32 / NT;  // chunks per thread
+    int64_t x[XC];  // element offset (row * K) of row (tid >> 5) + (NT / 32) i
     int64_t s;      // element offset (row * K / 16) of row min(tid >> 1, XR - 1)
 };
 
 // LDS of the loop: the x block of XR rows (+ its sub-block sums) and one weight
 // slab [32][RB + 16] per wave and weight.
-template <class F, int TA, int NW>
+template <class F, int TA, int NW, int NT = SK_THREADS>
 constexpr size_t sk_lds() {
-    return (size_t)32 * TA * SK_XLD * 2 + (size_t)32 * TA * 32 + (size_t)4 * NW * 32 * (F::RB + 16);
+    return (size_t)32 * TA * SK_XLD * 2 + (size_t)32 * TA * 32 + (size_t)(NT / 64) * NW * 32 * (F::RB + 16);
 }
 
 // Accumulates acc[w][t] (w < NW weights, t < TA 32-row x tiles) over the
@@ -245,15 +245,15 @@ constexpr size_t sk_lds() {
 // wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
 // `rows` gives the x rows this thread stages.  All 256 threads of the
 // workgroup call it with the same block range.
-template <class F, int TA, int NW>
+template <class F, int TA, int NW, int NT = SK_THREADS>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
-                                           int64_t nrows, const SkRows<TA> &rows,
+                                           int64_t nrows, const SkRows<TA, NT> &rows,
                                            const _Float16 *__restrict__ x,
                                            const uint16_t *__restrict__ xs, int b0, int b1,
                                            floatx16 (&acc)[NW][TA], _Float16 *lds) {
     constexpr int KIND = F::KIND;
     constexpr int XR = 32 * TA;  // x rows staged
-    constexpr int XC = SkRows<TA>::XC;
+    constexpr int XC = SkRows<TA, NT>::XC;
     constexpr int RL = F::RB / 16;          // lanes per weight row in a coalesced load
     constexpr int NI = 32 * F::RB / 1024;   // 16-byte loads per lane per block
     constexpr int SL = F::RB + 16;          // slab row stride (bytes)
@@ -274,7 +274,7 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
     auto xstore = [&]() {
 #pragma unroll
         for (int i = 0; i < XC; i++)
-            *reinterpret_cast<u32x4 *>(xl + ((tid >> 5) + 8 * i) * SK_XLD + 8 * (tid & 31)) = xv[i];
+            *reinterpret_cast<u32x4 *>(xl + ((tid >> 5) + (NT / 32) * i) * SK_XLD + 8 * (tid & 31)) = xv[i];
         if constexpr (KIND == 2) {
             if (tid < 2 * XR) *reinterpret_cast<u32x4 *>(sl + (tid >> 1) * 16 + 8 * (tid & 1)) = sv;
         }
@@ -400,12 +400,13 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
 
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.
-template <int TA, class RowOf>
-__device__ __forceinline__ SkRows<TA> sk_rows(int n, int K, RowOf row_of) {
-    SkRows<TA> r;
+template <int TA, int NT = SK_THREADS, class RowOf>
+__device__ __forceinline__ SkRows<TA, NT> sk_rows(int n, int K, RowOf row_of) {
+    SkRows<TA, NT> r;
     const int tid = threadIdx.x;
 #pragma unroll
-    for (int i = 0; i < SkRows<TA>::XC; i++) r.x[i] = (int64_t)row_of(min((tid >> 5) + 8 * i, n - 1)) * K;
+    for (int i = 0; i < SkRows<TA, NT>::XC; i++)
+        r.x[i] = (int64_t)row_of(min((tid >> 5) + (NT / 32) * i, n - 1)) * K;
     r.s = (int64_t)row_of(min(tid >> 1, min(32 * TA, n) - 1)) * (K / 16);
     return r;
 }
