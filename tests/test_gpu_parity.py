@@ -211,3 +211,61 @@ def test_c4_q4_k_gemm_full(gpu_ctx, oracle):
     _say("C4 rel err (48 sampled rows)", e)
     assert e <= TOL
     assert np.all(np.isfinite(got))
+
+
+# ------------------------------------------------------ edge cases ----
+def _run(ctx, qtype, raw, x, n):
+    from arf_amd import QType
+    m, k = x.shape
+    w = ctx.upload({"q4_k": QType.Q4_K, "q6_k": QType.Q6_K, "q8_0": QType.Q8_0}[qtype], raw, n, k)
+    y = ctx.empty((m, n), np.float32)
+    ctx.matmul(w, ctx.to_device(x), m, y)
+    got = y.numpy()
+    w.free()
+    return got
+
+
+def _dead_blocks(qtype, raw, every):
+    """Zero the block scale d of every `every`-th block (dmin stays: the min term remains)."""
+    raw = raw.copy()
+    bb = {"q4_k": 144, "q6_k": 210}[qtype]
+    off = {"q4_k": 0, "q6_k": 208}[qtype]
+    blocks = raw.reshape(-1, bb)
+    blocks[::every, off:off + 2] = 0
+    return blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("qtype", ["q4_k", "q6_k"])
+@pytest.mark.parametrize("m", [1, 2, 200])
+def test_x_dynamic_range_and_dead_blocks(gpu_ctx, oracle, qtype, m):
+    # x blocks of 32 scaled over 12 decades, some all zero; weight blocks with d = 0.
+    # The integer GEMVs quantize x per 32-element block, so each block keeps its own range;
+    # m = 200 runs the prefill path (Q4_K: the direct-operand kernel with its d = 0 handling).
+    from arf_amd import synth
+    n, k = 96, 2048
+    _say("case: dynamic range / dead blocks", qtype, m)
+    rng = np.random.default_rng(1234 + m)
+    raw = _dead_blocks(qtype, synth.weight(qtype, n, k, seed=77 + m), every=3)
+    x = synth.activations(m, k, seed=78 + m)
+    scale = 10.0 ** rng.uniform(-6, 6, size=(m, k // 32)).astype(np.float32)
+    scale[rng.random(size=scale.shape) < 0.1] = 0.0
+    x = (x.reshape(m, k // 32, 32) * scale[..., None]).reshape(m, k).astype(np.float32)
+    if m > 64:
+        x = x.astype(np.float16).astype(np.float32)  # prefill rounds x to f16 (as the reference)
+        x = np.clip(x, -6e4, 6e4)
+    got = _run(gpu_ctx, qtype, raw, x, n)
+    want = oracle.matmul_q(qtype, x, raw, n)
+    e = rel_err(got, want)
+    _say("rel err", e)
+    assert np.all(np.isfinite(got))
+    assert e <= TOL
+
+
+@pytest.mark.parametrize("qtype", ["q4_k", "q6_k"])
+def test_zero_x_gives_zero(gpu_ctx, qtype):
+    from arf_amd import synth
+    n, k = 64, 1024
+    raw = synth.weight(qtype, n, k, seed=5)
+    for m in (1, 2, 8, 100):
+        got = _run(gpu_ctx, qtype, raw, np.zeros((m, k), np.float32), n)
+        assert np.array_equal(got, np.zeros_like(got)), (qtype, m)
