@@ -251,8 +251,8 @@ def test_x_dynamic_range_and_dead_blocks(gpu_ctx, oracle, qtype, m):
     scale[rng.random(size=scale.shape) < 0.1] = 0.0
     x = (x.reshape(m, k // 32, 32) * scale[..., None]).reshape(m, k).astype(np.float32)
     if m > 64:
-        x = x.astype(np.float16).astype(np.float32)  # prefill rounds x to f16 (as the reference)
-        x = np.clip(x, -6e4, 6e4)
+        # prefill rounds x to f16 (as the reference): keep it in f16's range first
+        x = np.clip(x, -6e4, 6e4).astype(np.float16).astype(np.float32)
     got = _run(gpu_ctx, qtype, raw, x, n)
     want = oracle.matmul_q(qtype, x, raw, n)
     e = rel_err(got, want)
