@@ -268,8 +268,12 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
 #pragma unroll
         for (int i = 0; i < XC; i++)
             xv[i] = *reinterpret_cast<const u32x4 *>(x + rows.x[i] + 256 * b + 8 * (tid & 31));
-        if constexpr (KIND == 2)
-            sv = *reinterpret_cast<const u32x4 *>(xs + rows.s + 16 * b + 8 * (tid & 1));
+        // the sums' load sits in the same branch as their store: loaded
+        // unconditionally, it was sunk next to the store, where its wait
+        // covered every load in flight
+        if constexpr (KIND == 2) {
+            if (tid < 2 * XR) sv = *reinterpret_cast<const u32x4 *>(xs + rows.s + 16 * b + 8 * (tid & 1));
+        }
     };
     auto xstore = [&]() {
 #pragma unroll
@@ -327,10 +331,15 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
     for (int b = b0; b < b1; b++) {
         const int bn = min(b + 1, b1 - 1);  // past the end: a re-read of the last block
         wstore();                            // block b's weights (loaded one block ago)
-        wload(bn);
-        xload(bn);
+        // loads of the next block, in the order their data is waited for:
+        // the scales and x at this block's end, the weights at the next
+        // block's start (vector loads complete in order, so a weight load
+        // issued first would hold up the x hand-off)
 #pragma unroll
         for (int w = 0; w < NW; w++) wbn[w] = fmt[w].load_blk(myrow[w], bn);
+        xload(bn);
+        __builtin_amdgcn_sched_barrier(0);
+        wload(bn);
         // keep the scheduler from sinking the loads: they must be in flight
         // during this block, not issued at its end
         __builtin_amdgcn_sched_barrier(0);

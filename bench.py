@@ -57,8 +57,8 @@ def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.flo
     return ms / steps, ms
 
 
-def time_moe(ctx, steps, copies):
-    """Average ms per arfq_moe call (C5) rotating `copies` weight sets."""
+def time_moe(ctx, steps, warmup, copies):
+    """Average ms per arfq_moe call (C5) rotating `copies` weight sets, after `warmup` calls."""
     from arf_amd import QType, synth
     cfg = synth.CONFIGS["c5_moe"]
     E, T, k, hdim, inter = cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"], cfg["inter"]
@@ -74,7 +74,7 @@ def time_moe(ctx, steps, copies):
     x = ctx.to_device(synth.activations(T, hdim, seed=0xA7F00008, dtype=np.float16))
     lg = ctx.to_device(synth.router_logits(T, E, seed=0xA7F00009))
     y = ctx.empty((T, hdim), np.float32)
-    for i in range(3):
+    for i in range(warmup):
         g, u, d = sets[i % copies]
         ctx.moe(g, u, d, lg, T, k, True, x, y)
     ctx.sync()
@@ -211,7 +211,7 @@ def main():
             log(f"[bench] C3 m={mm}: {ms3 * 1e3:.2f} us/launch")
         # C4 Q4_K prefill GEMM
         try:
-            ms4, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, 20, 3, 2, seed=0xA7F00004,
+            ms4, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, 30, 10, 2, seed=0xA7F00004,
                                  x_dtype=np.float16)
             fl = 2.0 * 2048 * 17408 * 5120
             tf = fl / (ms4 * 1e-3) / 1e12
@@ -223,7 +223,8 @@ def main():
             configs["c4_q4_k_gemm_m2048_k5120_n17408"] = {"error": str(e)}
         # C5 MoE block
         try:
-            ms5 = time_moe(ctx, max(10, args.steps // 100), 3)
+            # steady state: the first few dozen calls after the C4 phase run ~10 % slower
+            ms5 = time_moe(ctx, 60, 30, 3)
             cfg = synth.CONFIGS["c5_moe"]
             E, T, topk, hdim, inter = (cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"],
                                        cfg["inter"])
