@@ -29,6 +29,34 @@ namespace arfq {
 // (summed in selection order) when norm != 0.
 constexpr int MOE_ROUTE_PL = 16;  // up to 1024 experts
 
+// Wave-wide max / min with every lane getting the result: a DPP butterfly
+// inside each 16-lane row (xor 1, xor 2, half-row mirror, row mirror), then
+// v_permlane16_swap and v_permlane32_swap across rows -- VALU only, no LDS
+// round trip per step.
+template <int CTRL>
+__device__ __forceinline__ int route_dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xf, 0xf, true);
+}
+template <class Op>
+__device__ __forceinline__ int route_wave_reduce(int v, Op op) {
+    v = op(v, route_dpp<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, route_dpp<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = op(v, route_dpp<0x141>(v));  // row_half_mirror
+    v = op(v, route_dpp<0x140>(v));  // row_mirror
+    const auto p16 = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    v = op((int)p16[0], (int)p16[1]);
+    const auto p32 = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return op((int)p32[0], (int)p32[1]);
+}
+__device__ __forceinline__ float route_wave_max(float v) {
+    return __int_as_float(route_wave_reduce(__float_as_int(v), [](int a, int b) {
+        return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+    }));
+}
+__device__ __forceinline__ int route_wave_min(int v) {
+    return route_wave_reduce(v, [](int a, int b) { return min(a, b); });
+}
+
 template <int PL>
 __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits,
                                                         int64_t tokens, int E, int top_k,
@@ -36,7 +64,7 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
                                                         float *__restrict__ wts) {
     const int lane = threadIdx.x & 63;
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= tokens) return;
+    if (t >= tokens) return;  // whole waves: every lane of a running wave is active
     const float *lg = logits + t * E;
     float v[PL];
     float mx = -INFINITY;
@@ -46,21 +74,28 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
         v[j] = i < E ? lg[i] : -INFINITY;
         mx = fmaxf(mx, v[j]);
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    mx = route_wave_max(mx);
 #pragma unroll
     for (int j = 0; j < PL; j++) v[j] = (j * 64 + lane < E) ? expf(v[j] - mx) : 0.f;
-    // sum in index order (the reference's sequential iterator sum)
+    // sum in index order (the reference's sequential iterator sum); the slots
+    // past E hold exact zeros, so summing whole rounds of 64 changes nothing
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < PL; j++) {
         if (j * 64 >= E) break;
-        const int cnt = min(64, E - j * 64);
-        for (int l = 0; l < cnt; l++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
+        if (PL <= 4) {
+#pragma unroll
+            for (int l = 0; l < 64; l++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
+        } else {
+            const int cnt = min(64, E - j * 64);
+            for (int l = 0; l < cnt; l++) s += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[j]), l));
+        }
     }
 #pragma unroll
     for (int j = 0; j < PL; j++) v[j] = (j * 64 + lane < E) ? v[j] / s : -INFINITY;
 
+    // top_k rounds: the wave's largest untaken probability, then the lowest
+    // index holding it (the stable sort's order for ties)
     uint32_t taken = 0;
     float myw = 0.f;
     int myid = 0;
@@ -76,21 +111,14 @@ __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict_
                 bi = i;
             }
         }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float op = __shfl_xor(bp, o);
-            const int oi = __shfl_xor(bi, o);
-            if (op > bp || (op == bp && oi < bi) || (bi == 0x7fffffff && oi != 0x7fffffff)) {
-                bp = op;
-                bi = oi;
-            }
-        }
-        if ((bi & 63) == lane) taken |= 1u << (bi >> 6);
+        const float wp = route_wave_max(bp);
+        const int wi = route_wave_min(bi != 0x7fffffff && bp == wp ? bi : 0x7fffffff);
+        if ((wi & 63) == lane) taken |= 1u << (wi >> 6);
         if (lane == r) {
-            myw = bp;
-            myid = bi;
+            myw = wp;
+            myid = wi;
         }
-        wsum += bp;
+        wsum += wp;
     }
     if (lane < top_k) {
         ids[t * top_k + lane] = myid;
