@@ -260,41 +260,84 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
 // largest |h| of the row is below 2^15: h16 = h / rs (exact scaling), the
 // down GEMM multiplies its output row by rs.  For Q4_K down weights also the
 // sub-block sums of h16 (bf16 hi + lo, the xs layout).  One wave per row.
+// One wave per row; lane l handles elements 8 (l % 4) .. + 7 of sub-block
+// (l / 4) + 16 q in pass q, so each quad owns a 32-element sub-block: the
+// row's values stay in registers between the max and the conversion (up to
+// HP_PASSES passes, inter <= 2048; longer rows are read twice), loads and
+// stores are 16-byte and coalesced, and the sub-block sums are quad DPP sums.
+constexpr int HP_PASSES = 4;
 __global__ __launch_bounds__(256) void moe_hprep_kernel(const float *__restrict__ h, int64_t P,
                                                         int inter, _Float16 *__restrict__ h16,
                                                         uint16_t *__restrict__ hs,
                                                         float *__restrict__ rs) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= P) return;
+    if (row >= P) return;  // whole waves: every lane of a running wave is active
     const float *src = h + row * inter;
-    float amax = 0.f;
-    for (int i = lane; i < inter; i += 64) amax = fmaxf(amax, fabsf(src[i]));
+    const int nsub = inter / 32;
+    const int npass = (nsub + 15) / 16;
+    const int qd = lane & 3;
+    auto load8 = [&](int q, float (&v)[8]) {
+        const int sub = (lane >> 2) + 16 * q;
+        if (sub < nsub) {
+            const float4 *p4 = reinterpret_cast<const float4 *>(src + sub * 32 + 8 * qd);
+            const float4 a = p4[0], b = p4[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+            for (int i = 0; i < 8; i++) v[i] = 0.f;
+        }
+    };
+    float val[HP_PASSES][8];
+    float amax = 0.f;
+    for (int q = 0; q < npass; q++) {
+        float v[8];
+        load8(q, v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+        for (int qq = 0; qq < HP_PASSES; qq++)
+            if (qq == q)
+#pragma unroll
+                for (int i = 0; i < 8; i++) val[qq][i] = v[i];
+    }
+    amax = route_wave_max(amax);
     const int ex = amax > 0.f ? __builtin_amdgcn_frexp_expf(amax) : 0;  // amax < 2^ex
     const int sh = ex > 15 ? ex - 15 : 0;
     const float inv = ldexpf(1.f, -sh);
     if (lane == 0) rs[row] = ldexpf(1.f, sh);
-    const int nsub = inter / 32;
-    for (int sub = lane; sub < nsub; sub += 64) {
+    for (int q = 0; q < npass; q++) {
+        float v[8];
+        if (q < HP_PASSES) {
+#pragma unroll
+            for (int qq = 0; qq < HP_PASSES; qq++)
+                if (qq == q)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) v[i] = val[qq][i];
+        } else {
+            load8(q, v);
+        }
+        const int sub = (lane >> 2) + 16 * q;
+        half8 hv;
         float sum = 0.f;
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            half8 hv;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                hv[i] = (_Float16)(src[sub * 32 + 8 * c + i] * inv);
-                sum += (float)hv[i];
-            }
-            reinterpret_cast<half8 *>(h16 + row * inter + sub * 32)[c] = hv;
+        for (int i = 0; i < 8; i++) {
+            hv[i] = (_Float16)(v[i] * inv);
+            sum += (float)hv[i];
         }
-        if (hs) {
-            const uint32_t hi = bf16_bits(sum);
-            const uint32_t lo = bf16_bits(sum - bf16_to_f32(hi));
-            uint16_t *d = hs + row * (inter / 16) + (sub >> 3) * 16 + (sub & 7);
-            d[0] = (uint16_t)hi;
-            d[8] = (uint16_t)lo;
+        // the sub-block's sum over its quad, in quad order
+        sum += __int_as_float(route_dpp<0xB1>(__float_as_int(sum)));
+        sum += __int_as_float(route_dpp<0x4E>(__float_as_int(sum)));
+        if (sub < nsub) {
+            reinterpret_cast<half8 *>(h16 + row * inter + sub * 32)[qd] = hv;
+            if (hs && qd == 0) {
+                const uint32_t hi = bf16_bits(sum);
+                const uint32_t lo = bf16_bits(sum - bf16_to_f32(hi));
+                uint16_t *d = hs + row * (inter / 16) + (sub >> 3) * 16 + (sub & 7);
+                d[0] = (uint16_t)hi;
+                d[8] = (uint16_t)lo;
+            }
         }
     }
 }
