@@ -166,9 +166,20 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restri
     __shared__ int cnt[MOE_MAX_EXPERTS];  // counts, then the placement cursors
     __shared__ int tmp[32];
     const int tid = threadIdx.x;
+    // the first GR_KEEP ids of each thread stay in registers for the placement
+    constexpr int GR_KEEP = 8;
+    int keep[GR_KEEP];
+#pragma unroll
+    for (int i = 0; i < GR_KEEP; i++) {
+        const int64_t p = tid + 1024 * (int64_t)i;
+        keep[i] = p < P ? ids[p] : -1;
+    }
     for (int e = tid; e < E; e += 1024) cnt[e] = 0;
     __syncthreads();
-    for (int64_t p = tid; p < P; p += 1024) {
+#pragma unroll
+    for (int i = 0; i < GR_KEEP; i++)
+        if (keep[i] >= 0 && keep[i] < E) atomicAdd(&cnt[keep[i]], 1);
+    for (int64_t p = tid + 1024 * (int64_t)GR_KEEP; p < P; p += 1024) {
         const int e = ids[p];
         if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
@@ -188,7 +199,10 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restri
         *ntiles = tiles_total;
     }
     __syncthreads();
-    for (int64_t p = tid; p < P; p += 1024) {
+#pragma unroll
+    for (int i = 0; i < GR_KEEP; i++)
+        if (keep[i] >= 0 && keep[i] < E) sorted[atomicAdd(&cnt[keep[i]], 1)] = tid + 1024 * i;
+    for (int64_t p = tid + 1024 * (int64_t)GR_KEEP; p < P; p += 1024) {
         const int e = ids[p];
         if (e >= 0 && e < E) sorted[atomicAdd(&cnt[e], 1)] = (int32_t)p;
     }
