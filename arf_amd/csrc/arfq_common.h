@@ -38,6 +38,14 @@ __device__ __forceinline__ float h2f(uint32_t bits16) {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// two f32 -> f16 (round to nearest even, as a scalar (_Float16) cast) packed
+// low | high << 16
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    const f16x2 h = {(_Float16)lo, (_Float16)hi};
+    return __builtin_bit_cast(uint32_t, h);
+}
 
 // 16-byte streaming load (non-temporal hint: each weight byte is read once).
 __device__ __forceinline__ uint4 ld_nt(const uint4 *p) {

@@ -26,7 +26,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q(
     F fmt, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
     const uint16_t *__restrict__ xs, float *__restrict__ y, int M, int N, int K, int mt,
     int xcd_order) {
-    extern __shared__ _Float16 lds[];
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int tid = threadIdx.x;
     int tm, tn;
     {
@@ -84,12 +84,20 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q(
 }
 
 // Skinny products (m <= 64): workgroup = 128 weight rows x all m rows, over the
-// 256-element blocks of split blockIdx.y (arfq_skinny.h).
-template <class F, int TA>
-__global__ __launch_bounds__(SK_THREADS) void gemm_sk(F fmt, const _Float16 *__restrict__ x,
+// 256-element blocks of split blockIdx.y (arfq_skinny.h).  x is f16, or f32
+// rounded to f16 as it is staged.  With S = gridDim.y > 1 splits each
+// workgroup stores its partial to part[sp][m][n]; the last of a column tile's
+// S workgroups to arrive (counted in tick[blockIdx.x], which it resets to 0)
+// sums the S partials in split order into y, so the result does not depend on
+// the arrival order.
+// (held to 256 VGPRs: two workgroups per CU)
+template <class F, int TA, class XT>
+__global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__restrict__ x,
                                                       const uint16_t *__restrict__ xs,
-                                                      float *__restrict__ y, int M, int N, int K) {
-    extern __shared__ _Float16 lds[];
+                                                      float *__restrict__ y, float *__restrict__ part,
+                                                      uint32_t *__restrict__ tick, int M, int N, int K) {
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * 128;
     const int nb = K / 256, S = gridDim.y, sp = blockIdx.y;
@@ -103,15 +111,86 @@ __global__ __launch_bounds__(SK_THREADS) void gemm_sk(F fmt, const _Float16 *__r
     for (int t = 0; t < TA; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    skinny_run<F, TA, 1>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds);
-    float *out = y + (int64_t)sp * M * N;
+    skinny_run<F, TA, 1, SK_THREADS, XT>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds);
+    if (S == 1) {
+#pragma unroll
+        for (int t = 0; t < TA; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int m = sk_out_row(t, i);
+                if (m < M && n < N) y[(int64_t)m * N + n] = acc[0][t][i];
+            }
+        return;
+    }
+    // Split K.  Each wave stores its accumulators as they sit in registers:
+    // float4 (row group gi = 4 t + g, lane) holds acc[t][4 g .. 4 g + 3], rows
+    // 32 t + 8 g + 4 (lane / 32) + 0..3 of column n, for the GT 8-row groups
+    // that hold rows < M.  The partials move with the device-scope cache
+    // policy (sc1: written through to, and read from, the level coherent
+    // across the XCDs' L2s, as the compiler encodes agent-scope atomic
+    // accesses) rather than by writing back and invalidating whole L2s; every
+    // store has completed before the counter moves, and the last arriver
+    // loads the others' partials only after it has seen the count.
+    const int GT = (M + 7) >> 3, nt = gridDim.x;
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        part, (short)0, (int)((uint32_t)S * nt * GT * 4096u), 0x00020000);
+    auto poff = [&](int j, int gi) -> uint32_t {
+        return ((((uint32_t)j * nt + blockIdx.x) * 4 + wave) * GT + gi) * 1024u + lane * 16u;
+    };
+    constexpr int SC1 = 16;  // cache-policy operand: device scope
 #pragma unroll
     for (int t = 0; t < TA; t++)
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            const int m = sk_out_row(t, i);
-            if (m < M && n < N) out[(int64_t)m * N + n] = acc[0][t][i];
-        }
+        for (int g = 0; g < 4; g++)
+            if (4 * t + g < GT) {
+                const u32x4 v = {__float_as_uint(acc[0][t][4 * g]), __float_as_uint(acc[0][t][4 * g + 1]),
+                                 __float_as_uint(acc[0][t][4 * g + 2]), __float_as_uint(acc[0][t][4 * g + 3])};
+                __builtin_amdgcn_raw_buffer_store_b128(v, prs, poff(sp, 4 * t + g), 0, SC1);
+            }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are done
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t before =
+            __hip_atomic_fetch_add(tick + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = before == (uint32_t)(S - 1);
+        if (last) __hip_atomic_store(tick + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last) return;
+    // Sum in split order, this workgroup's own partial from its registers;
+    // the next row group's loads are in flight while one group is summed.
+    // Straight-line code (branches around loads cost waits on every load in
+    // flight): loads of splits past S, of this workgroup's own split and of
+    // row groups past GT read past the end of the buffer, which returns 0
+    // and moves no data.
+    u32x4 v[2][16];
+    auto load = [&](u32x4(&d)[16], int gi) {
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+            d[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                prs, poff(j, gi) | (uint32_t)(j >= S || j == sp || gi >= GT) << 31, 0, SC1);
+    };
+    load(v[0], 0);
+#pragma unroll
+    for (int gi = 0; gi < 4 * TA; gi++) {
+        if (gi + 1 < 4 * TA) load(v[(gi + 1) & 1], gi + 1);
+        const int t = gi >> 2, g = gi & 3;
+        const u32x4(&d)[16] = v[gi & 1];
+        float r[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) r[c] = sp == 0 ? acc[0][t][4 * g + c] : __uint_as_float(d[0][c]);
+        // splits past S add the 0 their loads returned (exact but for a -0
+        // sum turning +0)
+#pragma unroll
+        for (int j = 1; j < 16; j++)
+#pragma unroll
+            for (int c = 0; c < 4; c++) r[c] += j == sp ? acc[0][t][4 * g + c] : __uint_as_float(d[j][c]);
+        const int row = 32 * t + 8 * g + 4 * (lane >> 5);
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            if (row + c < M && n < N) y[(int64_t)(row + c) * N + n] = r[c];
+    }
 }
 
 // y[i] = part[0][i] + part[1][i] + ... in split order
@@ -126,8 +205,9 @@ __global__ void splitk_reduce(const float *__restrict__ part, float *__restrict_
 
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
                         _Float16 *xl, uint16_t *xs, hipStream_t s) {
-    const int64_t items = m * (k / 32);
+    const int64_t items = m * (k / 8);
     if (items == 0 || (!xh && !xl && !xs)) return hipSuccess;
+    if (k % 32) return hipErrorInvalidValue;
     const unsigned grid = (unsigned)((items + 255) / 256);
     if (x_dtype == ARFQ_F32)
         xprep_kernel<float><<<grid, 256, 0, s>>>((const float *)x, m, (int)k, xh, xl, xs);
@@ -156,7 +236,10 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     // f32 x: rounded to f16 for the skinny kernel and for prefill shapes (m > 64,
     // as the reference's half tiles), split into f16 hi + lo otherwise
     p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && m <= 64;
-    p.convert = x_dtype == ARFQ_F32;
+    // the skinny kernel rounds an f32 x itself at m <= 32, except for Q4_K,
+    // whose x sub-block sums come from the same preparation pass (at m > 32
+    // the staging registers would not fit beside two waves per SIMD)
+    p.convert = x_dtype == ARFQ_F32 && !(p.skinny && m <= 32 && w->qtype != ARFQ_Q4_K);
     // Q4_K prefill: the direct-operand kernel (one launch, no split-K)
     p.bd = !p.skinny && w->qtype == ARFQ_Q4_K && m > 64 &&
            w->n * (w->k / 2) < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
@@ -204,32 +287,46 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     p.off_xs = o;
     o += p.sums ? al256((size_t)m * (w->k / 16) * 2) : 0;
     p.off_part = o;
-    o += p.splits > 1 ? al256((size_t)p.splits * m * w->n * 4) : al256(bd_part);
+    if (p.skinny)  // partials in register order: [split][column tile][wave][8-row group][lane] float4
+        o += p.splits > 1 ? al256((size_t)p.splits * ((w->n + 127) / 128) * ((m + 7) / 8) * 4096) : 0;
+    else
+        o += p.splits > 1 ? al256((size_t)p.splits * m * w->n * 4) : al256(bd_part);
     p.scratch_bytes = o;
     return p;
 }
 
-template <class F, int TA>
-static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
-                              const uint16_t *xs, float *out, int S, hipStream_t s) {
+template <class F, int TA, class XT>
+static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const XT *x,
+                              const uint16_t *xs, float *y, float *part, uint32_t *tick, int S,
+                              hipStream_t s) {
     static bool attr_set = false;
     constexpr size_t lds = sk_lds<F, TA, 1>();
     if (!attr_set) {
-        hipError_t err = hipFuncSetAttribute((const void *)gemm_sk<F, TA>,
+        hipError_t err = hipFuncSetAttribute((const void *)gemm_sk<F, TA, XT>,
                                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (err != hipSuccess) return err;
         attr_set = true;
     }
     const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
-    gemm_sk<F, TA><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, out, (int)m, (int)w->n, (int)w->k);
+    gemm_sk<F, TA, XT><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, y, part, tick, (int)m, (int)w->n,
+                                                     (int)w->k);
     return hipGetLastError();
 }
 
+// S > 1 splits need S <= 16 and one zeroed counter per 128-column tile
 template <class F>
-static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
-                            const uint16_t *xs, float *out, int S, hipStream_t s) {
-    return m <= 32 ? launch_sk_t<F, 1>(fmt, w, m, x, xs, out, S, s)
-                   : launch_sk_t<F, 2>(fmt, w, m, x, xs, out, S, s);
+static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const void *x,
+                            bool xf32, const uint16_t *xs, float *y, float *part, uint32_t *tick,
+                            int ntick, int S, hipStream_t s) {
+    if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;
+    if (xf32) {
+        if constexpr (F::KIND == 2) return hipErrorInvalidValue;  // Q4_K: prepared x only
+        else
+            return m <= 32 ? launch_sk_t<F, 1>(fmt, w, m, (const float *)x, xs, y, part, tick, S, s)
+                           : hipErrorInvalidValue;  // m > 32: prepared x only
+    }
+    return m <= 32 ? launch_sk_t<F, 1>(fmt, w, m, (const _Float16 *)x, xs, y, part, tick, S, s)
+                   : launch_sk_t<F, 2>(fmt, w, m, (const _Float16 *)x, xs, y, part, tick, S, s);
 }
 
 SkQ4K sk_q4k(const arfq_weight *w) {
@@ -312,7 +409,8 @@ static hipError_t launch_bd_q4k(const arfq_weight *w, int e, int64_t m, const _F
 }
 
 hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
-                       float *y, void *scratch, const GemmPlan &p, hipStream_t s) {
+                       float *y, void *scratch, uint32_t *tickets, int ntickets,
+                       const GemmPlan &p, hipStream_t s) {
     char *sc = (char *)scratch;
     if (p.scratch_bytes && !sc) return hipErrorInvalidValue;
     _Float16 *xh = p.convert ? (_Float16 *)(sc + p.off_xh) : (_Float16 *)x;
@@ -325,19 +423,20 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     float *out = p.splits > 1 ? (float *)(sc + p.off_part) : y;
     hipError_t err;
     if (p.skinny) {
+        // the split-K sum happens inside the kernel
+        const bool xf32 = x_dtype == ARFQ_F32 && !p.convert;
+        const void *xk = p.convert ? (const void *)xh : x;
+        const int64_t eb = (int64_t)e * w->n * (w->k / 256);
         switch (w->qtype) {
         case ARFQ_Q4_K:
-            err = launch_sk(sk_q4k(w).shifted((int64_t)e * w->n * (w->k / 256)), w, m, xh, xs, out,
-                            p.splits, s);
-            break;
+            return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets, ntickets,
+                             p.splits, s);
         case ARFQ_Q6_K:
-            err = launch_sk(sk_q6k(w).shifted((int64_t)e * w->n * (w->k / 256)), w, m, xh, xs, out,
-                            p.splits, s);
-            break;
+            return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets, ntickets,
+                             p.splits, s);
         case ARFQ_Q8_0:
-            err = launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xh, xs, out,
-                            p.splits, s);
-            break;
+            return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xf32, xs,
+                             y, out, tickets, ntickets, p.splits, s);
         default:
             return hipErrorInvalidValue;
         }

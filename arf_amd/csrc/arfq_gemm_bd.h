@@ -123,7 +123,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
     const uint4 *__restrict__ hdr, const uint4 *__restrict__ qs, const _Float16 *__restrict__ x,
     const uint16_t *__restrict__ xs, float *__restrict__ y, float *__restrict__ part, int m, int n,
     int k, int mt, int xcd_order, int full, int chunks) {
-    extern __shared__ _Float16 sx[];  // [2][BD_BM][BD_LD]
+    extern __shared__ __attribute__((aligned(16))) _Float16 sx[];  // [2][BD_BM][BD_LD]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nblk = k / 256;
 

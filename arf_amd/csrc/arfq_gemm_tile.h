@@ -560,49 +560,54 @@ __device__ __forceinline__ int tile_out_col(int b) {
 }
 
 // ---- activation preparation ------------------------------------------------
-// One thread per 32-element sub-block of a row-major [M, K] activation:
-// writes x as f16 (and, when `xl` is set, the f16 remainder x - hi) and, when
-// `xs` is set, the sub-block sum X (of the values the MFMAs will see) as bf16
-// hi + lo into xs[row][k / 256][j] and [8 + j] (j = sub-block within block).
+// One thread per 8 consecutive elements of a row-major [M, K] activation (K a
+// multiple of 32), so a quad of lanes covers a 32-element sub-block and every
+// load and store is 16 bytes wide and coalesced: writes x as f16 (and, when
+// `xl` is set, the f16 remainder x - hi) and, when `xs` is set, the sub-block
+// sum X (of the values the MFMAs will see: each lane's 8 in order, then the
+// quad's four partial sums pairwise) as bf16 hi + lo into xs[row][k / 256][j]
+// and [8 + j] (j = sub-block within block).
 template <typename TIn>
 __global__ void xprep_kernel(const TIn *__restrict__ x, int64_t M, int K, _Float16 *__restrict__ xh,
                              _Float16 *__restrict__ xl, uint16_t *__restrict__ xs) {
     const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int nsub = K / 32;
-    if (g >= M * nsub) return;
-    const int64_t row = g / nsub;
-    const int sub = (int)(g - row * nsub);
-    const TIn *src = x + row * K + sub * 32;
+    const int nch = K / 8;
+    if (g >= M * nch) return;  // K % 32 == 0: a quad's lanes leave together
+    const int64_t row = g / nch;
+    const int ch = (int)(g - row * nch);
+    float v[8];
+    if constexpr (sizeof(TIn) == 4) {
+        const float4 a = reinterpret_cast<const float4 *>(x + g * 8)[0];
+        const float4 b = reinterpret_cast<const float4 *>(x + g * 8)[1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+        const half8 a = reinterpret_cast<const half8 *>(x + g * 8)[0];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (float)a[i];
+    }
+    half8 hv, lv;
     float sum = 0.f;
 #pragma unroll
-    for (int c = 0; c < 4; c++) {
-        float v[8];
-        if constexpr (sizeof(TIn) == 4) {
-            const float4 a = reinterpret_cast<const float4 *>(src)[2 * c];
-            const float4 b = reinterpret_cast<const float4 *>(src)[2 * c + 1];
-            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
-            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        } else {
-            const half8 a = reinterpret_cast<const half8 *>(src)[c];
-#pragma unroll
-            for (int i = 0; i < 8; i++) v[i] = (float)a[i];
-        }
-        half8 hv, lv;
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            hv[i] = (_Float16)v[i];
-            lv[i] = (_Float16)(v[i] - (float)hv[i]);
-            sum += xl ? ((float)hv[i] + (float)lv[i]) : (float)hv[i];
-        }
-        if (xh) reinterpret_cast<half8 *>(xh + row * K + sub * 32)[c] = hv;
-        if (xl) reinterpret_cast<half8 *>(xl + row * K + sub * 32)[c] = lv;
+    for (int i = 0; i < 8; i++) {
+        hv[i] = (_Float16)v[i];
+        lv[i] = (_Float16)(v[i] - (float)hv[i]);
+        sum += xl ? ((float)hv[i] + (float)lv[i]) : (float)hv[i];
     }
+    if (xh) reinterpret_cast<half8 *>(xh)[g] = hv;
+    if (xl) reinterpret_cast<half8 *>(xl)[g] = lv;
     if (xs) {
-        const uint32_t hi = bf16_bits(sum);
-        const uint32_t lo = bf16_bits(sum - bf16_to_f32(hi));
-        uint16_t *d = xs + row * (K / 16) + (sub >> 3) * 16 + (sub & 7);
-        d[0] = (uint16_t)hi;
-        d[8] = (uint16_t)lo;
+        // (s0 + s1) + (s2 + s3) on every lane of the quad (quad_perm [1,0,3,2], then [2,3,0,1])
+        sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sum), 0xB1, 0xf, 0xf, true));
+        sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sum), 0x4E, 0xf, 0xf, true));
+        if ((ch & 3) == 0) {
+            const int sub = ch >> 2;
+            const uint32_t hi = bf16_bits(sum);
+            const uint32_t lo = bf16_bits(sum - bf16_to_f32(hi));
+            uint16_t *d = xs + row * (K / 16) + (sub >> 3) * 16 + (sub & 7);
+            d[0] = (uint16_t)hi;
+            d[8] = (uint16_t)lo;
+        }
     }
 }
 

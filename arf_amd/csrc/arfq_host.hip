@@ -88,6 +88,13 @@ int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
     if (e == hipSuccess) e = hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, device);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_stop);
+    if (e == hipSuccess) {
+        ctx->ntickets = std::max(1024, 2 * ctx->cus);
+        e = hipMalloc(&ctx->tickets, (size_t)ctx->ntickets * sizeof(uint32_t));
+    }
+    if (e == hipSuccess)
+        e = hipMemsetAsync(ctx->tickets, 0, (size_t)ctx->ntickets * sizeof(uint32_t), ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         g_create_err = std::string("arfq_ctx_create: ") + hipGetErrorString(e);
         arfq_ctx_destroy(ctx);
@@ -102,6 +109,7 @@ int arfq_ctx_destroy(arfq_ctx *ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->tickets) (void)hipFree(ctx->tickets);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
     if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -270,7 +278,8 @@ static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64
     } else if (arfq::gemm_supports(w, m)) {
         const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
         if (int rc = ensure_scratch(ctx, plan.scratch_bytes)) return rc;
-        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->scratch, plan, ctx->stream);
+        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->scratch, ctx->tickets,
+                              ctx->ntickets, plan, ctx->stream);
     } else {
         return fail(ctx, ARFQ_E_UNSUPPORTED,
                     "matmul: no kernel for qtype " + std::to_string(w->qtype) + " at m=" +

@@ -19,6 +19,10 @@ struct arfq_ctx {
     // growable scratch for the MoE pipeline (routing, grouping, intermediates)
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // split-K arrival counters, one per column tile: zero between launches (the
+    // last workgroup of a tile to arrive resets its counter)
+    uint32_t *tickets = nullptr;
+    int ntickets = 0;
 };
 
 struct arfq_weight {
@@ -71,9 +75,11 @@ struct GemmPlan {
 };
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype);
 bool gemm_supports(const arfq_weight *w, int64_t m);
-// y[m, n] = x[m, k] . W_e^T; `scratch` holds plan.scratch_bytes.
+// y[m, n] = x[m, k] . W_e^T; `scratch` holds plan.scratch_bytes; `tickets`
+// holds ntickets zeroed split-K counters (left zeroed).
 hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
-                       float *y, void *scratch, const GemmPlan &p, hipStream_t s);
+                       float *y, void *scratch, uint32_t *tickets, int ntickets,
+                       const GemmPlan &p, hipStream_t s);
 // Activation preparation: x (f32 or f16, [m, k]) -> f16 copy (xh), f16
 // remainder (xl), bf16 sub-block sums (xs, [m][k / 256][16]); null outputs are skipped.
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,

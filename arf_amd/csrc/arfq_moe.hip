@@ -225,7 +225,7 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     const uint16_t *__restrict__ xs, int K, int inter, int top_k, const int32_t *__restrict__ off,
     const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ h) {
-    extern __shared__ _Float16 lds[];
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     if ((int)blockIdx.x >= *ntiles) return;  // uniform over the workgroup
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
@@ -365,7 +365,7 @@ __global__ __launch_bounds__(SK_THREADS) void moe_down_kernel(
     const float *__restrict__ rs, int K, int hidden, const int32_t *__restrict__ off,
     const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ o) {
-    extern __shared__ _Float16 lds[];
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     if ((int)blockIdx.x >= *ntiles) return;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int2 tile = tiles[blockIdx.x];

@@ -245,10 +245,10 @@ constexpr size_t sk_lds() {
 // wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
 // `rows` gives the x rows this thread stages.  All 256 threads of the
 // workgroup call it with the same block range.
-template <class F, int TA, int NW, int NT = SK_THREADS>
+template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
-                                           const _Float16 *__restrict__ x,
+                                           const XT *__restrict__ x,
                                            const uint16_t *__restrict__ xs, int b0, int b1,
                                            floatx16 (&acc)[NW][TA], _Float16 *lds) {
     constexpr int KIND = F::KIND;
@@ -263,11 +263,18 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
     uint16_t *sl = reinterpret_cast<uint16_t *>(lds + XR * SK_XLD);  // [XR][16]
     uint8_t *slab = reinterpret_cast<uint8_t *>(sl + XR * 16) + (size_t)wave * NW * 32 * SL;
 
-    u32x4 xv[XC], sv;
+    // x chunks of 8 elements: one 16-byte load of f16, two of f32 (rounded to
+    // f16 when stored to LDS)
+    constexpr int XW = sizeof(XT) / 2;
+    static_assert(XW == 1 || XW == 2, "x is f16 or f32");
+    u32x4 xv[XC * XW], sv;
     auto xload = [&](int b) {
 #pragma unroll
         for (int i = 0; i < XC; i++)
-            xv[i] = *reinterpret_cast<const u32x4 *>(x + rows.x[i] + 256 * b + 8 * (tid & 31));
+#pragma unroll
+            for (int j = 0; j < XW; j++)
+                xv[XW * i + j] = *reinterpret_cast<const u32x4 *>(x + rows.x[i] + 256 * b +
+                                                                  8 * (tid & 31) + 4 * j);
         // the sums' load sits in the same branch as their store: loaded
         // unconditionally, it was sunk next to the store, where its wait
         // covered every load in flight
@@ -277,8 +284,19 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
     };
     auto xstore = [&]() {
 #pragma unroll
-        for (int i = 0; i < XC; i++)
-            *reinterpret_cast<u32x4 *>(xl + ((tid >> 5) + (NT / 32) * i) * SK_XLD + 8 * (tid & 31)) = xv[i];
+        for (int i = 0; i < XC; i++) {
+            u32x4 v;
+            if constexpr (XW == 1) {
+                v = xv[i];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const u32x4 &f = xv[2 * i + (j >> 1)];
+                    v[j] = pack_f16x2(__uint_as_float(f[2 * (j & 1)]), __uint_as_float(f[2 * (j & 1) + 1]));
+                }
+            }
+            *reinterpret_cast<u32x4 *>(xl + ((tid >> 5) + (NT / 32) * i) * SK_XLD + 8 * (tid & 31)) = v;
+        }
         if constexpr (KIND == 2) {
             if (tid < 2 * XR) *reinterpret_cast<u32x4 *>(sl + (tid >> 1) * 16 + 8 * (tid & 1)) = sv;
         }

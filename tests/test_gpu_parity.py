@@ -152,7 +152,8 @@ def test_gemm_q4k_f16_small(gpu_ctx, oracle, m, n, k):
 
 
 @pytest.mark.parametrize("m", [5, 16, 64, 65, 200])
-@pytest.mark.parametrize("qtype,n,k", [("q4_k", 96, 2048), ("q6_k", 130, 1792), ("q8_0", 77, 1216)])
+@pytest.mark.parametrize("qtype,n,k", [("q4_k", 96, 2048), ("q6_k", 130, 1792), ("q8_0", 77, 1216),
+                                       ("q8_0", 100, 2048)])
 def test_gemm_f32_x(gpu_ctx, oracle, qtype, n, k, m):
     # m > 4 goes through the MFMA path: f32 x split into an f16 hi + lo pair
     # for m <= 64, rounded to f16 above
@@ -186,6 +187,33 @@ def test_gemm_split_k_is_deterministic(gpu_ctx, n, k, m):
     gpu_ctx.matmul(w, x, m, y1)
     gpu_ctx.matmul(w, x, m, y2)
     assert np.array_equal(y1.numpy().view(np.uint32), y2.numpy().view(np.uint32))
+
+
+def test_skinny_split_counters_reset(gpu_ctx, oracle):
+    # skinny products split over K sum their partials in the kernel, the last
+    # workgroup of each column tile resetting that tile's arrival counter:
+    # interleaved shapes (split counts 16, 3 and 8; column counts a multiple of
+    # 4 and not) give the oracle's result, and the same bits, on every repeat
+    from arf_amd import QType, synth
+    cases = [("q6_k", 512, 8192, 8), ("q6_k", 130, 1792, 16), ("q8_0", 1000, 4096, 24)]
+    runs = []
+    for qtype, n, k, m in cases:
+        raw = synth.weight(qtype, n, k, seed=n + m)
+        x = synth.activations(m, k, seed=k + m)
+        runs.append((gpu_ctx.upload(QType[qtype.upper()], raw, n, k), gpu_ctx.to_device(x),
+                     oracle.matmul_q(qtype, x, raw, n), None))
+    for rep in range(3):
+        for i, (qtype, n, k, m) in enumerate(cases):
+            _say("case: skinny split repeat", rep, qtype, n, k, m)
+            w, xd, want, first = runs[i]
+            y = gpu_ctx.empty((m, n), np.float32)
+            gpu_ctx.matmul(w, xd, m, y)
+            got = y.numpy()
+            assert rel_err(got, want) <= TOL
+            if first is None:
+                runs[i] = (w, xd, want, got)
+            else:
+                assert np.array_equal(got.view(np.uint32), first.view(np.uint32))
 
 
 @pytest.mark.parametrize("m", [8, 32, 64])
