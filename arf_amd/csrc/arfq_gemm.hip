@@ -111,7 +111,7 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
     for (int t = 0; t < TA; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    skinny_run<F, TA, 1, SK_THREADS, XT>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds);
+    skinny_run<F, TA, 1, SK_THREADS, XT>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds, M);
     if (S == 1) {
 #pragma unroll
         for (int t = 0; t < TA; t++)

@@ -244,7 +244,8 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    skinny_run<F, 2, 1, MOE_GU_THREADS>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc, lds);
+    skinny_run<F, 2, 1, MOE_GU_THREADS, _Float16, true>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc,
+                                                        lds, rows);
     // the loop ends with a barrier after its last LDS use: hand up to gate
     float *ex = reinterpret_cast<float *>(lds);  // [4 waves][2 tiles][16][64 lanes]
     if (is_up) {
@@ -380,7 +381,9 @@ __global__ __launch_bounds__(SK_THREADS) void moe_down_kernel(
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    skinny_run<F, 2, 1>(fm, wrow0, hidden, xr, h, hs, 0, K / 256, acc, lds);
+    // (Q6_K: the second loop copy would not fit the registers)
+    skinny_run<F, 2, 1, SK_THREADS, _Float16, F::KIND != 1>(fm, wrow0, hidden, xr, h, hs, 0, K / 256,
+                                                           acc, lds, rows);
     const int n = n0 + (lane & 31);
 #pragma unroll
     for (int t = 0; t < 2; t++)

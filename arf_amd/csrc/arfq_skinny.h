@@ -243,14 +243,13 @@ constexpr size_t sk_lds() {
 // Accumulates acc[w][t] (w < NW weights, t < TA 32-row x tiles) over the
 // 256-element blocks [b0, b1) for the wave's 32 weight rows wrow0[w] ..
 // wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
-// `rows` gives the x rows this thread stages.  All 256 threads of the
-// workgroup call it with the same block range.
-template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16>
-__device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
-                                           int64_t nrows, const SkRows<TA, NT> &rows,
-                                           const XT *__restrict__ x,
-                                           const uint16_t *__restrict__ xs, int b0, int b1,
-                                           floatx16 (&acc)[NW][TA], _Float16 *lds) {
+// The block loop of skinny_run for the first TU (<= TA) x tiles.
+template <class F, int TA, int TU, int NW, int NT, class XT>
+__device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
+                                            int64_t nrows, const SkRows<TA, NT> &rows,
+                                            const XT *__restrict__ x,
+                                            const uint16_t *__restrict__ xs, int b0, int b1,
+                                            floatx16 (&acc)[NW][TA], _Float16 *lds) {
     constexpr int KIND = F::KIND;
     constexpr int XR = 32 * TA;  // x rows staged
     constexpr int XC = SkRows<TA, NT>::XC;
@@ -267,10 +266,11 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
     // f16 when stored to LDS)
     constexpr int XW = sizeof(XT) / 2;
     static_assert(XW == 1 || XW == 2, "x is f16 or f32");
-    u32x4 xv[XC * XW], sv;
+    constexpr int XU = XC * TU / TA;  // chunks of the x rows in use
+    u32x4 xv[XU * XW], sv;
     auto xload = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < XC; i++)
+        for (int i = 0; i < XU; i++)
 #pragma unroll
             for (int j = 0; j < XW; j++)
                 xv[XW * i + j] = *reinterpret_cast<const u32x4 *>(x + rows.x[i] + 256 * b +
@@ -279,12 +279,12 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
         // unconditionally, it was sunk next to the store, where its wait
         // covered every load in flight
         if constexpr (KIND == 2) {
-            if (tid < 2 * XR) sv = *reinterpret_cast<const u32x4 *>(xs + rows.s + 16 * b + 8 * (tid & 1));
+            if (tid < 64 * TU) sv = *reinterpret_cast<const u32x4 *>(xs + rows.s + 16 * b + 8 * (tid & 1));
         }
     };
     auto xstore = [&]() {
 #pragma unroll
-        for (int i = 0; i < XC; i++) {
+        for (int i = 0; i < XU; i++) {
             u32x4 v;
             if constexpr (XW == 1) {
                 v = xv[i];
@@ -298,7 +298,7 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
             *reinterpret_cast<u32x4 *>(xl + ((tid >> 5) + (NT / 32) * i) * SK_XLD + 8 * (tid & 31)) = v;
         }
         if constexpr (KIND == 2) {
-            if (tid < 2 * XR) *reinterpret_cast<u32x4 *>(sl + (tid >> 1) * 16 + 8 * (tid & 1)) = sv;
+            if (tid < 64 * TU) *reinterpret_cast<u32x4 *>(sl + (tid >> 1) * 16 + 8 * (tid & 1)) = sv;
         }
     };
 
@@ -370,7 +370,7 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
 #pragma unroll
-                    for (int t = 0; t < TA; t++) {
+                    for (int t = 0; t < TU; t++) {
                         const half8 af = *reinterpret_cast<const half8 *>(
                             xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
                         if (KIND != 0 && p == 0 && kk == 0) {
@@ -397,14 +397,14 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
                     bf16x8 bh, bl;
                     F::minsb(wb[w], bh, bl);
 #pragma unroll
-                    for (int t = 0; t < TA; t++) {
+                    for (int t = 0; t < TU; t++) {
                         const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sl + (32 * t + lr) * 16 + 8 * h);
                         cmin[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][t], 0, 0, 0);
                         cmin[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][t], 0, 0, 0);
                     }
                 }
 #pragma unroll
-                for (int t = 0; t < TA; t++)
+                for (int t = 0; t < TU; t++)
 #pragma unroll
                     for (int i = 0; i < 16; i++) acc[w][t][i] = fmaf(dd.x, cb[w][t][i], acc[w][t][i]);
             }
@@ -419,12 +419,31 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
 #pragma unroll
         for (int w = 0; w < NW; w++)
 #pragma unroll
-            for (int t = 0; t < TA; t++)
+            for (int t = 0; t < TU; t++)
 #pragma unroll
                 for (int i = 0; i < 16; i++) acc[w][t][i] += cmin[w][t][i];
     }
 }
 
+// `rows` gives the x rows this thread stages; xrows (<= 32 TA) of them are
+// real.  With TA = 2, xrows <= 32 and SHORT (tiles of varying height), the
+// second x tile is neither staged nor multiplied (acc[w][1] is left as it
+// is).  All threads of the workgroup call it with the same block range and
+// xrows.
+template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false>
+__device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
+                                           int64_t nrows, const SkRows<TA, NT> &rows,
+                                           const XT *__restrict__ x,
+                                           const uint16_t *__restrict__ xs, int b0, int b1,
+                                           floatx16 (&acc)[NW][TA], _Float16 *lds, int xrows) {
+    if constexpr (TA == 2 && SHORT) {
+        if (xrows <= 32) {
+            skinny_loop<F, TA, 1, NW, NT, XT>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+            return;
+        }
+    }
+    skinny_loop<F, TA, TA, NW, NT, XT>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+}
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.
 template <int TA, int NT = SK_THREADS, class RowOf>
