@@ -31,6 +31,9 @@ ARFQ_E_SHAPE = -2
 ARFQ_E_DEVICE = -3
 ARFQ_E_NOMEM = -4
 ARFQ_E_UNSUPPORTED = -5
+ARFQ_E_FORMAT = -6
+ARFQ_E_IO = -7
+ARFQ_E_NOT_FOUND = -8
 
 
 class QType(enum.IntEnum):
@@ -81,6 +84,19 @@ _SIGS = {
     "arfq_timer_start": (_int, [_vp]),
     "arfq_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
     "arfq_matmul_repeat": (_int, [_vp, ctypes.POINTER(_vp), _int, _int, _i64, _vp, _int, _vp]),
+    "arfq_gguf_is_gguf": (_int, [ctypes.c_char_p]),
+    "arfq_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
+    "arfq_gguf_close": (_int, [_vp]),
+    "arfq_gguf_last_error": (ctypes.c_char_p, [_vp]),
+    "arfq_gguf_tensor_count": (_int, [_vp, ctypes.POINTER(_i64)]),
+    "arfq_gguf_tensor_info": (_int, [_vp, _i64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_int),
+                                     ctypes.POINTER(_int), ctypes.POINTER(_i64), _int,
+                                     ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)]),
+    "arfq_gguf_find": (_int, [_vp, ctypes.c_char_p, ctypes.POINTER(_i64)]),
+    "arfq_gguf_blocks": (_int, [_vp, ctypes.c_char_p, _int, ctypes.POINTER(_vp),
+                                ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(_i64),
+                                ctypes.POINTER(_i64)]),
+    "arfq_gguf_upload": (_int, [_vp, _vp, ctypes.c_char_p, _i64, _i64, ctypes.POINTER(_vp)]),
 }
 
 _lib = None
@@ -233,6 +249,21 @@ class Context:
             int(n_experts), ctypes.byref(h)))
         return Weight(self, h.value, qtype, int(n_rows), int(k_cols), int(n_experts))
 
+    def upload_gguf(self, gguf, name, row0=0, n_rows=-1):
+        """Upload GGUF tensor `name`: a 2-D matrix (or its rows [row0, row0 + n_rows)) or a
+        3-D `*_exps` tensor as n_experts experts (arfq_gguf_upload)."""
+        L = load_library()
+        h = ctypes.c_void_p()
+        st = L.arfq_gguf_upload(self.handle, gguf.handle, name.encode(), int(row0), int(n_rows),
+                                ctypes.byref(h))
+        if st != ARFQ_OK:
+            msg = (L.arfq_gguf_last_error(gguf.handle) or b"").decode()
+            if not msg or st in (ARFQ_E_DEVICE, ARFQ_E_NOMEM):
+                msg = (L.arfq_last_error(self.handle) or b"").decode() or msg
+            raise (ValueError(msg) if st == ARFQ_E_SHAPE else ArfqError(st, msg))
+        qt, n, k, e = _weight_shape(h.value)
+        return Weight(self, h.value, QType(qt), n, k, e)
+
     # -- compute --
     def matmul(self, w, x, m, y, expert=0):
         """y[m, w.n] = x[m, w.k] . W_expert^T  (x: DeviceArray f32/f16, y: DeviceArray f32)."""
@@ -289,6 +320,99 @@ class Context:
         xd = DType.F16 if x.dtype == np.float16 else DType.F32
         _check(self.handle, load_library().arfq_matmul_repeat(
             self.handle, arr, len(ws), int(iters), int(m), x.ptr, int(xd), y.ptr))
+
+
+def _weight_shape(handle):
+    L = load_library()
+    qt, n, k, e = _int(), _i64(), _i64(), _int()
+    _check(None, L.arfq_weight_info(handle, ctypes.byref(qt), ctypes.byref(n), ctypes.byref(k),
+                                    ctypes.byref(e), None))
+    return qt.value, n.value, k.value, e.value
+
+
+class GgufTensor:
+    """One tensor table entry: ggml dims fastest-varying first, type id, absolute byte offset,
+    ggml_byte_len bytes (TensorDesc, crates/arf-core/src/model/gguf.rs:92-100)."""
+
+    def __init__(self, name, ggml_type, dims, offset, nbytes):
+        self.name, self.ggml_type, self.dims = name, ggml_type, tuple(dims)
+        self.offset, self.nbytes = offset, nbytes
+
+    def __repr__(self):
+        return f"GgufTensor({self.name!r}, type={self.ggml_type}, dims={self.dims}, offset={self.offset})"
+
+
+class Gguf:
+    """A GGUF v3 file opened read-only and memory-mapped by the library (LazyGguf::open_raw,
+    crates/arf-core/src/model/gguf.rs:509-564).  Raises ArfqError on a malformed file."""
+
+    def __init__(self, path):
+        L = load_library()
+        h = ctypes.c_void_p()
+        st = L.arfq_gguf_open(os.fsencode(path), ctypes.byref(h))
+        if st != ARFQ_OK:
+            raise ArfqError(st, (L.arfq_gguf_last_error(None) or b"").decode())
+        self.handle = h.value
+        n = _i64()
+        L.arfq_gguf_tensor_count(self.handle, ctypes.byref(n))
+        self.tensors = []
+        for i in range(n.value):
+            name, ty, nd = ctypes.c_char_p(), _int(), _int()
+            dims = (_i64 * 8)()
+            off, nb = ctypes.c_uint64(), ctypes.c_uint64()
+            self._check(L.arfq_gguf_tensor_info(self.handle, i, ctypes.byref(name), ctypes.byref(ty),
+                                                ctypes.byref(nd), dims, 8, ctypes.byref(off),
+                                                ctypes.byref(nb)))
+            self.tensors.append(GgufTensor(name.value.decode(), ty.value, dims[:min(nd.value, 8)],
+                                           off.value, nb.value))
+
+    @staticmethod
+    def is_gguf(path):
+        """is_gguf_file (gguf.rs:1115-1125): a regular file starting with the magic."""
+        return bool(load_library().arfq_gguf_is_gguf(os.fsencode(path)))
+
+    def _check(self, st):
+        if st != ARFQ_OK:
+            L = load_library()
+            raise ArfqError(st, (L.arfq_gguf_last_error(self.handle) or b"").decode())
+
+    def tensor_names(self):
+        return [t.name for t in self.tensors]
+
+    def find(self, name):
+        i = _i64()
+        self._check(load_library().arfq_gguf_find(self.handle, name.encode(), ctypes.byref(i)))
+        return self.tensors[i.value]
+
+    def blocks(self, name, ggml_type):
+        """(bytes, rows, cols) of a tensor stored as `ggml_type` (get_q4k_blocks_raw /
+        get_q8_0_blocks_raw, gguf.rs:774-828); None when it is stored as another type."""
+        L = load_library()
+        p, nb, r, c = ctypes.c_void_p(), ctypes.c_size_t(), _i64(), _i64()
+        st = L.arfq_gguf_blocks(self.handle, name.encode(), int(ggml_type), ctypes.byref(p),
+                                ctypes.byref(nb), ctypes.byref(r), ctypes.byref(c))
+        if st == ARFQ_E_UNSUPPORTED:
+            return None
+        self._check(st)
+        buf = (ctypes.c_uint8 * nb.value).from_address(p.value) if nb.value else b""
+        return np.frombuffer(buf, np.uint8).copy(), r.value, c.value
+
+    def close(self):
+        if self.handle:
+            load_library().arfq_gguf_close(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def add_matmul_m(ctx, m, a, weight, out, n, kdim, expert=0):

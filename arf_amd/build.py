@@ -2,8 +2,8 @@
 
     python -m arf_amd.build            # or arf_amd.build.build()
 
-Every arf_amd/csrc/*.hip file is compiled by hipcc to an object, then linked
-into arf_amd/libarfq.so.  Always rebuilds (the driver's build check compiles
+Every arf_amd/csrc/*.hip file is compiled by hipcc (and every host-only *.cpp
+file by g++) to an object, then linked into arf_amd/libarfq.so.  Always rebuilds (the driver's build check compiles
 every time).
 """
 import os
@@ -19,6 +19,7 @@ LIB = os.path.join(HERE, "libarfq.so")
 ARCH = "gfx950"
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+CXX = shutil.which("g++") or "c++"
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     # no packed-FP32 VALU ops in device code (v_pk_{add,mul,fma}_f32)
@@ -44,12 +45,25 @@ def _compile(src):
     return obj
 
 
+def _compile_host(src):
+    """Host-only C++ (no device code): the system compiler."""
+    obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+    cmd = [CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra", "-I",
+           os.path.join(HERE, "..", "include"), "-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"{CXX} failed on {src}:\n{r.stdout}\n{r.stderr}")
+    if r.stderr.strip():
+        sys.stderr.write(r.stderr)
+    return obj
+
+
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
-    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")))
     workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with ThreadPoolExecutor(workers) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda f: _compile(f) if f.endswith(".hip") else _compile_host(f), srcs))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -52,6 +52,9 @@ const char *arfq_status_string(int status) {
     case ARFQ_E_DEVICE: return "HIP device error";
     case ARFQ_E_NOMEM: return "device out of memory";
     case ARFQ_E_UNSUPPORTED: return "unsupported";
+    case ARFQ_E_FORMAT: return "malformed GGUF file";
+    case ARFQ_E_IO: return "file I/O error";
+    case ARFQ_E_NOT_FOUND: return "no such tensor";
     default: return "unknown status";
     }
 }

@@ -152,6 +152,66 @@ def traffic_probe(ctx, copies):
         f"{TRAFFIC_PROBE_LAUNCHES} C2 GEMVs over {copies} weight copies")
 
 
+def gguf_reader_bench(ctx):
+    """GGUF reader: open (header + key/values + tensor table) and upload (host -> device copy
+    of the mapped blocks plus the device repack) of a synthetic model file."""
+    import shutil
+    import tempfile
+
+    import arf_amd
+    from arf_amd import synth
+    c5 = synth.CONFIGS["c5_moe"]
+    E, hid, inter = c5["experts"], c5["hidden"], c5["inter"]
+    specs = [("blk.0.ffn_gate_exps.weight", [hid, inter, E], inter, hid, E, 1),
+             ("blk.0.ffn_up_exps.weight", [hid, inter, E], inter, hid, E, 2),
+             ("blk.0.ffn_down_exps.weight", [inter, hid, E], hid, inter, E, 3),
+             ("blk.1.ffn_up.weight", [5120, 17408], 17408, 5120, 1, 4)]
+    vocab = [f"tok{i}" for i in range(151936)]
+    kvs = [("general.architecture", 8, "qwen3moe"), ("general.alignment", 4, 32),
+           ("tokenizer.ggml.tokens", 9, (8, vocab)),
+           ("tokenizer.ggml.token_type", 9, (5, [1] * len(vocab)))]
+    tensors = []
+    for name, dims, n, k, e, seed in specs:
+        nbytes = e * n * (k // 256) * 144
+        tensors.append((name, dims, 12, nbytes,
+                        lambda f, n=n, k=k, e=e, seed=seed: synth.weight("q4_k", n, k, seed, e).tofile(f)))
+    tmp = tempfile.mkdtemp(prefix="arfq_gguf_")
+    try:
+        path = os.path.join(tmp, "model.gguf")
+        synth.gguf_write(path, kvs, tensors)
+        size = os.path.getsize(path)
+        opens = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            g = arf_amd.Gguf(path)
+            opens.append((time.perf_counter() - t0) * 1e3)
+            g.close()
+        g = arf_amd.Gguf(path)
+        table_end = min(t.offset for t in g.tensors)
+        ups = {}
+        for rep in range(2):  # the first pass also reads the file into the page cache
+            for name, *_ in specs:
+                t0 = time.perf_counter()
+                w = ctx.upload_gguf(g, name)
+                ms = (time.perf_counter() - t0) * 1e3
+                nb = g.find(name).nbytes
+                ups[name] = {"bytes": nb, "ms": round(ms, 2), "GB/s": round(nb / ms / 1e6, 2)}
+                w.free()
+        g.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    total = sum(u["bytes"] for u in ups.values())
+    out = {"metric": "GGUF reader: table parse ms, upload GB/s (host page cache -> HBM)",
+           "value": round(total / sum(u["ms"] for u in ups.values()) / 1e6, 2), "unit": "GB/s",
+           "higher_is_better": True, "n_gpus": 1, "data": "synthetic GGUF v3 file",
+           "config": {"workload": "gguf_c5_experts_c2_matrix", "file_bytes": size,
+                      "header_bytes": table_end, "tensors": len(specs), "vocab_strings": len(vocab)},
+           "open_ms_median": round(sorted(opens)[len(opens) // 2], 3), "upload": ups}
+    log(f"[gguf] open {out['open_ms_median']} ms for a {table_end} B header; "
+        f"upload {out['value']} GB/s")
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -161,6 +221,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--gguf-reader", action="store_true",
+                    help="time the GGUF reader instead: open a synthetic model file (C5's expert "
+                         "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
+                         "prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
                          "calibration), then TRAFFIC_PROBE_LAUNCHES C2 GEMVs; prints no JSON")
@@ -175,6 +239,10 @@ def main():
     ctx = arf_amd.Context(0)
     if args.traffic_probe:
         traffic_probe(ctx, args.copies)
+        ctx.close()
+        return
+    if args.gguf_reader:
+        gguf_reader_bench(ctx)
         ctx.close()
         return
 

@@ -43,6 +43,9 @@ extern "C" {
 #define ARFQ_E_DEVICE -3    /* HIP runtime error */
 #define ARFQ_E_NOMEM -4     /* device allocation failed */
 #define ARFQ_E_UNSUPPORTED -5 /* valid request this build does not implement */
+#define ARFQ_E_FORMAT -6    /* file is not a well-formed GGUF v3 */
+#define ARFQ_E_IO -7        /* file cannot be opened or mapped */
+#define ARFQ_E_NOT_FOUND -8 /* no tensor of that name */
 
 /* ggml type ids, crates/arf-core/src/model/gguf.rs:36-90 (GgmlType). */
 typedef enum {
@@ -170,6 +173,49 @@ int arfq_timer_stop(arfq_ctx *ctx, float *ms);
  * a cache), all with the same x and y.  For timing loops only. */
 int arfq_matmul_repeat(arfq_ctx *ctx, const arfq_weight *const *ws, int n_ws, int iters,
                        int64_t m, const void *x, int x_dtype, float *y);
+
+/* ---- GGUF reader ---------------------------------------------------------
+ * A GGUF v3 file opened read-only and memory-mapped; tensors are read in place
+ * (LazyGguf, crates/arf-core/src/model/gguf.rs:365-564).  Errors of
+ * arfq_gguf_open are read with arfq_gguf_last_error(NULL); those of calls on an
+ * open file with arfq_gguf_last_error(g). */
+typedef struct arfq_gguf arfq_gguf;
+/* 1 when `path` is a regular file starting with the GGUF magic, else 0
+ * (is_gguf_file, gguf.rs:1115-1125). */
+int arfq_gguf_is_gguf(const char *path);
+/* Parse the header, the key/value section (general.alignment is kept, other
+ * values skipped) and the tensor table (LazyGguf::open_raw, gguf.rs:509-564;
+ * Reader::skip_value, gguf.rs:323-360).  Unknown ggml type ids fail the open
+ * as GgmlType::from_id does (gguf.rs:60-90).  ARFQ_E_IO / ARFQ_E_FORMAT. */
+int arfq_gguf_open(const char *path, arfq_gguf **out);
+int arfq_gguf_close(arfq_gguf *g);
+const char *arfq_gguf_last_error(const arfq_gguf *g);
+/* Tensor table: count, and entry `index` in file order (tensor_names,
+ * shape_raw, raw_ggml_type_id, gguf.rs:720-760,830-842).  dims are ggml's,
+ * fastest-varying first (up to max_dims are written); file_offset is absolute;
+ * nbytes is ggml_byte_len (gguf.rs:1678-1705).  Any out-pointer may be NULL. */
+int arfq_gguf_tensor_count(const arfq_gguf *g, int64_t *n);
+int arfq_gguf_tensor_info(const arfq_gguf *g, int64_t index, const char **name, int *ggml_type,
+                          int *n_dims, int64_t *dims, int max_dims, uint64_t *file_offset,
+                          uint64_t *nbytes);
+int arfq_gguf_find(const arfq_gguf *g, const char *name, int64_t *index);
+/* The raw blocks of tensor `name` when it is stored as ggml type `ggml_type`:
+ * a pointer into the mapping (valid until arfq_gguf_close), its byte length,
+ * rows = elements / ne0 and cols = ne0 (get_q4k_blocks_raw,
+ * get_q8_0_blocks_raw, gguf.rs:774-828; any type id).  ARFQ_E_UNSUPPORTED
+ * when stored as another type (the reference returns None). */
+int arfq_gguf_blocks(const arfq_gguf *g, const char *name, int ggml_type, const void **blocks,
+                     size_t *nbytes, int64_t *rows, int64_t *cols);
+/* Upload tensor `name` (Q8_0, Q4_K or Q6_K) as a weight:
+ *   - 2-D [ne0 = k, ne1 = n]: rows [row0, row0 + n_rows) (n_rows < 0: to the
+ *     end) as one matrix (the fused-qkv row slice, Entry::RowSlice,
+ *     gguf.rs:125-140); rows start on block boundaries because blocks run along
+ *     k;
+ *   - 3-D [ne0 = k, ne1 = n, ne2 = experts] (`*_exps`): every expert, in
+ *     order (index_experts, gguf.rs:1479-1523); row0 = 0, n_rows = -1 or ne1.
+ * k must be a whole number of blocks.  Synchronous, as arfq_weight_upload. */
+int arfq_gguf_upload(arfq_ctx *ctx, const arfq_gguf *g, const char *name, int64_t row0,
+                     int64_t n_rows, arfq_weight **out);
 
 #ifdef __cplusplus
 }
