@@ -40,6 +40,7 @@ class QType(enum.IntEnum):
     """ggml type ids (crates/arf-core/src/model/gguf.rs:36-90)."""
     Q8_0 = 8
     Q4_K = 12
+    Q5_K = 13
     Q6_K = 14
 
 
@@ -49,7 +50,8 @@ class DType(enum.IntEnum):
 
 
 # (weights per block, bytes per block): crates/arf-core/src/model/gguf.rs:1657-1673
-BLOCK = {QType.Q8_0: (32, 34), QType.Q4_K: (256, 144), QType.Q6_K: (256, 210)}
+BLOCK = {QType.Q8_0: (32, 34), QType.Q4_K: (256, 144), QType.Q6_K: (256, 210),
+         QType.Q5_K: (256, 176)}
 
 # the C ABI, by name -> (restype, argtypes); tests check every name is exported
 _vp = ctypes.c_void_p

@@ -61,6 +61,16 @@ __global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
     d[b] = (uint16_t)(src[208] | (src[209] << 8));
 }
 
+// Q5_K: the 16-byte header (d, dmin, scales) and ggml's qh[32] + qs[128] as they are.
+__global__ void repack_q5k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr,
+                           uint8_t *__restrict__ q, int64_t nblk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *src = raw + b * 176;
+    for (int i = 0; i < 16; i++) hdr[b * 16 + i] = src[i];
+    for (int i = 0; i < 160; i++) q[b * 160 + i] = src[16 + i];
+}
+
 hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s) {
     const int tpb = 256;
     const unsigned grid = (unsigned)((w->nblk + tpb - 1) / tpb);
@@ -74,6 +84,9 @@ hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s
     case ARFQ_Q6_K:
         repack_q6k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1,
                                         (uint16_t *)w->s2, w->nblk);
+        break;
+    case ARFQ_Q5_K:
+        repack_q5k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, w->nblk);
         break;
     default:
         return hipErrorInvalidValue;
@@ -129,6 +142,27 @@ __global__ void dequant_q6k(const uint32_t *__restrict__ qb, const int8_t *__res
     }
 }
 
+// One thread per (block, sub-block j): q = low / high nibble of qs[32 (j / 2) + i]
+// | bit j of qh[i] << 4, weight (d * sc) * q - dmin * m as Q4_K
+// (crates/arf-core/src/model/gguf.rs:2053-2090).
+__global__ void dequant_q5k(const uint4 *__restrict__ hdr, const uint8_t *__restrict__ q,
+                            float *__restrict__ out, int64_t nblk) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 8) return;
+    const int64_t b = t >> 3;
+    const int j = (int)(t & 7);
+    const uint4 h = hdr[b];
+    const float d = h2f(h.x), dmin = h2f(h.x >> 16);
+    uint32_t sc, m;
+    q4k_scale_min(h.y, h.z, h.w, j, sc, m);
+    const float d1 = q4k_d1(d, sc);
+    const float m1 = q4k_d1(dmin, m);
+    const uint8_t *qh = q + b * 160, *qs = qh + 32 + 32 * (j >> 1);
+    float *o = out + b * 256 + j * 32;
+    for (int i = 0; i < 32; i++)
+        o[i] = q4k_weight(d1, m1, ((qs[i] >> (4 * (j & 1))) & 0xFu) | (((qh[i] >> j) & 1u) << 4));
+}
+
 hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s) {
     const int tpb = 256;
     switch (w->qtype) {
@@ -142,6 +176,11 @@ hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s) {
         const unsigned grid = (unsigned)((w->nblk + tpb - 1) / tpb);
         dequant_q80<<<grid, tpb, 0, s>>>((const int8_t *)w->s0, (const uint16_t *)w->s1, out,
                                          w->nblk);
+        break;
+    }
+    case ARFQ_Q5_K: {
+        const unsigned grid = (unsigned)((w->nblk * 8 + tpb - 1) / tpb);
+        dequant_q5k<<<grid, tpb, 0, s>>>((const uint4 *)w->s0, (const uint8_t *)w->s1, out, w->nblk);
         break;
     }
     case ARFQ_Q6_K: {

@@ -510,7 +510,8 @@ __device__ __forceinline__ void xq6_process(const XqRound &r, int items, int bas
     }
 }
 
-// sum(q * X) of one 16-code quadrant: codes cw[4] (one byte each), planes lo/hi.
+// sum(q * X) of one 16-code quadrant: codes cw[4] (one byte each, q < 64),
+// planes lo/hi.
 __device__ __forceinline__ int q6k_subdot(const uint32_t *cw, const u32x4 lo, const u32x4 hi) {
     uint32_t a = __builtin_amdgcn_udot4(cw[0], lo.x, 0u, false);
     int b = __builtin_amdgcn_sdot4((int)cw[0], (int)hi.x, 0, false);
@@ -526,11 +527,144 @@ __device__ __forceinline__ int q6k_subdot(const uint32_t *cw, const u32x4 lo, co
 
 }  // namespace
 
-template <int MX, int XR>
-__global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
-    const uint8_t *__restrict__ qb, uint32_t qb_bytes, const uint8_t *__restrict__ scb,
-    uint32_t sc_bytes, const uint8_t *__restrict__ db, uint32_t d_bytes,
-    const float *__restrict__ x, float *__restrict__ y, int n, int nblk, int m) {
+// Formats of the byte-code dot GEMV.  Lane c (0..3) of a block's quad holds
+// 64 codes as four 16-code quadrants t; quadrant t's x elements start at
+// xbase(b, c) + XSTEP * t.  codes() builds the quadrant's code bytes, scales()
+// the per-quadrant factors, term() the quadrant's contribution from
+// sdot = sum(q * X) (X: x in 16-bit fixed point, scale xsc) and xsum = sum(x).
+//
+// Q6_K: lane c = 48-byte chunk c of the repacked block (ql_a | ql_b | qh, see
+// repack_q6k); q = ql nibble | qh bits << 4 (0..63); weight (d * sc) * (q - 32).
+struct DotQ6K {
+    const uint8_t *qb, *scb, *db;
+    uint32_t qb_bytes, sc_bytes, d_bytes;
+    struct Res {
+        __amdgpu_buffer_rsrc_t q, s, d;
+    };
+    struct Lane {
+        u32x4 q0, q1, q2;
+        uint32_t sw, dw;
+    };
+    static constexpr int XSTEP = 32;
+    __device__ Res res() const {
+        return {__builtin_amdgcn_make_buffer_rsrc((void *)qb, (short)0, (int)qb_bytes, 0x00020000),
+                __builtin_amdgcn_make_buffer_rsrc((void *)scb, (short)0, (int)sc_bytes, 0x00020000),
+                __builtin_amdgcn_make_buffer_rsrc((void *)db, (short)0, (int)d_bytes, 0x00020000)};
+    }
+    __device__ static void load(const Res &r, Lane &l, uint32_t blk, bool live, int c) {
+        const uint32_t oq = live ? blk * 192u + (uint32_t)c * 48u : Q4K_OOB;
+        l.q0 = __builtin_amdgcn_raw_buffer_load_b128(r.q, oq, 0, 2);
+        l.q1 = __builtin_amdgcn_raw_buffer_load_b128(r.q, oq + 16u, 0, 2);
+        l.q2 = __builtin_amdgcn_raw_buffer_load_b128(r.q, oq + 32u, 0, 2);
+        l.sw = __builtin_amdgcn_raw_buffer_load_b32(r.s, live ? blk * 16u + (uint32_t)c * 4u : Q4K_OOB, 0, 0);
+        l.dw = __builtin_amdgcn_raw_buffer_load_b16(r.d, live ? blk * 2u : Q4K_OOB, 0, 0);
+    }
+    __device__ static void expand(Lane &) {}
+    __device__ static int xbase(int b, int c) { return 256 * b + 128 * (c >> 1) + 16 * (c & 1); }
+    // scales 8 n2 + isub + 2t: bytes isub, isub + 2 of dwords 2 n2 and 2 n2 + 1 of
+    // the quad's scale dwords (all lanes take part in the DPP broadcasts)
+    __device__ static void scales(const Lane &l, int c, float A[4], float B[4]) {
+        const uint32_t s0 = quad_bcast<0>(l.sw), s1 = quad_bcast<1>(l.sw);
+        const uint32_t s2 = quad_bcast<2>(l.sw), s3 = quad_bcast<3>(l.sw);
+        const int n2 = c >> 1;
+        const uint32_t sa = n2 ? s2 : s0, sb = n2 ? s3 : s1;
+        const float d = h2f(l.dw);
+        const uint32_t sh = 8u * (uint32_t)(c & 1);
+        A[0] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh, 8);
+        A[1] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh + 16u, 8);
+        A[2] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh, 8);
+        A[3] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh + 16u, 8);
+        (void)B;
+    }
+    // quadrant t: ql_a / ql_b (t odd), low / high nibble (t >= 2), qh bits 2t..2t+1
+    __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
+        (void)c;
+        const uint32_t w[12] = {l.q0.x, l.q0.y, l.q0.z, l.q0.w, l.q1.x, l.q1.y,
+                                l.q1.z, l.q1.w, l.q2.x, l.q2.y, l.q2.z, l.q2.w};
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            cw[j] = ((w[4 * (t & 1) + j] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) |
+                    (((w[8 + j] >> (2 * t)) << 4) & 0x30303030u);
+    }
+    __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
+        (void)B;
+        return A * (xsc * (float)sdot - 32.f * xsum);
+    }
+};
+
+// Q5_K: streams hdr (d, dmin, the 12 scale bytes: 16 B per block) and q
+// (ggml's qh[32] then qs[128]: 160 B).  Lane c takes sub-blocks 2c (low
+// nibbles of qs[32c + l]) and 2c + 1 (high nibbles), the 5th bits in qh[l] bits
+// 2c and 2c + 1; quadrant t = sub-block 2c + t / 2, elements 16 (t % 2) ..+15.
+// Each lane loads its own 32 qs bytes, a quarter of qh (bytes 8c..8c+7) and
+// header dword c; expand() gathers the whole qh and header of the block from
+// the quad by DPP, so no byte is loaded twice.  q = nibble | bit << 4 (0..31);
+// weight (d * sc) * q - dmin * m (crates/arf-core/src/model/gguf.rs:2053-2090).
+struct DotQ5K {
+    const uint8_t *hdr, *q;
+    uint32_t hdr_bytes, q_bytes;
+    struct Res {
+        __amdgpu_buffer_rsrc_t h, q;
+    };
+    struct Lane {
+        u32x4 qs0, qs1;
+        u32x2 qh;
+        uint32_t hw;
+        uint32_t qhd[8], hd[4];  // filled by expand()
+    };
+    static constexpr int XSTEP = 16;
+    __device__ Res res() const {
+        return {__builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)hdr_bytes, 0x00020000),
+                __builtin_amdgcn_make_buffer_rsrc((void *)q, (short)0, (int)q_bytes, 0x00020000)};
+    }
+    __device__ static void load(const Res &r, Lane &l, uint32_t blk, bool live, int c) {
+        const uint32_t oq = live ? blk * 160u : Q4K_OOB;
+        l.qs0 = __builtin_amdgcn_raw_buffer_load_b128(r.q, oq + 32u + 32u * (uint32_t)c, 0, 2);
+        l.qs1 = __builtin_amdgcn_raw_buffer_load_b128(r.q, oq + 48u + 32u * (uint32_t)c, 0, 2);
+        l.qh = __builtin_amdgcn_raw_buffer_load_b64(r.q, oq + 8u * (uint32_t)c, 0, 2);
+        l.hw = __builtin_amdgcn_raw_buffer_load_b32(r.h, live ? blk * 16u + 4u * (uint32_t)c : Q4K_OOB, 0, 0);
+    }
+    __device__ static void expand(Lane &l) {
+        l.qhd[0] = quad_bcast<0>(l.qh.x), l.qhd[1] = quad_bcast<0>(l.qh.y);
+        l.qhd[2] = quad_bcast<1>(l.qh.x), l.qhd[3] = quad_bcast<1>(l.qh.y);
+        l.qhd[4] = quad_bcast<2>(l.qh.x), l.qhd[5] = quad_bcast<2>(l.qh.y);
+        l.qhd[6] = quad_bcast<3>(l.qh.x), l.qhd[7] = quad_bcast<3>(l.qh.y);
+        l.hd[0] = quad_bcast<0>(l.hw), l.hd[1] = quad_bcast<1>(l.hw);
+        l.hd[2] = quad_bcast<2>(l.hw), l.hd[3] = quad_bcast<3>(l.hw);
+    }
+    __device__ static int xbase(int b, int c) { return 256 * b + 64 * c; }
+    // the 6-bit (sc, m) of sub-blocks 2c and 2c + 1 (q4k_scale_min without a
+    // per-lane branch)
+    __device__ static void scales(const Lane &l, int c, float A[4], float B[4]) {
+        const float d = h2f(l.hd[0]), dmin = h2f(l.hd[0] >> 16);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int j = 2 * c + u, i = j & 3;
+            const uint32_t a = byte_of(l.hd[1], i), bb = byte_of(l.hd[2], i), cc = byte_of(l.hd[3], i);
+            const uint32_t sc = j < 4 ? (a & 63u) : ((cc & 0xFu) | ((a >> 6) << 4));
+            const uint32_t m = j < 4 ? (bb & 63u) : ((cc >> 4) | ((bb >> 6) << 4));
+            A[2 * u] = A[2 * u + 1] = d * (float)sc;
+            B[2 * u] = B[2 * u + 1] = dmin * (float)m;
+        }
+    }
+    // quadrant t: qs bytes 16 (t % 2) + 4j ..+3 and qh dword 4 (t % 2) + j
+    __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
+        const int nib = t >> 1;
+        const u32x4 qs = (t & 1) ? l.qs1 : l.qs0;
+        const uint32_t hs = (uint32_t)(2 * c + nib);
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            cw[j] = ((qs[j] >> (4 * nib)) & 0x0F0F0F0Fu) | (((l.qhd[4 * (t & 1) + j] >> hs) & 0x01010101u) << 4);
+    }
+    __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
+        return A * (xsc * (float)sdot) - B * xsum;
+    }
+};
+
+template <class F, int MX, int XR>
+__global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot(F fmt, const float *__restrict__ x,
+                                                            float *__restrict__ y, int n, int nblk,
+                                                            int m) {
     constexpr bool XREG = MX == 1;
     constexpr int C = Q6K_GEMV_CHUNK, PF = Q6K_GEMV_PF;
     static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
@@ -543,16 +677,11 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
     float *xe = s16 + (size_t)MX * (k / 16);
     float *part = xe + (size_t)MX * (k / 32);  // [MX][R][spr]
 
-    const __amdgpu_buffer_rsrc_t qrs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)qb, (short)0, (int)qb_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t srs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)scb, (short)0, (int)sc_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t drs =
-        __builtin_amdgcn_make_buffer_rsrc((void *)db, (short)0, (int)d_bytes, 0x00020000);
+    const typename F::Res res = fmt.res();
 
     const int tid = threadIdx.x;
     const int l16 = tid & 15, grp = tid >> 4;
-    const int bq = l16 >> 2, c = l16 & 3, n2 = c >> 1, isub = c & 1;
+    const int bq = l16 >> 2, c = l16 & 3;
 
     const int G = gridDim.x;
     const int r0 = (int)((int64_t)blockIdx.x * n / G);
@@ -567,8 +696,7 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
         icol = kc < nchunks ? kc / cpc : spr;
         irow = (kc - icol * cpc) * C;
     };
-    u32x4 q0[PF], q1[PF], q2[PF];
-    uint32_t sw[PF], dw[PF];
+    typename F::Lane ld[PF];
     int srow[PF], scol[PF];
     auto issue = [&](int u, bool first) {
         if (u % C == 0) {
@@ -584,12 +712,7 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
         const int b = 4 * icol + bq;
         const bool live = icol < spr && irow < R && b < nblk;
         const uint32_t blk = (uint32_t)(r0 + irow) * (uint32_t)nblk + (uint32_t)b;
-        const uint32_t oq = live ? blk * 192u + (uint32_t)c * 48u : Q4K_OOB;
-        q0[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oq, 0, 2);
-        q1[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oq + 16u, 0, 2);
-        q2[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oq + 32u, 0, 2);
-        sw[u] = __builtin_amdgcn_raw_buffer_load_b32(srs, live ? blk * 16u + (uint32_t)c * 4u : Q4K_OOB, 0, 0);
-        dw[u] = __builtin_amdgcn_raw_buffer_load_b16(drs, live ? blk * 2u : Q4K_OOB, 0, 0);
+        F::load(res, ld[u], blk, live, c);
         srow[u] = irow;
         scol[u] = icol;
     };
@@ -615,20 +738,21 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
     }
 
     // x of the column being consumed: the lane's 4 quadrants (elements
-    // 256 b + 128 n2 + 16 isub + 32 t .. + 15)
+    // xbase + XSTEP t .. + 15)
     int xcol = -1, xbase = 0;
     u32x4 XL[4], XH[4];
     float XS[4], XE[4];
     auto load_x = [&](int col) {
         xcol = col;
-        xbase = min(4 * col + bq, nblk - 1) * 256 + 128 * n2 + 16 * isub;
+        xbase = F::xbase(min(4 * col + bq, nblk - 1), c);
         if (XREG) {
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                XL[t] = *reinterpret_cast<const u32x4 *>(xlo + xbase + 32 * t);
-                XH[t] = *reinterpret_cast<const u32x4 *>(xhi + xbase + 32 * t);
-                XS[t] = s16[(xbase >> 4) + 2 * t];
-                XE[t] = xe[(xbase >> 5) + t];
+                const int eo = xbase + F::XSTEP * t;
+                XL[t] = *reinterpret_cast<const u32x4 *>(xlo + eo);
+                XH[t] = *reinterpret_cast<const u32x4 *>(xhi + eo);
+                XS[t] = s16[eo >> 4];
+                XE[t] = xe[eo >> 5];
             }
         }
     };
@@ -637,31 +761,17 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
         const int col = scol[u], row = srow[u];
         const bool live = col < spr && row < R;
         if (live && col != xcol) load_x(col);
-        // scales 8 n2 + isub + 2t: bytes isub, isub + 2 of dwords 2 n2 and 2 n2 + 1
-        const uint32_t s0 = quad_bcast<0>(sw[u]), s1 = quad_bcast<1>(sw[u]);
-        const uint32_t s2 = quad_bcast<2>(sw[u]), s3 = quad_bcast<3>(sw[u]);
-        const uint32_t sa = n2 ? s2 : s0, sb = n2 ? s3 : s1;
-        const float d = h2f(dw[u]);
-        const uint32_t sh = 8u * (uint32_t)isub;
-        float dsc[4];
-        dsc[0] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh, 8);
-        dsc[1] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh + 16u, 8);
-        dsc[2] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh, 8);
-        dsc[3] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh + 16u, 8);
-        const uint32_t w[12] = {q0[u].x, q0[u].y, q0[u].z, q0[u].w, q1[u].x, q1[u].y,
-                                q1[u].z, q1[u].w, q2[u].x, q2[u].y, q2[u].z, q2[u].w};
+        F::expand(ld[u]);  // DPP: every lane, live or not
+        float A[4], B[4];
+        F::scales(ld[u], c, A, B);
 #pragma unroll
         for (int mi = 0; mi < MX; mi++) {
             if (MX == 1 || mi < m) {
                 float v = 0.f;
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
-                    // quadrant t: ql_a / ql_b (t odd), low / high nibble (t >= 2), qh bits 2t..2t+1
                     uint32_t cw[4];
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        cw[j] = ((w[4 * (t & 1) + j] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) |
-                                (((w[8 + j] >> (2 * t)) << 4) & 0x30303030u);
+                    F::codes(ld[u], c, t, cw);
                     int sdot;
                     float xsum, xsc;
                     if (XREG) {
@@ -669,13 +779,13 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_q6k_dot(
                         xsum = XS[t];
                         xsc = XE[t];
                     } else {
-                        const size_t eo = (size_t)mi * k + xbase + 32 * t;
+                        const size_t eo = (size_t)mi * k + xbase + F::XSTEP * t;
                         sdot = q6k_subdot(cw, *reinterpret_cast<const u32x4 *>(xlo + eo),
                                           *reinterpret_cast<const u32x4 *>(xhi + eo));
                         xsum = s16[eo >> 4];
                         xsc = xe[eo >> 5];
                     }
-                    v += dsc[t] * (xsc * (float)sdot - 32.f * xsum);
+                    v += F::term(A[t], B[t], xsc, sdot, xsum);
                 }
                 v = row16_sum(v);
                 if (l16 == 0 && live) part[((size_t)mi * R + row) * spr + col] = v;
@@ -839,10 +949,17 @@ __global__ __launch_bounds__(64) void gemv_q6k(const uint4 *__restrict__ qb,
 constexpr int GEMV_MAX_M = 4;
 
 static size_t q4k_gemv_lds(const arfq_weight *w, int mx);
-static size_t q6k_dot_lds(const arfq_weight *w, int mx);
-static bool q6k_dot_ok(const arfq_weight *w, int64_t m) {
-    return m <= 2 && q6k_dot_lds(w, (int)m) <= 64 * 1024 &&
-           w->n * (w->k / 256) * 192 < (int64_t)Q4K_OOB;
+static size_t dot_lds(const arfq_weight *w, int mx);
+// the byte-code dot GEMV: Q6_K at m <= 2, Q5_K at m <= 4, while x fits in LDS and
+// one expert's streams fit 31-bit buffer offsets
+static int dot_mx(int64_t m) { return m <= 2 ? (int)m : 4; }
+static bool dot_ok(const arfq_weight *w, int64_t m) {
+    const int64_t nb = w->n * (w->k / 256);
+    if (w->qtype == ARFQ_Q6_K)
+        return m <= 2 && dot_lds(w, (int)m) <= 64 * 1024 && nb * 192 < (int64_t)Q4K_OOB;
+    if (w->qtype == ARFQ_Q5_K)
+        return m <= 4 && dot_lds(w, dot_mx(m)) <= 64 * 1024 && nb * 160 < (int64_t)Q4K_OOB;
+    return false;
 }
 
 bool gemv_supports(const arfq_weight *w, int64_t m) {
@@ -851,6 +968,7 @@ bool gemv_supports(const arfq_weight *w, int64_t m) {
     if (w->qtype == ARFQ_Q4_K)
         return q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
                w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
+    if (w->qtype == ARFQ_Q5_K) return dot_ok(w, m);
     return w->qtype == ARFQ_Q8_0 || w->qtype == ARFQ_Q6_K;
 }
 
@@ -905,32 +1023,40 @@ static int64_t gemv_grid(const arfq_weight *w, int groups) {
     grid = std::min<int64_t>(grid, w->n);
     return grid < 1 ? 1 : grid;
 }
-static size_t q6k_dot_lds(const arfq_weight *w, int mx) {
+static size_t dot_lds(const arfq_weight *w, int mx) {
     const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
     const int64_t grid = gemv_grid(w, Q6K_GEMV_GROUPS);
     const int64_t rows = (w->n + grid - 1) / grid;
     return (size_t)mx * w->k * 2 + (size_t)mx * (w->k / 16) * 4 + (size_t)mx * (w->k / 32) * 4 +
            (size_t)mx * rows * spr * 4;
 }
-template <int MX, int XR>
-static hipError_t launch_q6k_dot_t(const arfq_weight *w, int e, int m, const float *x, float *y,
-                                   hipStream_t s) {
-    const int n = (int)w->n, nblk = (int)(w->k / 256);
-    const int64_t nb = w->n * nblk;
-    const int64_t eb = (int64_t)e * nb;
+// the streams of expert e
+static DotQ6K dot_q6k(const arfq_weight *w, int e) {
+    const int64_t nb = w->n * (w->k / 256), eb = (int64_t)e * nb;
+    return {(const uint8_t *)w->s0 + eb * 192, (const uint8_t *)w->s1 + eb * 16,
+            (const uint8_t *)w->s2 + eb * 2, (uint32_t)(nb * 192), (uint32_t)(nb * 16),
+            (uint32_t)(nb * 2)};
+}
+static DotQ5K dot_q5k(const arfq_weight *w, int e) {
+    const int64_t nb = w->n * (w->k / 256), eb = (int64_t)e * nb;
+    return {(const uint8_t *)w->s0 + eb * 16, (const uint8_t *)w->s1 + eb * 160, (uint32_t)(nb * 16),
+            (uint32_t)(nb * 160)};
+}
+template <class F, int MX, int XR>
+static hipError_t launch_dot_t(const F &fmt, const arfq_weight *w, int m, const float *x, float *y,
+                               hipStream_t s) {
     const int64_t grid = gemv_grid(w, Q6K_GEMV_GROUPS);
-    gemv_q6k_dot<MX, XR><<<(unsigned)grid, Q6K_GEMV_THREADS, q6k_dot_lds(w, MX), s>>>(
-        (const uint8_t *)w->s0 + eb * 192, (uint32_t)(nb * 192), (const uint8_t *)w->s1 + eb * 16,
-        (uint32_t)(nb * 16), (const uint8_t *)w->s2 + eb * 2, (uint32_t)(nb * 2), x, y, n, nblk, m);
+    gemv_dot<F, MX, XR><<<(unsigned)grid, Q6K_GEMV_THREADS, dot_lds(w, MX), s>>>(
+        fmt, x, y, (int)w->n, (int)(w->k / 256), m);
     return hipGetLastError();
 }
-template <int MX>
-static hipError_t launch_q6k_dot(const arfq_weight *w, int e, int m, const float *x, float *y,
-                                 hipStream_t s) {
+template <class F, int MX>
+static hipError_t launch_dot(const F &fmt, const arfq_weight *w, int m, const float *x, float *y,
+                             hipStream_t s) {
     const int64_t rounds = ((int64_t)m * (w->k / 8) + Q6K_GEMV_THREADS - 1) / Q6K_GEMV_THREADS;
-    if (rounds <= 1) return launch_q6k_dot_t<MX, 1>(w, e, m, x, y, s);
-    if (rounds <= 2) return launch_q6k_dot_t<MX, 2>(w, e, m, x, y, s);
-    return launch_q6k_dot_t<MX, 4>(w, e, m, x, y, s);
+    if (rounds <= 1) return launch_dot_t<F, MX, 1>(fmt, w, m, x, y, s);
+    if (rounds <= 2) return launch_dot_t<F, MX, 2>(fmt, w, m, x, y, s);
+    return launch_dot_t<F, MX, 4>(fmt, w, m, x, y, s);
 }
 static size_t q4k_gemv_lds(const arfq_weight *w, int mx) {
     const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
@@ -972,8 +1098,16 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
         if (m == 2) return launch_gemv_q4k<2>(w, e, 2, x, y, s);
         return launch_gemv_q4k<4>(w, e, (int)m, x, y, s);
     }
-    if (w->qtype == ARFQ_Q6_K && q6k_dot_ok(w, m))
-        return m == 1 ? launch_q6k_dot<1>(w, e, 1, x, y, s) : launch_q6k_dot<2>(w, e, 2, x, y, s);
+    if (w->qtype == ARFQ_Q5_K) {
+        const DotQ5K f = dot_q5k(w, e);
+        if (m == 1) return launch_dot<DotQ5K, 1>(f, w, 1, x, y, s);
+        if (m == 2) return launch_dot<DotQ5K, 2>(f, w, 2, x, y, s);
+        return launch_dot<DotQ5K, 4>(f, w, (int)m, x, y, s);
+    }
+    if (w->qtype == ARFQ_Q6_K && dot_ok(w, m)) {
+        const DotQ6K f = dot_q6k(w, e);
+        return m == 1 ? launch_dot<DotQ6K, 1>(f, w, 1, x, y, s) : launch_dot<DotQ6K, 2>(f, w, 2, x, y, s);
+    }
     if (m == 1) return launch_gemv_t<4, 1>(w, e, 1, x, y, s);
     if (m == 2) return launch_gemv_t<4, 2>(w, e, 2, x, y, s);
     return launch_gemv_t<2, 4>(w, e, (int)m, x, y, s);

@@ -5,6 +5,8 @@ Block contents follow the generation rules the benchmark is quoted on:
   Q4_K  d, dmin = f16(|N(0,1)| * 0.01), 12 scale bytes and 128 qs bytes uniform
   Q6_K  ql[128], qh[64] uniform bytes, 16 i8 scales uniform in [-32, 31],
         d = f16(|N(0,1)| * 0.005)
+  Q5_K  as Q4_K, plus 32 uniform bytes of 5th bits (no benchmark config; the
+        survey's next row)
 f16 rounding is IEEE round-to-nearest-even with subnormals kept (numpy).
 Everything is drawn from numpy's PCG64 seeded per call, so the CPU oracle and
 the GPU read the same bytes.  gguf_write() lays such tensors out as a GGUF v3
@@ -14,8 +16,8 @@ import struct
 
 import numpy as np
 
-BLOCK_BYTES = {"q8_0": 34, "q4_k": 144, "q6_k": 210}
-QK = {"q8_0": 32, "q4_k": 256, "q6_k": 256}
+BLOCK_BYTES = {"q8_0": 34, "q4_k": 144, "q6_k": 210, "q5_k": 176}
+QK = {"q8_0": 32, "q4_k": 256, "q6_k": 256, "q5_k": 256}
 
 
 def _f16_bytes(v):
@@ -45,7 +47,16 @@ def q6_k_blocks(rng, nblk):
     return out
 
 
-_GEN = {"q8_0": q8_0_blocks, "q4_k": q4_k_blocks, "q6_k": q6_k_blocks}
+def q5_k_blocks(rng, nblk):
+    """Q5_K as Q4_K (d, dmin, scale bytes) plus 32 uniform bytes of 5th bits."""
+    out = np.empty((nblk, 176), np.uint8)
+    out[:, 0:2] = _f16_bytes(np.abs(rng.standard_normal(nblk)) * 0.01)
+    out[:, 2:4] = _f16_bytes(np.abs(rng.standard_normal(nblk)) * 0.01)
+    out[:, 4:176] = rng.integers(0, 256, size=(nblk, 172), dtype=np.uint8)
+    return out
+
+
+_GEN = {"q8_0": q8_0_blocks, "q4_k": q4_k_blocks, "q6_k": q6_k_blocks, "q5_k": q5_k_blocks}
 
 
 def weight(qtype, n, k, seed, experts=1):

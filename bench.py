@@ -41,7 +41,7 @@ def algorithmic_bytes(qtype, m, n, k, x_bytes=4):
 def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.float32):
     """Average ms per launch of arfq_matmul over `steps` launches rotating `copies` weights."""
     from arf_amd import QType, synth
-    qt = {"q4_k": QType.Q4_K, "q6_k": QType.Q6_K, "q8_0": QType.Q8_0}[qtype]
+    qt = QType[qtype.upper()]
     raw = synth.weight(qtype, n, k, seed=seed)
     ws = [ctx.upload(qt, raw, n, k) for _ in range(copies)]
     x = ctx.to_device(synth.activations(m, k, seed=seed + 1).astype(x_dtype))
@@ -277,6 +277,16 @@ def main():
                 "us_per_launch": round(ms3 * 1e3, 3), "GB/s": round(b3 / ms3 / 1e6, 1),
                 "hbm_frac": round(b3 / ms3 / 1e6 / HBM_PEAK_GBS, 4)}
             log(f"[bench] C3 m={mm}: {ms3 * 1e3:.2f} us/launch")
+        # Q5_K GEMV at C2's shape: the survey's next row (no benchmark config of its own)
+        try:
+            ms5k, _ = time_matmul(ctx, "q5_k", 1, 17408, 5120, steps2, 50, 6, seed=0xA7F00005)
+            b5k = algorithmic_bytes("q5_k", 1, 17408, 5120)
+            configs["q5_k_gemv_m1_k5120_n17408"] = {
+                "us_per_launch": round(ms5k * 1e3, 3), "GB/s": round(b5k / ms5k / 1e6, 1),
+                "hbm_frac": round(b5k / ms5k / 1e6 / HBM_PEAK_GBS, 4)}
+            log(f"[bench] Q5_K m=1 (C2 shape): {ms5k * 1e3:.2f} us/launch")
+        except arf_amd.ArfqError as e:
+            configs["q5_k_gemv_m1_k5120_n17408"] = {"error": str(e)}
         # C4 Q4_K prefill GEMM
         try:
             ms4, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, 30, 10, 2, seed=0xA7F00004,

@@ -51,6 +51,8 @@ extern "C" {
 typedef enum {
     ARFQ_Q8_0 = 8,  /* 34 B per 32 weights: f16 d, 32 x i8 */
     ARFQ_Q4_K = 12, /* 144 B per 256 weights: f16 d, f16 dmin, 12 B 6-bit scales/mins, 128 B nibbles */
+    ARFQ_Q5_K = 13, /* 176 B per 256 weights: Q4_K's d, dmin, scales, then qh[32] 5th bits, qs[128];
+                       decode GEMV (m <= 4) and dequant only */
     ARFQ_Q6_K = 14  /* 210 B per 256 weights: ql[128], qh[64], i8 scales[16], f16 d */
 } arfq_qtype;
 
@@ -206,7 +208,7 @@ int arfq_gguf_find(const arfq_gguf *g, const char *name, int64_t *index);
  * when stored as another type (the reference returns None). */
 int arfq_gguf_blocks(const arfq_gguf *g, const char *name, int ggml_type, const void **blocks,
                      size_t *nbytes, int64_t *rows, int64_t *cols);
-/* Upload tensor `name` (Q8_0, Q4_K or Q6_K) as a weight:
+/* Upload tensor `name` (Q8_0, Q4_K, Q5_K or Q6_K) as a weight:
  *   - 2-D [ne0 = k, ne1 = n]: rows [row0, row0 + n_rows) (n_rows < 0: to the
  *     end) as one matrix (the fused-qkv row slice, Entry::RowSlice,
  *     gguf.rs:125-140); rows start on block boundaries because blocks run along

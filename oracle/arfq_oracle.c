@@ -143,6 +143,69 @@ void arfo_dequant_q6_k(const uint8_t *bytes, int64_t n, float *out) {
     }
 }
 
+/* ---- next row f2: Q5_K dequant.  crates/arf-core/src/model/gguf.rs:2053-2090.
+ * Block = 176 B: f16 d, f16 dmin, scales[12] (Q4_K packing), qh[32] (the 5th bit),
+ * qs[128] (low nibbles).  Group g (64 weights): sub-blocks 2g (low nibbles of
+ * qs[32g + l], 5th bit qh[l] & (1 << 2g)) and 2g + 1 (high nibbles, 5th bit
+ * qh[l] & (2 << 2g)); y = d1 * q - m1 with d1 = d * sc, m1 = dmin * m. */
+void arfo_dequant_q5_k(const uint8_t *bytes, int64_t n, float *out) {
+    int64_t nblocks = n / QK_K;
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t *p = bytes + b * 176;
+        float d = arfo_f16_to_f32(rd16(p));
+        float dmin = arfo_f16_to_f32(rd16(p + 2));
+        const uint8_t *scales = p + 4, *qh = p + 16, *qs = p + 48;
+        float *o = out + b * QK_K;
+        for (int g = 0; g < 4; g++) {
+            uint8_t sc1, m1, sc2, m2;
+            arfo_q4k_get_scale_min(scales, 2 * g, &sc1, &m1);
+            arfo_q4k_get_scale_min(scales, 2 * g + 1, &sc2, &m2);
+            float d1 = d * (float)sc1, mm1 = dmin * (float)m1;
+            float d2 = d * (float)sc2, mm2 = dmin * (float)m2;
+            uint8_t u1 = (uint8_t)(1u << (2 * g)), u2 = (uint8_t)(2u << (2 * g));
+            for (int l = 0; l < 32; l++) {
+                float q = (float)(qs[32 * g + l] & 0xF) + ((qh[l] & u1) ? 16.0f : 0.0f);
+                o[64 * g + l] = d1 * q - mm1;
+            }
+            for (int l = 0; l < 32; l++) {
+                float q = (float)(qs[32 * g + l] >> 4) + ((qh[l] & u2) ? 16.0f : 0.0f);
+                o[64 * g + 32 + l] = d2 * q - mm2;
+            }
+        }
+    }
+}
+
+/* Q5KSMatrix::from_ggml_q5k (crates/arf-ml/src/weight.rs:551-632): low nibbles 8 per
+ * u32 in element order, the 5th bit 32 per u32 (bit 1 << ss of qh[i] for sub-block
+ * ss, element i), sub-block scales u8, mins -m as i8, d / dmin widened to f32. */
+void arfo_q5ks_from_ggml(const uint8_t *blocks, int64_t rows, int64_t cols, uint32_t *codes_lo,
+                         uint32_t *codes_hi, uint8_t *scales, int8_t *mins, float *d, float *dmin) {
+    int64_t spr = cols / 32, bpr = cols / QK_K;
+    memset(codes_lo, 0, (size_t)(rows * cols / 8) * 4);
+    memset(codes_hi, 0, (size_t)(rows * cols / 32) * 4);
+    for (int64_t r = 0; r < rows; r++)
+        for (int64_t sb = 0; sb < bpr; sb++) {
+            const uint8_t *p = blocks + (r * bpr + sb) * 176;
+            d[r * bpr + sb] = arfo_f16_to_f32(rd16(p));
+            dmin[r * bpr + sb] = arfo_f16_to_f32(rd16(p + 2));
+            const uint8_t *qh = p + 16, *qs = p + 48;
+            for (int ss = 0; ss < 8; ss++) {
+                uint8_t sc, m;
+                arfo_q4k_get_scale_min(p + 4, ss, &sc, &m);
+                scales[r * spr + sb * 8 + ss] = sc;
+                mins[r * spr + sb * 8 + ss] = (int8_t)(-(int)m);
+                int shift = (ss % 2) ? 4 : 0;
+                for (int i = 0; i < 32; i++) {
+                    uint32_t lo = (uint32_t)((qs[(ss / 2) * 32 + i] >> shift) & 0xF);
+                    uint32_t hi = (qh[i] >> ss) & 1u;
+                    int64_t pos = r * cols + sb * QK_K + ss * 32 + i;
+                    codes_lo[pos / 8] |= lo << ((pos % 8) * 4);
+                    codes_hi[pos / 32] |= hi << (pos % 32);
+                }
+            }
+        }
+}
+
 /* ---- a6: lossless ggml Q4_K -> Q4_K_S transcode.
  *      crates/arf-ml/src/weight.rs:1000-1080 (from_ggml_q4k) ---------------- */
 void arfo_q4ks_from_ggml(const uint8_t *blocks, int64_t rows, int64_t cols, uint32_t *codes,
@@ -388,6 +451,17 @@ void arfo_matmul_nt_q6_k(const float *a, int64_t m, int64_t k, const uint8_t *bl
                          float *out) {
     float *w = (float *)malloc((size_t)(n * k) * 4);
     arfo_dequant_q6_k(blocks, n * k, w);
+    arfo_matmul_nt(a, m, k, w, n, out);
+    free(w);
+}
+
+/* Q5_K reference matmul: dequant_q5_k then matmul_nt (the CPU path reads a Q5_K
+ * tensor through its f32 dequant; crates/arf-core/src/model/gguf.rs:2053-2090 then
+ * matmul.rs:84-99). */
+void arfo_matmul_nt_q5_k(const float *a, int64_t m, int64_t k, const uint8_t *blocks, int64_t n,
+                         float *out) {
+    float *w = (float *)malloc((size_t)(n * k) * 4);
+    arfo_dequant_q5_k(blocks, n * k, w);
     arfo_matmul_nt(a, m, k, w, n, out);
     free(w);
 }

@@ -73,6 +73,27 @@ def q6k_exact(d, sc, q):
     return [D * sc[e // 16] * (q[e] - 32) for e in range(256)]
 
 
+def make_q5k_block(d, dmin, sc, m, q):
+    """q: 256 five-bit codes in element order.  Element e = 32*j + i (sub-block j):
+    low nibble in qs[32*(j//2) + i] (low half for even j, high for odd j), the 5th
+    bit in qh[i] bit j (block_q5_K, crates/arf-core/src/model/gguf.rs:2053-2090)."""
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([f16_bits(d)], np.uint16).view(np.uint8)
+    b[2:4] = np.array([f16_bits(dmin)], np.uint16).view(np.uint8)
+    b[4:16] = pack_q4k_scales(sc, m)
+    for e in range(256):
+        j, i = divmod(e, 32)
+        b[48 + 32 * (j // 2) + i] |= (q[e] & 0xF) << (4 * (j % 2))
+        b[16 + i] |= (q[e] >> 4) << j
+    return b
+
+
+def q5k_exact(d, dmin, sc, m, q):
+    """Exact weights d*sc*q - dmin*m as Fractions (d, dmin f16-representable)."""
+    D, M = Fraction(float(np.float16(d))), Fraction(float(np.float16(dmin)))
+    return [D * sc[e // 32] * q[e] - M * m[e // 32] for e in range(256)]
+
+
 def make_q80_block(d, q):
     b = np.zeros(34, np.uint8)
     b[0:2] = np.array([f16_bits(d)], np.uint16).view(np.uint8)

@@ -10,9 +10,9 @@ import numpy as np
 import pytest
 
 from conftest import rel_err
-from formats import (lcg_q4k_blocks, make_q4k_block, make_q6k_block, make_q80_block,
-                     moe_route_lcg_logits, pack_q4k_scales, q4k_exact, q6k_exact,
-                     ref_make_q4k_block)
+from formats import (f16_bits, lcg_q4k_blocks, make_q4k_block, make_q5k_block, make_q6k_block,
+                     make_q80_block, moe_route_lcg_logits, pack_q4k_scales, q4k_exact, q5k_exact,
+                     q6k_exact, ref_make_q4k_block)
 
 
 # ---------------------------------------------------------------- f16 ----
@@ -157,6 +157,65 @@ def test_dequant_q6k_each_quadrant_and_qh_pair(oracle):
 
 
 # ------------------------------------------------------------ Q8_0 dequant ----
+def test_dequant_q5k_known_block(oracle):
+    # dequant_q5_k_known_block (gguf.rs:2541-2561): d=2, dmin=1, sc0=3, m0=5, q0=4 -> 19;
+    # with the 5th bit of weight 0 set, q0 = 20 -> 115
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([f16_bits(2.0)], np.uint16).view(np.uint8)
+    b[2:4] = np.array([f16_bits(1.0)], np.uint16).view(np.uint8)
+    b[4], b[8], b[48] = 3, 5, 0x04
+    assert oracle.dequant("q5_k", b, 256)[0] == 19.0
+    b[16] = 0x01
+    assert oracle.dequant("q5_k", b, 256)[0] == 115.0
+
+
+def test_dequant_q5k_exact_forward_packing(oracle):
+    # the dequant is exact here (d, dmin powers of two, products exact in f32)
+    rng = np.random.default_rng(17)
+    for trial in range(40):
+        d, dmin = 2.0 ** int(rng.integers(-10, 1)), 2.0 ** int(rng.integers(-10, 1))
+        sc, m = rng.integers(0, 64, 8).tolist(), rng.integers(0, 64, 8).tolist()
+        q = rng.integers(0, 32, 256).tolist()
+        got = oracle.dequant("q5_k", make_q5k_block(d, dmin, sc, m, q), 256)
+        want = np.array([float(v) for v in q5k_exact(d, dmin, sc, m, q)], np.float64)
+        assert np.array_equal(got.astype(np.float64), want), trial
+
+
+def test_dequant_q5k_each_high_bit_lands_on_its_weight(oracle):
+    # one 5th bit at a time: a transposed qh read puts it on another weight
+    for e in range(256):
+        q = [0] * 256
+        q[e] = 16
+        got = oracle.dequant("q5_k", make_q5k_block(1.0, 0.0, [1] * 8, [0] * 8, q), 256)
+        want = np.zeros(256)
+        want[e] = 16.0
+        assert np.array_equal(got, want), e
+
+
+def test_q5k_native_unpack_matches_dequant(oracle):
+    # q5k_native_unpack_matches_the_reference_dequantizer (crates/arf-core/tests/q5k_native.rs):
+    # the same deterministic bytes, rebuilt from the Q5KS unpack, against dequant_q5_k
+    rows, cols = 2, 512
+    nb = rows * cols // 256
+    b = np.zeros(nb * 176, np.uint8)
+    for blk in range(nb):
+        p = blk * 176
+        b[p:p + 2] = np.array([f16_bits(0.05)], np.uint16).view(np.uint8)
+        b[p + 2:p + 4] = np.array([f16_bits(-0.01)], np.uint16).view(np.uint8)
+        b[p + 4:p + 16] = [(blk * 13 + i * 7) % 256 for i in range(12)]
+        b[p + 16:p + 48] = [(blk * 31 + i * 11) % 256 for i in range(32)]
+        b[p + 48:p + 176] = [(blk * 17 + i * 3) % 256 for i in range(128)]
+    want = oracle.dequant("q5_k", b, rows * cols)
+    lo, hi, scales, mins, d, dmin = oracle.q5ks_from_ggml(b, rows, cols)
+    pos = np.arange(rows * cols)
+    code = ((lo[pos // 8] >> ((pos % 8) * 4)) & 0xF) | (((hi[pos // 32] >> (pos % 32)) & 1) << 4)
+    r, c = pos // cols, pos % cols
+    sub, sup = r * (cols // 32) + c // 32, r * (cols // 256) + c // 256
+    got = code.astype(np.float32) * (d[sup] * scales[sub].astype(np.float32)) + \
+        dmin[sup] * mins[sub].astype(np.float32)
+    assert np.max(np.abs(got - want)) < 1e-5
+
+
 def test_dequant_q80_closed_form(oracle):
     qs = np.arange(-128, 128, dtype=np.int32)
     for d in (1.0, 0.5, 0.001, 6.0e-8, 65504.0):
@@ -184,7 +243,7 @@ def test_matmul_nt_integer_exact(oracle):
     assert np.array_equal(oracle.matmul_nt(a, b), (a.astype(np.int64) @ b.astype(np.int64).T))
 
 
-@pytest.mark.parametrize("qtype,k", [("q4_k", 512), ("q6_k", 512), ("q8_0", 256)])
+@pytest.mark.parametrize("qtype,k", [("q4_k", 512), ("q6_k", 512), ("q8_0", 256), ("q5_k", 512)])
 def test_quantized_linear_equals_dequant_matmul(oracle, qtype, k):
     # weight.rs:1693-1709: quantized linear == dequant + f32 matmul
     from arf_amd import synth
