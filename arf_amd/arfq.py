@@ -42,6 +42,7 @@ class QType(enum.IntEnum):
     Q4_K = 12
     Q5_K = 13
     Q6_K = 14
+    IQ4_XS = 23
 
 
 class DType(enum.IntEnum):
@@ -51,7 +52,7 @@ class DType(enum.IntEnum):
 
 # (weights per block, bytes per block): crates/arf-core/src/model/gguf.rs:1657-1673
 BLOCK = {QType.Q8_0: (32, 34), QType.Q4_K: (256, 144), QType.Q6_K: (256, 210),
-         QType.Q5_K: (256, 176)}
+         QType.Q5_K: (256, 176), QType.IQ4_XS: (256, 136)}
 
 # the C ABI, by name -> (restype, argtypes); tests check every name is exported
 _vp = ctypes.c_void_p

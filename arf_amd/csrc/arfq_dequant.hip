@@ -71,6 +71,16 @@ __global__ void repack_q5k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
     for (int i = 0; i < 160; i++) q[b * 160 + i] = src[16 + i];
 }
 
+// IQ4_XS: the 8-byte header (d, scales_h, scales_l) and qs[128] as they are.
+__global__ void repack_iq4xs(const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr,
+                             uint8_t *__restrict__ qs, int64_t nblk) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nblk) return;
+    const uint8_t *src = raw + b * 136;
+    for (int i = 0; i < 8; i++) hdr[b * 8 + i] = src[i];
+    for (int i = 0; i < 128; i++) qs[b * 128 + i] = src[8 + i];
+}
+
 hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s) {
     const int tpb = 256;
     const unsigned grid = (unsigned)((w->nblk + tpb - 1) / tpb);
@@ -87,6 +97,9 @@ hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s
         break;
     case ARFQ_Q5_K:
         repack_q5k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, w->nblk);
+        break;
+    case ARFQ_IQ4_XS:
+        repack_iq4xs<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, w->nblk);
         break;
     default:
         return hipErrorInvalidValue;
@@ -163,6 +176,30 @@ __global__ void dequant_q5k(const uint4 *__restrict__ hdr, const uint8_t *__rest
         o[i] = q4k_weight(d1, m1, ((qs[i] >> (4 * (j & 1))) & 0xFu) | (((qh[i] >> j) & 1u) << 4));
 }
 
+// One thread per (block, sub-block j): dl = d * (ls - 32), weight dl * kv with kv
+// the codebook value of the nibble (crates/arf-core/src/model/gguf.rs:1937-1976).
+__constant__ int8_t IQ4_KV[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                  1,    13,   25,  38,  53,  69,  89,  113};
+__global__ void dequant_iq4xs(const uint8_t *__restrict__ hdr, const uint8_t *__restrict__ qs,
+                              float *__restrict__ out, int64_t nblk) {
+#pragma clang fp contract(off)
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nblk * 8) return;
+    const int64_t b = t >> 3;
+    const int j = (int)(t & 7);
+    const uint8_t *h = hdr + b * 8;
+    const float d = h2f((uint32_t)h[0] | ((uint32_t)h[1] << 8));
+    const uint32_t sh = (uint32_t)h[2] | ((uint32_t)h[3] << 8);
+    const int ls = (int)(((h[4 + j / 2] >> (4 * (j % 2))) & 0xFu) | (((sh >> (2 * j)) & 3u) << 4));
+    const float dl = d * (float)(ls - 32);
+    const uint8_t *q = qs + b * 128 + 16 * j;
+    float *o = out + b * 256 + 32 * j;
+    for (int i = 0; i < 16; i++) {
+        o[i] = dl * (float)IQ4_KV[q[i] & 0xF];
+        o[i + 16] = dl * (float)IQ4_KV[q[i] >> 4];
+    }
+}
+
 hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s) {
     const int tpb = 256;
     switch (w->qtype) {
@@ -176,6 +213,11 @@ hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s) {
         const unsigned grid = (unsigned)((w->nblk + tpb - 1) / tpb);
         dequant_q80<<<grid, tpb, 0, s>>>((const int8_t *)w->s0, (const uint16_t *)w->s1, out,
                                          w->nblk);
+        break;
+    }
+    case ARFQ_IQ4_XS: {
+        const unsigned grid = (unsigned)((w->nblk * 8 + tpb - 1) / tpb);
+        dequant_iq4xs<<<grid, tpb, 0, s>>>((const uint8_t *)w->s0, (const uint8_t *)w->s1, out, w->nblk);
         break;
     }
     case ARFQ_Q5_K: {

@@ -545,7 +545,7 @@ struct DotQ6K {
         u32x4 q0, q1, q2;
         uint32_t sw, dw;
     };
-    static constexpr int XSTEP = 32;
+    static constexpr int XSTEP = 32, PF = Q6K_GEMV_PF;
     __device__ Res res() const {
         return {__builtin_amdgcn_make_buffer_rsrc((void *)qb, (short)0, (int)qb_bytes, 0x00020000),
                 __builtin_amdgcn_make_buffer_rsrc((void *)scb, (short)0, (int)sc_bytes, 0x00020000),
@@ -586,6 +586,9 @@ struct DotQ6K {
             cw[j] = ((w[4 * (t & 1) + j] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) |
                     (((w[8 + j] >> (2 * t)) << 4) & 0x30303030u);
     }
+    __device__ static int subdot(const uint32_t cw[4], const u32x4 lo, const u32x4 hi) {
+        return q6k_subdot(cw, lo, hi);
+    }
     __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
         (void)B;
         return A * (xsc * (float)sdot - 32.f * xsum);
@@ -612,7 +615,7 @@ struct DotQ5K {
         uint32_t hw;
         uint32_t qhd[8], hd[4];  // filled by expand()
     };
-    static constexpr int XSTEP = 16;
+    static constexpr int XSTEP = 16, PF = Q6K_GEMV_PF;
     __device__ Res res() const {
         return {__builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)hdr_bytes, 0x00020000),
                 __builtin_amdgcn_make_buffer_rsrc((void *)q, (short)0, (int)q_bytes, 0x00020000)};
@@ -656,8 +659,93 @@ struct DotQ5K {
         for (int j = 0; j < 4; j++)
             cw[j] = ((qs[j] >> (4 * nib)) & 0x0F0F0F0Fu) | (((l.qhd[4 * (t & 1) + j] >> hs) & 0x01010101u) << 4);
     }
+    __device__ static int subdot(const uint32_t cw[4], const u32x4 lo, const u32x4 hi) {
+        return q6k_subdot(cw, lo, hi);
+    }
     __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
         return A * (xsc * (float)sdot) - B * xsum;
+    }
+};
+
+// IQ4_XS: streams hdr (d, scales_h, scales_l[4]: 8 B per block) and qs (128 B).
+// Lane c takes sub-blocks 2c and 2c + 1 (qs bytes 32c .. 32c + 31); quadrant
+// t = sub-block 2c + t / 2, low (t even) or high nibbles: elements 16 t ..+15
+// of the lane's 64.  Lanes 0 and 1 load the header's two dwords and expand()
+// shares them over the quad.  A code is the non-linear codebook's int8 value
+// (kvalues_iq4nl), looked up with two v_perm over the 16 entries; weight
+// (d * (ls - 32)) * kv (crates/arf-core/src/model/gguf.rs:1908-1976).
+struct DotIQ4XS {
+    const uint8_t *hdr, *qs;
+    uint32_t hdr_bytes, qs_bytes;
+    struct Res {
+        __amdgpu_buffer_rsrc_t h, q;
+    };
+    struct Lane {
+        u32x4 q0, q1;
+        uint32_t hw;
+        uint32_t hd[2];  // filled by expand()
+    };
+    static constexpr int XSTEP = 16, PF = Q6K_GEMV_PF;
+    __device__ Res res() const {
+        return {__builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)hdr_bytes, 0x00020000),
+                __builtin_amdgcn_make_buffer_rsrc((void *)qs, (short)0, (int)qs_bytes, 0x00020000)};
+    }
+    __device__ static void load(const Res &r, Lane &l, uint32_t blk, bool live, int c) {
+        const uint32_t oq = live ? blk * 128u + 32u * (uint32_t)c : Q4K_OOB;
+        l.q0 = __builtin_amdgcn_raw_buffer_load_b128(r.q, oq, 0, 2);
+        l.q1 = __builtin_amdgcn_raw_buffer_load_b128(r.q, oq + 16u, 0, 2);
+        l.hw = __builtin_amdgcn_raw_buffer_load_b32(r.h, live && c < 2 ? blk * 8u + 4u * (uint32_t)c : Q4K_OOB,
+                                                     0, 0);
+    }
+    __device__ static void expand(Lane &l) {
+        l.hd[0] = quad_bcast<0>(l.hw), l.hd[1] = quad_bcast<1>(l.hw);
+    }
+    __device__ static int xbase(int b, int c) { return 256 * b + 64 * c; }
+    __device__ static void scales(const Lane &l, int c, float A[4], float B[4]) {
+        const float d = h2f(l.hd[0]);
+        const uint32_t sh = l.hd[0] >> 16, sl = byte_of(l.hd[1], c);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int j = 2 * c + u;
+            const int ls = (int)(((sl >> (4 * u)) & 0xFu) | (((sh >> (2 * j)) & 3u) << 4));
+            A[2 * u] = A[2 * u + 1] = d * (float)(ls - 32);
+            B[2 * u] = B[2 * u + 1] = 0.f;
+        }
+    }
+    __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
+        (void)c;
+        // kvalues_iq4nl as bytes: entries 0..7 and 8..15, little-endian
+        constexpr uint32_t T0lo = 0xBFAD9881u, T0hi = 0xF6EADDCFu;
+        constexpr uint32_t T1lo = 0x26190D01u, T1hi = 0x71594535u;
+        const u32x4 q = (t >> 1) ? l.q1 : l.q0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t sel = (q[j] >> (4 * (t & 1))) & 0x0F0F0F0Fu;
+            const uint32_t s7 = sel & 0x07070707u;
+            const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
+            const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
+            const uint32_t hi = (sel >> 3) & 0x01010101u;
+            const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
+            cw[j] = (v1 & mask) | (v0 & ~mask);
+        }
+    }
+    // sum(kv * X) with signed kv: the high plane by sdot4; the low (unsigned)
+    // plane by udot4 of kv + 128 (kv xor 0x80), less 128 * sum(X_lo)
+    __device__ static int subdot(const uint32_t cw[4], const u32x4 lo, const u32x4 hi) {
+        uint32_t a = 0u, sl = 0u;
+        int b = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            a = __builtin_amdgcn_udot4(cw[j] ^ 0x80808080u, lo[j], a, false);
+            sl = __builtin_amdgcn_udot4(0x01010101u, lo[j], sl, false);
+            b = __builtin_amdgcn_sdot4((int)cw[j], (int)hi[j], b, false);
+        }
+        // |sum| <= 16 * 127 * 32767 < 2^26: exact in int32 and in f32
+        return b * 256 + (int)a - 128 * (int)sl;
+    }
+    __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
+        (void)B, (void)xsum;
+        return A * (xsc * (float)sdot);
     }
 };
 
@@ -666,7 +754,7 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot(F fmt, const float 
                                                             float *__restrict__ y, int n, int nblk,
                                                             int m) {
     constexpr bool XREG = MX == 1;
-    constexpr int C = Q6K_GEMV_CHUNK, PF = Q6K_GEMV_PF;
+    constexpr int C = Q6K_GEMV_CHUNK, PF = F::PF;
     static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
     extern __shared__ uint4 smem4[];
     __shared__ int next_chunk;
@@ -775,13 +863,13 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot(F fmt, const float 
                     int sdot;
                     float xsum, xsc;
                     if (XREG) {
-                        sdot = q6k_subdot(cw, XL[t], XH[t]);
+                        sdot = F::subdot(cw, XL[t], XH[t]);
                         xsum = XS[t];
                         xsc = XE[t];
                     } else {
                         const size_t eo = (size_t)mi * k + xbase + F::XSTEP * t;
-                        sdot = q6k_subdot(cw, *reinterpret_cast<const u32x4 *>(xlo + eo),
-                                          *reinterpret_cast<const u32x4 *>(xhi + eo));
+                        sdot = F::subdot(cw, *reinterpret_cast<const u32x4 *>(xlo + eo),
+                                         *reinterpret_cast<const u32x4 *>(xhi + eo));
                         xsum = s16[eo >> 4];
                         xsc = xe[eo >> 5];
                     }
@@ -959,6 +1047,8 @@ static bool dot_ok(const arfq_weight *w, int64_t m) {
         return m <= 2 && dot_lds(w, (int)m) <= 64 * 1024 && nb * 192 < (int64_t)Q4K_OOB;
     if (w->qtype == ARFQ_Q5_K)
         return m <= 4 && dot_lds(w, dot_mx(m)) <= 64 * 1024 && nb * 160 < (int64_t)Q4K_OOB;
+    if (w->qtype == ARFQ_IQ4_XS)
+        return m <= 4 && dot_lds(w, dot_mx(m)) <= 64 * 1024 && nb * 128 < (int64_t)Q4K_OOB;
     return false;
 }
 
@@ -968,7 +1058,7 @@ bool gemv_supports(const arfq_weight *w, int64_t m) {
     if (w->qtype == ARFQ_Q4_K)
         return q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
                w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
-    if (w->qtype == ARFQ_Q5_K) return dot_ok(w, m);
+    if (w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS) return dot_ok(w, m);
     return w->qtype == ARFQ_Q8_0 || w->qtype == ARFQ_Q6_K;
 }
 
@@ -1042,6 +1132,11 @@ static DotQ5K dot_q5k(const arfq_weight *w, int e) {
     return {(const uint8_t *)w->s0 + eb * 16, (const uint8_t *)w->s1 + eb * 160, (uint32_t)(nb * 16),
             (uint32_t)(nb * 160)};
 }
+static DotIQ4XS dot_iq4xs(const arfq_weight *w, int e) {
+    const int64_t nb = w->n * (w->k / 256), eb = (int64_t)e * nb;
+    return {(const uint8_t *)w->s0 + eb * 8, (const uint8_t *)w->s1 + eb * 128, (uint32_t)(nb * 8),
+            (uint32_t)(nb * 128)};
+}
 template <class F, int MX, int XR>
 static hipError_t launch_dot_t(const F &fmt, const arfq_weight *w, int m, const float *x, float *y,
                                hipStream_t s) {
@@ -1103,6 +1198,12 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
         if (m == 1) return launch_dot<DotQ5K, 1>(f, w, 1, x, y, s);
         if (m == 2) return launch_dot<DotQ5K, 2>(f, w, 2, x, y, s);
         return launch_dot<DotQ5K, 4>(f, w, (int)m, x, y, s);
+    }
+    if (w->qtype == ARFQ_IQ4_XS) {
+        const DotIQ4XS f = dot_iq4xs(w, e);
+        if (m == 1) return launch_dot<DotIQ4XS, 1>(f, w, 1, x, y, s);
+        if (m == 2) return launch_dot<DotIQ4XS, 2>(f, w, 2, x, y, s);
+        return launch_dot<DotIQ4XS, 4>(f, w, (int)m, x, y, s);
     }
     if (w->qtype == ARFQ_Q6_K && dot_ok(w, m)) {
         const DotQ6K f = dot_q6k(w, e);

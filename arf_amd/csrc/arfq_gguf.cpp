@@ -351,9 +351,10 @@ int arfq_gguf_upload(arfq_ctx *ctx, const arfq_gguf *g, const char *name, int64_
     arfq_gguf *gm = const_cast<arfq_gguf *>(g);
     const arfq_gguf_tensor *t = find(g, name);
     if (!t) return fail(gm, ARFQ_E_NOT_FOUND, std::string("no tensor named ") + name);
-    if (t->type != ARFQ_Q8_0 && t->type != ARFQ_Q4_K && t->type != ARFQ_Q6_K && t->type != ARFQ_Q5_K)
+    if (t->type != ARFQ_Q8_0 && t->type != ARFQ_Q4_K && t->type != ARFQ_Q6_K && t->type != ARFQ_Q5_K &&
+        t->type != ARFQ_IQ4_XS)
         return fail(gm, ARFQ_E_UNSUPPORTED, "tensor " + t->name + ": ggml type " + std::to_string(t->type) +
-                                                " has no matmul kernel here (Q8_0, Q4_K, Q5_K, Q6_K)");
+                                                " has no matmul kernel here (Q8_0, Q4_K, Q5_K, Q6_K, IQ4_XS)");
     const TypeGeom tg = type_geom(t->type);
     const uint8_t *p = tensor_bytes(g, *t);
     if (!p) return fail(gm, ARFQ_E_FORMAT, "tensor " + t->name + ": data past the end of the file");

@@ -170,6 +170,7 @@ static int weight_create(arfq_ctx *ctx, int qtype, size_t nbytes, int64_t n_rows
     case ARFQ_Q8_0: sz[0] = nblk * 32; sz[1] = nblk * 2; break;
     case ARFQ_Q6_K: sz[0] = nblk * 192; sz[1] = nblk * 16; sz[2] = nblk * 2; break;
     case ARFQ_Q5_K: sz[0] = nblk * 16; sz[1] = nblk * 160; break;
+    case ARFQ_IQ4_XS: sz[0] = nblk * 8; sz[1] = nblk * 128; break;
     }
     void **dst[3] = {&w->s0, &w->s1, &w->s2};
     for (int i = 0; i < 3; i++) {
@@ -351,8 +352,9 @@ static int check_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *
         return fail(ctx, ARFQ_E_SHAPE, "moe: gate/up/down expert counts differ");
     if (E > arfq::MOE_EXPERTS_MAX) return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: more than 512 experts");
     if (up->qtype != gate->qtype) return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: gate and up differ in qtype");
-    if (gate->qtype == ARFQ_Q5_K || down->qtype == ARFQ_Q5_K)
-        return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: Q5_K experts have no grouped GEMM here (Q4_K, Q6_K, Q8_0)");
+    if (gate->qtype == ARFQ_Q5_K || down->qtype == ARFQ_Q5_K || gate->qtype == ARFQ_IQ4_XS ||
+        down->qtype == ARFQ_IQ4_XS)
+        return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: Q5_K / IQ4_XS experts have no grouped GEMM here (Q4_K, Q6_K, Q8_0)");
     if (up->n != gate->n || up->k != gate->k || down->n != gate->k || down->k != gate->n)
         return fail(ctx, ARFQ_E_SHAPE,
                     "moe: want gate/up [inter, hidden] and down [hidden, inter]");

@@ -32,8 +32,8 @@ struct arfq_weight {
     int experts = 1;
     int64_t nblk = 0;  // blocks over all experts
     // device streams (see arfq_common.h for what each holds per qtype)
-    void *s0 = nullptr;  // Q4_K hdr | Q8_0 qs | Q6_K qb | Q5_K hdr
-    void *s1 = nullptr;  // Q4_K qs  | Q8_0 d  | Q6_K sc | Q5_K qh + qs
+    void *s0 = nullptr;  // Q4_K hdr | Q8_0 qs | Q6_K qb | Q5_K hdr     | IQ4_XS hdr
+    void *s1 = nullptr;  // Q4_K qs  | Q8_0 d  | Q6_K sc | Q5_K qh + qs | IQ4_XS qs
     void *s2 = nullptr;  //                      Q6_K d
     size_t bytes = 0;    // ggml bytes of one expert (what one matmul streams)
 };
@@ -44,7 +44,7 @@ namespace arfq {
 inline int qk_of(int qtype) { return qtype == ARFQ_Q8_0 ? 32 : 256; }
 inline int block_bytes_of(int qtype) {
     return qtype == ARFQ_Q8_0 ? 34 : qtype == ARFQ_Q4_K ? 144 : qtype == ARFQ_Q6_K ? 210
-         : qtype == ARFQ_Q5_K ? 176 : 0;
+         : qtype == ARFQ_Q5_K ? 176 : qtype == ARFQ_IQ4_XS ? 136 : 0;
 }
 
 // ---- arfq_dequant.hip ----

@@ -7,6 +7,7 @@ Block contents follow the generation rules the benchmark is quoted on:
         d = f16(|N(0,1)| * 0.005)
   Q5_K  as Q4_K, plus 32 uniform bytes of 5th bits (no benchmark config; the
         survey's next row)
+  IQ4_XS d = f16(|N(0,1)| * 0.0005), scale and code bytes uniform (likewise)
 f16 rounding is IEEE round-to-nearest-even with subnormals kept (numpy).
 Everything is drawn from numpy's PCG64 seeded per call, so the CPU oracle and
 the GPU read the same bytes.  gguf_write() lays such tensors out as a GGUF v3
@@ -16,8 +17,8 @@ import struct
 
 import numpy as np
 
-BLOCK_BYTES = {"q8_0": 34, "q4_k": 144, "q6_k": 210, "q5_k": 176}
-QK = {"q8_0": 32, "q4_k": 256, "q6_k": 256, "q5_k": 256}
+BLOCK_BYTES = {"q8_0": 34, "q4_k": 144, "q6_k": 210, "q5_k": 176, "iq4_xs": 136}
+QK = {"q8_0": 32, "q4_k": 256, "q6_k": 256, "q5_k": 256, "iq4_xs": 256}
 
 
 def _f16_bytes(v):
@@ -56,7 +57,16 @@ def q5_k_blocks(rng, nblk):
     return out
 
 
-_GEN = {"q8_0": q8_0_blocks, "q4_k": q4_k_blocks, "q6_k": q6_k_blocks, "q5_k": q5_k_blocks}
+def iq4_xs_blocks(rng, nblk):
+    """IQ4_XS: d = f16(|N(0,1)| * 0.0005), scale and code bytes uniform."""
+    out = np.empty((nblk, 136), np.uint8)
+    out[:, 0:2] = _f16_bytes(np.abs(rng.standard_normal(nblk)) * 0.0005)
+    out[:, 2:136] = rng.integers(0, 256, size=(nblk, 134), dtype=np.uint8)
+    return out
+
+
+_GEN = {"q8_0": q8_0_blocks, "q4_k": q4_k_blocks, "q6_k": q6_k_blocks, "q5_k": q5_k_blocks,
+        "iq4_xs": iq4_xs_blocks}
 
 
 def weight(qtype, n, k, seed, experts=1):

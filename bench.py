@@ -277,7 +277,7 @@ def main():
                 "us_per_launch": round(ms3 * 1e3, 3), "GB/s": round(b3 / ms3 / 1e6, 1),
                 "hbm_frac": round(b3 / ms3 / 1e6 / HBM_PEAK_GBS, 4)}
             log(f"[bench] C3 m={mm}: {ms3 * 1e3:.2f} us/launch")
-        # Q5_K GEMV at C2's shape: the survey's next row (no benchmark config of its own)
+        # Q5_K and IQ4_XS GEMVs at C2's shape: the survey's next row (no benchmark config)
         try:
             ms5k, _ = time_matmul(ctx, "q5_k", 1, 17408, 5120, steps2, 50, 6, seed=0xA7F00005)
             b5k = algorithmic_bytes("q5_k", 1, 17408, 5120)
@@ -287,6 +287,15 @@ def main():
             log(f"[bench] Q5_K m=1 (C2 shape): {ms5k * 1e3:.2f} us/launch")
         except arf_amd.ArfqError as e:
             configs["q5_k_gemv_m1_k5120_n17408"] = {"error": str(e)}
+        try:
+            ms4x, _ = time_matmul(ctx, "iq4_xs", 1, 17408, 5120, steps2, 50, 6, seed=0xA7F00006)
+            b4x = algorithmic_bytes("iq4_xs", 1, 17408, 5120)
+            configs["iq4_xs_gemv_m1_k5120_n17408"] = {
+                "us_per_launch": round(ms4x * 1e3, 3), "GB/s": round(b4x / ms4x / 1e6, 1),
+                "hbm_frac": round(b4x / ms4x / 1e6 / HBM_PEAK_GBS, 4)}
+            log(f"[bench] IQ4_XS m=1 (C2 shape): {ms4x * 1e3:.2f} us/launch")
+        except arf_amd.ArfqError as e:
+            configs["iq4_xs_gemv_m1_k5120_n17408"] = {"error": str(e)}
         # C4 Q4_K prefill GEMM
         try:
             ms4, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, 30, 10, 2, seed=0xA7F00004,

@@ -53,7 +53,9 @@ typedef enum {
     ARFQ_Q4_K = 12, /* 144 B per 256 weights: f16 d, f16 dmin, 12 B 6-bit scales/mins, 128 B nibbles */
     ARFQ_Q5_K = 13, /* 176 B per 256 weights: Q4_K's d, dmin, scales, then qh[32] 5th bits, qs[128];
                        decode GEMV (m <= 4) and dequant only */
-    ARFQ_Q6_K = 14  /* 210 B per 256 weights: ql[128], qh[64], i8 scales[16], f16 d */
+    ARFQ_Q6_K = 14, /* 210 B per 256 weights: ql[128], qh[64], i8 scales[16], f16 d */
+    ARFQ_IQ4_XS = 23 /* 136 B per 256 weights: f16 d, u16 scales_h, scales_l[4], qs[128] codebook
+                        indices; decode GEMV (m <= 4) and dequant only */
 } arfq_qtype;
 
 /* activation element type */
@@ -208,7 +210,7 @@ int arfq_gguf_find(const arfq_gguf *g, const char *name, int64_t *index);
  * when stored as another type (the reference returns None). */
 int arfq_gguf_blocks(const arfq_gguf *g, const char *name, int ggml_type, const void **blocks,
                      size_t *nbytes, int64_t *rows, int64_t *cols);
-/* Upload tensor `name` (Q8_0, Q4_K, Q5_K or Q6_K) as a weight:
+/* Upload tensor `name` (Q8_0, Q4_K, Q5_K, Q6_K or IQ4_XS) as a weight:
  *   - 2-D [ne0 = k, ne1 = n]: rows [row0, row0 + n_rows) (n_rows < 0: to the
  *     end) as one matrix (the fused-qkv row slice, Entry::RowSlice,
  *     gguf.rs:125-140); rows start on block boundaries because blocks run along

@@ -175,6 +175,43 @@ void arfo_dequant_q5_k(const uint8_t *bytes, int64_t n, float *out) {
     }
 }
 
+/* ---- next row f2: IQ4_XS dequant.  crates/arf-core/src/model/gguf.rs:1908-1976.
+ * Block = 136 B: f16 d, u16 scales_h, scales_l[4], qs[128].  Sub-block j (32
+ * weights): ls = ((scales_l[j/2] >> 4 (j%2)) & 15) | (((scales_h >> 2j) & 3) << 4),
+ * dl = d * (ls - 32); weight 32j + i = dl * kvalues[qs[16j + i] & 15] (i < 16),
+ * dl * kvalues[qs[16j + i - 16] >> 4] (i >= 16), kvalues the non-linear IQ4 codebook. */
+static const int8_t IQ4_KVALUES[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                       1,    13,   25,  38,  53,  69,  89,  113};
+void arfo_dequant_iq4_xs(const uint8_t *bytes, int64_t n, float *out) {
+    int64_t nblocks = n / QK_K;
+    for (int64_t b = 0; b < nblocks; b++) {
+        const uint8_t *p = bytes + b * 136;
+        float d = arfo_f16_to_f32(rd16(p));
+        uint16_t scales_h = rd16(p + 2);
+        const uint8_t *scales_l = p + 4, *qs = p + 8;
+        float *o = out + b * QK_K;
+        for (int j = 0; j < 8; j++) {
+            int lo = (scales_l[j / 2] >> (4 * (j % 2))) & 0xF;
+            int hi = (scales_h >> (2 * j)) & 3;
+            float dl = d * (float)(((hi << 4) | lo) - 32);
+            for (int i = 0; i < 16; i++) {
+                o[32 * j + i] = dl * (float)IQ4_KVALUES[qs[16 * j + i] & 0xF];
+                o[32 * j + i + 16] = dl * (float)IQ4_KVALUES[qs[16 * j + i] >> 4];
+            }
+        }
+    }
+}
+
+/* IQ4_XS reference matmul: dequant then matmul_nt (the CPU path reads IQ4_XS
+ * through its f32 dequant; gguf.rs:1937-1976 then matmul.rs:84-99). */
+void arfo_matmul_nt_iq4_xs(const float *a, int64_t m, int64_t k, const uint8_t *blocks, int64_t n,
+                           float *out) {
+    float *w = (float *)malloc((size_t)(n * k) * 4);
+    arfo_dequant_iq4_xs(blocks, n * k, w);
+    arfo_matmul_nt(a, m, k, w, n, out);
+    free(w);
+}
+
 /* Q5KSMatrix::from_ggml_q5k (crates/arf-ml/src/weight.rs:551-632): low nibbles 8 per
  * u32 in element order, the 5th bit 32 per u32 (bit 1 << ss of qh[i] for sub-block
  * ss, element i), sub-block scales u8, mins -m as i8, d / dmin widened to f32. */

@@ -40,7 +40,7 @@ def lib():
         L.arfo_f16_to_f32.argtypes = [ctypes.c_uint16]
         L.arfo_q4k_get_scale_min.argtypes = [_u8p, ctypes.c_int, _u8p, _u8p]
         for name in ("arfo_dequant_q8_0", "arfo_dequant_q4_k", "arfo_dequant_q6_k",
-                     "arfo_dequant_q5_k"):
+                     "arfo_dequant_q5_k", "arfo_dequant_iq4_xs"):
             getattr(L, name).argtypes = [_u8p, _i64, _f32p]
         L.arfo_q4ks_from_ggml.argtypes = [_u8p, _i64, _i64, _u32p, _u8p, _i8p, _f32p, _f32p]
         L.arfo_q5ks_from_ggml.argtypes = [_u8p, _i64, _i64, _u32p, _u32p, _u8p, _i8p, _f32p,
@@ -48,7 +48,7 @@ def lib():
         L.arfo_q4ks_to_f32.argtypes = [_u32p, _u8p, _i8p, _f32p, _f32p, _i64, _i64, _f32p]
         L.arfo_matmul_nt.argtypes = [_f32p, _i64, _i64, _f32p, _i64, _f32p]
         for name in ("arfo_matmul_nt_q8_0", "arfo_matmul_nt_q4_k", "arfo_matmul_nt_q6_k",
-                     "arfo_matmul_nt_q5_k"):
+                     "arfo_matmul_nt_q5_k", "arfo_matmul_nt_iq4_xs"):
             getattr(L, name).argtypes = [_f32p, _i64, _i64, _u8p, _i64, _f32p]
         L.arfo_matmul_nt_q4ks.argtypes = [_f32p, _i64, _i64, _u32p, _u8p, _i8p, _f32p, _f32p,
                                           _i64, _f32p]
@@ -93,12 +93,14 @@ def q4k_get_scale_min(scales12, j):
     return sc.value, m.value
 
 
-_BLOCK = {"q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210), "q5_k": (256, 176)}
+_BLOCK = {"q8_0": (32, 34), "q4_k": (256, 144), "q6_k": (256, 210), "q5_k": (256, 176),
+          "iq4_xs": (256, 136)}
 
 
 def dequant(qtype, blocks, n):
-    """dequant_q8_0 / dequant_q4_k / dequant_q6_k / dequant_q5_k (crates/arf-core/src/model/
-    gguf.rs:1633-1649, 2004-2035, 2092-2131, 2053-2090): raw ggml block bytes -> n f32 values."""
+    """dequant_q8_0 / dequant_q4_k / dequant_q6_k / dequant_q5_k / dequant_iq4_xs
+    (crates/arf-core/src/model/gguf.rs:1633-1649, 2004-2035, 2092-2131, 2053-2090, 1937-1976):
+    raw ggml block bytes -> n f32 values."""
     qk, bb = _BLOCK[qtype]
     b = _c(blocks, np.uint8).reshape(-1)
     assert n % qk == 0 and b.size == n // qk * bb, "block byte count mismatch"
@@ -174,7 +176,7 @@ def matmul_q4ks(a, q4ks, n):
 def matmul_q(qtype, a, blocks, n):
     """The reference CPU matmul for a ggml-quantized weight [n, k]:
     q8_0 -> matmul_nt_q8_0 (matmul.rs:174-204); q4_k -> from_ggml_q4k + matmul_nt_q4ks
-    (weight.rs:1000-1080, matmul.rs:322-400); q6_k / q5_k -> dequant + matmul_nt."""
+    (weight.rs:1000-1080, matmul.rs:322-400); q6_k / q5_k / iq4_xs -> dequant + matmul_nt."""
     a = _c(a, np.float32)
     if a.ndim == 1:
         a = a.reshape(1, -1)

@@ -240,6 +240,7 @@ def _model_file(tmp_path, E=4, hidden=512, inter=256):
     q6 = synth.weight("q6_k", 40, 768, seed=2)
     q8 = synth.weight("q8_0", 72, 320, seed=3)
     q5 = synth.weight("q5_k", 56, 768, seed=8)
+    iq4 = synth.weight("iq4_xs", 24, 1280, seed=9)
     qkv = synth.weight("q4_k", 48 + 2 * 16, 512, seed=4)
     gate = synth.weight("q4_k", inter, hidden, seed=5, experts=E)
     up = synth.weight("q4_k", inter, hidden, seed=6, experts=E)
@@ -248,6 +249,7 @@ def _model_file(tmp_path, E=4, hidden=512, inter=256):
                ("blk.0.ffn_down.weight", [768, 40], 14, q6.tobytes()),
                ("output.weight", [320, 72], 8, q8.tobytes()),
                ("token_embd.weight", [768, 56], 13, q5.tobytes()),
+               ("blk.2.ffn_gate.weight", [1280, 24], 23, iq4.tobytes()),
                ("blk.0.attn_qkv.weight", [512, 80], 12, qkv.tobytes()),
                ("blk.0.ffn_gate_exps.weight", [hidden, inter, E], 12, gate.tobytes()),
                ("blk.0.ffn_up_exps.weight", [hidden, inter, E], 12, up.tobytes()),
@@ -255,8 +257,8 @@ def _model_file(tmp_path, E=4, hidden=512, inter=256):
                ("blk.0.attn_norm.weight", [512], 0, bytes(2048))]
     data, _ = build([("general.architecture", 8, "qwen3moe"), ("general.alignment", 4, 64)],
                     tensors, alignment=64)
-    return _write(tmp_path, "model.gguf", data), dict(q4=q4, q6=q6, q8=q8, q5=q5, qkv=qkv,
-                                                      gate=gate, up=up, down=down)
+    return _write(tmp_path, "model.gguf", data), dict(q4=q4, q6=q6, q8=q8, q5=q5, iq4=iq4,
+                                                      qkv=qkv, gate=gate, up=up, down=down)
 
 
 @pytest.mark.gpu
@@ -268,6 +270,7 @@ def test_gpu_upload_matrices_and_row_slices(gpu_ctx, oracle, tmp_path):
              ("blk.0.ffn_down.weight", "q6_k", raw["q6"], 40, 768, 0, -1),
              ("output.weight", "q8_0", raw["q8"], 72, 320, 0, -1),
              ("token_embd.weight", "q5_k", raw["q5"], 56, 768, 0, -1),
+             ("blk.2.ffn_gate.weight", "iq4_xs", raw["iq4"], 24, 1280, 0, -1),
              # the fused q/k/v rows: q = rows 0..47, k = 48..63, v = 64..79
              ("blk.0.attn_qkv.weight", "q4_k", raw["qkv"][:48 * 2 * 144], 48, 512, 0, 48),
              ("blk.0.attn_qkv.weight", "q4_k", raw["qkv"][48 * 2 * 144:64 * 2 * 144], 16, 512, 48, 16),
@@ -278,7 +281,7 @@ def test_gpu_upload_matrices_and_row_slices(gpu_ctx, oracle, tmp_path):
         assert (w.n, w.k, w.experts) == (n, k, 1)
         deq = gpu_ctx.dequant(w).numpy().reshape(-1)
         assert np.array_equal(deq.view(np.uint32), oracle.dequant(qt, blocks, n * k).view(np.uint32))
-        for m in ((1, 3) if qt == "q5_k" else (1, 5)):
+        for m in ((1, 3) if qt in ("q5_k", "iq4_xs") else (1, 5)):
             x = synth.activations(m, k, seed=m + n)
             y = gpu_ctx.empty((m, n), np.float32)
             gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)

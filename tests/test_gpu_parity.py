@@ -39,7 +39,7 @@ def test_f16_conversion_exhaustive_via_q8_0(gpu_ctx, oracle):
     assert np.array_equal(np.isinf(got), np.isinf(want))
 
 
-@pytest.mark.parametrize("qtype", ["q4_k", "q6_k", "q8_0", "q5_k"])
+@pytest.mark.parametrize("qtype", ["q4_k", "q6_k", "q8_0", "q5_k", "iq4_xs"])
 def test_dequant_bit_exact(gpu_ctx, oracle, qtype):
     _say("case: dequant", qtype)
     from arf_amd import QType, synth
@@ -48,7 +48,7 @@ def test_dequant_bit_exact(gpu_ctx, oracle, qtype):
     bb = synth.BLOCK_BYTES[qtype]
     blk = raw.reshape(-1, bb)
     # f16-subnormal and zero scales in some blocks
-    dofs = {"q4_k": 0, "q8_0": 0, "q6_k": 208, "q5_k": 0}[qtype]
+    dofs = {"q4_k": 0, "q8_0": 0, "q6_k": 208, "q5_k": 0, "iq4_xs": 0}[qtype]
     blk[::5, dofs:dofs + 2] = np.array([3, 0], np.uint8)
     blk[1::9, dofs:dofs + 2] = 0
     w = gpu_ctx.upload(QType[qtype.upper()], raw, n, k, E)
@@ -85,6 +85,7 @@ def _matmul(ctx, qtype, n, k, m, seed, x_dtype=np.float32, experts=1, expert=0):
     ("q8_0", 64, 2048), ("q8_0", 31, 96), ("q8_0", 100, 512),
     ("q6_k", 64, 4352), ("q6_k", 21, 256), ("q6_k", 50, 17408),
     ("q5_k", 64, 256), ("q5_k", 37, 1024), ("q5_k", 130, 5120), ("q5_k", 33, 2816),
+    ("iq4_xs", 64, 256), ("iq4_xs", 37, 1024), ("iq4_xs", 130, 5120), ("iq4_xs", 33, 2816),
 ])
 @pytest.mark.parametrize("m", [1, 2, 3, 4])
 def test_gemv_small_shapes(gpu_ctx, oracle, qtype, n, k, m):
@@ -94,7 +95,8 @@ def test_gemv_small_shapes(gpu_ctx, oracle, qtype, n, k, m):
     assert rel_err(got, want) <= TOL
 
 
-@pytest.mark.parametrize("qtype,m", [("q4_k", 1), ("q6_k", 1), ("q6_k", 2), ("q5_k", 1), ("q5_k", 3)])
+@pytest.mark.parametrize("qtype,m", [("q4_k", 1), ("q6_k", 1), ("q6_k", 2), ("q5_k", 1), ("q5_k", 3),
+                                     ("iq4_xs", 1), ("iq4_xs", 4)])
 def test_gemv_expert_offset(gpu_ctx, oracle, qtype, m):
     _say("case: gemv expert offset", qtype, m)
     got, raw, x = _matmul(gpu_ctx, qtype, 48, 512, m, seed=5, experts=4, expert=3)
@@ -124,19 +126,21 @@ def test_c3_q6_k_gemv_m1_full(gpu_ctx, oracle):
     assert e <= TOL
 
 
-def test_q5_k_gemv_c2_shape(gpu_ctx, oracle):
-    # Q5_K at C2's shape (the survey's next row: no benchmark config of its own)
-    _say("case: Q5_K C2 shape")
-    got, raw, x = _matmul(gpu_ctx, "q5_k", 17408, 5120, 1, seed=0xA7F00005)
-    e = rel_err(got, oracle.matmul_q("q5_k", x, raw, 17408))
-    _say("Q5_K rel err", e)
+@pytest.mark.parametrize("qtype", ["q5_k", "iq4_xs"])
+def test_next_formats_gemv_c2_shape(gpu_ctx, oracle, qtype):
+    # Q5_K / IQ4_XS at C2's shape (the survey's next row: no benchmark config of its own)
+    _say("case: C2 shape", qtype)
+    got, raw, x = _matmul(gpu_ctx, qtype, 17408, 5120, 1, seed=0xA7F00005)
+    e = rel_err(got, oracle.matmul_q(qtype, x, raw, 17408))
+    _say(qtype, "rel err", e)
     assert e <= TOL
 
 
-def test_q5_k_beyond_the_gemv_is_unsupported(gpu_ctx):
+@pytest.mark.parametrize("qtype", ["q5_k", "iq4_xs"])
+def test_next_formats_beyond_the_gemv_are_unsupported(gpu_ctx, qtype):
     from arf_amd import ArfqError, QType, synth
     from arf_amd.arfq import ARFQ_E_UNSUPPORTED
-    w = gpu_ctx.upload(QType.Q5_K, synth.weight("q5_k", 32, 512, seed=3), 32, 512)
+    w = gpu_ctx.upload(QType[qtype.upper()], synth.weight(qtype, 32, 512, seed=3), 32, 512)
     for m, dt in ((5, np.float32), (1, np.float16)):
         x = gpu_ctx.to_device(synth.activations(m, 512, seed=4).astype(dt))
         y = gpu_ctx.empty((m, 32), np.float32)

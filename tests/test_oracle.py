@@ -216,6 +216,52 @@ def test_q5k_native_unpack_matches_dequant(oracle):
     assert np.max(np.abs(got - want)) < 1e-5
 
 
+def _iq4_block(d=1.0):
+    b = np.zeros(136, np.uint8)
+    b[0:2] = np.array([f16_bits(d)], np.uint16).view(np.uint8)
+    return b
+
+
+IQ4 = [-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113]
+
+
+def test_dequant_iq4_xs_known_block(oracle):
+    # dequant_iq4_xs_known_block (gguf.rs:2994-3005): ls = 0 -> dl = -32
+    b = _iq4_block()
+    b[8] = 0x10
+    out = oracle.dequant("iq4_xs", b, 256)
+    assert out[0] == -32.0 * -127.0 and out[16] == -32.0 * -104.0 and out[1] == -32.0 * -127.0
+
+
+def test_iq4_xs_sub_scale_32_is_the_zero_point(oracle):
+    # iq4_xs_sub_scale_32_is_the_zero_point (gguf.rs:3007-3028)
+    b = _iq4_block()
+    b[2:4] = np.array([sum(2 << (2 * j) for j in range(8))], np.uint16).view(np.uint8)
+    b[8:] = 0xFF
+    assert not oracle.dequant("iq4_xs", b, 256).any()
+
+
+def test_iq4_xs_each_sub_block_uses_its_own_scale_and_the_codebook(oracle):
+    # iq4_xs_each_sub_block_uses_its_own_scale (gguf.rs:3030-3055), then every code of every
+    # sub-block against the codebook (iq4_xs_codebook_is_not_a_linear_ramp, gguf.rs:3057-3064)
+    b = _iq4_block()
+    sh = 0
+    for j in range(8):
+        ls = 33 + j
+        b[4 + j // 2] |= (ls & 0xF) << (4 * (j % 2))
+        sh |= ((ls >> 4) & 3) << (2 * j)
+    b[2:4] = np.array([sh], np.uint16).view(np.uint8)
+    rng = np.random.default_rng(5)
+    codes = rng.integers(0, 16, 256)
+    for j in range(8):
+        for i in range(16):
+            b[8 + 16 * j + i] = codes[32 * j + i] | (codes[32 * j + 16 + i] << 4)
+    out = oracle.dequant("iq4_xs", b, 256)
+    want = np.array([(e // 32 + 1) * IQ4[codes[e]] for e in range(256)], np.float32)
+    assert np.array_equal(out, want)
+    assert IQ4 != [(c - 8) * 16 for c in range(16)]
+
+
 def test_dequant_q80_closed_form(oracle):
     qs = np.arange(-128, 128, dtype=np.int32)
     for d in (1.0, 0.5, 0.001, 6.0e-8, 65504.0):
@@ -243,7 +289,8 @@ def test_matmul_nt_integer_exact(oracle):
     assert np.array_equal(oracle.matmul_nt(a, b), (a.astype(np.int64) @ b.astype(np.int64).T))
 
 
-@pytest.mark.parametrize("qtype,k", [("q4_k", 512), ("q6_k", 512), ("q8_0", 256), ("q5_k", 512)])
+@pytest.mark.parametrize("qtype,k", [("q4_k", 512), ("q6_k", 512), ("q8_0", 256), ("q5_k", 512),
+                                     ("iq4_xs", 512)])
 def test_quantized_linear_equals_dequant_matmul(oracle, qtype, k):
     # weight.rs:1693-1709: quantized linear == dequant + f32 matmul
     from arf_amd import synth
