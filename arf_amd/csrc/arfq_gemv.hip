@@ -148,6 +148,55 @@ __device__ __forceinline__ XqRound xq_load(const float *__restrict__ x, int item
     return r;
 }
 
+// x sources of gemv_q4k: a row-major f32 x (the plain GEMV), and for the MoE
+// decode path one row per (token, expert) pair: the token's f32 or f16 row, or
+// silu(g) * u of the pair's gate and up rows (crates/arf-ml/src/lib.rs:160-162;
+// the same expression as the grouped path's gate|up kernel).
+struct XsF32 {
+    const float *x;
+    __device__ XqRound load(int items, int base) const { return xq_load(x, items, base); }
+};
+struct XsRowF32 {
+    const float *x;
+    int64_t stride;
+    int div;  // pair p reads row p / div
+    __device__ void pair(int p) { x += (int64_t)(p / div) * stride; }
+    __device__ XqRound load(int items, int base) const { return xq_load(x, items, base); }
+};
+struct XsRowF16 {
+    const _Float16 *x;
+    int64_t stride;
+    int div;
+    __device__ void pair(int p) { x += (int64_t)(p / div) * stride; }
+    __device__ XqRound load(int items, int base) const {
+        const int it = min(base + (int)threadIdx.x, items - 1);
+        typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+        const f16x8 h = reinterpret_cast<const f16x8 *>(x)[it];
+        XqRound r;
+        r.v0 = make_float4((float)h[0], (float)h[1], (float)h[2], (float)h[3]);
+        r.v1 = make_float4((float)h[4], (float)h[5], (float)h[6], (float)h[7]);
+        return r;
+    }
+};
+struct XsSwiglu {
+    const float *g, *u;
+    int64_t stride;
+    __device__ void pair(int p) {
+        g += (int64_t)p * stride;
+        u += (int64_t)p * stride;
+    }
+    __device__ static float silu_mul(float a, float b) { return a / (1.0f + expf(-a)) * b; }
+    __device__ XqRound load(int items, int base) const {
+        const XqRound a = xq_load(g, items, base), b = xq_load(u, items, base);
+        XqRound r;
+        r.v0 = make_float4(silu_mul(a.v0.x, b.v0.x), silu_mul(a.v0.y, b.v0.y),
+                           silu_mul(a.v0.z, b.v0.z), silu_mul(a.v0.w, b.v0.w));
+        r.v1 = make_float4(silu_mul(a.v1.x, b.v1.x), silu_mul(a.v1.y, b.v1.y),
+                           silu_mul(a.v1.z, b.v1.z), silu_mul(a.v1.w, b.v1.w));
+        return r;
+    }
+};
+
 __device__ __forceinline__ void xq_process(const XqRound &r, int items, int base, int nsub,
                                            uint4 *dg, float2 *xs) {
     const int it = base + (int)threadIdx.x;
@@ -293,11 +342,10 @@ constexpr uint32_t Q4K_OOB = 0x80000000u;               // buffer offset past an
 // sizes XR for), then all waves pass a barrier before any weight load is
 // issued (the CU serves requests in issue order, and x gates all compute),
 // then x is quantized into LDS and the weight ring starts.
-template <int MX, int XR, int PF = Q4K_GEMV_PF>
-__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
+template <int MX, int XR, int PF, class XSRC>
+__device__ __forceinline__ void gemv_q4k_body(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
-    uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk,
-    int m) {
+    uint32_t qs_bytes, const XSRC &xsrc, float *__restrict__ y, int n, int nblk, int m) {
     constexpr bool XREG = MX == 1;
     constexpr int C = Q4K_GEMV_CHUNK;
     static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
@@ -365,7 +413,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     const int xitems = m * nsub * 4;
     XqRound xr[XR];
 #pragma unroll
-    for (int r = 0; r < XR; r++) xr[r] = xq_load(x, xitems, r * Q4K_GEMV_THREADS);
+    for (int r = 0; r < XR; r++) xr[r] = xsrc.load(xitems, r * Q4K_GEMV_THREADS);
     __builtin_amdgcn_s_barrier();
     issue(0, true);
     __builtin_amdgcn_sched_barrier(0);
@@ -373,7 +421,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     for (int r = 0; r < XR; r++)
         if (r * Q4K_GEMV_THREADS < xitems) xq_process(xr[r], xitems, r * Q4K_GEMV_THREADS, nsub, dg, xs);
     for (int base = XR * Q4K_GEMV_THREADS; base < xitems; base += Q4K_GEMV_THREADS)
-        xq_process(xq_load(x, xitems, base), xitems, base, nsub, dg, xs);
+        xq_process(xsrc.load(xitems, base), xitems, base, nsub, dg, xs);
     __syncthreads();  // x digits and next_chunk are visible from here on
 #pragma unroll
     for (int u = 1; u < PF; u++) {
@@ -455,6 +503,33 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
             y[(int64_t)mi * n + r0 + r] = v;
         }
     }
+}
+
+template <int MX, int XR, int PF = Q4K_GEMV_PF>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
+    const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
+    uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk,
+    int m) {
+    gemv_q4k_body<MX, XR, PF>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n, nblk, m);
+}
+
+// MoE decode: blockIdx.y = pair p, one x row each, the weight of expert ids[p]
+// (its n rows split over gridDim.x workgroups) into y row p.  A pair whose id
+// is out of range is dropped (its row is not written; the combine skips it).
+// Reference: the indirect GEMVs gemv_q4ks_id / gemv_q4ks_id_down
+// (shaders/metal/gemv_q4ks_id_msl.metal:40-153, gemv_q4ks_id_down_msl.metal:186-275).
+template <int XR, class XSRC>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
+    const uint8_t *__restrict__ hdr, const uint8_t *__restrict__ qs, uint32_t e_hdr_bytes,
+    uint32_t e_qs_bytes, XSRC xsrc, float *__restrict__ y, int n, int nblk,
+    const int32_t *__restrict__ ids, int E) {
+    const int p = blockIdx.y;
+    const int e = ids[p];
+    if (e < 0 || e >= E) return;  // uniform over the workgroup
+    xsrc.pair(p);
+    gemv_q4k_body<1, XR, Q4K_GEMV_PF>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+                                      qs + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
+                                      y + (int64_t)p * n, n, nblk, 1);
 }
 
 // ------------------------------------------------------------ Q6_K (dot) ----
@@ -1183,6 +1258,49 @@ static hipError_t launch_gemv_q4k(const arfq_weight *w, int e, int m, const floa
     if (rounds <= 1) return launch_gemv_q4k_t<MX, 1>(w, e, m, x, y, s);
     if (rounds <= 2) return launch_gemv_q4k_t<MX, 2>(w, e, m, x, y, s);
     return launch_gemv_q4k_t<MX, 4>(w, e, m, x, y, s);
+}
+
+// LDS of gemv_q4k_pairs with g workgroups per pair.
+static size_t q4k_pairs_lds(const arfq_weight *w, int64_t g) {
+    const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4, rows = (w->n + g - 1) / g;
+    return (size_t)(w->k / 32) * (16 * 4 + 8) + (size_t)rows * spr * 4;
+}
+
+bool gemv_pairs_supports(const arfq_weight *w) {
+    return w->qtype == ARFQ_Q4_K && w->k % 256 == 0 && w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB &&
+           q4k_pairs_lds(w, 1) <= 64 * 1024;
+}
+
+template <class XS>
+static hipError_t launch_pairs_t(const arfq_weight *w, int64_t P, const int32_t *ids, const XS &xs,
+                                 float *y, hipStream_t s) {
+    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
+    // about two workgroups per CU over all pairs, >= 4 rows per workgroup
+    const int64_t g = std::max<int64_t>(1, std::min<int64_t>((2 * (int64_t)cus + P - 1) / P, w->n / 4));
+    const int64_t nb = w->n * (w->k / 256);
+    const dim3 grid((unsigned)g, (unsigned)P);
+    const int nsub = (int)(w->k / 32);
+    const size_t lds = q4k_pairs_lds(w, g);
+    if (nsub * 4 <= Q4K_GEMV_THREADS)
+        gemv_q4k_pairs<1, XS><<<grid, Q4K_GEMV_THREADS, lds, s>>>(
+            (const uint8_t *)w->s0, (const uint8_t *)w->s1, (uint32_t)(nb * 16), (uint32_t)(nb * 128), xs, y,
+            (int)w->n, (int)(w->k / 256), ids, w->experts);
+    else
+        gemv_q4k_pairs<2, XS><<<grid, Q4K_GEMV_THREADS, lds, s>>>(
+            (const uint8_t *)w->s0, (const uint8_t *)w->s1, (uint32_t)(nb * 16), (uint32_t)(nb * 128), xs, y,
+            (int)w->n, (int)(w->k / 256), ids, w->experts);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,
+                             int x_dtype, int x_div, const float *g, const float *u, float *y,
+                             hipStream_t s) {
+    if (P == 0) return hipSuccess;
+    if (!gemv_pairs_supports(w) || P > 65535) return hipErrorInvalidValue;
+    if (g) return launch_pairs_t(w, P, ids, XsSwiglu{g, u, w->k}, y, s);
+    if (x_dtype == ARFQ_F16)
+        return launch_pairs_t(w, P, ids, XsRowF16{(const _Float16 *)x, w->k, x_div}, y, s);
+    return launch_pairs_t(w, P, ids, XsRowF32{(const float *)x, w->k, x_div}, y, s);
 }
 
 hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, float *y,

@@ -375,6 +375,41 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     if (tokens == 0) return ARFQ_OK;
     const int E = gate->experts;
     const int64_t hidden = gate->k, inter = gate->n, P = tokens * top_k;
+    // Few (token, expert) pairs: one indirect GEMV per weight over the pairs (route ->
+    // gate -> up -> down with SwiGLU on its x -> combine), instead of grouping pairs
+    // into expert tiles the grouped GEMMs would mostly leave empty (the reference's
+    // mul_mv_id crossover, crates/arf-gpu/src/gpu/metal/island.rs:4048-4070).
+    if (P <= arfq::MOE_DECODE_PAIRS_MAX && gate->qtype == ARFQ_Q4_K && down->qtype == ARFQ_Q4_K &&
+        arfq::gemv_pairs_supports(gate) && arfq::gemv_pairs_supports(down)) {
+        size_t o = 0;
+        const size_t o_ids = o;  o += ids_in ? 0 : align256((size_t)P * 4);
+        const size_t o_w = o;    o += ids_in ? 0 : align256((size_t)P * 4);
+        const size_t o_g = o;    o += align256((size_t)P * inter * 4);
+        const size_t o_u = o;    o += align256((size_t)P * inter * 4);
+        const size_t o_o = o;    o += align256((size_t)P * hidden * 4);
+        if (int rc = ensure_scratch(ctx, o)) return rc;
+        char *sc = (char *)ctx->scratch;
+        hipError_t e;
+        const int32_t *ids = ids_in;
+        const float *wts = wts_in;
+        if (!ids_in) {
+            e = arfq::launch_moe_route(logits, tokens, E, top_k, norm_topk ? 1 : 0,
+                                       (int32_t *)(sc + o_ids), (float *)(sc + o_w), ctx->stream);
+            if (e != hipSuccess) return hip_fail(ctx, e, "moe: route launch");
+            ids = (const int32_t *)(sc + o_ids);
+            wts = (const float *)(sc + o_w);
+        }
+        float *g = (float *)(sc + o_g), *u = (float *)(sc + o_u), *ob = (float *)(sc + o_o);
+        e = arfq::launch_gemv_pairs(gate, P, ids, x, x_dtype, top_k, nullptr, nullptr, g, ctx->stream);
+        if (e == hipSuccess)
+            e = arfq::launch_gemv_pairs(up, P, ids, x, x_dtype, top_k, nullptr, nullptr, u, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "moe: gate/up GEMV launch");
+        e = arfq::launch_gemv_pairs(down, P, ids, nullptr, ARFQ_F32, 1, g, u, ob, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "moe: down GEMV launch");
+        e = arfq::launch_moe_combine(ob, ids, wts, tokens, top_k, E, hidden, y, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "moe: combine launch");
+        return ARFQ_OK;
+    }
     const int64_t max_tiles = arfq::moe_max_tiles(P, E);
     const bool gsums = gate->qtype == ARFQ_Q4_K, dsums = down->qtype == ARFQ_Q4_K;
     size_t o = 0;

@@ -59,6 +59,14 @@ hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s);
 hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, float *y,
                        hipStream_t s);
 bool gemv_supports(const arfq_weight *w, int64_t m);
+// MoE decode GEMVs over P (token, expert) pairs, Q4_K: y[p] (w->n floats) = W_ids[p] .
+// x_p, where x_p is row p / x_div of x (f32 or f16, [*, w->k]) or, when g is
+// set, silu(g[p]) * u[p] (g, u: [P, w->k] f32).  Pairs with an out-of-range id
+// are skipped.
+bool gemv_pairs_supports(const arfq_weight *w);
+hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,
+                             int x_dtype, int x_div, const float *g, const float *u, float *y,
+                             hipStream_t s);
 
 // ---- arfq_gemm.hip ----
 // Launch shape and scratch layout of the dequant-into-LDS MFMA GEMM.
@@ -116,5 +124,7 @@ hipError_t launch_moe_combine(const float *o, const int32_t *ids, const float *w
 constexpr int MOE_EXPERTS_MAX = 512;
 constexpr int MOE_ROUTE_EXPERTS_MAX = 1024;
 constexpr int MOE_TOPK_MAX = 64;
+// at most this many (token, expert) pairs take the indirect-GEMV decode path
+constexpr int64_t MOE_DECODE_PAIRS_MAX = 128;
 
 }  // namespace arfq

@@ -57,11 +57,13 @@ def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.flo
     return ms / steps, ms
 
 
-def time_moe(ctx, steps, warmup, copies):
-    """Average ms per arfq_moe call (C5) rotating `copies` weight sets, after `warmup` calls."""
+def time_moe(ctx, steps, warmup, copies, tokens=None):
+    """Average ms per arfq_moe call (C5's experts; `tokens` defaults to C5's 512) rotating
+    `copies` weight sets, after `warmup` calls."""
     from arf_amd import QType, synth
     cfg = synth.CONFIGS["c5_moe"]
     E, T, k, hdim, inter = cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"], cfg["inter"]
+    T = tokens or T
     sets = []
     for c in range(copies):
         g = ctx.upload(QType.Q4_K, synth.weight("q4_k", inter, hdim, seed=0xA7F00005 + 3 * c, experts=E),
@@ -325,6 +327,34 @@ def main():
             log(f"[bench] C5: {ms5 * 1e3:.1f} us/launch")
         except arf_amd.ArfqError as e:
             configs["c5_moe_q4_k_e128_top8_t512_h2048_i768"] = {"error": str(e)}
+        # the survey's next rows, on the kernels above: small-T MoE decode (C5's experts at
+        # T = 1, 4, 16: bytes = the distinct experts' weights the routing touches, at most
+        # T * top_k) and a vocab-wide lm_head GEMV (Q6_K, N = 151936, K = 5120)
+        cfg = synth.CONFIGS["c5_moe"]
+        per_expert = 3 * cfg["inter"] * cfg["hidden"] // 256 * 144
+        for T in (1, 4, 16):
+            try:
+                msT = time_moe(ctx, 200, 50, 3, tokens=T)
+                ids = set()
+                lg = synth.router_logits(T, cfg["experts"], seed=0xA7F00009)
+                for t in range(T):
+                    ids.update(np.argsort(-lg[t], kind="stable")[:cfg["top_k"]].tolist())
+                bT = len(ids) * per_expert
+                configs[f"moe_decode_q4_k_e128_top8_t{T}"] = {
+                    "us_per_launch": round(msT * 1e3, 2), "experts_touched": len(ids),
+                    "GB/s": round(bT / msT / 1e6, 1), "hbm_frac": round(bT / msT / 1e6 / HBM_PEAK_GBS, 4)}
+                log(f"[bench] MoE T={T}: {msT * 1e3:.1f} us/launch ({len(ids)} experts)")
+            except arf_amd.ArfqError as e:
+                configs[f"moe_decode_q4_k_e128_top8_t{T}"] = {"error": str(e)}
+        try:
+            msv, _ = time_matmul(ctx, "q6_k", 1, 151936, 5120, 200, 20, 2, seed=0xA7F0000A)
+            bv = algorithmic_bytes("q6_k", 1, 151936, 5120)
+            configs["lm_head_q6_k_gemv_m1_k5120_n151936"] = {
+                "us_per_launch": round(msv * 1e3, 2), "GB/s": round(bv / msv / 1e6, 1),
+                "hbm_frac": round(bv / msv / 1e6 / HBM_PEAK_GBS, 4)}
+            log(f"[bench] lm_head Q6_K m=1 n=151936: {msv * 1e3:.1f} us/launch")
+        except arf_amd.ArfqError as e:
+            configs["lm_head_q6_k_gemv_m1_k5120_n151936"] = {"error": str(e)}
 
     cpu = None
     if not args.no_cpu:

@@ -107,6 +107,23 @@ def _moe_gpu(ctx, ws, x, logits, top_k, norm):
     return y.numpy()
 
 
+@pytest.mark.parametrize("T", [1, 4, 16])
+def test_moe_decode_small_T_at_c5_experts(gpu_ctx, oracle, T):
+    # the survey's next row (small-T MoE decode) on C5's expert shapes: 128 experts, top-8
+    from arf_amd import synth
+    E, k, hidden, inter = 128, 8, 2048, 768
+    _say("case: moe decode T =", T)
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=900 + T)
+    x = synth.activations(T, hidden, seed=T + 17, dtype=np.float16)
+    logits = synth.router_logits(T, E, seed=T + 18)
+    got = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    want = oracle.moe_forward(x.astype(np.float32), raw[0], raw[1], raw[2], E, inter, logits, k,
+                              True)
+    e = rel_err(got, want)
+    _say("rel err", e)
+    assert e <= TOL
+
+
 @pytest.mark.parametrize("T,E,k,hidden,inter", [(5, 8, 2, 256, 256), (70, 16, 4, 512, 768),
                                                 (1, 4, 4, 256, 512), (129, 6, 2, 768, 256),
                                                 (70, 16, 4, 512, 256)])

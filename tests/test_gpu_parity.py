@@ -149,6 +149,15 @@ def test_next_formats_beyond_the_gemv_are_unsupported(gpu_ctx, qtype):
         assert e.value.status == ARFQ_E_UNSUPPORTED
 
 
+@pytest.mark.parametrize("qtype", ["q6_k", "q8_0"])
+def test_vocab_wide_lm_head_gemv(gpu_ctx, oracle, qtype):
+    # the survey's next row: an lm_head GEMV over a 151936-token vocabulary (K cut to 512
+    # so the oracle stays quick; the bench runs K = 5120)
+    _say("case: lm_head", qtype)
+    got, raw, x = _matmul(gpu_ctx, qtype, 151936, 512, 1, seed=0xA7F0000A)
+    assert rel_err(got, oracle.matmul_q(qtype, x, raw, 151936)) <= TOL
+
+
 def test_shape_errors_raise(gpu_ctx):
     from arf_amd import QType, synth
     raw = synth.weight("q4_k", 4, 256, seed=1)
