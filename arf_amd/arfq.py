@@ -87,6 +87,7 @@ _SIGS = {
     "arfq_timer_start": (_int, [_vp]),
     "arfq_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
     "arfq_matmul_repeat": (_int, [_vp, ctypes.POINTER(_vp), _int, _int, _i64, _vp, _int, _vp]),
+    "arfq_ffn": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _vp]),
     "arfq_gguf_is_gguf": (_int, [ctypes.c_char_p]),
     "arfq_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "arfq_gguf_close": (_int, [_vp]),
@@ -289,6 +290,11 @@ class Context:
         _check(self.handle, load_library().arfq_moe_route(
             self.handle, logits.ptr, int(tokens), int(n_experts), int(top_k), int(bool(norm_topk)),
             ids.ptr, weights.ptr))
+
+    def ffn(self, gate, up, down, x, m, y):
+        """y[m, hidden] = down . (silu(gate . x) * (up . x)) (ffn_dispatch / Mlp::forward)."""
+        _check(self.handle, load_library().arfq_ffn(self.handle, gate.handle, up.handle, down.handle,
+                                                    int(m), x.ptr, y.ptr))
 
     def moe(self, gate, up, down, logits, tokens, top_k, norm_topk, x, y):
         xd = DType.F16 if x.dtype == np.float16 else DType.F32

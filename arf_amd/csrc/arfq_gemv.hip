@@ -513,6 +513,15 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     gemv_q4k_body<MX, XR, PF>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n, nblk, m);
 }
 
+// The FFN's down GEMV: x = silu(g) * u over m row-major rows (g, u: [m][k]).
+template <int MX, int XR>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_swiglu(
+    const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
+    uint32_t qs_bytes, const float *__restrict__ g, const float *__restrict__ u,
+    float *__restrict__ y, int n, int nblk, int m) {
+    gemv_q4k_body<MX, XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsSwiglu{g, u, 0}, y, n, nblk, m);
+}
+
 // MoE decode: blockIdx.y = pair p, one x row each, the weight of expert ids[p]
 // (its n rows split over gridDim.x workgroups) into y row p.  A pair whose id
 // is out of range is dropped (its row is not written; the combine skips it).
@@ -1290,6 +1299,34 @@ static hipError_t launch_pairs_t(const arfq_weight *w, int64_t P, const int32_t 
             (const uint8_t *)w->s0, (const uint8_t *)w->s1, (uint32_t)(nb * 16), (uint32_t)(nb * 128), xs, y,
             (int)w->n, (int)(w->k / 256), ids, w->experts);
     return hipGetLastError();
+}
+
+template <int MX, int XR>
+static hipError_t launch_swiglu_t(const arfq_weight *w, int m, const float *g, const float *u,
+                                  float *y, hipStream_t s) {
+    const int64_t nb = w->n * (w->k / 256);
+    gemv_q4k_swiglu<MX, XR><<<(unsigned)q4k_gemv_grid(w), Q4K_GEMV_THREADS, q4k_gemv_lds(w, MX), s>>>(
+        (const uint8_t *)w->s0, (uint32_t)(nb * 16), (const uint8_t *)w->s1, (uint32_t)(nb * 128), g, u,
+        y, (int)w->n, (int)(w->k / 256), m);
+    return hipGetLastError();
+}
+template <int MX>
+static hipError_t launch_swiglu_mx(const arfq_weight *w, int m, const float *g, const float *u,
+                                   float *y, hipStream_t s) {
+    const int64_t rounds = ((int64_t)m * (w->k / 8) + Q4K_GEMV_THREADS - 1) / Q4K_GEMV_THREADS;
+    if (rounds <= 1) return launch_swiglu_t<MX, 1>(w, m, g, u, y, s);
+    if (rounds <= 2) return launch_swiglu_t<MX, 2>(w, m, g, u, y, s);
+    return launch_swiglu_t<MX, 4>(w, m, g, u, y, s);
+}
+bool gemv_swiglu_supports(const arfq_weight *w, int64_t m) {
+    return w->qtype == ARFQ_Q4_K && w->experts == 1 && gemv_supports(w, m);
+}
+hipError_t launch_gemv_swiglu(const arfq_weight *w, int64_t m, const float *g, const float *u,
+                              float *y, hipStream_t s) {
+    if (!gemv_swiglu_supports(w, m)) return hipErrorInvalidValue;
+    if (m == 1) return launch_swiglu_mx<1>(w, 1, g, u, y, s);
+    if (m == 2) return launch_swiglu_mx<2>(w, 2, g, u, y, s);
+    return launch_swiglu_mx<4>(w, (int)m, g, u, y, s);
 }
 
 hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,

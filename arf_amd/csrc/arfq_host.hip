@@ -487,6 +487,49 @@ int arfq_moe_ids(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
     return moe_enqueue(ctx, gate, up, down, nullptr, ids, weights, tokens, top_k, 0, x, x_dtype, y);
 }
 
+// -------------------------------------------------------------------- FFN ----
+
+// Scratch bytes a matmul of w at m rows needs (GEMM plans; the GEMV needs none).
+static size_t matmul_scratch(const arfq_weight *w, int64_t m) {
+    if (arfq::gemv_supports(w, m)) return 0;
+    return arfq::gemm_supports(w, m) ? arfq::gemm_plan(w, m, ARFQ_F32).scratch_bytes : 0;
+}
+
+int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
+             int64_t m, const float *x, float *y) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (!gate || !up || !down) return fail(ctx, ARFQ_E_INVALID, "ffn: null weight");
+    if (m < 0) return fail(ctx, ARFQ_E_SHAPE, "ffn: m < 0");
+    if (m > 0 && (!x || !y)) return fail(ctx, ARFQ_E_INVALID, "ffn: null x or y");
+    if (gate->experts != 1 || up->experts != 1 || down->experts != 1)
+        return fail(ctx, ARFQ_E_SHAPE, "ffn: expert-stacked weights (use arfq_moe)");
+    if (up->n != gate->n || up->k != gate->k || down->n != gate->k || down->k != gate->n)
+        return fail(ctx, ARFQ_E_SHAPE, "ffn: want gate/up [inter, hidden] and down [hidden, inter]");
+    if (m == 0) return ARFQ_OK;
+    if (int rc = use_device(ctx)) return rc;
+    const int64_t inter = gate->n;
+    const bool fused = arfq::gemv_swiglu_supports(down, m);
+    // the GEMM plans use the scratch from offset 0; g, u (and h) sit above the largest
+    size_t base = std::max({matmul_scratch(gate, m), matmul_scratch(up, m),
+                            fused ? (size_t)0 : matmul_scratch(down, m)});
+    base = align256(base);
+    const size_t gb = align256((size_t)m * inter * 4);
+    if (int rc = ensure_scratch(ctx, base + (fused ? 2 : 3) * gb)) return rc;
+    char *sc = (char *)ctx->scratch;
+    float *g = (float *)(sc + base), *u = (float *)(sc + base + gb), *h = (float *)(sc + base + 2 * gb);
+    if (int rc = matmul_enqueue(ctx, gate, 0, m, x, ARFQ_F32, g)) return rc;
+    if (int rc = matmul_enqueue(ctx, up, 0, m, x, ARFQ_F32, u)) return rc;
+    hipError_t e;
+    if (fused) {
+        e = arfq::launch_gemv_swiglu(down, m, g, u, y, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "ffn: down GEMV launch");
+        return ARFQ_OK;
+    }
+    e = arfq::launch_swiglu(g, u, h, m * inter, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn: swiglu launch");
+    return matmul_enqueue(ctx, down, 0, m, h, ARFQ_F32, y);
+}
+
 int arfq_dequant_f32(arfq_ctx *ctx, const arfq_weight *w, float *out) {
     if (!ctx) return ARFQ_E_INVALID;
     if (!w || !out) return fail(ctx, ARFQ_E_INVALID, "dequant: null argument");

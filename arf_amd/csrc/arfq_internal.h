@@ -63,6 +63,13 @@ bool gemv_supports(const arfq_weight *w, int64_t m);
 // x_p, where x_p is row p / x_div of x (f32 or f16, [*, w->k]) or, when g is
 // set, silu(g[p]) * u[p] (g, u: [P, w->k] f32).  Pairs with an out-of-range id
 // are skipped.
+// The FFN's down projection: y[m, n] = W . (silu(g) * u), g and u [m, w->k] f32
+// (Q4_K, m <= 4).
+bool gemv_swiglu_supports(const arfq_weight *w, int64_t m);
+hipError_t launch_gemv_swiglu(const arfq_weight *w, int64_t m, const float *g, const float *u,
+                              float *y, hipStream_t s);
+// h = silu(g) * u elementwise (n floats)
+hipError_t launch_swiglu(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 bool gemv_pairs_supports(const arfq_weight *w);
 hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,
                              int x_dtype, int x_div, const float *g, const float *u, float *y,

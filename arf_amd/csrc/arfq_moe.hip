@@ -420,6 +420,21 @@ __global__ void moe_combine_kernel(const float *__restrict__ o, const int32_t *_
     reinterpret_cast<float4 *>(y + t * hidden)[c4] = acc;
 }
 
+// ---- SwiGLU --------------------------------------------------------------------
+// h = silu(g) * u, silu(v) = v / (1 + exp(-v)) (crates/arf-ml/src/lib.rs:160-162;
+// the gate|up kernel's expression).
+__global__ void swiglu_kernel(const float *__restrict__ g, const float *__restrict__ u,
+                              float *__restrict__ h, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) h[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+}
+
+hipError_t launch_swiglu(const float *g, const float *u, float *h, int64_t n, hipStream_t s) {
+    if (n == 0) return hipSuccess;
+    swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(g, u, h, n);
+    return hipGetLastError();
+}
+
 // ---- launchers -----------------------------------------------------------------
 
 hipError_t launch_moe_route(const float *logits, int64_t tokens, int E, int top_k, int norm,

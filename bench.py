@@ -57,6 +57,28 @@ def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.flo
     return ms / steps, ms
 
 
+def time_ffn(ctx, qts, hidden, inter, m, steps, warmup, copies):
+    """Average ms per arfq_ffn call (gate/up/down of qtypes qts) over `copies` weight sets."""
+    from arf_amd import QType, synth
+    shapes = [(inter, hidden), (inter, hidden), (hidden, inter)]
+    sets = [[ctx.upload(QType[q.upper()], synth.weight(q, n, k, seed=0xA7F00010 + 3 * c + i), n, k)
+             for i, (q, (n, k)) in enumerate(zip(qts, shapes))] for c in range(copies)]
+    x = ctx.to_device(synth.activations(m, hidden, seed=0xA7F0000F))
+    y = ctx.empty((m, hidden), np.float32)
+    for i in range(warmup):
+        ctx.ffn(*sets[i % copies], x, m, y)
+    ctx.sync()
+    ctx.timer_start()
+    for i in range(steps):
+        ctx.ffn(*sets[i % copies], x, m, y)
+    ms = ctx.timer_stop()
+    ctx.sync()
+    for ws in sets:
+        for w in ws:
+            w.free()
+    return ms / steps
+
+
 def time_moe(ctx, steps, warmup, copies, tokens=None):
     """Average ms per arfq_moe call (C5's experts; `tokens` defaults to C5's 512) rotating
     `copies` weight sets, after `warmup` calls."""
@@ -355,6 +377,18 @@ def main():
             log(f"[bench] lm_head Q6_K m=1 n=151936: {msv * 1e3:.1f} us/launch")
         except arf_amd.ArfqError as e:
             configs["lm_head_q6_k_gemv_m1_k5120_n151936"] = {"error": str(e)}
+        # the dense FFN (gate / up / SwiGLU / down) of one decode step at C2's shape
+        for qts, tag in ((("q4_k", "q4_k", "q4_k"), "q4_k"), (("q4_k", "q4_k", "q6_k"), "q4_k_down_q6_k")):
+            try:
+                msf = time_ffn(ctx, qts, 5120, 17408, 1, 300, 30, 2)
+                bf = sum(algorithmic_bytes(q, 1, n_, k_) for q, (n_, k_) in
+                         zip(qts, [(17408, 5120), (17408, 5120), (5120, 17408)]))
+                configs[f"ffn_{tag}_m1_h5120_i17408"] = {
+                    "us_per_launch": round(msf * 1e3, 2), "GB/s": round(bf / msf / 1e6, 1),
+                    "hbm_frac": round(bf / msf / 1e6 / HBM_PEAK_GBS, 4)}
+                log(f"[bench] FFN {tag} m=1: {msf * 1e3:.1f} us/launch")
+            except arf_amd.ArfqError as e:
+                configs[f"ffn_{tag}_m1_h5120_i17408"] = {"error": str(e)}
 
     cpu = None
     if not args.no_cpu:

@@ -178,6 +178,17 @@ int arfq_timer_stop(arfq_ctx *ctx, float *ms);
 int arfq_matmul_repeat(arfq_ctx *ctx, const arfq_weight *const *ws, int n_ws, int iters,
                        int64_t m, const void *x, int x_dtype, float *y);
 
+/* The dense FFN of one decode/prefill step on already-normalised x (f32,
+ * [m, hidden], device): y = down . (silu(gate . x) * (up . x)), f32 [m, hidden];
+ * gate/up [inter, hidden], down [hidden, inter], single matrices of any qtype
+ * the matmul takes.  Replaces the island's ffn_dispatch (gate GEMV, up GEMV,
+ * the SwiGLU kernel, down GEMV on one queue;
+ * crates/arf-gpu/src/gpu/metal/island.rs:13436-13529) and Mlp::forward
+ * (crates/arf-core/src/model/mlp.rs:20-24).  With Q4_K down weights at m <= 4
+ * the SwiGLU is applied as the down GEMV reads its x (no intermediate). */
+int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
+             int64_t m, const float *x, float *y);
+
 /* ---- GGUF reader ---------------------------------------------------------
  * A GGUF v3 file opened read-only and memory-mapped; tensors are read in place
  * (LazyGguf, crates/arf-core/src/model/gguf.rs:365-564).  Errors of

@@ -253,3 +253,41 @@ def test_c5_moe_full(gpu_ctx, oracle):
     _say("C5 rel err (24 sampled tokens)", e)
     assert e <= TOL
     assert np.all(np.isfinite(got))
+
+
+# ------------------------------------------------------------------- FFN ----
+def _ffn_oracle(oracle, x, raws, qts, inter, hidden):
+    g = oracle.matmul_q(qts[0], x, raws[0], inter)
+    u = oracle.matmul_q(qts[1], x, raws[1], inter)
+    h = (g / (np.float32(1.0) + np.exp(-g)) * u).astype(np.float32)
+    return oracle.matmul_q(qts[2], h, raws[2], hidden)
+
+
+@pytest.mark.parametrize("qts,hidden,inter,m", [
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 1), (("q4_k", "q4_k", "q4_k"), 512, 768, 3),
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 8), (("q4_k", "q4_k", "q6_k"), 1024, 512, 1),
+    (("q8_0", "q8_0", "q5_k"), 768, 256, 2), (("q4_k", "q4_k", "q4_k"), 5120, 17408, 1)])
+def test_ffn_matches_mlp_forward(gpu_ctx, oracle, qts, hidden, inter, m):
+    # ffn_dispatch / Mlp::forward (island.rs:13436-13529, mlp.rs:20-24): the fused SwiGLU-into-
+    # down GEMV (Q4_K down, m <= 4) and the SwiGLU kernel + matmul path
+    from arf_amd import QType, synth
+    _say("case: ffn", qts, hidden, inter, m)
+    shapes = [(inter, hidden), (inter, hidden), (hidden, inter)]
+    raws = [synth.weight(q, n, k, seed=31 + i) for i, (q, (n, k)) in enumerate(zip(qts, shapes))]
+    ws = [gpu_ctx.upload(QType[q.upper()], r, n, k) for q, r, (n, k) in zip(qts, raws, shapes)]
+    x = synth.activations(m, hidden, seed=37)
+    y = gpu_ctx.empty((m, hidden), np.float32)
+    gpu_ctx.ffn(ws[0], ws[1], ws[2], gpu_ctx.to_device(x), m, y)
+    e = rel_err(y.numpy(), _ffn_oracle(oracle, x, raws, qts, inter, hidden))
+    _say("rel err", e)
+    assert e <= TOL
+
+
+def test_ffn_shape_errors(gpu_ctx):
+    from arf_amd import QType, synth
+    g = gpu_ctx.upload(QType.Q4_K, synth.weight("q4_k", 256, 512, seed=1), 256, 512)
+    d = gpu_ctx.upload(QType.Q4_K, synth.weight("q4_k", 256, 512, seed=2), 256, 512)  # not [512, 256]
+    x = gpu_ctx.to_device(np.zeros((1, 512), np.float32))
+    y = gpu_ctx.empty((1, 512), np.float32)
+    with pytest.raises(ValueError):
+        gpu_ctx.ffn(g, g, d, x, 1, y)
