@@ -299,14 +299,9 @@ template <class F, int TA, class XT>
 static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const XT *x,
                               const uint16_t *xs, float *y, float *part, uint32_t *tick, int S,
                               hipStream_t s) {
-    static bool attr_set = false;
     constexpr size_t lds = sk_lds<F, TA, 1>();
-    if (!attr_set) {
-        hipError_t err = hipFuncSetAttribute((const void *)gemm_sk<F, TA, XT>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (err != hipSuccess) return err;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, XT>, lds, lds_set)) return err;
     const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
     gemm_sk<F, TA, XT><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, y, part, tick, (int)m, (int)w->n,
                                                      (int)w->k);
@@ -343,14 +338,9 @@ template <class F, int BM, bool XS>
 static hipError_t launch_gemm_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *xh,
                                 const _Float16 *xl, const uint16_t *xs, float *out, int S,
                                 hipStream_t s) {
-    static bool attr_set = false;  // the attribute belongs to the kernel: set once per process
     constexpr size_t lds = gm_lds(BM, XS);
-    if (!attr_set) {
-        hipError_t err = hipFuncSetAttribute((const void *)gemm_q<F, BM, XS>,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (err != hipSuccess) return err;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)gemm_q<F, BM, XS>, lds, lds_set)) return err;
     const int mt = (int)((m + BM - 1) / BM), nt = (int)((w->n + GM_BN - 1) / GM_BN);
     const int xcd = (mt % 8 == 0) ? 1 : 0;
     const dim3 grid((unsigned)(mt * nt), (unsigned)S);
@@ -390,13 +380,8 @@ static hipError_t launch_bd_q4k(const arfq_weight *w, int e, int64_t m, const _F
     const int tiles = mt * nt, nsplit = tiles - p.bd_full;
     const int xcd = (mt % 8 == 0 && p.bd_full % mt == 0) ? 1 : 0;
     if (nsplit && !part) return hipErrorInvalidValue;
-    static bool attr_set = false;  // the attribute belongs to the kernel: set once per process
-    if (!attr_set) {
-        hipError_t err = hipFuncSetAttribute((const void *)gemm_bd_q4k,
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)bd_lds());
-        if (err != hipSuccess) return err;
-        attr_set = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)gemm_bd_q4k, bd_lds(), lds_set)) return err;
     const unsigned items = (unsigned)(p.bd_full + nsplit * p.bd_chunks);
     gemm_bd_q4k<<<items, BD_THREADS, bd_lds(), s>>>(
         (const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8, x, xs, y, part, (int)m,

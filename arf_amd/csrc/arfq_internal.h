@@ -5,6 +5,7 @@
 #include <hip/hip_fp16.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <atomic>
 #include <string>
 
 #include "../../include/arfq.h"
@@ -39,6 +40,20 @@ struct arfq_weight {
 };
 
 namespace arfq {
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) for `fn` on the current
+// device, once per device: `done` (one per kernel, zero-initialised static)
+// holds a bit per device index already set.
+inline hipError_t set_max_lds_once(const void *fn, size_t bytes, std::atomic<uint64_t> &done) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+    return e;
+}
 
 // block geometry
 inline int qk_of(int qtype) { return qtype == ARFQ_Q8_0 ? 32 : 256; }

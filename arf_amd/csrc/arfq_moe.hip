@@ -465,15 +465,10 @@ static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const 
                            const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
                            const void *tiles, const int32_t *ntiles, int64_t max_tiles, float *h,
                            hipStream_t s) {
-    static bool attr = false;
     constexpr size_t lds = sk_lds<F, 2, 1, MOE_GU_THREADS>();
     static_assert(lds >= (size_t)4 * 2 * 16 * 64 * 4, "room for the up -> gate hand-off");
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)moe_gateup_kernel<F>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)moe_gateup_kernel<F>, lds, lds_set)) return err;
     const int64_t eb = gw->n * g.nblk;
     const dim3 grid((unsigned)max_tiles, (unsigned)((gw->n + 127) / 128));
     moe_gateup_kernel<F><<<grid, MOE_GU_THREADS, lds, s>>>(g, u, eb, x, xs, (int)gw->k, (int)gw->n,
@@ -487,14 +482,9 @@ static hipError_t down_t(const F &d, const arfq_weight *dw, const _Float16 *h, c
                          const float *rs, const int32_t *off, const int32_t *sorted,
                          const void *tiles, const int32_t *ntiles, int64_t max_tiles, float *o,
                          hipStream_t s) {
-    static bool attr = false;
     constexpr size_t lds = sk_lds<F, 2, 1>();
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute((const void *)moe_down_kernel<F>,
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)moe_down_kernel<F>, lds, lds_set)) return err;
     const int64_t eb = dw->n * d.nblk;
     const dim3 grid((unsigned)max_tiles, (unsigned)((dw->n + 127) / 128));
     moe_down_kernel<F><<<grid, SK_THREADS, lds, s>>>(d, eb, h, hs, rs, (int)dw->k, (int)dw->n, off,
