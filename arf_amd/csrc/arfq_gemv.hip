@@ -541,8 +541,9 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
                                       y + (int64_t)p * n, n, nblk, 1);
 }
 
-// ------------------------------------------------------------ Q6_K (dot) ----
-// Integer-dot GEMV for one or two x rows.  x is quantized per 32-element
+// --------------------------------------------- Q6_K / Q5_K / IQ4_XS (dot) ----
+// Integer-dot GEMV for up to four x rows (gemv_dot<Format, MX, XR>; the
+// formats are below).  x is quantized per 32-element
 // block to 16-bit fixed point X = rint(x * 2^(15-e)) (as for Q4_K) and held in
 // LDS as a low-byte plane (u8) and a high-byte plane (i8, X >> 8), both in
 // element order, with the sum of every 16 elements and 2^(e-15) per 32.  A
@@ -552,9 +553,9 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
 // (d*sc)*(q-32) per weight (gguf.rs:2120-2123), factorised.
 // Work split as gemv_q4k: two 512-thread workgroups per CU, steps = (row,
 // column of 4 blocks) claimed in chunks of 2 rows of one column.  Lane l of a
-// 16-lane group serves block 4*column + l/4 and its 48-byte chunk c = l%4
-// (64 codes: 4 quadrant sub-blocks of 16), one scale dword (c) whose
-// neighbours come from its quad by DPP, and the block's d.
+// 16-lane group serves block 4*column + l/4 and its 64 codes c = l%4 (four
+// 16-code quadrants); for Q6_K that is its 48-byte chunk c, one scale dword (c)
+// whose neighbours come from its quad by DPP, and the block's d.
 constexpr int Q6K_GEMV_THREADS = 512;
 constexpr int Q6K_GEMV_GROUPS = Q6K_GEMV_THREADS / 16;
 constexpr int Q6K_GEMV_PF = 2;
