@@ -220,7 +220,9 @@ bool gemm_supports(const arfq_weight *w, int64_t m) {
     if (m < 1 || m > INT32_MAX / 2 || w->n > INT32_MAX / 2 || w->k > INT32_MAX / 2) return false;
     switch (w->qtype) {
     case ARFQ_Q4_K:
-    case ARFQ_Q6_K: return true;
+    case ARFQ_Q6_K:
+    case ARFQ_Q5_K:
+    case ARFQ_IQ4_XS: return true;
     case ARFQ_Q8_0: return w->k % GM_BK == 0;
     default: return false;
     }
@@ -231,20 +233,24 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     GemmPlan p;
     const int cus = w->ctx && w->ctx->cus > 0 ? w->ctx->cus : 256;
-    p.skinny = m <= 64 && w->k % 256 == 0;
+    // Q5_K and IQ4_XS have only the skinny kernel: above 64 rows it runs once
+    // per 64-row chunk of x
+    const bool chunked = w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS;
+    const bool kind2 = w->qtype == ARFQ_Q4_K || w->qtype == ARFQ_Q5_K;  // min term: x sums
+    p.skinny = (m <= 64 || chunked) && w->k % 256 == 0;
     p.bm = m > 64 ? 128 : 64;
     // f32 x: rounded to f16 for the skinny kernel and for prefill shapes (m > 64,
     // as the reference's half tiles), split into f16 hi + lo otherwise
     p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && m <= 64;
-    // the skinny kernel rounds an f32 x itself at m <= 32, except for Q4_K,
-    // whose x sub-block sums come from the same preparation pass (at m > 32
-    // the staging registers would not fit beside two waves per SIMD)
-    p.convert = x_dtype == ARFQ_F32 && !(p.skinny && m <= 32 && w->qtype != ARFQ_Q4_K);
+    // the skinny kernel rounds an f32 x itself at m <= 32, except for Q4_K and
+    // Q5_K, whose x sub-block sums come from the same preparation pass (at
+    // m > 32 the staging registers would not fit beside two waves per SIMD)
+    p.convert = x_dtype == ARFQ_F32 && !(p.skinny && m <= 32 && !kind2);
     // Q4_K prefill: the direct-operand kernel (one launch, no split-K)
     p.bd = !p.skinny && w->qtype == ARFQ_Q4_K && m > 64 &&
            w->n * (w->k / 2) < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
     // the exact Q4_K paths read x sub-block sums (min term)
-    p.sums = (p.skinny || p.bd) && w->qtype == ARFQ_Q4_K;
+    p.sums = (p.skinny || p.bd) && kind2;
     int64_t S;
     size_t bd_part = 0;
     if (p.bd) {
@@ -288,7 +294,8 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     o += p.sums ? al256((size_t)m * (w->k / 16) * 2) : 0;
     p.off_part = o;
     if (p.skinny)  // partials in register order: [split][column tile][wave][8-row group][lane] float4
-        o += p.splits > 1 ? al256((size_t)p.splits * ((w->n + 127) / 128) * ((m + 7) / 8) * 4096) : 0;
+        o += p.splits > 1 ? al256((size_t)p.splits * ((w->n + 127) / 128) * ((std::min<int64_t>(m, 64) + 7) / 8) * 4096)
+                          : 0;
     else
         o += p.splits > 1 ? al256((size_t)p.splits * m * w->n * 4) : al256(bd_part);
     p.scratch_bytes = o;
@@ -332,6 +339,30 @@ SkQ6K sk_q6k(const arfq_weight *w) {
 }
 SkQ80 sk_q80(const arfq_weight *w) {
     return {(const uint4 *)w->s0, (const uint16_t *)w->s1, (int)(w->k / 32)};
+}
+SkQ5K sk_q5k(const arfq_weight *w) {
+    return {(const uint4 *)w->s0, (const uint8_t *)w->s1, (int)(w->k / 256)};
+}
+SkIQ4XS sk_iq4xs(const arfq_weight *w) {
+    return {(const uint2 *)w->s0, (const uint4 *)w->s1, (int)(w->k / 256)};
+}
+
+// The skinny kernel over x rows in chunks of 64 (one launch per chunk; m <= 64
+// is one launch).  Chunks run in stream order and reuse the partials and
+// counters.
+template <class F>
+static hipError_t launch_sk_rows(const F &fmt, const arfq_weight *w, int64_t m, const void *x,
+                                 bool xf32, const uint16_t *xs, float *y, float *part,
+                                 uint32_t *tick, int ntick, int S, hipStream_t s) {
+    for (int64_t r0 = 0; r0 < m; r0 += 64) {
+        const int64_t mc = std::min<int64_t>(64, m - r0);
+        const void *xc = xf32 ? (const void *)((const float *)x + r0 * w->k)
+                              : (const void *)((const _Float16 *)x + r0 * w->k);
+        if (hipError_t err = launch_sk(fmt, w, mc, xc, xf32, xs ? xs + r0 * (w->k / 16) : nullptr,
+                                       y + r0 * w->n, part, tick, ntick, S, s))
+            return err;
+    }
+    return hipSuccess;
 }
 
 template <class F, int BM, bool XS>
@@ -422,6 +453,12 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         case ARFQ_Q8_0:
             return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xf32, xs,
                              y, out, tickets, ntickets, p.splits, s);
+        case ARFQ_Q5_K:
+            return launch_sk_rows(sk_q5k(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets,
+                                  ntickets, p.splits, s);
+        case ARFQ_IQ4_XS:
+            return launch_sk_rows(sk_iq4xs(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets,
+                                  ntickets, p.splits, s);
         default:
             return hipErrorInvalidValue;
         }

@@ -352,9 +352,6 @@ static int check_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *
         return fail(ctx, ARFQ_E_SHAPE, "moe: gate/up/down expert counts differ");
     if (E > arfq::MOE_EXPERTS_MAX) return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: more than 512 experts");
     if (up->qtype != gate->qtype) return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: gate and up differ in qtype");
-    if (gate->qtype == ARFQ_Q5_K || down->qtype == ARFQ_Q5_K || gate->qtype == ARFQ_IQ4_XS ||
-        down->qtype == ARFQ_IQ4_XS)
-        return fail(ctx, ARFQ_E_UNSUPPORTED, "moe: Q5_K / IQ4_XS experts have no grouped GEMM here (Q4_K, Q6_K, Q8_0)");
     if (up->n != gate->n || up->k != gate->k || down->n != gate->k || down->k != gate->n)
         return fail(ctx, ARFQ_E_SHAPE,
                     "moe: want gate/up [inter, hidden] and down [hidden, inter]");
@@ -411,7 +408,9 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
         return ARFQ_OK;
     }
     const int64_t max_tiles = arfq::moe_max_tiles(P, E);
-    const bool gsums = gate->qtype == ARFQ_Q4_K, dsums = down->qtype == ARFQ_Q4_K;
+    // the formats with a min term read x sub-block sums
+    const bool gsums = gate->qtype == ARFQ_Q4_K || gate->qtype == ARFQ_Q5_K;
+    const bool dsums = down->qtype == ARFQ_Q4_K || down->qtype == ARFQ_Q5_K;
     size_t o = 0;
     const size_t o_x = o;     o += x_dtype == ARFQ_F32 ? align256((size_t)tokens * hidden * 2) : 0;
     const size_t o_xs = o;    o += gsums ? align256((size_t)tokens * (hidden / 16) * 2) : 0;
@@ -430,7 +429,7 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     char *sc = (char *)ctx->scratch;
     hipError_t e;
     // the grouped GEMMs read f16 activation tiles (as the reference's half mm_id
-    // tiles) and, for Q4_K, the x sub-block sums
+    // tiles) and, for Q4_K and Q5_K, the x sub-block sums
     const _Float16 *xh = x_dtype == ARFQ_F32 ? (const _Float16 *)(sc + o_x) : (const _Float16 *)x;
     uint16_t *xs = gsums ? (uint16_t *)(sc + o_xs) : nullptr;
     e = arfq::launch_xprep(x, x_dtype, tokens, hidden,

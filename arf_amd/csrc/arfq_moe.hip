@@ -495,6 +495,8 @@ static hipError_t down_t(const F &d, const arfq_weight *dw, const _Float16 *h, c
 SkQ4K sk_q4k(const arfq_weight *w);  // arfq_gemm.hip
 SkQ6K sk_q6k(const arfq_weight *w);
 SkQ80 sk_q80(const arfq_weight *w);
+SkQ5K sk_q5k(const arfq_weight *w);
+SkIQ4XS sk_iq4xs(const arfq_weight *w);
 
 hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, const _Float16 *x,
                              const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
@@ -510,6 +512,12 @@ hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, con
     case ARFQ_Q8_0:
         return gateup_t(sk_q80(gate), sk_q80(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
+    case ARFQ_Q5_K:
+        return gateup_t(sk_q5k(gate), sk_q5k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+                        max_tiles, h, s);
+    case ARFQ_IQ4_XS:
+        return gateup_t(sk_iq4xs(gate), sk_iq4xs(up), gate, x, xs, top_k, off, sorted, tiles,
+                        ntiles, max_tiles, h, s);
     default: return hipErrorInvalidValue;
     }
 }
@@ -525,6 +533,10 @@ hipError_t launch_moe_down(const arfq_weight *down, const _Float16 *h, const uin
         return down_t(sk_q6k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
     case ARFQ_Q8_0:
         return down_t(sk_q80(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+    case ARFQ_Q5_K:
+        return down_t(sk_q5k(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
+    case ARFQ_IQ4_XS:
+        return down_t(sk_iq4xs(down), down, h, hs, rs, off, sorted, tiles, ntiles, max_tiles, o, s);
     default: return hipErrorInvalidValue;
     }
 }

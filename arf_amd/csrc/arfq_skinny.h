@@ -17,7 +17,9 @@
 // scaled by the lane's own d at the block end (lane l's C column is its weight
 // row, so d is a register, not a broadcast).  Q4_K's min term
 // -dmin * sum_j m_j * X_j enters as two bf16 MFMAs against the x sub-block
-// sums X_j.  Q8_0 lanes hold d * q rounded to f16.
+// sums X_j.  Q8_0 lanes hold d * q rounded to f16.  Q5_K is Q4_K with a 5-bit
+// q.  IQ4_XS lanes hold the codebook values; each MFMA covers one sub-block
+// and its result is scaled by that sub-block's d * (ls - 32).
 //
 // K-slot map of step p (64 elements) of block b: lane half h and MFMA kk use
 // elements a_off(p, kk, h) + 0..7 of the block; the x operand is read from LDS
@@ -221,6 +223,122 @@ struct SkQ80 {
     }
 };
 
+// Q5_K: Q4_K's step map, header, scales and min term; the slab row is ggml's
+// qh[32] | qs[128].  Element e of sub-block s = 2p + h is the low (h = 0) or
+// high (h = 1) nibble of qs[32p + e] plus bit s of qh[e] as bit 4 (0..31), so
+// the B operand sc_j * q <= 63 * 31 is an exact f16 integer.
+// (dequant_q5_k, crates/arf-core/src/model/gguf.rs:2053-2090)
+struct SkQ5K {
+    static constexpr int KIND = 2, RB = 160;
+    using Blk = SkQ4K::Blk;
+    const uint4 *hdr;
+    const uint8_t *q;
+    int nblk;
+    __host__ __device__ SkQ5K shifted(int64_t nb) const { return {hdr + nb, q + nb * 160, nblk}; }
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    __device__ const uint8_t *raw(int64_t row, int b) const { return q + (row * nblk + b) * 160; }
+    __device__ Blk load_blk(int64_t row, int b) const { return {ldv(hdr + row * nblk + b)}; }
+    __device__ static float2 scale(const Blk &k) { return SkQ4K::scale(k); }
+    __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
+        const u32x4 q0 = *reinterpret_cast<const u32x4 *>(srow + 32 + 32 * p);
+        const u32x4 q1 = *reinterpret_cast<const u32x4 *>(srow + 48 + 32 * p);
+        const u32x4 h0 = *reinterpret_cast<const u32x4 *>(srow);
+        const u32x4 h1 = *reinterpret_cast<const u32x4 *>(srow + 16);
+        const int s = 2 * p + h;
+        uint32_t sc, mm;
+        q4k_scale_min(k.h.y, k.h.z, k.h.w, s, sc, mm);
+        const float scf = (float)sc;
+        // (1024 + q) * sc - 1024 sc: one fused rounding of the exact q * sc
+        const half2v s1 = h2splat(scf), c1 = h2splat(-1024.f * scf);
+        const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        const uint32_t hw[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            uint32_t o[4];
+#pragma unroll
+            for (int u = 0; u < 2; u++) {
+                // elements 8kk + 4u + 0..3 of the sub-block, one per byte
+                const uint32_t v = ((qw[2 * kk + u] >> (4 * h)) & 0x0F0F0F0Fu) |
+                                   (((hw[2 * kk + u] >> s) & 0x01010101u) << 4);
+                o[2 * u] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), s1, c1);
+                o[2 * u + 1] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u), s1, c1);
+            }
+            f[kk] = u4_to_h8(o[0], o[1], o[2], o[3]);
+        }
+    }
+    __device__ static void minsb(const Blk &k, bf16x8 &hi, bf16x8 &lo) { SkQ4K::minsb(k, hi, lo); }
+};
+
+// IQ4_XS (KIND 3: exact codes, a scale per sub-block): step p = sub-blocks
+// 2p (MFMAs kk = 0, 1) and 2p + 1 (kk = 2, 3), so each MFMA stays inside one
+// sub-block and its f32 result is scaled by d * (ls - 32) of that sub-block
+// (ls - 32 times a code can pass 2048, where f16 integers stop being exact).
+// The slab row is qs[128], sub-block s in bytes 16s .. 16s + 15 (elements
+// 0..15 the low nibbles, 16..31 the high ones); MFMA kk, lane half h takes
+// element 16 (kk & 1) + 8h + i of its sub-block: nibble (kk & 1) of byte 8h + i.
+// The B operand is the codebook value kv (exact in f16).
+// (dequant_iq4_xs, crates/arf-core/src/model/gguf.rs:1937-1976)
+struct SkIQ4XS {
+    static constexpr int KIND = 3, RB = 128;
+    struct Blk {
+        u32x2 h;  // d | scales_h << 16, scales_l
+    };
+    const uint2 *hdr;
+    const uint4 *qs;
+    int nblk;
+    __host__ __device__ SkIQ4XS shifted(int64_t nb) const { return {hdr + nb, qs + nb * 8, nblk}; }
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * (kk >> 1) + 16 * (kk & 1) + 8 * h; }
+    __device__ const uint8_t *raw(int64_t row, int b) const {
+        return reinterpret_cast<const uint8_t *>(qs + (row * nblk + b) * 8);
+    }
+    __device__ Blk load_blk(int64_t row, int b) const { return {ldv(hdr + row * nblk + b)}; }
+    // d * (ls - 32) of sub-blocks 2p and 2p + 1
+    __device__ static float2 sub_scales(const Blk &k, int p) {
+        const float d = h2f(k.h.x);
+        float r[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int s = 2 * p + u;
+            const int ls = (int)(((k.h.y >> (8 * p + 4 * u)) & 0xFu) | (((k.h.x >> (16 + 2 * s)) & 3u) << 4));
+            r[u] = d * (float)(ls - 32);
+        }
+        return make_float2(r[0], r[1]);
+    }
+    __device__ static void frag(const uint8_t *srow, const Blk &, int p, int h, half8 f[4]) {
+        // kvalues_iq4nl + 128 as bytes: entries 0..7 and 8..15, little-endian
+        constexpr uint32_t T0lo = 0xBFAD9881u ^ 0x80808080u, T0hi = 0xF6EADDCFu ^ 0x80808080u;
+        constexpr uint32_t T1lo = 0x26190D01u ^ 0x80808080u, T1hi = 0x71594535u ^ 0x80808080u;
+        const half2v one = h2splat(1.f), m1152 = h2splat(-1152.f);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const u32x2 c = *reinterpret_cast<const u32x2 *>(srow + 16 * (2 * p + u) + 8 * h);
+#pragma unroll
+            for (int nib = 0; nib < 2; nib++) {
+                uint32_t o[4];
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const uint32_t sel = (c[j] >> (4 * nib)) & 0x0F0F0F0Fu;
+                    const uint32_t s7 = sel & 0x07070707u;
+                    const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
+                    const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
+                    const uint32_t hi = (sel >> 3) & 0x01010101u;
+                    const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
+                    const uint32_t v = (v1 & mask) | (v0 & ~mask);
+                    // (1024 + kv + 128) - 1152 = kv, exact
+                    o[2 * j] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), one, m1152);
+                    o[2 * j + 1] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u), one, m1152);
+                }
+                f[2 * u + nib] = u4_to_h8(o[0], o[1], o[2], o[3]);
+            }
+        }
+    }
+    __device__ static float2 scale(const Blk &) { return make_float2(1.f, 0.f); }
+    __device__ static void minsb(const Blk &, bf16x8 &hi, bf16x8 &lo) {
+        hi = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
+        lo = hi;
+    }
+};
+
 // ---- the loop -------------------------------------------------------------------
 // x staging: XR = 32 TA rows x 256 k per block = XR * 32 chunks of 16 B over
 // the NT threads; thread tid stages chunks c = tid + NT i (row c / 32 =
@@ -337,7 +455,8 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
     xstore();
     __syncthreads();
 
-    floatx16 cb[NW][TA], cmin[NW][KIND == 2 ? TA : 1];
+    // KIND 3: cb holds the step's first sub-block (MFMAs 0, 1), cq its second
+    floatx16 cb[NW][TA], cmin[NW][KIND == 2 ? TA : 1], cq[NW][KIND == 3 ? TA : 1];
     if constexpr (KIND == 2) {
 #pragma unroll
         for (int w = 0; w < NW; w++)
@@ -373,7 +492,17 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                     for (int t = 0; t < TU; t++) {
                         const half8 af = *reinterpret_cast<const half8 *>(
                             xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
-                        if (KIND != 0 && p == 0 && kk == 0) {
+                        if constexpr (KIND == 3) {
+                            floatx16 &c = kk < 2 ? cb[w][t] : cq[w][t];
+                            if (kk % 2 == 0) {
+                                floatx16 z;
+#pragma unroll
+                                for (int i = 0; i < 16; i++) z[i] = 0.f;
+                                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], z, 0, 0, 0);
+                            } else {
+                                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], c, 0, 0, 0);
+                            }
+                        } else if (KIND != 0 && p == 0 && kk == 0) {
                             floatx16 z;
 #pragma unroll
                             for (int i = 0; i < 16; i++) z[i] = 0.f;
@@ -385,9 +514,18 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                         }
                     }
                 }
+                if constexpr (KIND == 3) {
+                    // the step's two sub-blocks, each times its own d * (ls - 32)
+                    const float2 ss = F::sub_scales(wb[w], p);
+#pragma unroll
+                    for (int t = 0; t < TU; t++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++)
+                            acc[w][t][i] = fmaf(ss.y, cq[w][t][i], fmaf(ss.x, cb[w][t][i], acc[w][t][i]));
+                }
             }
         }
-        if constexpr (KIND != 0) {
+        if constexpr (KIND == 1 || KIND == 2) {
             // block end: acc += d * C_block; the min term (two bf16 MFMAs)
             // accumulates across blocks in its own registers
 #pragma unroll

@@ -88,15 +88,14 @@ def test_route_shape_errors(gpu_ctx):
 
 
 # ---------------------------------------------------------------- block ----
-def _weights(ctx, E, hidden, inter, seed, qd="q4_k"):
+def _weights(ctx, E, hidden, inter, seed, qd="q4_k", qg="q4_k"):
     from arf_amd import QType, synth
-    qt = {"q4_k": QType.Q4_K, "q6_k": QType.Q6_K, "q8_0": QType.Q8_0}
-    gate = synth.weight("q4_k", inter, hidden, seed=seed, experts=E)
-    up = synth.weight("q4_k", inter, hidden, seed=seed + 1, experts=E)
+    gate = synth.weight(qg, inter, hidden, seed=seed, experts=E)
+    up = synth.weight(qg, inter, hidden, seed=seed + 1, experts=E)
     down = synth.weight(qd, hidden, inter, seed=seed + 2, experts=E)
-    wg = ctx.upload(QType.Q4_K, gate, inter, hidden, E)
-    wu = ctx.upload(QType.Q4_K, up, inter, hidden, E)
-    wd = ctx.upload(qt[qd], down, hidden, inter, E)
+    wg = ctx.upload(QType[qg.upper()], gate, inter, hidden, E)
+    wu = ctx.upload(QType[qg.upper()], up, inter, hidden, E)
+    wd = ctx.upload(QType[qd.upper()], down, hidden, inter, E)
     return (gate, up, down), (wg, wu, wd)
 
 
@@ -157,12 +156,24 @@ def test_moe_f32_x_and_no_renorm(gpu_ctx, oracle):
     assert rel_err(got, want) <= TOL
 
 
-def test_moe_down_q6_k(gpu_ctx, oracle):
-    # down projection in Q6_K (as Q4_K_M GGUFs ship ffn_down_exps); composed from oracle parts
+def _h_f16(h):
+    # the grouped down GEMM reads the intermediate as f16 (as the reference's half
+    # mm_id tiles), each row scaled by 2^-sh first so that its max stays below 2^15
+    amax = float(np.abs(h).max())
+    ex = int(np.frexp(np.float32(amax))[1]) if amax > 0 else 0
+    sc = np.float32(2.0 ** max(ex - 15, 0))
+    return ((h / sc).astype(np.float16).astype(np.float32) * sc).astype(np.float32)
+
+
+@pytest.mark.parametrize("qg,qd", [("q4_k", "q6_k"), ("q5_k", "q5_k"), ("iq4_xs", "iq4_xs"),
+                                   ("q5_k", "iq4_xs")])
+def test_moe_expert_formats(gpu_ctx, oracle, qg, qd):
+    # down projection in Q6_K (as Q4_K_M GGUFs ship ffn_down_exps), and Q5_K / IQ4_XS
+    # experts through the grouped GEMMs; composed from oracle parts
     from arf_amd import synth
-    _say("case: moe q6_k down")
+    _say("case: moe experts", qg, qd)
     T, E, k, hidden, inter = 9, 4, 2, 256, 512
-    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=400, qd="q6_k")
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=400, qd=qd, qg=qg)
     x = synth.activations(T, hidden, seed=401, dtype=np.float16)
     logits = synth.router_logits(T, E, seed=402)
     got = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
@@ -174,11 +185,13 @@ def test_moe_down_q6_k(gpu_ctx, oracle):
     for t in range(T):
         ids, w = oracle.top_k_softmax(logits[t], k, True)
         for e, wt in zip(ids, w):
-            g = oracle.matmul_q("q4_k", xf[t:t + 1], g_e[e], inter)
-            u = oracle.matmul_q("q4_k", xf[t:t + 1], u_e[e], inter)
-            h = (g / (1.0 + np.exp(-g))) * u
-            want[t] += wt * oracle.matmul_q("q6_k", h.astype(np.float32), d_e[e], hidden)[0]
-    assert rel_err(got, want) <= TOL
+            g = oracle.matmul_q(qg, xf[t:t + 1], g_e[e], inter)
+            u = oracle.matmul_q(qg, xf[t:t + 1], u_e[e], inter)
+            h = ((g / (1.0 + np.exp(-g))) * u).astype(np.float32)
+            want[t] += wt * oracle.matmul_q(qd, _h_f16(h), d_e[e], hidden)[0]
+    e = rel_err(got, want)
+    _say("rel err", e)
+    assert e <= TOL
 
 
 def test_moe_ids_matches_moe_and_drops_invalid(gpu_ctx, oracle):

@@ -137,16 +137,19 @@ def test_next_formats_gemv_c2_shape(gpu_ctx, oracle, qtype):
 
 
 @pytest.mark.parametrize("qtype", ["q5_k", "iq4_xs"])
-def test_next_formats_beyond_the_gemv_are_unsupported(gpu_ctx, qtype):
-    from arf_amd import ArfqError, QType, synth
-    from arf_amd.arfq import ARFQ_E_UNSUPPORTED
-    w = gpu_ctx.upload(QType[qtype.upper()], synth.weight(qtype, 32, 512, seed=3), 32, 512)
-    for m, dt in ((5, np.float32), (1, np.float16)):
-        x = gpu_ctx.to_device(synth.activations(m, 512, seed=4).astype(dt))
-        y = gpu_ctx.empty((m, 32), np.float32)
-        with pytest.raises(ArfqError) as e:
-            gpu_ctx.matmul(w, x, m, y)
-        assert e.value.status == ARFQ_E_UNSUPPORTED
+@pytest.mark.parametrize("m,n,k,x16", [(1, 130, 1024, True), (4, 64, 256, True), (5, 130, 1024, False),
+                                       (8, 37, 2816, True), (32, 200, 5120, False),
+                                       (33, 130, 1024, False), (64, 256, 2816, True),
+                                       (100, 130, 1024, False), (130, 64, 512, True)])
+def test_next_formats_skinny_and_chunked(gpu_ctx, oracle, qtype, m, n, k, x16):
+    # Q5_K / IQ4_XS beyond the decode GEMV: the skinny MFMA kernel (m <= 64, f16 x
+    # at any m), run per 64-row chunk above 64 rows; f16 x is what the oracle sees
+    _say("case: next-format skinny", qtype, m, n, k, "f16" if x16 else "f32")
+    dt = np.float16 if x16 else np.float32
+    got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=11 * m + n, x_dtype=dt)
+    e = rel_err(got, oracle.matmul_q(qtype, x.astype(np.float32), raw, n))
+    _say("rel err", e)
+    assert e <= TOL
 
 
 @pytest.mark.parametrize("qtype", ["q6_k", "q8_0"])
