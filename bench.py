@@ -301,25 +301,30 @@ def main():
                 "us_per_launch": round(ms3 * 1e3, 3), "GB/s": round(b3 / ms3 / 1e6, 1),
                 "hbm_frac": round(b3 / ms3 / 1e6 / HBM_PEAK_GBS, 4)}
             log(f"[bench] C3 m={mm}: {ms3 * 1e3:.2f} us/launch")
-        # Q5_K and IQ4_XS GEMVs at C2's shape: the survey's next row (no benchmark config)
-        try:
-            ms5k, _ = time_matmul(ctx, "q5_k", 1, 17408, 5120, steps2, 50, 6, seed=0xA7F00005)
-            b5k = algorithmic_bytes("q5_k", 1, 17408, 5120)
-            configs["q5_k_gemv_m1_k5120_n17408"] = {
-                "us_per_launch": round(ms5k * 1e3, 3), "GB/s": round(b5k / ms5k / 1e6, 1),
-                "hbm_frac": round(b5k / ms5k / 1e6 / HBM_PEAK_GBS, 4)}
-            log(f"[bench] Q5_K m=1 (C2 shape): {ms5k * 1e3:.2f} us/launch")
-        except arf_amd.ArfqError as e:
-            configs["q5_k_gemv_m1_k5120_n17408"] = {"error": str(e)}
-        try:
-            ms4x, _ = time_matmul(ctx, "iq4_xs", 1, 17408, 5120, steps2, 50, 6, seed=0xA7F00006)
-            b4x = algorithmic_bytes("iq4_xs", 1, 17408, 5120)
-            configs["iq4_xs_gemv_m1_k5120_n17408"] = {
-                "us_per_launch": round(ms4x * 1e3, 3), "GB/s": round(b4x / ms4x / 1e6, 1),
-                "hbm_frac": round(b4x / ms4x / 1e6 / HBM_PEAK_GBS, 4)}
-            log(f"[bench] IQ4_XS m=1 (C2 shape): {ms4x * 1e3:.2f} us/launch")
-        except arf_amd.ArfqError as e:
-            configs["iq4_xs_gemv_m1_k5120_n17408"] = {"error": str(e)}
+        # Q5_K and IQ4_XS at C2's shape: the survey's next row (no benchmark config): the
+        # decode GEMV (m = 1), the skinny MFMA kernel (m = 8, 64) and, at m = 2048 (f16 x),
+        # the skinny kernel per 64-row chunk
+        for qt, seed in (("q5_k", 0xA7F00005), ("iq4_xs", 0xA7F00006)):
+            for mm in (1, 8, 64, 2048):
+                key = f"{qt}_gemv_m1_k5120_n17408" if mm == 1 else f"{qt}_m{mm}_k5120_n17408"
+                try:
+                    if mm == 2048:
+                        msq, _ = time_matmul(ctx, qt, mm, 17408, 5120, 10, 3, 2, seed=seed,
+                                             x_dtype=np.float16)
+                    else:
+                        msq, _ = time_matmul(ctx, qt, mm, 17408, 5120, steps2, 50 if mm == 1 else 20,
+                                             6, seed=seed)
+                except arf_amd.ArfqError as e:
+                    configs[key] = {"error": str(e)}
+                    continue
+                bq = algorithmic_bytes(qt, mm, 17408, 5120)
+                configs[key] = {"us_per_launch": round(msq * 1e3, 3), "GB/s": round(bq / msq / 1e6, 1),
+                                "hbm_frac": round(bq / msq / 1e6 / HBM_PEAK_GBS, 4)}
+                if mm == 2048:
+                    tq = 2.0 * mm * 17408 * 5120 / (msq * 1e-3) / 1e12
+                    configs[key].update({"TFLOP/s": round(tq, 1), "mfma_frac": round(tq / FP16_MFMA_PEAK_TFLOPS, 4),
+                                         "x": "f16", "launches": (mm + 63) // 64})
+                log(f"[bench] {qt} m={mm} (C2 shape): {msq * 1e3:.2f} us/launch")
         # C4 Q4_K prefill GEMM
         try:
             ms4, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, 30, 10, 2, seed=0xA7F00004,

@@ -52,10 +52,10 @@ typedef enum {
     ARFQ_Q8_0 = 8,  /* 34 B per 32 weights: f16 d, 32 x i8 */
     ARFQ_Q4_K = 12, /* 144 B per 256 weights: f16 d, f16 dmin, 12 B 6-bit scales/mins, 128 B nibbles */
     ARFQ_Q5_K = 13, /* 176 B per 256 weights: Q4_K's d, dmin, scales, then qh[32] 5th bits, qs[128];
-                       decode GEMV (m <= 4) and dequant only */
+                       every m (decode GEMV at m <= 4), MoE experts, dequant */
     ARFQ_Q6_K = 14, /* 210 B per 256 weights: ql[128], qh[64], i8 scales[16], f16 d */
     ARFQ_IQ4_XS = 23 /* 136 B per 256 weights: f16 d, u16 scales_h, scales_l[4], qs[128] codebook
-                        indices; decode GEMV (m <= 4) and dequant only */
+                        indices; every m (decode GEMV at m <= 4), MoE experts, dequant */
 } arfq_qtype;
 
 /* activation element type */
@@ -138,7 +138,7 @@ int arfq_moe_route(arfq_ctx *ctx, const float *logits, int64_t tokens, int n_exp
  * expert's SwiGLU  down(silu(gate . x) * (up . x)), and scatter-add the results
  * weighted by the router weights into y[tokens, hidden] (f32, overwritten).
  * gate/up hold n_experts x [inter, hidden]; down holds n_experts x [hidden,
- * inter]; all Q4_K.  Replaces add_moe_block_batched
+ * inter]; Q4_K, Q5_K, Q6_K, Q8_0 or IQ4_XS (gate and up alike).  Replaces add_moe_block_batched
  * (crates/arf-gpu/src/gpu/batch.rs:355-460) and the island's sorted mm_id chain
  * (crates/arf-gpu/src/gpu/metal/island.rs:4033-4134); oracle MoeMlp::forward
  * (crates/arf-core/src/model/moe.rs:53-86).  Scratch memory is owned by the
