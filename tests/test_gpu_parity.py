@@ -152,6 +152,27 @@ def test_next_formats_skinny_and_chunked(gpu_ctx, oracle, qtype, m, n, k, x16):
     assert e <= TOL
 
 
+@pytest.mark.parametrize("m", [1, 8, 64, 130])
+def test_q6_k_full_range_scales(gpu_ctx, oracle, m):
+    # quantizers put each block's largest sub-block scale near +-127, where the MFMA
+    # paths' f16 operand sc * (q - 32) passes 2048 and rounds (relative error <= 2^-12);
+    # the synthetic blocks keep scales in [-32, 31], so this test draws them from all of i8
+    from arf_amd import QType, synth
+    _say("case: q6_k full-range scales", m)
+    n, k = 384, 4096
+    raw = synth.weight("q6_k", n, k, seed=0xA7F0000C)
+    blk = raw.reshape(-1, 210)
+    rng = np.random.default_rng(0xA7F0000D)
+    blk[:, 192:208] = rng.integers(-128, 128, size=(blk.shape[0], 16)).astype(np.int8).view(np.uint8)
+    x = synth.activations(m, k, seed=0xA7F0000E)
+    w = gpu_ctx.upload(QType.Q6_K, raw, n, k)
+    y = gpu_ctx.empty((m, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)
+    e = rel_err(y.numpy(), oracle.matmul_q("q6_k", x, raw, n))
+    _say("rel err", e)
+    assert e <= TOL
+
+
 @pytest.mark.parametrize("qtype", ["q6_k", "q8_0"])
 def test_vocab_wide_lm_head_gemv(gpu_ctx, oracle, qtype):
     # the survey's next row: an lm_head GEMV over a 151936-token vocabulary (K cut to 512
