@@ -35,6 +35,9 @@ ARFQ_E_FORMAT = -6
 ARFQ_E_IO = -7
 ARFQ_E_NOT_FOUND = -8
 
+# context options (include/arfq.h ARFQ_OPT_*)
+OPT_GEMV_X16 = 1
+
 
 class QType(enum.IntEnum):
     """ggml type ids (crates/arf-core/src/model/gguf.rs:36-90)."""
@@ -66,6 +69,7 @@ _SIGS = {
     "arfq_ctx_stream": (_vp, [_vp]),
     "arfq_last_error": (ctypes.c_char_p, [_vp]),
     "arfq_ctx_sync": (_int, [_vp]),
+    "arfq_ctx_set_options": (_int, [_vp, ctypes.c_uint]),
     "arfq_weight_upload": (_int, [_vp, _int, _vp, ctypes.c_size_t, _i64, _i64, _int,
                                   ctypes.POINTER(_vp)]),
     "arfq_weight_upload_device": (_int, [_vp, _int, _vp, ctypes.c_size_t, _i64, _i64, _int,
@@ -242,6 +246,10 @@ class Context:
 
     def sync(self):
         _check(self.handle, load_library().arfq_ctx_sync(self.handle))
+
+    def set_options(self, options):
+        """ARFQ_OPT_* bits (OPT_GEMV_X16: 16-bit fixed-point x in the m = 1 Q4_K GEMV)."""
+        _check(self.handle, load_library().arfq_ctx_set_options(self.handle, int(options)))
 
     # -- weights --
     def upload(self, qtype, blocks, n_rows, k_cols, n_experts=1):

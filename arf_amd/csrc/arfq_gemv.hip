@@ -522,9 +522,245 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_swiglu(
     gemv_q4k_body<MX, XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsSwiglu{g, u, 0}, y, n, nblk, m);
 }
 
+// ------------------------------------------------- Q4_K, f32 activations ----
+// The decode GEMV at the reference's arithmetic (one x row): f32 x times the
+// exact 4-bit codes, accumulated in f32 per 32-weight sub-block, then
+//     (d*sc) * code_sum - (dmin*m) * x_sum
+// as dot_q4ks (crates/arf-ml/src/matmul.rs:327-358) and the reference GEMV
+// (shaders/metal/matmul_vec_q4ks_msl.metal:46-165) compute it.  Nothing about
+// x is rounded; only the order of the f32 sums differs from the reference.
+//
+// The product x*q is one v_fma_mix_f32 per weight, its f16 operand taken
+// straight from the code dword: masking a dword with 0x000F000F leaves two
+// nibbles q as the mantissas of two f16 subnormals, i.e. the exact values
+// q * 2^-24 (0x00F000F0 gives 16q * 2^-24).  x is held pre-multiplied by
+// 2^24 (2^20 for the high-nibble elements), so each product is exactly x * q.
+// Five bit operations unpack eight weights.  A sub-block whose max |x| is
+// 2^76 or more is held at 2^s with s < 24 instead, so that x * 2^s stays
+// below 2^100, and its code sum is multiplied back by 2^(24 - s).
+//
+// LDS per x row: the scaled x (k floats, element order) and per sub-block the
+// pair (sum of x, 2^(24 - s)).  Work split, loads and the load ring are those
+// of gemv_q4k (above); for m = 1 the lane keeps the 64 scaled x of its column's
+// two sub-blocks in registers.
+namespace {
+
+// One round of x items (8 elements each, a quad per 32-element sub-block) into
+// the scaled copy xf (as float4 pairs) and the sub-block pairs xs.
+__device__ __forceinline__ void xf_process(const XqRound &r, int items, int base, float4 *xf,
+                                           float2 *xs) {
+    const int it = base + (int)threadIdx.x;
+    const float4 v0 = r.v0, v1 = r.v1;
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                       fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+    float sum = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+    amax = fmaxf(amax, quad_perm<QP_XOR1>(amax));
+    sum += quad_perm<QP_XOR1>(sum);
+    amax = fmaxf(amax, quad_perm<QP_XOR2>(amax));
+    sum += quad_perm<QP_XOR2>(sum);
+    // amax < 2^ex; keep max |x| * 2^s below 2^100
+    const int ex = (amax > 0.f) ? __builtin_amdgcn_frexp_expf(amax) : 0;
+    const int s = min(24, 100 - ex);
+    if (it < items) {
+        xf[2 * it] = make_float4(ldexpf(v0.x, s), ldexpf(v0.y, s), ldexpf(v0.z, s), ldexpf(v0.w, s));
+        xf[2 * it + 1] = make_float4(ldexpf(v1.x, s - 4), ldexpf(v1.y, s - 4), ldexpf(v1.z, s - 4),
+                                     ldexpf(v1.w, s - 4));
+        if ((it & 3) == 0) xs[it >> 2] = make_float2(sum, ldexpf(1.f, 24 - s));
+    }
+}
+
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+
+// acc + x * h, h the low (H = 0) or high (H = 1) f16 half of w: v_fma_mix_f32
+template <int H>
+__device__ __forceinline__ float fmix(float x, uint32_t w, float acc) {
+    const f16x2v h = __builtin_bit_cast(f16x2v, w);
+    return __builtin_fmaf(x, H ? (float)h.y : (float)h.x, acc);
+}
+
+// sum_i x_i * q_i over one 32-weight sub-block: code dwords c, scaled x X[32]
+// (element order; X[8w + 4..7] carry the extra 2^-4)
+__device__ __forceinline__ float q4k_fdot(const uint4 c, const float *X) {
+    const uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const uint32_t v = cw[w], t = v >> 8;
+        const uint32_t A = v & 0x000F000Fu, B = v & 0x00F000F0u;
+        const uint32_t C = t & 0x000F000Fu, D = t & 0x00F000F0u;
+        const float *xw = X + 8 * w;
+        acc = fmix<0>(xw[0], A, acc);
+        acc = fmix<1>(xw[2], A, acc);
+        acc = fmix<0>(xw[1], C, acc);
+        acc = fmix<1>(xw[3], C, acc);
+        acc = fmix<0>(xw[4], B, acc);
+        acc = fmix<1>(xw[6], B, acc);
+        acc = fmix<0>(xw[5], D, acc);
+        acc = fmix<1>(xw[7], D, acc);
+    }
+    return acc;
+}
+
+}  // namespace
+
+template <int XR, int PF, class XSRC>
+__device__ __forceinline__ void gemv_q4k_f32_body(
+    const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
+    uint32_t qs_bytes, const XSRC &xsrc, float *__restrict__ y, int n, int nblk) {
+    constexpr int C = Q4K_GEMV_CHUNK;
+    static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
+    extern __shared__ uint4 smem4[];
+    __shared__ int next_chunk;
+    const int nsub = nblk * 8;
+    float4 *xf = reinterpret_cast<float4 *>(smem4);                 // [k / 4]
+    float2 *xs = reinterpret_cast<float2 *>(xf + (size_t)nsub * 8);  // [nsub]
+    float *part = reinterpret_cast<float *>(xs + nsub);              // [R][spr]
+
+    const __amdgpu_buffer_rsrc_t hrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)hdr_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t qrs =
+        __builtin_amdgcn_make_buffer_rsrc((void *)qs, (short)0, (int)qs_bytes, 0x00020000);
+
+    const int tid = threadIdx.x;
+    const int l16 = tid & 15, grp = tid >> 4;
+    const int bq = l16 >> 2, jj = l16 & 3;
+
+    const int G = gridDim.x;
+    const int r0 = (int)((int64_t)blockIdx.x * n / G);
+    const int r1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
+    const int R = r1 - r0;
+    const int spr = (nblk + 3) >> 2;
+    const int cpc = (R + C - 1) / C;
+    const int nchunks = cpc * spr;
+
+    int icol = 0, irow = 0;
+    auto start_chunk = [&](int k) {
+        icol = k < nchunks ? k / cpc : spr;
+        irow = (k - icol * cpc) * C;
+    };
+    u32x4 clo[PF], chi[PF];
+    uint32_t hbuf[PF];
+    int srow[PF], scol[PF];
+    auto issue = [&](int u, bool first) {
+        if (u % C == 0) {
+            int k = grp;
+            if (!first) {
+                if (l16 == 0) k = atomicAdd(&next_chunk, 1);
+                k = __builtin_amdgcn_ds_swizzle(k, 0x10);  // lane 0 of each 16-lane group
+            }
+            start_chunk(k);
+        } else {
+            irow++;
+        }
+        const int b = 4 * icol + bq;
+        const bool live = icol < spr && irow < R && b < nblk;
+        const uint32_t blk = (uint32_t)(r0 + irow) * (uint32_t)nblk + (uint32_t)b;
+        const uint32_t oc = live ? blk * 128u + (uint32_t)jj * 16u : Q4K_OOB;
+        const uint32_t oh = live ? blk * 16u + (uint32_t)jj * 4u : Q4K_OOB;
+        clo[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oc, 0, 2);
+        chi[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oc + 64u, 0, 2);
+        hbuf[u] = __builtin_amdgcn_raw_buffer_load_b32(hrs, oh, 0, 0);
+        srow[u] = irow;
+        scol[u] = icol;
+    };
+
+    if (tid == 0) next_chunk = Q4K_GEMV_GROUPS;
+    const int xitems = nsub * 4;
+    XqRound xr[XR];
+#pragma unroll
+    for (int r = 0; r < XR; r++) xr[r] = xsrc.load(xitems, r * Q4K_GEMV_THREADS);
+    __builtin_amdgcn_s_barrier();
+    issue(0, true);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < XR; r++)
+        if (r * Q4K_GEMV_THREADS < xitems) xf_process(xr[r], xitems, r * Q4K_GEMV_THREADS, xf, xs);
+    for (int base = XR * Q4K_GEMV_THREADS; base < xitems; base += Q4K_GEMV_THREADS)
+        xf_process(xsrc.load(xitems, base), xitems, base, xf, xs);
+    __syncthreads();  // scaled x and next_chunk are visible from here on
+#pragma unroll
+    for (int u = 1; u < PF; u++) {
+        issue(u, u < C);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // scaled x of the column being consumed (sub-blocks jj, jj + 4)
+    int xcol = -1;
+    float X[2][32];
+    float2 XS[2];
+    auto load_x = [&](int col) {
+        xcol = col;
+        const int ub = min(4 * col + bq, nblk - 1) * 8 + jj;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const float4 *src = xf + (size_t)(ub + 4 * h) * 8;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 t = src[i];
+                X[h][4 * i] = t.x;
+                X[h][4 * i + 1] = t.y;
+                X[h][4 * i + 2] = t.z;
+                X[h][4 * i + 3] = t.w;
+            }
+            XS[h] = xs[ub + 4 * h];
+        }
+    };
+    const uint32_t sh = 8u * (uint32_t)jj;
+
+    auto consume = [&](int u) {
+        const int col = scol[u], row = srow[u];
+        const bool live = col < spr && row < R;
+        if (live && col != xcol) load_x(col);
+        const uint32_t hw = hbuf[u];
+        const PairScales ps = q4k_pair_scales(quad_bcast<0>(hw), quad_bcast<1>(hw),
+                                              quad_bcast<2>(hw), quad_bcast<3>(hw), sh);
+        const uint4 cl = make_uint4(clo[u].x, clo[u].y, clo[u].z, clo[u].w);
+        const uint4 ch = make_uint4(chi[u].x, chi[u].y, chi[u].z, chi[u].w);
+        const float s_lo = q4k_fdot(cl, X[0]) * XS[0].y;
+        const float s_hi = q4k_fdot(ch, X[1]) * XS[1].y;
+        float v = ps.d_lo * s_lo - ps.m_lo * XS[0].x;
+        v += ps.d_hi * s_hi - ps.m_hi * XS[1].x;
+        v = row16_sum(v);
+        if (l16 == 0 && live) part[(size_t)row * spr + col] = v;
+    };
+
+    while (scol[0] < spr) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            consume(u);
+            issue(u, false);
+        }
+    }
+    __syncthreads();
+
+    for (int t = tid; t < R; t += Q4K_GEMV_THREADS) {
+        const float *pr = part + (size_t)t * spr;
+        float v = 0.f;
+        for (int c = 0; c < spr; c++) v += pr[c];
+        y[r0 + t] = v;
+    }
+}
+
+template <int XR>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32(
+    const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
+    uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk) {
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n, nblk);
+}
+
+// The FFN's down GEMV at one x row: x = silu(g) * u, f32 arithmetic.
+template <int XR>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_swiglu(
+    const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
+    uint32_t qs_bytes, const float *__restrict__ g, const float *__restrict__ u,
+    float *__restrict__ y, int n, int nblk) {
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsSwiglu{g, u, 0}, y, n, nblk);
+}
+
 // MoE decode: blockIdx.y = pair p, one x row each, the weight of expert ids[p]
-// (its n rows split over gridDim.x workgroups) into y row p.  A pair whose id
-// is out of range is dropped (its row is not written; the combine skips it).
+// (its n rows split over gridDim.x workgroups) into y row p, at f32
+// arithmetic.  A pair whose id is out of range is dropped (its row is not
+// written; the combine skips it).
 // Reference: the indirect GEMVs gemv_q4ks_id / gemv_q4ks_id_down
 // (shaders/metal/gemv_q4ks_id_msl.metal:40-153, gemv_q4ks_id_down_msl.metal:186-275).
 template <int XR, class XSRC>
@@ -536,9 +772,9 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
     const int e = ids[p];
     if (e < 0 || e >= E) return;  // uniform over the workgroup
     xsrc.pair(p);
-    gemv_q4k_body<1, XR, Q4K_GEMV_PF>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
-                                      qs + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
-                                      y + (int64_t)p * n, n, nblk, 1);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+                                       qs + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
+                                       y + (int64_t)p * n, n, nblk);
 }
 
 // --------------------------------------------- Q6_K / Q5_K / IQ4_XS (dot) ----
@@ -1122,6 +1358,7 @@ __global__ __launch_bounds__(64) void gemv_q6k(const uint4 *__restrict__ qb,
 constexpr int GEMV_MAX_M = 4;
 
 static size_t q4k_gemv_lds(const arfq_weight *w, int mx);
+static bool q4k_f32_ok(const arfq_weight *w);
 static size_t dot_lds(const arfq_weight *w, int mx);
 // the byte-code dot GEMV: Q6_K at m <= 2, Q5_K at m <= 4, while x fits in LDS and
 // one expert's streams fit 31-bit buffer offsets
@@ -1140,6 +1377,7 @@ static bool dot_ok(const arfq_weight *w, int64_t m) {
 bool gemv_supports(const arfq_weight *w, int64_t m) {
     if (m < 1 || m > GEMV_MAX_M) return false;
     // the buffer loads address one expert's code stream with 32-bit offsets
+    if (w->qtype == ARFQ_Q4_K && m == 1 && q4k_f32_ok(w)) return true;
     if (w->qtype == ARFQ_Q4_K)
         return q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
                w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
@@ -1270,15 +1508,74 @@ static hipError_t launch_gemv_q4k(const arfq_weight *w, int e, int m, const floa
     return launch_gemv_q4k_t<MX, 4>(w, e, m, x, y, s);
 }
 
-// LDS of gemv_q4k_pairs with g workgroups per pair.
-static size_t q4k_pairs_lds(const arfq_weight *w, int64_t g) {
-    const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4, rows = (w->n + g - 1) / g;
-    return (size_t)(w->k / 32) * (16 * 4 + 8) + (size_t)rows * spr * 4;
+// ---- the f32-x Q4_K GEMV (one x row) ----
+// LDS: the scaled x (4 B per element), a (sum, factor) pair per sub-block and
+// the column sums of the workgroup's `rows` rows.  Two workgroups per CU share
+// its 160 KB while each needs at most 80 KB; longer x (k above ~19K) runs one
+// workgroup per CU.  (The static LDS of the kernel -- the chunk counter -- sits
+// beside the dynamic part, so the dynamic part stays 1 KB short of 160 KB.)
+constexpr size_t Q4K_F32_LDS_MAX = 159 * 1024;
+static size_t q4k_f32_lds_rows(const arfq_weight *w, int64_t rows) {
+    const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
+    return (size_t)w->k * 4 + (size_t)(w->k / 32) * 8 + (size_t)rows * spr * 4;
 }
+static int64_t q4k_f32_grid(const arfq_weight *w) {
+    const int64_t g2 = q4k_gemv_grid(w);
+    if (q4k_f32_lds_rows(w, (w->n + g2 - 1) / g2) <= Q4K_F32_LDS_MAX / 2) return g2;
+    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
+    return std::max<int64_t>(1, std::min<int64_t>(g2, cus));
+}
+static size_t q4k_f32_lds(const arfq_weight *w) {
+    const int64_t grid = q4k_f32_grid(w);
+    return q4k_f32_lds_rows(w, (w->n + grid - 1) / grid);
+}
+static bool q4k_f32_ok(const arfq_weight *w) {
+    return w->qtype == ARFQ_Q4_K && q4k_f32_lds(w) <= Q4K_F32_LDS_MAX &&
+           w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
+}
+// rounds of x loads issued ahead of the weight ring (8 elements per thread and round)
+static int q4k_f32_xr(const arfq_weight *w) {
+    const int64_t rounds = (w->k / 8 + Q4K_GEMV_THREADS - 1) / Q4K_GEMV_THREADS;
+    return rounds <= 1 ? 1 : rounds <= 2 ? 2 : 4;
+}
+template <int XR>
+static hipError_t launch_q4k_f32_t(const arfq_weight *w, int e, const float *x, float *y, hipStream_t s) {
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_f32<XR>, Q4K_F32_LDS_MAX, lds_set))
+        return err;
+    const int nblk = (int)(w->k / 256);
+    const int64_t nb = w->n * nblk, eb = (int64_t)e * nb;
+    gemv_q4k_f32<XR><<<(unsigned)q4k_f32_grid(w), Q4K_GEMV_THREADS, q4k_f32_lds(w), s>>>(
+        (const uint8_t *)w->s0 + eb * 16, (uint32_t)(nb * 16), (const uint8_t *)w->s1 + eb * 128,
+        (uint32_t)(nb * 128), x, y, (int)w->n, nblk);
+    return hipGetLastError();
+}
+static hipError_t launch_q4k_f32(const arfq_weight *w, int e, const float *x, float *y, hipStream_t s) {
+    switch (q4k_f32_xr(w)) {
+    case 1: return launch_q4k_f32_t<1>(w, e, x, y, s);
+    case 2: return launch_q4k_f32_t<2>(w, e, x, y, s);
+    default: return launch_q4k_f32_t<4>(w, e, x, y, s);
+    }
+}
+template <int XR>
+static hipError_t launch_q4k_f32_swiglu_t(const arfq_weight *w, const float *g, const float *u, float *y,
+                                          hipStream_t s) {
+    static std::atomic<uint64_t> lds_set{0};
+    if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_f32_swiglu<XR>, Q4K_F32_LDS_MAX, lds_set))
+        return err;
+    const int64_t nb = w->n * (w->k / 256);
+    gemv_q4k_f32_swiglu<XR><<<(unsigned)q4k_f32_grid(w), Q4K_GEMV_THREADS, q4k_f32_lds(w), s>>>(
+        (const uint8_t *)w->s0, (uint32_t)(nb * 16), (const uint8_t *)w->s1, (uint32_t)(nb * 128), g, u, y,
+        (int)w->n, (int)(w->k / 256));
+    return hipGetLastError();
+}
+
+// LDS of gemv_q4k_pairs with g workgroups per pair.
+static size_t q4k_pairs_lds(const arfq_weight *w, int64_t g) { return q4k_f32_lds_rows(w, (w->n + g - 1) / g); }
 
 bool gemv_pairs_supports(const arfq_weight *w) {
     return w->qtype == ARFQ_Q4_K && w->k % 256 == 0 && w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB &&
-           q4k_pairs_lds(w, 1) <= 64 * 1024;
+           q4k_pairs_lds(w, 1) <= Q4K_F32_LDS_MAX;
 }
 
 template <class XS>
@@ -1291,14 +1588,21 @@ static hipError_t launch_pairs_t(const arfq_weight *w, int64_t P, const int32_t 
     const dim3 grid((unsigned)g, (unsigned)P);
     const int nsub = (int)(w->k / 32);
     const size_t lds = q4k_pairs_lds(w, g);
-    if (nsub * 4 <= Q4K_GEMV_THREADS)
+    if (nsub * 4 <= Q4K_GEMV_THREADS) {
+        static std::atomic<uint64_t> lds_set{0};
+        if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_pairs<1, XS>, Q4K_F32_LDS_MAX, lds_set))
+            return err;
         gemv_q4k_pairs<1, XS><<<grid, Q4K_GEMV_THREADS, lds, s>>>(
             (const uint8_t *)w->s0, (const uint8_t *)w->s1, (uint32_t)(nb * 16), (uint32_t)(nb * 128), xs, y,
             (int)w->n, (int)(w->k / 256), ids, w->experts);
-    else
+    } else {
+        static std::atomic<uint64_t> lds_set{0};
+        if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_pairs<2, XS>, Q4K_F32_LDS_MAX, lds_set))
+            return err;
         gemv_q4k_pairs<2, XS><<<grid, Q4K_GEMV_THREADS, lds, s>>>(
             (const uint8_t *)w->s0, (const uint8_t *)w->s1, (uint32_t)(nb * 16), (uint32_t)(nb * 128), xs, y,
             (int)w->n, (int)(w->k / 256), ids, w->experts);
+    }
     return hipGetLastError();
 }
 
@@ -1323,8 +1627,15 @@ bool gemv_swiglu_supports(const arfq_weight *w, int64_t m) {
     return w->qtype == ARFQ_Q4_K && w->experts == 1 && gemv_supports(w, m);
 }
 hipError_t launch_gemv_swiglu(const arfq_weight *w, int64_t m, const float *g, const float *u,
-                              float *y, hipStream_t s) {
+                              float *y, hipStream_t s, bool x16) {
     if (!gemv_swiglu_supports(w, m)) return hipErrorInvalidValue;
+    if (m == 1 && !x16 && q4k_f32_ok(w)) {
+        switch (q4k_f32_xr(w)) {
+        case 1: return launch_q4k_f32_swiglu_t<1>(w, g, u, y, s);
+        case 2: return launch_q4k_f32_swiglu_t<2>(w, g, u, y, s);
+        default: return launch_q4k_f32_swiglu_t<4>(w, g, u, y, s);
+        }
+    }
     if (m == 1) return launch_swiglu_mx<1>(w, 1, g, u, y, s);
     if (m == 2) return launch_swiglu_mx<2>(w, 2, g, u, y, s);
     return launch_swiglu_mx<4>(w, (int)m, g, u, y, s);
@@ -1342,9 +1653,10 @@ hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids
 }
 
 hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, float *y,
-                       hipStream_t s) {
+                       hipStream_t s, bool x16) {
     if (!gemv_supports(w, m)) return hipErrorInvalidValue;
     if (w->qtype == ARFQ_Q4_K) {
+        if (m == 1 && !x16 && q4k_f32_ok(w)) return launch_q4k_f32(w, e, x, y, s);
         if (m == 1) return launch_gemv_q4k<1>(w, e, 1, x, y, s);
         if (m == 2) return launch_gemv_q4k<2>(w, e, 2, x, y, s);
         return launch_gemv_q4k<4>(w, e, (int)m, x, y, s);

@@ -133,6 +133,13 @@ int arfq_ctx_sync(arfq_ctx *ctx) {
     return ARFQ_OK;
 }
 
+int arfq_ctx_set_options(arfq_ctx *ctx, unsigned options) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (options & ~ARFQ_OPT_GEMV_X16) return fail(ctx, ARFQ_E_INVALID, "set_options: unknown option bits");
+    ctx->options = options;
+    return ARFQ_OK;
+}
+
 // ---------------------------------------------------------------- weights ----
 
 static int weight_create(arfq_ctx *ctx, int qtype, size_t nbytes, int64_t n_rows, int64_t k_cols,
@@ -279,7 +286,8 @@ static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64
                           const void *x, int x_dtype, float *y) {
     hipError_t e;
     if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
-        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream);
+        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream,
+                              (ctx->options & ARFQ_OPT_GEMV_X16) != 0);
     } else if (arfq::gemm_supports(w, m)) {
         const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
         if (int rc = ensure_scratch(ctx, plan.scratch_bytes)) return rc;
@@ -520,7 +528,8 @@ int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, cons
     if (int rc = matmul_enqueue(ctx, up, 0, m, x, ARFQ_F32, u)) return rc;
     hipError_t e;
     if (fused) {
-        e = arfq::launch_gemv_swiglu(down, m, g, u, y, ctx->stream);
+        e = arfq::launch_gemv_swiglu(down, m, g, u, y, ctx->stream,
+                                     (ctx->options & ARFQ_OPT_GEMV_X16) != 0);
         if (e != hipSuccess) return hip_fail(ctx, e, "ffn: down GEMV launch");
         return ARFQ_OK;
     }

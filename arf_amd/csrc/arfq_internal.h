@@ -17,6 +17,7 @@ struct arfq_ctx {
     bool own_stream = false;
     std::string err;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
+    unsigned options = 0;  // ARFQ_OPT_* bits
     // growable scratch for the MoE pipeline (routing, grouping, intermediates)
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
@@ -71,8 +72,10 @@ hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s);
 // ---- arfq_gemv.hip ----
 // Small-m GEMV for expert `e`: y[m, n] = x[m, k] . W_e^T, x f32.  Returns
 // hipErrorInvalidValue when (qtype, m) has no GEMV kernel.
+// x16: m = 1 takes the 16-bit fixed-point x kernel instead of f32 arithmetic
+// (ARFQ_OPT_GEMV_X16).
 hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, float *y,
-                       hipStream_t s);
+                       hipStream_t s, bool x16 = false);
 bool gemv_supports(const arfq_weight *w, int64_t m);
 // MoE decode GEMVs over P (token, expert) pairs, Q4_K: y[p] (w->n floats) = W_ids[p] .
 // x_p, where x_p is row p / x_div of x (f32 or f16, [*, w->k]) or, when g is
@@ -82,7 +85,7 @@ bool gemv_supports(const arfq_weight *w, int64_t m);
 // (Q4_K, m <= 4).
 bool gemv_swiglu_supports(const arfq_weight *w, int64_t m);
 hipError_t launch_gemv_swiglu(const arfq_weight *w, int64_t m, const float *g, const float *u,
-                              float *y, hipStream_t s);
+                              float *y, hipStream_t s, bool x16 = false);
 // h = silu(g) * u elementwise (n floats)
 hipError_t launch_swiglu(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
 bool gemv_pairs_supports(const arfq_weight *w);

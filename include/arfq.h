@@ -84,6 +84,17 @@ const char *arfq_last_error(const arfq_ctx *ctx);
 /* Block until all work enqueued on the context's stream has finished. */
 int arfq_ctx_sync(arfq_ctx *ctx);
 
+/* Context options (bit set; default 0).
+ * ARFQ_OPT_GEMV_X16: Q4_K decode GEMVs at m = 1 (arfq_matmul, arfq_ffn) round
+ *   each 32-element block of f32 x to 16-bit fixed point (relative to the
+ *   block's max |x|) and take exact integer dots; faster, max relative error
+ *   ~1e-4 of the output's rms.  By default they multiply f32 x by the exact
+ *   weights in f32, as the reference GEMV does
+ *   (crates/arf-gpu/src/shaders/metal/matmul_vec_q4ks_msl.metal:46-165).
+ * No counterpart in the reference (which has only the f32 form). */
+#define ARFQ_OPT_GEMV_X16 1u
+int arfq_ctx_set_options(arfq_ctx *ctx, unsigned options);
+
 /* Upload `n_experts` stacked [n_rows, k_cols] matrices of raw ggml blocks from
  * HOST memory.  `nbytes` must equal n_experts * n_rows * k_cols / QK *
  * block_bytes (QK = 32 / 256; block_bytes = 34 / 144 / 210).  Experts are

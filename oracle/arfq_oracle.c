@@ -36,6 +36,9 @@
 #define QK_K 256
 #define QK8 32
 
+/* f32 matmul (a9), defined below; the dequant-then-matmul oracles above it use it */
+void arfo_matmul_nt(const float *a, int64_t m, int64_t k, const float *b, int64_t n, float *out);
+
 /* ---- a1: f16 -> f32.  crates/arf-ml/src/dtype.rs:41-70 ------------------- */
 float arfo_f16_to_f32(uint16_t h) {
     uint32_t sign = (h >> 15) & 1u;

@@ -52,6 +52,7 @@ def test_null_handles_are_rejected():
     assert L.arfq_moe_route(None, None, 1, 8, 2, 1, None, None) == arfq.ARFQ_E_INVALID
     assert L.arfq_moe(None, None, None, None, None, 1, 2, 1, None, 0, None) == arfq.ARFQ_E_INVALID
     assert L.arfq_ctx_create(0, None, None) == arfq.ARFQ_E_INVALID
+    assert L.arfq_ctx_set_options(None, 0) == arfq.ARFQ_E_INVALID
 
 
 def test_no_gpu_here_fails_loudly():

@@ -109,13 +109,90 @@ def test_c1_q8_0_gemv_full(gpu_ctx, oracle):
     assert rel_err(got, oracle.matmul_q("q8_0", x, raw, 2048)) <= TOL
 
 
+# The m = 1 Q4_K GEMV multiplies f32 x by the exact weights in f32 (only the
+# order of the f32 sums differs from matmul_nt_q4ks), so it is held to 1e-5.
+F32_TOL = 1e-5
+
+
 def test_c2_q4_k_gemv_full(gpu_ctx, oracle):
     _say("case: C2 full")
     got, raw, x = _matmul(gpu_ctx, "q4_k", 17408, 5120, 1, seed=0xA7F00002)
     want = oracle.matmul_q("q4_k", x, raw, 17408)
     e = rel_err(got, want)
     _say("C2 rel err", e)
+    assert e <= F32_TOL
+
+
+def test_c2_q4_k_gemv_x16_option(gpu_ctx, oracle):
+    # ARFQ_OPT_GEMV_X16: the 16-bit fixed-point x kernel, within the matmul gate
+    _say("case: C2 full, x16 option")
+    import arf_amd
+    gpu_ctx.set_options(arf_amd.arfq.OPT_GEMV_X16)
+    try:
+        got, raw, x = _matmul(gpu_ctx, "q4_k", 17408, 5120, 1, seed=0xA7F00002)
+    finally:
+        gpu_ctx.set_options(0)
+    e = rel_err(got, oracle.matmul_q("q4_k", x, raw, 17408))
+    _say("C2 x16 rel err", e)
     assert e <= TOL
+
+
+def _q4k_dyadic_blocks(n, k, seed):
+    """Q4_K blocks with d = 2^-4, dmin = 2^-5 and random 6-bit scales / nibbles:
+    every weight is a multiple of 2^-9 below 64."""
+    from arf_amd import synth
+    raw = synth.weight("q4_k", n, k, seed=seed).reshape(-1, 144)
+    raw[:, 0:2] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)
+    raw[:, 2:4] = np.frombuffer(np.float16(2.0 ** -5).tobytes(), np.uint8)
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("n,k", [(17408, 5120), (300, 256), (64, 2048)])
+def test_q4k_gemv_f32_exact_on_integer_x(gpu_ctx, oracle, n, k):
+    # integer x in [-8, 8] and dyadic weights: every product, sub-block sum and
+    # row sum is exact in f32 in any order, so the GEMV must equal the oracle bit
+    # for bit -- any rounding of x or of the codes would show
+    _say("case: q4k f32 exact", n, k)
+    from arf_amd import QType
+    raw = _q4k_dyadic_blocks(n, k, seed=n + k)
+    rng = np.random.default_rng(k)
+    x = rng.integers(-8, 9, size=(1, k)).astype(np.float32)
+    w = gpu_ctx.upload(QType.Q4_K, raw, n, k)
+    y = gpu_ctx.empty((1, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), 1, y)
+    got = y.numpy()
+    want = oracle.matmul_q("q4_k", x, raw, n)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("case", ["huge", "tiny", "mixed"])
+def test_q4k_gemv_f32_dynamic_range(gpu_ctx, oracle, case):
+    # sub-blocks of x at very different magnitudes: above 2^76 the kernel holds x at
+    # a smaller power of two; f32 subnormal x is scaled up exactly
+    _say("case: q4k f32 range", case)
+    from arf_amd import QType, synth
+    n, k = 96, 2048
+    raw = synth.weight("q4_k", n, k, seed=77)
+    rng = np.random.default_rng(78)
+    x = rng.standard_normal((1, k)).astype(np.float32)
+    sub = x.reshape(-1, 32)
+    if case == "huge":
+        sub *= np.float32(2.0 ** 90)
+    elif case == "tiny":
+        sub *= np.float32(2.0 ** -130)  # mostly f32 subnormals
+    else:
+        exps = rng.integers(-60, 100, size=(sub.shape[0], 1))
+        sub *= np.exp2(exps).astype(np.float32)
+    x = sub.reshape(1, k)
+    w = gpu_ctx.upload(QType.Q4_K, raw, n, k)
+    y = gpu_ctx.empty((1, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), 1, y)
+    got = y.numpy()
+    want = oracle.matmul_q("q4_k", x, raw, n)
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, want)
+    _say("rel err", e)
+    assert e <= (1e-4 if case == "tiny" else F32_TOL)
 
 
 def test_c3_q6_k_gemv_m1_full(gpu_ctx, oracle):
