@@ -47,6 +47,15 @@ __device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, h);
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits
+// for every outstanding global load of the wave (s_waitcnt vmcnt(0)); this one
+// leaves weight loads issued before it in flight.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // 16-byte streaming load (non-temporal hint: each weight byte is read once).
 __device__ __forceinline__ uint4 ld_nt(const uint4 *p) {
     const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));

@@ -610,11 +610,12 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     constexpr int C = Q4K_GEMV_CHUNK;
     static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
     extern __shared__ uint4 smem4[];
-    __shared__ int next_chunk;
     const int nsub = nblk * 8;
+    const int spr = (nblk + 3) >> 2;
     float4 *xf = reinterpret_cast<float4 *>(smem4);                 // [k / 4]
     float2 *xs = reinterpret_cast<float2 *>(xf + (size_t)nsub * 8);  // [nsub]
-    float *part = reinterpret_cast<float *>(xs + nsub);              // [R][spr]
+    int *cnt = reinterpret_cast<int *>(xs + nsub);                   // [spr] chunk counters
+    float *part = reinterpret_cast<float *>(cnt + ((spr + 3) & ~3));  // [R][spr]
 
     const __amdgpu_buffer_rsrc_t hrs =
         __builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)hdr_bytes, 0x00020000);
@@ -629,27 +630,36 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     const int r0 = (int)((int64_t)blockIdx.x * n / G);
     const int r1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
     const int R = r1 - r0;
-    const int spr = (nblk + 3) >> 2;
-    const int cpc = (R + C - 1) / C;
-    const int nchunks = cpc * spr;
+    const int cpc = (R + C - 1) / C;  // chunks (of C rows) per column
 
-    int icol = 0, irow = 0;
-    auto start_chunk = [&](int k) {
-        icol = k < nchunks ? k / cpc : spr;
-        irow = (k - icol * cpc) * C;
+    // Each 16-lane group has a home column (group % spr) and starts on chunk
+    // group / spr of it; further chunks are claimed from that column's counter,
+    // and only when it runs out from the next columns, so a group keeps the x
+    // of one column in registers for most of its work.
+    int icol = grp % spr, irow = (grp / spr) * C;
+    auto claim = [&]() {
+        int col = icol;
+        for (int t = 0; t < spr; t++) {
+            int k = 0;
+            if (l16 == 0) k = atomicAdd(&cnt[col], 1);
+            k = __builtin_amdgcn_ds_swizzle(k, 0x10);  // lane 0 of each 16-lane group
+            if (k < cpc) {
+                icol = col;
+                irow = k * C;
+                return;
+            }
+            col = col + 1 == spr ? 0 : col + 1;
+        }
+        icol = spr;  // no work left
     };
     u32x4 clo[PF], chi[PF];
     uint32_t hbuf[PF];
     int srow[PF], scol[PF];
     auto issue = [&](int u, bool first) {
-        if (u % C == 0) {
-            int k = grp;
-            if (!first) {
-                if (l16 == 0) k = atomicAdd(&next_chunk, 1);
-                k = __builtin_amdgcn_ds_swizzle(k, 0x10);  // lane 0 of each 16-lane group
-            }
-            start_chunk(k);
-        } else {
+        if (!first) {
+            if (u % C == 0) claim();
+            else irow++;
+        } else if (u > 0) {
             irow++;
         }
         const int b = 4 * icol + bq;
@@ -664,25 +674,28 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
         scol[u] = icol;
     };
 
-    if (tid == 0) next_chunk = Q4K_GEMV_GROUPS;
+    // counters start past the chunks the groups begin on
+    for (int c = tid; c < spr; c += Q4K_GEMV_THREADS)
+        cnt[c] = (Q4K_GEMV_GROUPS - c + spr - 1) / spr;
+    // x loads, then (after every wave has issued them) the first chunk of
+    // weights, then x is scaled into LDS; the barrier after it orders LDS only,
+    // so the weight loads stay in flight across it
     const int xitems = nsub * 4;
     XqRound xr[XR];
 #pragma unroll
     for (int r = 0; r < XR; r++) xr[r] = xsrc.load(xitems, r * Q4K_GEMV_THREADS);
+    asm volatile("" ::: "memory");  // keep the x loads ahead of the weight loads
     __builtin_amdgcn_s_barrier();
-    issue(0, true);
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < XR; r++)
-        if (r * Q4K_GEMV_THREADS < xitems) xf_process(xr[r], xitems, r * Q4K_GEMV_THREADS, xf, xs);
+    for (int u = 0; u < PF; u++) issue(u, true);
+    asm volatile("" ::: "memory");
+    // (every round is processed: items past the end load a clamped index and
+    // store nothing, and an unconditional use keeps the loads where they are)
+#pragma unroll
+    for (int r = 0; r < XR; r++) xf_process(xr[r], xitems, r * Q4K_GEMV_THREADS, xf, xs);
     for (int base = XR * Q4K_GEMV_THREADS; base < xitems; base += Q4K_GEMV_THREADS)
         xf_process(xsrc.load(xitems, base), xitems, base, xf, xs);
-    __syncthreads();  // scaled x and next_chunk are visible from here on
-#pragma unroll
-    for (int u = 1; u < PF; u++) {
-        issue(u, u < C);
-        __builtin_amdgcn_sched_barrier(0);
-    }
+    lds_barrier();  // scaled x and the counters are visible from here on
 
     // scaled x of the column being consumed (sub-blocks jj, jj + 4)
     int xcol = -1;
@@ -724,6 +737,8 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
         if (l16 == 0 && live) part[(size_t)row * spr + col] = v;
     };
 
+    // consume a slot, then refill it; a group that has run out of work (icol ==
+    // spr) stays out, so once slot 0 holds no work neither does any later slot
     while (scol[0] < spr) {
 #pragma unroll
         for (int u = 0; u < PF; u++) {
@@ -731,7 +746,7 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
             issue(u, false);
         }
     }
-    __syncthreads();
+    lds_barrier();
 
     for (int t = tid; t < R; t += Q4K_GEMV_THREADS) {
         const float *pr = part + (size_t)t * spr;
@@ -1517,7 +1532,8 @@ static hipError_t launch_gemv_q4k(const arfq_weight *w, int e, int m, const floa
 constexpr size_t Q4K_F32_LDS_MAX = 159 * 1024;
 static size_t q4k_f32_lds_rows(const arfq_weight *w, int64_t rows) {
     const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
-    return (size_t)w->k * 4 + (size_t)(w->k / 32) * 8 + (size_t)rows * spr * 4;
+    return (size_t)w->k * 4 + (size_t)(w->k / 32) * 8 + (size_t)((spr + 3) & ~3) * 4 +
+           (size_t)rows * spr * 4;
 }
 static int64_t q4k_f32_grid(const arfq_weight *w) {
     const int64_t g2 = q4k_gemv_grid(w);
