@@ -24,8 +24,8 @@ namespace arfq {
 template <class F, int BM, bool XSPLIT>
 __global__ __launch_bounds__(GM_THREADS) void gemm_q(
     F fmt, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
-    const uint16_t *__restrict__ xs, float *__restrict__ y, int M, int N, int K, int mt,
-    int xcd_order) {
+    const uint16_t *__restrict__ xs, const float *__restrict__ rs, float *__restrict__ y, int M,
+    int N, int K, int mt, int xcd_order) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int tid = threadIdx.x;
     int tm, tn;
@@ -77,7 +77,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q(
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int m = m0 + tile_out_row<BM>(t, i);
-                if (m < M && n < N) out[(int64_t)m * N + n] = acc[t][b][i];
+                if (m < M && n < N) out[(int64_t)m * N + n] = rs ? acc[t][b][i] * rs[m] : acc[t][b][i];
             }
         }
     }
@@ -91,9 +91,10 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q(
 // sums the S partials in split order into y, so the result does not depend on
 // the arrival order.
 // (held to 256 VGPRs: two workgroups per CU)
-template <class F, int TA, class XT>
+template <class F, int TA, class XT, bool PAIR>
 __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__restrict__ x,
                                                       const uint16_t *__restrict__ xs,
+                                                      const float *__restrict__ rs,
                                                       float *__restrict__ y, float *__restrict__ part,
                                                       uint32_t *__restrict__ tick, int M, int N, int K) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
@@ -102,7 +103,12 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
     const int n0 = blockIdx.x * 128;
     const int nb = K / 256, S = gridDim.y, sp = blockIdx.y;
     const int b0 = (int)((int64_t)sp * nb / S), b1 = (int)((int64_t)(sp + 1) * nb / S);
-    const SkRows<TA> rows = sk_rows<TA>(M, K, [](int r) { return r; });
+    // PAIR (M <= 16 TA): x row r < M stages hi row r of x, row PO + r its lo row
+    // M + r (PO = 16 in one 32-row tile, 32 = the second tile with two)
+    constexpr int PO = 16 * TA;
+    const SkRows<TA> rows =
+        PAIR ? sk_rows<TA>(PO + M, K, [M](int r) { return r < M ? r : r >= PO ? M + r - PO : 0; })
+             : sk_rows<TA>(M, K, [](int r) { return r; });
     const int n = n0 + 32 * wave + (lane & 31);
     const F fm[1] = {fmt};
     const int64_t wrow0[1] = {n0 + 32 * wave};
@@ -111,14 +117,23 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
     for (int t = 0; t < TA; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    skinny_run<F, TA, 1, SK_THREADS, XT>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds, M);
+    skinny_run<F, TA, 1, SK_THREADS, XT>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds, PAIR ? PO + M : M);
+    if constexpr (PAIR && TA == 1) {
+        // rows r and r + 16 of a lane's accumulator are elements i and i + 8
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[0][0][i] += acc[0][0][i + 8];
+    } else if constexpr (PAIR) {
+        // rows r and r + 32: element i of tiles 0 and 1
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[0][0][i] += acc[0][1][i];
+    }
     if (S == 1) {
 #pragma unroll
         for (int t = 0; t < TA; t++)
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int m = sk_out_row(t, i);
-                if (m < M && n < N) y[(int64_t)m * N + n] = acc[0][t][i];
+                if (m < M && n < N) y[(int64_t)m * N + n] = rs ? acc[0][t][i] * rs[m] : acc[0][t][i];
             }
         return;
     }
@@ -189,30 +204,31 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
         const int row = 32 * t + 8 * g + 4 * (lane >> 5);
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            if (row + c < M && n < N) y[(int64_t)(row + c) * N + n] = r[c];
+            if (row + c < M && n < N) y[(int64_t)(row + c) * N + n] = rs ? r[c] * rs[row + c] : r[c];
     }
 }
 
-// y[i] = part[0][i] + part[1][i] + ... in split order
+// y[i] = part[0][i] + part[1][i] + ... in split order, times the row's x
+// scale rs[i / N] when there is one
 __global__ void splitk_reduce(const float *__restrict__ part, float *__restrict__ y, int64_t n,
-                              int S) {
+                              int S, const float *__restrict__ rs, int64_t N) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     float v = part[i];
     for (int s = 1; s < S; s++) v += part[(int64_t)s * n + i];
-    y[i] = v;
+    y[i] = rs ? v * rs[i / N] : v;
 }
 
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
-                        _Float16 *xl, uint16_t *xs, hipStream_t s) {
-    const int64_t items = m * (k / 8);
-    if (items == 0 || (!xh && !xl && !xs)) return hipSuccess;
-    if (k % 32) return hipErrorInvalidValue;
-    const unsigned grid = (unsigned)((items + 255) / 256);
+                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair) {
+    if (m == 0 || (!xh && !xl && !xs)) return hipSuccess;
+    if (k % 32 || m > INT32_MAX || (pair && (!xh || xl != xh + m * k))) return hipErrorInvalidValue;
     if (x_dtype == ARFQ_F32)
-        xprep_kernel<float><<<grid, 256, 0, s>>>((const float *)x, m, (int)k, xh, xl, xs);
+        xprep_kernel<float><<<(unsigned)m, XPREP_THREADS, 0, s>>>((const float *)x, m, (int)k, xh, xl, xs, rs,
+                                                                  pair ? 1 : 0);
     else
-        xprep_kernel<_Float16><<<grid, 256, 0, s>>>((const _Float16 *)x, m, (int)k, xh, xl, xs);
+        xprep_kernel<_Float16><<<(unsigned)m, XPREP_THREADS, 0, s>>>((const _Float16 *)x, m, (int)k, xh, xl,
+                                                                     xs, nullptr, pair ? 1 : 0);
     return hipGetLastError();
 }
 
@@ -239,13 +255,16 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     const bool kind2 = w->qtype == ARFQ_Q4_K || w->qtype == ARFQ_Q5_K;  // min term: x sums
     p.skinny = (m <= 64 || chunked) && w->k % 256 == 0;
     p.bm = m > 64 ? 128 : 64;
-    // f32 x: rounded to f16 for the skinny kernel and for prefill shapes (m > 64,
-    // as the reference's half tiles), split into f16 hi + lo otherwise
+    // f32 x: scaled per row by a power of two into f16 range and rounded to f16
+    // for the skinny kernel and for prefill shapes (m > 64), split into f16 hi +
+    // lo otherwise; the output rows are multiplied back by the scale
     p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && m <= 64;
-    // the skinny kernel rounds an f32 x itself at m <= 32, except for Q4_K and
-    // Q5_K, whose x sub-block sums come from the same preparation pass (at
-    // m > 32 the staging registers would not fit beside two waves per SIMD)
-    p.convert = x_dtype == ARFQ_F32 && !(p.skinny && m <= 32 && !kind2);
+    p.convert = x_dtype == ARFQ_F32;
+    // skinny kernel, f32 x, m <= 32: x as f16 hi + lo (about 22 bits, as close
+    // to the reference's f32 batched GEMV as the f16 MFMA gets): at m <= 16 the
+    // lo rows fill the other half of the 32-row x tile staged anyway (no extra
+    // MFMAs), at m <= 32 a second tile (twice the MFMAs)
+    p.pair = p.skinny && x_dtype == ARFQ_F32 && m <= 32;
     // Q4_K prefill: the direct-operand kernel (one launch, no split-K)
     p.bd = !p.skinny && w->qtype == ARFQ_Q4_K && m > 64 &&
            w->n * (w->k / 2) < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
@@ -287,11 +306,13 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     p.splits = (int)std::min<int64_t>(S, 16);
     size_t o = 0;
     p.off_xh = o;
-    o += p.convert ? al256((size_t)m * w->k * 2) : 0;
+    o += p.convert ? al256((size_t)(p.pair ? 2 : 1) * m * w->k * 2) : 0;  // pair: lo rows follow
     p.off_xl = o;
     o += p.xsplit ? al256((size_t)m * w->k * 2) : 0;
     p.off_xs = o;
-    o += p.sums ? al256((size_t)m * (w->k / 16) * 2) : 0;
+    o += p.sums ? al256((size_t)(p.pair ? 2 : 1) * m * (w->k / 16) * 2) : 0;
+    p.off_rs = o;
+    o += p.convert ? al256((size_t)m * 4) : 0;
     p.off_part = o;
     if (p.skinny)  // partials in register order: [split][column tile][wave][8-row group][lane] float4
         o += p.splits > 1 ? al256((size_t)p.splits * ((w->n + 127) / 128) * ((std::min<int64_t>(m, 64) + 7) / 8) * 4096)
@@ -302,33 +323,35 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     return p;
 }
 
-template <class F, int TA, class XT>
-static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const XT *x,
-                              const uint16_t *xs, float *y, float *part, uint32_t *tick, int S,
-                              hipStream_t s) {
+template <class F, int TA, bool PAIR>
+static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
+                              const uint16_t *xs, const float *rs, float *y, float *part,
+                              uint32_t *tick, int S, hipStream_t s) {
     constexpr size_t lds = sk_lds<F, TA, 1>();
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
-    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, XT>, lds, lds_set)) return err;
+    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PAIR>, lds, lds_set))
+        return err;
     const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
-    gemm_sk<F, TA, XT><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, y, part, tick, (int)m, (int)w->n,
-                                                     (int)w->k);
+    gemm_sk<F, TA, _Float16, PAIR><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
+                                                                 (int)w->n, (int)w->k);
     return hipGetLastError();
 }
 
-// S > 1 splits need S <= 16 and one zeroed counter per 128-column tile
+// S > 1 splits need S <= 16 and one zeroed counter per 128-column tile.  x is
+// f16 (an f32 x arrives prepared and row-scaled, rs its row scales); with pair
+// (m <= 16) it is [2m, K]: the hi rows, then the lo rows.
 template <class F>
-static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const void *x,
-                            bool xf32, const uint16_t *xs, float *y, float *part, uint32_t *tick,
-                            int ntick, int S, hipStream_t s) {
+static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
+                            const uint16_t *xs, const float *rs, float *y, float *part, uint32_t *tick,
+                            int ntick, int S, hipStream_t s, bool pair) {
     if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;
-    if (xf32) {
-        if constexpr (F::KIND == 2) return hipErrorInvalidValue;  // Q4_K: prepared x only
-        else
-            return m <= 32 ? launch_sk_t<F, 1>(fmt, w, m, (const float *)x, xs, y, part, tick, S, s)
-                           : hipErrorInvalidValue;  // m > 32: prepared x only
+    if (pair) {
+        if (m > 32) return hipErrorInvalidValue;
+        return m <= 16 ? launch_sk_t<F, 1, true>(fmt, w, m, x, xs, rs, y, part, tick, S, s)
+                       : launch_sk_t<F, 2, true>(fmt, w, m, x, xs, rs, y, part, tick, S, s);
     }
-    return m <= 32 ? launch_sk_t<F, 1>(fmt, w, m, (const _Float16 *)x, xs, y, part, tick, S, s)
-                   : launch_sk_t<F, 2>(fmt, w, m, (const _Float16 *)x, xs, y, part, tick, S, s);
+    return m <= 32 ? launch_sk_t<F, 1, false>(fmt, w, m, x, xs, rs, y, part, tick, S, s)
+                   : launch_sk_t<F, 2, false>(fmt, w, m, x, xs, rs, y, part, tick, S, s);
 }
 
 SkQ4K sk_q4k(const arfq_weight *w) {
@@ -351,15 +374,15 @@ SkIQ4XS sk_iq4xs(const arfq_weight *w) {
 // is one launch).  Chunks run in stream order and reuse the partials and
 // counters.
 template <class F>
-static hipError_t launch_sk_rows(const F &fmt, const arfq_weight *w, int64_t m, const void *x,
-                                 bool xf32, const uint16_t *xs, float *y, float *part,
-                                 uint32_t *tick, int ntick, int S, hipStream_t s) {
+static hipError_t launch_sk_rows(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
+                                 const uint16_t *xs, const float *rs, float *y, float *part,
+                                 uint32_t *tick, int ntick, int S, hipStream_t s, bool pair) {
+    if (pair) return launch_sk(fmt, w, m, x, xs, rs, y, part, tick, ntick, S, s, true);  // m <= 32
     for (int64_t r0 = 0; r0 < m; r0 += 64) {
         const int64_t mc = std::min<int64_t>(64, m - r0);
-        const void *xc = xf32 ? (const void *)((const float *)x + r0 * w->k)
-                              : (const void *)((const _Float16 *)x + r0 * w->k);
-        if (hipError_t err = launch_sk(fmt, w, mc, xc, xf32, xs ? xs + r0 * (w->k / 16) : nullptr,
-                                       y + r0 * w->n, part, tick, ntick, S, s))
+        if (hipError_t err = launch_sk(fmt, w, mc, x + r0 * w->k, xs ? xs + r0 * (w->k / 16) : nullptr,
+                                       rs ? rs + r0 : nullptr, y + r0 * w->n, part, tick, ntick, S, s,
+                                       false))
             return err;
     }
     return hipSuccess;
@@ -367,28 +390,28 @@ static hipError_t launch_sk_rows(const F &fmt, const arfq_weight *w, int64_t m, 
 
 template <class F, int BM, bool XS>
 static hipError_t launch_gemm_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *xh,
-                                const _Float16 *xl, const uint16_t *xs, float *out, int S,
-                                hipStream_t s) {
+                                const _Float16 *xl, const uint16_t *xs, const float *rs, float *out,
+                                int S, hipStream_t s) {
     constexpr size_t lds = gm_lds(BM, XS);
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)gemm_q<F, BM, XS>, lds, lds_set)) return err;
     const int mt = (int)((m + BM - 1) / BM), nt = (int)((w->n + GM_BN - 1) / GM_BN);
     const int xcd = (mt % 8 == 0) ? 1 : 0;
     const dim3 grid((unsigned)(mt * nt), (unsigned)S);
-    gemm_q<F, BM, XS><<<grid, GM_THREADS, lds, s>>>(fmt, xh, xl, xs, out, (int)m, (int)w->n,
+    gemm_q<F, BM, XS><<<grid, GM_THREADS, lds, s>>>(fmt, xh, xl, xs, rs, out, (int)m, (int)w->n,
                                                    (int)w->k, mt, xcd);
     return hipGetLastError();
 }
 
 template <class F>
 static hipError_t launch_fmt(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *xh,
-                             const _Float16 *xl, const uint16_t *xs, float *out, const GemmPlan &p,
-                             hipStream_t s) {
+                             const _Float16 *xl, const uint16_t *xs, const float *rs, float *out,
+                             const GemmPlan &p, hipStream_t s) {
     if (p.bm == 128)
-        return p.xsplit ? launch_gemm_t<F, 128, true>(fmt, w, m, xh, xl, xs, out, p.splits, s)
-                        : launch_gemm_t<F, 128, false>(fmt, w, m, xh, xl, xs, out, p.splits, s);
-    return p.xsplit ? launch_gemm_t<F, 64, true>(fmt, w, m, xh, xl, xs, out, p.splits, s)
-                    : launch_gemm_t<F, 64, false>(fmt, w, m, xh, xl, xs, out, p.splits, s);
+        return p.xsplit ? launch_gemm_t<F, 128, true>(fmt, w, m, xh, xl, xs, rs, out, p.splits, s)
+                        : launch_gemm_t<F, 128, false>(fmt, w, m, xh, xl, xs, rs, out, p.splits, s);
+    return p.xsplit ? launch_gemm_t<F, 64, true>(fmt, w, m, xh, xl, xs, rs, out, p.splits, s)
+                    : launch_gemm_t<F, 64, false>(fmt, w, m, xh, xl, xs, rs, out, p.splits, s);
 }
 
 FmtQ4K fmt_q4k(const arfq_weight *w) {
@@ -403,8 +426,8 @@ FmtQ80 fmt_q80(const arfq_weight *w) {
 
 // Q4_K prefill: weights straight into the MFMA operands (arfq_gemm_bd.h)
 static hipError_t launch_bd_q4k(const arfq_weight *w, int e, int64_t m, const _Float16 *x,
-                                const uint16_t *xs, float *y, float *part, const GemmPlan &p,
-                                hipStream_t s) {
+                                const uint16_t *xs, const float *rs, float *y, float *part,
+                                const GemmPlan &p, hipStream_t s) {
     const int64_t nblk = w->k / 256;
     const int64_t eb = (int64_t)e * w->n * nblk;
     const int mt = (int)((m + BD_BM - 1) / BD_BM), nt = (int)((w->n + BD_BN - 1) / BD_BN);
@@ -415,12 +438,12 @@ static hipError_t launch_bd_q4k(const arfq_weight *w, int e, int64_t m, const _F
     if (hipError_t err = set_max_lds_once((const void *)gemm_bd_q4k, bd_lds(), lds_set)) return err;
     const unsigned items = (unsigned)(p.bd_full + nsplit * p.bd_chunks);
     gemm_bd_q4k<<<items, BD_THREADS, bd_lds(), s>>>(
-        (const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8, x, xs, y, part, (int)m,
+        (const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8, x, xs, rs, y, part, (int)m,
         (int)w->n, (int)w->k, mt, xcd, p.bd_full, p.bd_chunks);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !nsplit) return err;
     bd_reduce_kernel<<<dim3(BD_BM * BD_BN / 256, (unsigned)nsplit), 256, 0, s>>>(
-        part, y, (int)m, (int)w->n, mt, p.bd_full, p.bd_chunks);
+        part, rs, y, (int)m, (int)w->n, mt, p.bd_full, p.bd_chunks);
     return hipGetLastError();
 }
 
@@ -430,56 +453,56 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     char *sc = (char *)scratch;
     if (p.scratch_bytes && !sc) return hipErrorInvalidValue;
     _Float16 *xh = p.convert ? (_Float16 *)(sc + p.off_xh) : (_Float16 *)x;
-    _Float16 *xl = p.xsplit ? (_Float16 *)(sc + p.off_xl) : nullptr;
+    _Float16 *xl = p.xsplit ? (_Float16 *)(sc + p.off_xl) : p.pair ? xh + m * w->k : nullptr;
     uint16_t *xs = p.sums ? (uint16_t *)(sc + p.off_xs) : nullptr;
+    float *rs = p.convert ? (float *)(sc + p.off_rs) : nullptr;  // row scales of an f32 x
     if (p.convert || p.sums) {
-        hipError_t err = launch_xprep(x, x_dtype, m, w->k, p.convert ? xh : nullptr, xl, xs, s);
+        hipError_t err = launch_xprep(x, x_dtype, m, w->k, p.convert ? xh : nullptr, xl, xs, rs, s, p.pair);
         if (err != hipSuccess) return err;
     }
     float *out = p.splits > 1 ? (float *)(sc + p.off_part) : y;
     hipError_t err;
     if (p.skinny) {
         // the split-K sum happens inside the kernel
-        const bool xf32 = x_dtype == ARFQ_F32 && !p.convert;
-        const void *xk = p.convert ? (const void *)xh : x;
+        const _Float16 *xk = p.convert ? xh : (const _Float16 *)x;
         const int64_t eb = (int64_t)e * w->n * (w->k / 256);
         switch (w->qtype) {
         case ARFQ_Q4_K:
-            return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets, ntickets,
-                             p.splits, s);
+            return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets, ntickets,
+                             p.splits, s, p.pair);
         case ARFQ_Q6_K:
-            return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets, ntickets,
-                             p.splits, s);
+            return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets, ntickets,
+                             p.splits, s, p.pair);
         case ARFQ_Q8_0:
-            return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xf32, xs,
-                             y, out, tickets, ntickets, p.splits, s);
+            return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xs, rs,
+                             y, out, tickets, ntickets, p.splits, s, p.pair);
         case ARFQ_Q5_K:
-            return launch_sk_rows(sk_q5k(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets,
-                                  ntickets, p.splits, s);
+            return launch_sk_rows(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets,
+                                  ntickets, p.splits, s, p.pair);
         case ARFQ_IQ4_XS:
-            return launch_sk_rows(sk_iq4xs(w).shifted(eb), w, m, xk, xf32, xs, y, out, tickets,
-                                  ntickets, p.splits, s);
+            return launch_sk_rows(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets,
+                                  ntickets, p.splits, s, p.pair);
         default:
             return hipErrorInvalidValue;
         }
     } else switch (w->qtype) {
     case ARFQ_Q4_K: {
         if (p.bd) {
-            err = launch_bd_q4k(w, e, m, xh, xs, out, (float *)(sc + p.off_part), p, s);
+            err = launch_bd_q4k(w, e, m, xh, xs, rs, out, (float *)(sc + p.off_part), p, s);
             break;
         }
         const FmtQ4KR f{fmt_q4k(w).shifted((int64_t)e * w->n * (w->k / 256))};
-        err = launch_fmt(f, w, m, xh, xl, xs, out, p, s);
+        err = launch_fmt(f, w, m, xh, xl, xs, p.splits == 1 ? rs : nullptr, out, p, s);
         break;
     }
     case ARFQ_Q6_K: {
         const FmtQ6KR f{fmt_q6k(w).shifted((int64_t)e * w->n * (w->k / 256))};
-        err = launch_fmt(f, w, m, xh, xl, xs, out, p, s);
+        err = launch_fmt(f, w, m, xh, xl, xs, p.splits == 1 ? rs : nullptr, out, p, s);
         break;
     }
     case ARFQ_Q8_0: {
         const FmtQ80 f = fmt_q80(w).shifted((int64_t)e * w->n * (w->k / 32));
-        err = launch_fmt(f, w, m, xh, xl, xs, out, p, s);
+        err = launch_fmt(f, w, m, xh, xl, xs, p.splits == 1 ? rs : nullptr, out, p, s);
         break;
     }
     default:
@@ -487,7 +510,7 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     }
     if (err != hipSuccess || p.splits == 1) return err;
     const int64_t n = m * w->n;
-    splitk_reduce<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(out, y, n, p.splits);
+    splitk_reduce<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(out, y, n, p.splits, rs, w->n);
     return hipGetLastError();
 }
 

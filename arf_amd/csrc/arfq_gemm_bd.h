@@ -121,8 +121,8 @@ __device__ __forceinline__ void bd_mins(const u32x4 hd, float inv_su, int h, bf1
 // fills the last round of workgroups when the tiles do not divide the CUs.
 __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
     const uint4 *__restrict__ hdr, const uint4 *__restrict__ qs, const _Float16 *__restrict__ x,
-    const uint16_t *__restrict__ xs, float *__restrict__ y, float *__restrict__ part, int m, int n,
-    int k, int mt, int xcd_order, int full, int chunks) {
+    const uint16_t *__restrict__ xs, const float *__restrict__ rs, float *__restrict__ y,
+    float *__restrict__ part, int m, int n, int k, int mt, int xcd_order, int full, int chunks) {
     extern __shared__ __attribute__((aligned(16))) _Float16 sx[];  // [2][BD_BM][BD_LD]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nblk = k / 256;
@@ -385,7 +385,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
                 if (split) {
                     pt[(size_t)rl * BD_BN + cl] = acc[mg][g][i];
                 } else if (cn < n && m0 + rl < m) {
-                    y[(int64_t)(m0 + rl) * n + cn] = acc[mg][g][i];
+                    y[(int64_t)(m0 + rl) * n + cn] = rs ? acc[mg][g][i] * rs[m0 + rl] : acc[mg][g][i];
                 }
             }
         }
@@ -395,6 +395,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
 // y of the split tiles: the chunks' partial tiles added in chunk order.
 // One thread per output; grid (BD_BM * BD_BN / 256, split tiles).
 __global__ __launch_bounds__(256) void bd_reduce_kernel(const float *__restrict__ part,
+                                                        const float *__restrict__ rs,
                                                         float *__restrict__ y, int m, int n,
                                                         int mt, int full, int chunks) {
     const int lt = blockIdx.y;
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(256) void bd_reduce_kernel(const float *__restrict_
     const float *pp = part + (size_t)lt * chunks * BD_BM * BD_BN + e;
     float v = 0.f;
     for (int j = 0; j < chunks; j++) v += pp[(size_t)j * BD_BM * BD_BN];
-    y[(int64_t)r * n + c] = v;
+    y[(int64_t)r * n + c] = rs ? v * rs[r] : v;
 }
 
 }  // namespace arfq

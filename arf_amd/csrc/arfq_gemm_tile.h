@@ -560,53 +560,104 @@ __device__ __forceinline__ int tile_out_col(int b) {
 }
 
 // ---- activation preparation ------------------------------------------------
-// One thread per 8 consecutive elements of a row-major [M, K] activation (K a
-// multiple of 32), so a quad of lanes covers a 32-element sub-block and every
-// load and store is 16 bytes wide and coalesced: writes x as f16 (and, when
-// `xl` is set, the f16 remainder x - hi) and, when `xs` is set, the sub-block
-// sum X (of the values the MFMAs will see: each lane's 8 in order, then the
-// quad's four partial sums pairwise) as bf16 hi + lo into xs[row][k / 256][j]
-// and [8 + j] (j = sub-block within block).
+// One workgroup per row of a row-major [M, K] activation (K a multiple of 32),
+// one thread per 8 consecutive elements in each pass, so a quad of lanes covers
+// a 32-element sub-block and every load and store is 16 bytes wide and
+// coalesced.  Writes x as f16 (and, when `xl` is set, the f16 remainder
+// x - hi) and, when `xs` is set, the sub-block sum X (of the values the MFMAs
+// will see: each lane's 8 in order, then the quad's four partial sums
+// pairwise) as bf16 hi + lo into xs[row][k / 256][j] and [8 + j] (j =
+// sub-block within block).
+// With `pair` set, xl must be xh + M * K: the lo remainders are stored as rows
+// M .. 2M - 1 after the hi rows, and xs holds the sums of each hi row at row r
+// and of each lo row at row M + r (xs then has 2M rows); otherwise the sums
+// are of hi + lo.
+// With `rs` set (f32 x), the row is first scanned for its max |x| and every
+// element is stored divided by rs[row] = 2^(e - 15), e the exponent of that
+// max (max in [2^(e-1), 2^e)): an exact power-of-two scaling that puts the
+// row's largest value in [2^14, 2^15), so no finite f32 x overflows f16 and
+// small rows do not fall into f16 subnormals.  The products' consumers
+// multiply their output rows by rs.  Rows whose max is 0 or not finite keep
+// rs = 1.
+constexpr int XPREP_THREADS = 512;
 template <typename TIn>
-__global__ void xprep_kernel(const TIn *__restrict__ x, int64_t M, int K, _Float16 *__restrict__ xh,
-                             _Float16 *__restrict__ xl, uint16_t *__restrict__ xs) {
-    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int nch = K / 8;
-    if (g >= M * nch) return;  // K % 32 == 0: a quad's lanes leave together
-    const int64_t row = g / nch;
-    const int ch = (int)(g - row * nch);
-    float v[8];
+__device__ __forceinline__ void xprep_load8(const TIn *__restrict__ p, float v[8]) {
     if constexpr (sizeof(TIn) == 4) {
-        const float4 a = reinterpret_cast<const float4 *>(x + g * 8)[0];
-        const float4 b = reinterpret_cast<const float4 *>(x + g * 8)[1];
+        const float4 a = reinterpret_cast<const float4 *>(p)[0];
+        const float4 b = reinterpret_cast<const float4 *>(p)[1];
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
         v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     } else {
-        const half8 a = reinterpret_cast<const half8 *>(x + g * 8)[0];
+        const half8 a = reinterpret_cast<const half8 *>(p)[0];
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = (float)a[i];
     }
-    half8 hv, lv;
-    float sum = 0.f;
+}
+template <typename TIn>
+__global__ __launch_bounds__(XPREP_THREADS) void xprep_kernel(
+    const TIn *__restrict__ x, int64_t M, int K, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
+    uint16_t *__restrict__ xs, float *__restrict__ rs, int pair) {
+    __shared__ float wmax[XPREP_THREADS / 64];
+    const int64_t row = blockIdx.x;
+    const int nch = K / 8;
+    const TIn *xr = x + row * K;
+    int sh = 0;  // elements are stored times 2^sh
+    if (rs) {
+        float amax = 0.f;
+        for (int ch = threadIdx.x; ch < nch; ch += XPREP_THREADS) {
+            float v[8];
+            xprep_load8(xr + (int64_t)ch * 8, v);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        hv[i] = (_Float16)v[i];
-        lv[i] = (_Float16)(v[i] - (float)hv[i]);
-        sum += xl ? ((float)hv[i] + (float)lv[i]) : (float)hv[i];
+            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        amax = wmax[0];
+#pragma unroll
+        for (int w = 1; w < XPREP_THREADS / 64; w++) amax = fmaxf(amax, wmax[w]);
+        if (amax > 0.f && amax < INFINITY) sh = 15 - __builtin_amdgcn_frexp_expf(amax);
+        if (threadIdx.x == 0) rs[row] = ldexpf(1.f, -sh);
     }
-    if (xh) reinterpret_cast<half8 *>(xh)[g] = hv;
-    if (xl) reinterpret_cast<half8 *>(xl)[g] = lv;
-    if (xs) {
-        // (s0 + s1) + (s2 + s3) on every lane of the quad (quad_perm [1,0,3,2], then [2,3,0,1])
-        sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sum), 0xB1, 0xf, 0xf, true));
-        sum += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(sum), 0x4E, 0xf, 0xf, true));
-        if ((ch & 3) == 0) {
-            const int sub = ch >> 2;
-            const uint32_t hi = bf16_bits(sum);
-            const uint32_t lo = bf16_bits(sum - bf16_to_f32(hi));
-            uint16_t *d = xs + row * (K / 16) + (sub >> 3) * 16 + (sub & 7);
-            d[0] = (uint16_t)hi;
-            d[8] = (uint16_t)lo;
+    // K % 32 == 0 and the stride is a multiple of 4: a quad's lanes run the
+    // same iterations, so the quad DPP sums below see the whole sub-block
+    for (int ch = threadIdx.x; ch < nch; ch += XPREP_THREADS) {
+        const int64_t g = row * nch + ch;
+        float v[8];
+        xprep_load8(xr + (int64_t)ch * 8, v);
+        half8 hv, lv;
+        float sum = 0.f, suml = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float u = sh ? ldexpf(v[i], sh) : v[i];
+            hv[i] = (_Float16)u;
+            lv[i] = (_Float16)(u - (float)hv[i]);
+            sum += (xl && !pair) ? ((float)hv[i] + (float)lv[i]) : (float)hv[i];
+            suml += (float)lv[i];
+        }
+        if (xh) reinterpret_cast<half8 *>(xh)[g] = hv;
+        if (xl) reinterpret_cast<half8 *>(xl)[g] = lv;
+        if (xs) {
+            // (s0 + s1) + (s2 + s3) on every lane of the quad (quad_perm [1,0,3,2], then [2,3,0,1])
+            auto quad_sum = [](float t) {
+                t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, true));
+                return t + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, true));
+            };
+            sum = quad_sum(sum);
+            if (pair) suml = quad_sum(suml);
+            if ((ch & 3) == 0) {
+                const int sub = ch >> 2;
+                auto put = [&](int64_t r, float t) {
+                    const uint32_t hi = bf16_bits(t);
+                    const uint32_t lo = bf16_bits(t - bf16_to_f32(hi));
+                    uint16_t *d = xs + r * (K / 16) + (sub >> 3) * 16 + (sub & 7);
+                    d[0] = (uint16_t)hi;
+                    d[8] = (uint16_t)lo;
+                };
+                put(row, sum);
+                if (pair) put(M + row, suml);
+            }
         }
     }
 }

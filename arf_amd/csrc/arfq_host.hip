@@ -421,6 +421,7 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     const bool dsums = down->qtype == ARFQ_Q4_K || down->qtype == ARFQ_Q5_K;
     size_t o = 0;
     const size_t o_x = o;     o += x_dtype == ARFQ_F32 ? align256((size_t)tokens * hidden * 2) : 0;
+    const size_t o_xrs = o;   o += x_dtype == ARFQ_F32 ? align256((size_t)tokens * 4) : 0;
     const size_t o_xs = o;    o += gsums ? align256((size_t)tokens * (hidden / 16) * 2) : 0;
     const size_t o_ids = o;   o += ids_in ? 0 : align256((size_t)P * 4);
     const size_t o_w = o;     o += ids_in ? 0 : align256((size_t)P * 4);
@@ -440,8 +441,10 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     // tiles) and, for Q4_K and Q5_K, the x sub-block sums
     const _Float16 *xh = x_dtype == ARFQ_F32 ? (const _Float16 *)(sc + o_x) : (const _Float16 *)x;
     uint16_t *xs = gsums ? (uint16_t *)(sc + o_xs) : nullptr;
+    // an f32 x is stored row-scaled into f16 range; gate|up multiply back
+    float *xrs = x_dtype == ARFQ_F32 ? (float *)(sc + o_xrs) : nullptr;
     e = arfq::launch_xprep(x, x_dtype, tokens, hidden,
-                           x_dtype == ARFQ_F32 ? (_Float16 *)(sc + o_x) : nullptr, nullptr, xs,
+                           x_dtype == ARFQ_F32 ? (_Float16 *)(sc + o_x) : nullptr, nullptr, xs, xrs,
                            ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "moe: x preparation launch");
     const int32_t *ids = ids_in;
@@ -463,7 +466,7 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     float *ob = (float *)(sc + o_o);
     e = arfq::launch_moe_group(ids, P, E, off, srt, tiles, nt, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "moe: group launch");
-    e = arfq::launch_moe_gateup(gate, up, xh, xs, top_k, off, srt, tiles, nt, max_tiles, h,
+    e = arfq::launch_moe_gateup(gate, up, xh, xs, xrs, top_k, off, srt, tiles, nt, max_tiles, h,
                                 ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "moe: gate/up launch");
     e = arfq::launch_moe_hprep(h, P, (int)inter, h16, hs, rs, ctx->stream);

@@ -103,9 +103,10 @@ struct GemmPlan {
     bool sums = false;     // the format needs x sub-block sums (Q4_K)
     bool skinny = false;   // m <= 64: the weight-streaming kernel (arfq_skinny.h)
     bool bd = false;       // Q4_K prefill: weights straight into MFMA operands (arfq_gemm_bd.h)
+    bool pair = false;     // skinny, m <= 16, f32 x: x as f16 hi rows + lo rows in one x tile
     int bd_full = 0;       // bd: whole tiles; the rest are split into bd_chunks K ranges
     int bd_chunks = 1;
-    size_t off_xh = 0, off_xl = 0, off_xs = 0, off_part = 0, scratch_bytes = 0;
+    size_t off_xh = 0, off_xl = 0, off_xs = 0, off_rs = 0, off_part = 0, scratch_bytes = 0;
 };
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype);
 bool gemm_supports(const arfq_weight *w, int64_t m);
@@ -115,9 +116,14 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
                        float *y, void *scratch, uint32_t *tickets, int ntickets,
                        const GemmPlan &p, hipStream_t s);
 // Activation preparation: x (f32 or f16, [m, k]) -> f16 copy (xh), f16
-// remainder (xl), bf16 sub-block sums (xs, [m][k / 256][16]); null outputs are skipped.
+// remainder (xl), bf16 sub-block sums (xs, [m][k / 256][16]); null outputs are
+// skipped.  With rs (f32 x only) each row is stored divided by a power of two
+// rs[row] that puts its max |x| in [2^14, 2^15); products of it must be
+// multiplied back by rs[row].
+// With pair (xl == xh + m * k) the lo rows follow the hi rows and xs has the
+// hi rows' sums, then the lo rows' sums.
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
-                        _Float16 *xl, uint16_t *xs, hipStream_t s);
+                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair = false);
 
 // ---- arfq_moe.hip ----
 // Routing: ids/weights [tokens, top_k] from logits [tokens, E] (E <= 1024, top_k <= 64).
@@ -130,10 +136,12 @@ hipError_t launch_moe_group(const int32_t *ids, int64_t P, int E, int32_t *off, 
 int64_t moe_max_tiles(int64_t P, int E);
 // h[P, inter] (f32, sorted order) = silu(x . gate^T) * (x . up^T) per pair;
 // xs: x sub-block sums (Q4_K weights only, else null).
+// xrs: row scales of a prepared f32 x (null for f16 x); g and u are multiplied
+// back by the token's scale before the SwiGLU.
 hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, const _Float16 *x,
-                             const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
-                             const void *tiles, const int32_t *ntiles, int64_t max_tiles,
-                             float *h, hipStream_t s);
+                             const uint16_t *xs, const float *xrs, int top_k, const int32_t *off,
+                             const int32_t *sorted, const void *tiles, const int32_t *ntiles,
+                             int64_t max_tiles, float *h, hipStream_t s);
 // h (f32) -> h16 = h / rs[row] (rs a power of two keeping h16 in f16 range)
 // and, when hs is set, the bf16 sub-block sums of h16.
 hipError_t launch_moe_hprep(const float *h, int64_t P, int inter, _Float16 *h16, uint16_t *hs,

@@ -222,8 +222,8 @@ constexpr int MOE_GU_THREADS = 512;
 template <class F>
 __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     F gate, F up, int64_t expert_blocks, const _Float16 *__restrict__ x,
-    const uint16_t *__restrict__ xs, int K, int inter, int top_k, const int32_t *__restrict__ off,
-    const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
+    const uint16_t *__restrict__ xs, const float *__restrict__ xrs, int K, int inter, int top_k,
+    const int32_t *__restrict__ off, const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ h) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     if ((int)blockIdx.x >= *ntiles) return;  // uniform over the workgroup
@@ -263,7 +263,12 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
             for (int i = 0; i < 16; i++) {
                 const int r = sk_out_row(t, i);
                 if (r < rows && n < inter) {
-                    const float g = acc[0][t][i], u = ex[((wq * 2 + t) * 16 + i) * 64 + lane];
+                    float g = acc[0][t][i], u = ex[((wq * 2 + t) * 16 + i) * 64 + lane];
+                    if (xrs) {  // the token row was stored divided by xrs (exact)
+                        const float sc = xrs[sorted[row0 + r] / top_k];
+                        g *= sc;
+                        u *= sc;
+                    }
                     const float sg = g / (1.0f + expf(-g));
                     h[(int64_t)(row0 + r) * inter + n] = sg * u;
                 }
@@ -462,18 +467,18 @@ int64_t moe_max_tiles(int64_t P, int E) { return (P + MOE_BM - 1) / MOE_BM + E; 
 
 template <class F>
 static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const _Float16 *x,
-                           const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
-                           const void *tiles, const int32_t *ntiles, int64_t max_tiles, float *h,
-                           hipStream_t s) {
+                           const uint16_t *xs, const float *xrs, int top_k, const int32_t *off,
+                           const int32_t *sorted, const void *tiles, const int32_t *ntiles,
+                           int64_t max_tiles, float *h, hipStream_t s) {
     constexpr size_t lds = sk_lds<F, 2, 1, MOE_GU_THREADS>();
     static_assert(lds >= (size_t)4 * 2 * 16 * 64 * 4, "room for the up -> gate hand-off");
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)moe_gateup_kernel<F>, lds, lds_set)) return err;
     const int64_t eb = gw->n * g.nblk;
     const dim3 grid((unsigned)max_tiles, (unsigned)((gw->n + 127) / 128));
-    moe_gateup_kernel<F><<<grid, MOE_GU_THREADS, lds, s>>>(g, u, eb, x, xs, (int)gw->k, (int)gw->n,
-                                                       top_k, off, sorted, (const int2 *)tiles,
-                                                       ntiles, h);
+    moe_gateup_kernel<F><<<grid, MOE_GU_THREADS, lds, s>>>(g, u, eb, x, xs, xrs, (int)gw->k,
+                                                       (int)gw->n, top_k, off, sorted,
+                                                       (const int2 *)tiles, ntiles, h);
     return hipGetLastError();
 }
 
@@ -499,24 +504,24 @@ SkQ5K sk_q5k(const arfq_weight *w);
 SkIQ4XS sk_iq4xs(const arfq_weight *w);
 
 hipError_t launch_moe_gateup(const arfq_weight *gate, const arfq_weight *up, const _Float16 *x,
-                             const uint16_t *xs, int top_k, const int32_t *off, const int32_t *sorted,
-                             const void *tiles, const int32_t *ntiles, int64_t max_tiles,
-                             float *h, hipStream_t s) {
+                             const uint16_t *xs, const float *xrs, int top_k, const int32_t *off,
+                             const int32_t *sorted, const void *tiles, const int32_t *ntiles,
+                             int64_t max_tiles, float *h, hipStream_t s) {
     switch (gate->qtype) {
     case ARFQ_Q4_K:
-        return gateup_t(sk_q4k(gate), sk_q4k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+        return gateup_t(sk_q4k(gate), sk_q4k(up), gate, x, xs, xrs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
     case ARFQ_Q6_K:
-        return gateup_t(sk_q6k(gate), sk_q6k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+        return gateup_t(sk_q6k(gate), sk_q6k(up), gate, x, xs, xrs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
     case ARFQ_Q8_0:
-        return gateup_t(sk_q80(gate), sk_q80(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+        return gateup_t(sk_q80(gate), sk_q80(up), gate, x, xs, xrs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
     case ARFQ_Q5_K:
-        return gateup_t(sk_q5k(gate), sk_q5k(up), gate, x, xs, top_k, off, sorted, tiles, ntiles,
+        return gateup_t(sk_q5k(gate), sk_q5k(up), gate, x, xs, xrs, top_k, off, sorted, tiles, ntiles,
                         max_tiles, h, s);
     case ARFQ_IQ4_XS:
-        return gateup_t(sk_iq4xs(gate), sk_iq4xs(up), gate, x, xs, top_k, off, sorted, tiles,
+        return gateup_t(sk_iq4xs(gate), sk_iq4xs(up), gate, x, xs, xrs, top_k, off, sorted, tiles,
                         ntiles, max_tiles, h, s);
     default: return hipErrorInvalidValue;
     }

@@ -17,9 +17,9 @@
 // scaled by the lane's own d at the block end (lane l's C column is its weight
 // row, so d is a register, not a broadcast).  Q4_K's min term
 // -dmin * sum_j m_j * X_j enters as two bf16 MFMAs against the x sub-block
-// sums X_j.  Q8_0 lanes hold d * q rounded to f16.  Q5_K is Q4_K with a 5-bit
-// q.  IQ4_XS lanes hold the codebook values; each MFMA covers one sub-block
-// and its result is scaled by that sub-block's d * (ls - 32).
+// sums X_j.  Q5_K is Q4_K with a 5-bit q.  IQ4_XS lanes hold the codebook
+// values and Q8_0 lanes the int8 codes; each MFMA covers one sub-block (one
+// Q8_0 block) and its result is scaled by that sub-block's d * (ls - 32) (d).
 //
 // K-slot map of step p (64 elements) of block b: lane half h and MFMA kk use
 // elements a_off(p, kk, h) + 0..7 of the block; the x operand is read from LDS
@@ -182,7 +182,10 @@ struct SkQ6K {
 // 8b + 2p + 1 (h = 1); MFMA kk = bytes 8kk .. 8kk + 7 of the lane's block.
 // Weights d * q rounded to f16 (the format's scale is per 32 weights).
 struct SkQ80 {
-    static constexpr int KIND = 0, RB = 256;
+    // exact operands: the int8 codes as f16; MFMAs 0, 1 of step p cover Q8_0
+    // block 2p, MFMAs 2, 3 block 2p + 1, and each block's product is scaled by
+    // its own d in f32 (KIND 3, as IQ4_XS)
+    static constexpr int KIND = 3, RB = 256;
     struct Blk {
         u32x4 d;  // the 8 f16 scales of the 8 Q8_0 blocks
     };
@@ -190,33 +193,36 @@ struct SkQ80 {
     const uint16_t *dd;
     int nblk;  // Q8_0 blocks per row
     __host__ __device__ SkQ80 shifted(int64_t nb) const { return {qs + nb * 2, dd + nb, nblk}; }
-    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * (kk >> 1) + 16 * (kk & 1) + 8 * h; }
     __device__ const uint8_t *raw(int64_t row, int b) const {
         return reinterpret_cast<const uint8_t *>(qs + (row * nblk + 8 * b) * 2);
     }
     __device__ Blk load_blk(int64_t row, int b) const {
         return {*reinterpret_cast<const u32x4 *>(dd + row * nblk + 8 * b)};
     }
-    __device__ static float2 scale(const Blk &) { return make_float2(1.f, 0.f); }
-    __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(srow + 64 * p + 32 * h);
-        const u32x4 bq = *reinterpret_cast<const u32x4 *>(srow + 64 * p + 32 * h + 16);
-        const int bi = 2 * p + h;
-        const uint32_t dw[4] = {k.d.x, k.d.y, k.d.z, k.d.w};
-        const float d = h2f(dw[bi >> 1] >> (16 * (bi & 1)));
-        const uint32_t cw[8] = {a.x, a.y, a.z, a.w, bq.x, bq.y, bq.z, bq.w};
+    // d of Q8_0 blocks 2p and 2p + 1
+    __device__ static float2 sub_scales(const Blk &k, int p) {
+        const uint32_t dw = k.d[p];
+        return make_float2(h2f(dw), h2f(dw >> 16));
+    }
+    __device__ static void frag(const uint8_t *srow, const Blk &, int p, int h, half8 f[4]) {
+        // byte q ^ 0x80 = q + 128 under the f16 pattern of 1024 is 1152 + q,
+        // less 1152: q exactly
+        const half2v one = h2splat(1.f), m1152 = h2splat(-1152.f);
 #pragma unroll
         for (int kk = 0; kk < 4; kk++) {
+            const u32x2 c = *reinterpret_cast<const u32x2 *>(srow + a_off(p, kk, h));
             uint32_t o[4];
 #pragma unroll
             for (int u = 0; u < 2; u++) {
-                const uint32_t v = cw[2 * kk + u];
-                o[2 * u] = pack2h(d * (float)(int8_t)(v & 0xffu), d * (float)(int8_t)((v >> 8) & 0xffu));
-                o[2 * u + 1] = pack2h(d * (float)(int8_t)((v >> 16) & 0xffu), d * (float)(int8_t)(v >> 24));
+                const uint32_t v = c[u] ^ 0x80808080u;
+                o[2 * u] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), one, m1152);
+                o[2 * u + 1] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u), one, m1152);
             }
             f[kk] = u4_to_h8(o[0], o[1], o[2], o[3]);
         }
     }
+    __device__ static float2 scale(const Blk &) { return make_float2(1.f, 0.f); }
     __device__ static void minsb(const Blk &, bf16x8 &hi, bf16x8 &lo) {
         hi = __builtin_bit_cast(bf16x8, u32x4{0u, 0u, 0u, 0u});
         lo = hi;

@@ -272,27 +272,39 @@ def test_c5_moe_full(gpu_ctx, oracle):
 def _ffn_oracle(oracle, x, raws, qts, inter, hidden):
     g = oracle.matmul_q(qts[0], x, raws[0], inter)
     u = oracle.matmul_q(qts[1], x, raws[1], inter)
-    h = (g / (np.float32(1.0) + np.exp(-g)) * u).astype(np.float32)
-    return oracle.matmul_q(qts[2], h, raws[2], hidden)
+    with np.errstate(over="ignore"):  # exp(-g) overflows to inf for g << 0: silu -> 0, as in f32
+        h = (g / (np.float32(1.0) + np.exp(-g)) * u).astype(np.float32)
+    return oracle.matmul_q(qts[2], h, raws[2], hidden), g
 
 
-@pytest.mark.parametrize("qts,hidden,inter,m", [
-    (("q4_k", "q4_k", "q4_k"), 512, 768, 1), (("q4_k", "q4_k", "q4_k"), 512, 768, 3),
-    (("q4_k", "q4_k", "q4_k"), 512, 768, 8), (("q4_k", "q4_k", "q6_k"), 1024, 512, 1),
-    (("q8_0", "q8_0", "q5_k"), 768, 256, 2), (("q4_k", "q4_k", "q4_k"), 5120, 17408, 1)])
-def test_ffn_matches_mlp_forward(gpu_ctx, oracle, qts, hidden, inter, m):
+@pytest.mark.parametrize("qts,hidden,inter,m,xscale", [
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 1, 1.0), (("q4_k", "q4_k", "q4_k"), 512, 768, 3, 1.0),
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 8, 1.0), (("q4_k", "q4_k", "q6_k"), 1024, 512, 1, 1.0),
+    (("q8_0", "q8_0", "q5_k"), 768, 256, 2, 1.0), (("q4_k", "q4_k", "q4_k"), 5120, 17408, 1, 1.0),
+    # m = 8 at C2's shape: gate/up on the skinny MFMA kernel, h = silu(g) * u far above f16's
+    # range into the down GEMM's f32 x (row-scaled into f16 range)
+    (("q4_k", "q4_k", "q4_k"), 5120, 17408, 8, 1.0),
+    # x scaled down so that most g fall in [-10, 10], where silu is neither 0 nor the identity
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 1, 0.02), (("q4_k", "q4_k", "q6_k"), 512, 768, 8, 0.02),
+    (("q5_k", "q5_k", "iq4_xs"), 1024, 512, 5, 0.02)])
+def test_ffn_matches_mlp_forward(gpu_ctx, oracle, qts, hidden, inter, m, xscale):
     # ffn_dispatch / Mlp::forward (island.rs:13436-13529, mlp.rs:20-24): the fused SwiGLU-into-
     # down GEMV (Q4_K down, m <= 4) and the SwiGLU kernel + matmul path
     from arf_amd import QType, synth
-    _say("case: ffn", qts, hidden, inter, m)
+    _say("case: ffn", qts, hidden, inter, m, xscale)
     shapes = [(inter, hidden), (inter, hidden), (hidden, inter)]
     raws = [synth.weight(q, n, k, seed=31 + i) for i, (q, (n, k)) in enumerate(zip(qts, shapes))]
     ws = [gpu_ctx.upload(QType[q.upper()], r, n, k) for q, r, (n, k) in zip(qts, raws, shapes)]
-    x = synth.activations(m, hidden, seed=37)
+    x = (synth.activations(m, hidden, seed=37) * np.float32(xscale)).astype(np.float32)
     y = gpu_ctx.empty((m, hidden), np.float32)
     gpu_ctx.ffn(ws[0], ws[1], ws[2], gpu_ctx.to_device(x), m, y)
-    e = rel_err(y.numpy(), _ffn_oracle(oracle, x, raws, qts, inter, hidden))
-    _say("rel err", e)
+    want, g = _ffn_oracle(oracle, x, raws, qts, inter, hidden)
+    got = y.numpy()
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, want)
+    _say("rel err", e, "share of g in [-10, 10]", float(np.mean(np.abs(g) <= 10)))
+    if xscale < 1:
+        assert np.mean(np.abs(g) <= 10) > 0.5
     assert e <= TOL
 
 

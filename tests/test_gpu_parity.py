@@ -289,13 +289,47 @@ def test_gemm_q4k_f16_small(gpu_ctx, oracle, m, n, k):
 @pytest.mark.parametrize("qtype,n,k", [("q4_k", 96, 2048), ("q6_k", 130, 1792), ("q8_0", 77, 1216),
                                        ("q8_0", 100, 2048)])
 def test_gemm_f32_x(gpu_ctx, oracle, qtype, n, k, m):
-    # m > 4 goes through the MFMA path: f32 x split into an f16 hi + lo pair
-    # for m <= 64, rounded to f16 above
+    # m > 4 goes through the MFMA kernels: f32 x scaled per row into f16 range and
+    # rounded to f16 (split into an f16 hi + lo pair on the tiled kernel at m <= 64)
     _say("case: gemm f32 x", qtype, n, k, m)
     got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=91 + m + n)
     e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
     _say("rel err", e)
     assert e <= TOL
+
+
+@pytest.mark.parametrize("m", [5, 8, 32, 64, 130])
+@pytest.mark.parametrize("qtype", ["q4_k", "q5_k", "q6_k", "q8_0", "iq4_xs"])
+def test_mfma_paths_f32_x_beyond_f16_range(gpu_ctx, oracle, qtype, m):
+    # m >= 5 runs the MFMA kernels on f16 operands: an f32 x is scaled per row by a power
+    # of two into f16 range first (and the output rows back), so x blocks up to 1e6 -- far
+    # past f16's 65504 -- stay finite.  At m <= 32 x goes in as f16 hi + lo (~22 bits), so
+    # even sub-blocks spread over 9 decades stay close to the f32 reference; above 32 rows
+    # x is rounded to f16 (11 bits), checked here on N(0,1) x with 1 block in 8 at 1e6.
+    _say("case: mfma f32 x range", qtype, m)
+    from arf_amd import QType, synth
+    n, k = 96, 2048
+    raw = synth.weight(qtype, n, k, seed=11 * m + len(qtype))
+    rng = np.random.default_rng(m)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    sub = x.reshape(m, -1, 32)
+    if m <= 32:
+        sub *= (10.0 ** rng.uniform(-3, 6, size=(m, sub.shape[1], 1))).astype(np.float32)
+    else:
+        f = np.ones((m, sub.shape[1], 1), np.float32)
+        f[rng.random(f.shape) < 0.125] = 1e6
+        f[:, 0] = 1e6  # every row has one
+        sub *= f
+    x = sub.reshape(m, k)
+    assert np.abs(x).max() > 65504
+    w = gpu_ctx.upload(QType[qtype.upper()], raw, n, k)
+    y = gpu_ctx.empty((m, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)
+    got = y.numpy()
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
+    _say("rel err", e)
+    assert e <= (1e-4 if m <= 32 else TOL)
 
 
 @pytest.mark.parametrize("qtype,m,n,k", [("q6_k", 33, 64, 4096), ("q8_0", 129, 300, 640),
@@ -401,8 +435,10 @@ def _dead_blocks(qtype, raw, every):
 @pytest.mark.parametrize("m", [1, 2, 200])
 def test_x_dynamic_range_and_dead_blocks(gpu_ctx, oracle, qtype, m):
     # x blocks of 32 scaled over 12 decades, some all zero; weight blocks with d = 0.
-    # The integer GEMVs quantize x per 32-element block, so each block keeps its own range;
-    # m = 200 runs the prefill path (Q4_K: the direct-operand kernel with its d = 0 handling).
+    # m = 1, 2 run the decode GEMVs (the f32 Q4_K GEMV scales x per sub-block, the
+    # integer GEMVs quantize x per 32-element block); m = 200 runs the prefill path
+    # (Q4_K: the direct-operand kernel with its d = 0 handling) on x scaled per row
+    # into f16 range, with no clipping: the largest blocks are far beyond 65504.
     from arf_amd import synth
     n, k = 96, 2048
     _say("case: dynamic range / dead blocks", qtype, m)
@@ -413,8 +449,11 @@ def test_x_dynamic_range_and_dead_blocks(gpu_ctx, oracle, qtype, m):
     scale[rng.random(size=scale.shape) < 0.1] = 0.0
     x = (x.reshape(m, k // 32, 32) * scale[..., None]).reshape(m, k).astype(np.float32)
     if m > 64:
-        # prefill rounds x to f16 (as the reference): keep it in f16's range first
-        x = np.clip(x, -6e4, 6e4).astype(np.float16).astype(np.float32)
+        # prefill keeps 11 bits of x (f16 after the row's power-of-two scale): give the
+        # oracle that same x, so the check is of range handling, not of x's rounding
+        e = np.frexp(np.abs(x).max(axis=1, keepdims=True))[1]
+        sc = np.ldexp(np.float32(1), 15 - e).astype(np.float32)
+        x = ((x * sc).astype(np.float16).astype(np.float32) / sc).astype(np.float32)
     got = _run(gpu_ctx, qtype, raw, x, n)
     want = oracle.matmul_q(qtype, x, raw, n)
     e = rel_err(got, want)
