@@ -79,6 +79,7 @@ _SIGS = {
                                 ctypes.POINTER(_i64), ctypes.POINTER(_int),
                                 ctypes.POINTER(ctypes.c_size_t)]),
     "arfq_matmul": (_int, [_vp, _vp, _int, _i64, _vp, _int, _vp]),
+    "arfq_matmul_noalloc": (_int, [_vp, _vp, _int, _i64, _vp, _int, _vp]),
     "arfq_dequant_f32": (_int, [_vp, _vp, _vp]),
     "arfq_moe_route": (_int, [_vp, _vp, _i64, _int, _int, _int, _vp, _vp]),
     "arfq_moe": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _int, _int, _vp, _int, _vp]),

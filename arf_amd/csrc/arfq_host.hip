@@ -11,9 +11,35 @@
 
 #include <algorithm>
 
+// ---- scratch of the allocation-free matmul (arfq_matmul_noalloc) ----
+// One fixed array per GPU, in the library's code object: resident from the
+// module load until the process ends.  Host code never passes `scratch`
+// itself (in host code the name is a stand-in, not a device address); its
+// device address on each GPU is read once with hipGetSymbolAddress when the
+// first context on that GPU is created and kept in g_noalloc_ptr[device].
+static __device__ __align__(256) uint8_t scratch[ARFQ_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local std::string g_create_err;
+
+constexpr int NOALLOC_DEVICES = 64;
+std::atomic<void *> g_noalloc_ptr[NOALLOC_DEVICES];
+
+// The device address of `scratch` on the current device `device` (looked up
+// once per device); null when the lookup fails.
+hipError_t noalloc_scratch_of(int device, void **out) {
+    *out = nullptr;
+    if (device < 0 || device >= NOALLOC_DEVICES) return hipErrorInvalidDevice;
+    void *p = g_noalloc_ptr[device].load(std::memory_order_acquire);
+    if (!p) {
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_noalloc_ptr[device].store(p, std::memory_order_release);
+    }
+    *out = p;
+    return hipSuccess;
+}
 
 int fail(arfq_ctx *ctx, int code, const std::string &msg) {
     if (ctx) ctx->err = msg;
@@ -89,6 +115,8 @@ int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
         }
     }
     if (e == hipSuccess) e = hipDeviceGetAttribute(&ctx->cus, hipDeviceAttributeMultiprocessorCount, device);
+    // the allocation-free entry point's scratch on this device (resolved here, at set-up)
+    if (e == hipSuccess) e = noalloc_scratch_of(device, &ctx->noalloc_scratch);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_stop);
     if (e == hipSuccess) {
@@ -307,6 +335,37 @@ int arfq_matmul(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m, cons
     if (int rc = check_matmul(ctx, w, expert, m, x, x_dtype, y)) return rc;
     if (int rc = use_device(ctx)) return rc;
     return matmul_enqueue(ctx, w, expert, m, x, x_dtype, y);
+}
+
+int arfq_matmul_noalloc(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m, const void *x,
+                        int x_dtype, float *y) {
+    if (int rc = check_matmul(ctx, w, expert, m, x, x_dtype, y)) return rc;
+    if (int rc = use_device(ctx)) return rc;
+    if (!ctx->noalloc_scratch) return fail(ctx, ARFQ_E_DEVICE, "matmul_noalloc: no scratch on this device");
+    hipError_t e;
+    if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
+        // the decode GEMVs use no scratch
+        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream,
+                              (ctx->options & ARFQ_OPT_GEMV_X16) != 0);
+    } else if (arfq::gemm_supports(w, m)) {
+        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
+        if (plan.scratch_bytes > ARFQ_NOALLOC_SCRATCH_BYTES)
+            return fail(ctx, ARFQ_E_UNSUPPORTED,
+                        "matmul_noalloc: this product needs " + std::to_string(plan.scratch_bytes) +
+                            " bytes of scratch, above the " + std::to_string(ARFQ_NOALLOC_SCRATCH_BYTES) +
+                            "-byte limit (use arfq_matmul)");
+        // every scratch byte a plan reads is written earlier in the same call
+        // (x preparation, then split-K partials before their counter moves); the
+        // split-K counters are the context's, zero between calls
+        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->noalloc_scratch, ctx->tickets,
+                              ctx->ntickets, plan, ctx->stream);
+    } else {
+        return fail(ctx, ARFQ_E_UNSUPPORTED,
+                    "matmul_noalloc: no kernel for qtype " + std::to_string(w->qtype) + " at m=" +
+                        std::to_string(m));
+    }
+    if (e != hipSuccess) return hip_fail(ctx, e, "matmul_noalloc launch");
+    return ARFQ_OK;
 }
 
 int arfq_matmul_repeat(arfq_ctx *ctx, const arfq_weight *const *ws, int n_ws, int iters,

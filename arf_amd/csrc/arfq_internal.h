@@ -21,6 +21,8 @@ struct arfq_ctx {
     // growable scratch for the MoE pipeline (routing, grouping, intermediates)
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // device address of the allocation-free matmul's fixed scratch on this device
+    void *noalloc_scratch = nullptr;
     // split-K arrival counters, one per column tile: zero between launches (the
     // last workgroup of a tile to arrive resets its counter)
     uint32_t *tickets = nullptr;

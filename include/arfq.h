@@ -127,6 +127,23 @@ int arfq_weight_info(const arfq_weight *w, int *qtype, int64_t *n_rows, int64_t 
 int arfq_matmul(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m, const void *x,
                 int x_dtype, float *y);
 
+/* Bytes of the fixed device scratch behind arfq_matmul_noalloc (one array per
+ * GPU, resident from the library's load until the process ends). */
+#define ARFQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/* As arfq_matmul, but allocates nothing: no hipMalloc/hipFree or allocating
+ * library call, on the first call or any other.  The GEMM paths take their
+ * scratch (x preparation, split-K partials) from a fixed 32 MiB device array
+ * per GPU instead of the context's growable buffer; a product that would need
+ * more returns ARFQ_E_UNSUPPORTED (decode shapes, m <= 64 at k, n up to ~20K,
+ * fit; the GEMVs need none).  Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (two streams, two threads) race and must be
+ * ordered by the caller.  No counterpart in the reference: for callers that
+ * cannot allocate -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid device allocation. */
+int arfq_matmul_noalloc(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m, const void *x,
+                        int x_dtype, float *y);
+
 /* Dequantize every expert of `w` into out[n_experts * n_rows * k_cols] (device,
  * f32) with the same device dequant code the matmuls use.  Bit-identical to
  * dequant_q8_0 / dequant_q4_k / dequant_q6_k
