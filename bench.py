@@ -2,15 +2,19 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--quick]
 
-Headline (the JSON `value`): Q4_K decode GEMV, m=1, k=5120, n=17408 -- one step
-is one GEMV launch over one activation vector.  Weights are 8 distinct seeded
+Headline (the JSON `value`): Q4_K decode GEMV, m=1, k=5120, n=17408, f32 x times the
+exact weights in f32 (the reference's arithmetic) -- one step is one GEMV launch over one
+activation vector.  Weights are 8 distinct seeded
 copies (8 x 50 MB, above the 256 MB MALL) used round-robin so the timed loop
 streams from HBM.  Timing: HIP events recorded on the library's stream around
-exactly K back-to-back launches, after W warm-up launches and a stream sync.
+exactly K back-to-back launches, after one set-up launch per weight copy, W warm-up
+launches and a stream sync.
 Secondary configs are measured the same way and reported under "configs".
 
-The CPU baseline runs the oracle (a C restatement of Arf's CPU matmul) on the
-host on a bounded sample; it is a reported baseline, not the target.
+The CPU baselines run the oracle (a C restatement of Arf's CPU matmuls) on the host
+cores, partitioned as the reference does, on bounded samples of every config (the
+headline's in `cpu_baseline`, the others under `configs`); they are reported baselines,
+not targets.
 """
 import argparse
 import json
@@ -39,13 +43,16 @@ def algorithmic_bytes(qtype, m, n, k, x_bytes=4):
 
 
 def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.float32):
-    """Average ms per launch of arfq_matmul over `steps` launches rotating `copies` weights."""
+    """Average ms per launch of arfq_matmul over `steps` launches rotating `copies` weights.
+    Set-up runs one untimed launch per weight copy (so no copy is first touched inside the
+    timed region, whatever `warmup` is), then the `warmup` launches."""
     from arf_amd import QType, synth
     qt = QType[qtype.upper()]
     raw = synth.weight(qtype, n, k, seed=seed)
     ws = [ctx.upload(qt, raw, n, k) for _ in range(copies)]
     x = ctx.to_device(synth.activations(m, k, seed=seed + 1).astype(x_dtype))
     y = ctx.empty((m, n), np.float32)
+    ctx.matmul_repeat(ws, copies, m, x, y)  # set-up: each copy once
     ctx.matmul_repeat(ws, warmup, m, x, y)
     ctx.sync()
     ctx.timer_start()
@@ -114,30 +121,134 @@ def time_moe(ctx, steps, warmup, copies, tokens=None):
     return ms / steps
 
 
-def cpu_baseline_c2(budget_s):
-    """Oracle matmul_nt_q4ks at m=1 (serial, as the reference's par_rows runs m<2) on
-    the full C2 weight, repeated for about `budget_s` seconds."""
+def cpu_model():
+    """The host CPU's model name (from /proc/cpuinfo) and logical CPU count."""
+    name = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return name, os.cpu_count() or 1
+
+
+# threads for the reference's par_rows (std::thread::available_parallelism on the GPU box,
+# capped at the 16-core share a one-GPU box gives a job)
+CPU_PAR_THREADS = max(1, min(os.cpu_count() or 1, 16))
+
+
+def _timed(fn, budget_s, min_reps=1):
+    """Seconds per call of fn, repeated for about budget_s (at least min_reps calls)."""
+    t0 = time.perf_counter()
+    reps = 0
+    while reps < min_reps or time.perf_counter() - t0 < budget_s:
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def cpu_baselines(budget_s):
+    """The repo's CPU path (the oracle: a C restatement of arf-ml's matmuls) on the host,
+    partitioned as the reference partitions it: par_rows over M with one thread per core,
+    serial when M < 2 (crates/arf-ml/src/matmul.rs:16-45), the MoE token loop serial
+    (crates/arf-core/src/model/moe.rs:69).  Q4_K weights are transcoded to Q4_K_S first and
+    Q6_K ones dequantized to f32 first, as the reference does at load time; neither is
+    timed in the matmul figures (Q6_K's dequant is reported beside).  C4 and C5 run a
+    bounded sample of rows / tokens and report the full-size rate by linear scaling."""
     from arf_amd import synth
     from oracle import oracle
+    model, ncpu = cpu_model()
+    out = {}
+    host = f"host {model}, {ncpu} logical CPUs"
+
+    # C2 (headline): matmul_nt_q4ks, m = 1 (serial), full size
     n, k = 17408, 5120
     raw = synth.weight("q4_k", n, k, seed=0xA7F00002)
     x = synth.activations(1, k, seed=0xA7F00003)
-    q4ks = oracle.q4ks_from_ggml(raw, n, k)  # load-time transcode, not timed
+    q4ks = oracle.q4ks_from_ggml(raw, n, k)
     oracle.set_threads(1)
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        oracle.matmul_q4ks(x, q4ks, n)
-        reps += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = (time.perf_counter() - t0) / reps
-    oracle.set_threads(0)
+    dt, reps = _timed(lambda: oracle.matmul_q4ks(x, q4ks, n), budget_s)
     gbs = algorithmic_bytes("q4_k", 1, n, k) / dt / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} full C2 GEMVs (m=1, k=5120, n=17408) in {dt * reps:.1f} s, "
-                      f"{dt * 1e3:.1f} ms each, oracle matmul_nt_q4ks serial (reference "
-                      f"par_rows is serial at m<2); host {platform.processor() or platform.machine()}"}
+    out["c2"] = {"value": round(gbs, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                 "sample": f"{reps} full C2 GEMVs (m=1, k=5120, n=17408), {dt * 1e3:.1f} ms each, "
+                           f"oracle matmul_nt_q4ks serial (par_rows is serial at m<2); {host}"}
+    # C1: matmul_nt_q8_0, m = 1 (serial)
+    raw = synth.weight("q8_0", 2048, 2048, seed=0xA7F00001)
+    x = synth.activations(1, 2048, seed=0xA7F00002)
+    dt, reps = _timed(lambda: oracle.matmul_q("q8_0", x, raw, 2048), budget_s / 10)
+    out["c1"] = {"us_per_call": round(dt * 1e6, 1),
+                 "GB/s": round(algorithmic_bytes("q8_0", 1, 2048, 2048) / dt / 1e9, 3), "cores": 1,
+                 "kind": "port", "sample": f"{reps} full C1 GEMVs, oracle matmul_nt_q8_0 serial; {host}"}
+    # C3: dequant_q6_k (load time) + matmul_nt at m = 1 (serial), 8, 32, 64 (par_rows)
+    n, k = 5120, 17408
+    raw = synth.weight("q6_k", n, k, seed=0xA7F00003)
+    t0 = time.perf_counter()
+    wf = oracle.dequant("q6_k", raw, n * k).reshape(n, k)
+    deq = time.perf_counter() - t0
+    for mm in (1, 8, 32, 64):
+        x = synth.activations(mm, k, seed=0xA7F00004)
+        oracle.set_threads(1 if mm < 2 else CPU_PAR_THREADS)
+        dt, reps = _timed(lambda: oracle.matmul_nt(x, wf), budget_s / 20)
+        cores = 1 if mm < 2 else CPU_PAR_THREADS
+        out[f"c3_m{mm}"] = {"us_per_call": round(dt * 1e6, 1),
+                            "GB/s": round(algorithmic_bytes("q6_k", mm, n, k) / dt / 1e9, 3),
+                            "cores": cores, "kind": "port",
+                            "sample": f"{reps} full C3 products at m={mm}, oracle matmul_nt on the "
+                                      f"f32 dequant ({cores} thread(s)); dequant_q6_k of the weight "
+                                      f"(serial, load time) took {deq * 1e3:.0f} ms; {host}"}
+    # C4: matmul_nt_q4ks with par_rows over the 2048 rows: a sample of 128 rows, scaled
+    n, k, M, ms_ = 17408, 5120, 2048, 128
+    raw = synth.weight("q4_k", n, k, seed=0xA7F00004)
+    q4ks = oracle.q4ks_from_ggml(raw, n, k)
+    x = synth.activations(ms_, k, seed=0xA7F00005, dtype=np.float16).astype(np.float32)
+    oracle.set_threads(CPU_PAR_THREADS)
+    dt, reps = _timed(lambda: oracle.matmul_q4ks(x, q4ks, n), budget_s / 5)
+    full = dt * M / ms_
+    out["c4"] = {"ms_full_estimate": round(full * 1e3, 1),
+                 "TFLOP/s": round(2.0 * M * n * k / full / 1e12, 5), "cores": CPU_PAR_THREADS,
+                 "kind": "port",
+                 "sample": f"{reps} runs of {ms_} of C4's 2048 rows ({dt * 1e3:.0f} ms each, scaled "
+                           f"x{M // ms_}), oracle matmul_nt_q4ks with par_rows over "
+                           f"{CPU_PAR_THREADS} threads; {host}"}
+    # C5: MoeMlp::forward, serial token loop, each expert's three projections at m = 1
+    cfg = synth.CONFIGS["c5_moe"]
+    E, T, topk, hid, inter = cfg["experts"], cfg["tokens"], cfg["top_k"], cfg["hidden"], cfg["inter"]
+    g = synth.weight("q4_k", inter, hid, seed=0xA7F00005, experts=E).reshape(E, -1)
+    u = synth.weight("q4_k", inter, hid, seed=0xA7F00006, experts=E).reshape(E, -1)
+    d = synth.weight("q4_k", hid, inter, seed=0xA7F00007, experts=E).reshape(E, -1)
+    gs = [oracle.q4ks_from_ggml(g[e], inter, hid) for e in range(E)]
+    us = [oracle.q4ks_from_ggml(u[e], inter, hid) for e in range(E)]
+    ds = [oracle.q4ks_from_ggml(d[e], hid, inter) for e in range(E)]
+    ts = 16
+    x = synth.activations(ts, hid, seed=0xA7F00008, dtype=np.float16).astype(np.float32)
+    lg = synth.router_logits(ts, E, seed=0xA7F00009)
+    oracle.set_threads(1)
+
+    def moe_sample():
+        y = np.zeros((ts, hid), np.float32)
+        for t in range(ts):
+            ids, wts = oracle.top_k_softmax(lg[t], topk, True)
+            for e, wj in zip(ids, wts):
+                gg = oracle.matmul_q4ks(x[t], gs[e], inter)
+                uu = oracle.matmul_q4ks(x[t], us[e], inter)
+                h = (gg / (np.float32(1) + np.exp(-gg)) * uu).astype(np.float32)
+                y[t] += wj * oracle.matmul_q4ks(h, ds[e], hid)[0]
+        return y
+
+    with np.errstate(over="ignore"):
+        dt, reps = _timed(moe_sample, budget_s / 5)
+    full = dt * T / ts
+    out["c5"] = {"ms_full_estimate": round(full * 1e3, 1),
+                 "TFLOP/s": round(2.0 * T * topk * 3 * inter * hid / full / 1e12, 5), "cores": 1,
+                 "kind": "port",
+                 "sample": f"{reps} runs of {ts} of C5's 512 tokens ({dt * 1e3:.0f} ms each, scaled "
+                           f"x{T // ts}): serial token loop, top-8 routing, three matmul_nt_q4ks "
+                           f"per (token, expert) at m=1; {host}"}
+    oracle.set_threads(0)
+    return out
 
 
 def load_traffic(name):
@@ -153,27 +264,32 @@ COPY_PROBE_LAUNCHES = 4
 TRAFFIC_PROBE_LAUNCHES = 16
 
 
-def traffic_probe(ctx, copies):
+def traffic_probe(ctx, copies, config="c2"):
     """Kernels for the HBM byte counters (FETCH_SIZE / WRITE_SIZE, one rocprofv3
     --pmc pass each): COPY_PROBE_LAUNCHES copies of COPY_PROBE_BYTES (the known
     size that calibrates the counters: a copy reads and writes exactly that many
-    bytes), then TRAFFIC_PROBE_LAUNCHES C2 GEMVs rotating `copies` weights, as
-    in the timed loop."""
-    from arf_amd import QType, synth
+    bytes), then TRAFFIC_PROBE_LAUNCHES calls of `config` (C2 by default; any
+    --only name) rotating `copies` weights, as in the timed loop."""
     a = ctx.empty((COPY_PROBE_BYTES,), np.uint8)
     b = ctx.empty((COPY_PROBE_BYTES,), np.uint8)
     for _ in range(COPY_PROBE_LAUNCHES):
         ctx.copy_d2d(b, a)
     ctx.sync()
-    n, k = 17408, 5120
-    raw = synth.weight("q4_k", n, k, seed=0xA7F00002)
-    ws = [ctx.upload(QType.Q4_K, raw, n, k) for _ in range(copies)]
-    x = ctx.to_device(synth.activations(1, k, seed=0xA7F00003))
-    y = ctx.empty((1, n), np.float32)
-    ctx.matmul_repeat(ws, TRAFFIC_PROBE_LAUNCHES, 1, x, y)
+    a.free()
+    b.free()
+    shape = {"c1": ("q8_0", 1, 2048, 2048), "c2": ("q4_k", 1, 17408, 5120),
+             "c3m1": ("q6_k", 1, 5120, 17408), "c3m8": ("q6_k", 8, 5120, 17408),
+             "c3m32": ("q6_k", 32, 5120, 17408), "c3m64": ("q6_k", 64, 5120, 17408),
+             "c4": ("q4_k", 2048, 17408, 5120)}
+    if config == "c5":
+        time_moe(ctx, TRAFFIC_PROBE_LAUNCHES, 0, copies)
+    else:
+        qt, m, n, k = shape[config]
+        time_matmul(ctx, qt, m, n, k, TRAFFIC_PROBE_LAUNCHES, 0, copies, 0xA7F00002,
+                    x_dtype=np.float16 if m == 2048 else np.float32)
     ctx.sync()
-    log(f"[probe] {COPY_PROBE_LAUNCHES} copies of {COPY_PROBE_BYTES} B, "
-        f"{TRAFFIC_PROBE_LAUNCHES} C2 GEMVs over {copies} weight copies")
+    log(f"[probe] {COPY_PROBE_LAUNCHES} copies of {COPY_PROBE_BYTES} B, then {config}: "
+        f"{copies} set-up + {TRAFFIC_PROBE_LAUNCHES} launches over {copies} weight copies")
 
 
 def gguf_reader_bench(ctx):
@@ -236,6 +352,35 @@ def gguf_reader_bench(ctx):
     print(json.dumps(out), flush=True)
 
 
+def only_config(ctx, args):
+    """One config, timed as in the full run (args.steps launches after args.warmup)."""
+    from arf_amd import synth
+    import arf_amd.arfq as _arfq
+    c = args.only
+    if c in ("c2", "c2x16"):
+        if c == "c2x16":
+            ctx.set_options(_arfq.OPT_GEMV_X16)
+        ms, _ = time_matmul(ctx, "q4_k", 1, 17408, 5120, args.steps, args.warmup, args.copies, 0xA7F00002)
+        ctx.set_options(0)
+        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q4_k", 1, 17408, 5120) / ms / 1e6}
+    elif c == "c1":
+        ms, _ = time_matmul(ctx, "q8_0", 1, 2048, 2048, args.steps, args.warmup, 64, 0xA7F00001)
+        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q8_0", 1, 2048, 2048) / ms / 1e6}
+    elif c.startswith("c3"):
+        mm = int(c[3:])
+        ms, _ = time_matmul(ctx, "q6_k", mm, 5120, 17408, args.steps, args.warmup, 6, 0xA7F00003)
+        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q6_k", mm, 5120, 17408) / ms / 1e6}
+    elif c == "c4":
+        ms, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, args.steps, args.warmup, 2, 0xA7F00004,
+                            x_dtype=np.float16)
+        res = {"us_per_launch": ms * 1e3, "TFLOP/s": 2.0 * 2048 * 17408 * 5120 / ms / 1e9}
+    else:  # c5
+        ms = time_moe(ctx, args.steps, args.warmup, 3)
+        res = {"us_per_launch": ms * 1e3}
+    log(f"[bench] {c}: {res}")
+    print(json.dumps({"only": c, "steps": args.steps, "warmup": args.warmup, **res}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -249,6 +394,8 @@ def main():
                     help="time the GGUF reader instead: open a synthetic model file (C5's expert "
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
+    ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m8", "c3m32", "c3m64", "c4", "c5"],
+                    help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
                          "calibration), then TRAFFIC_PROBE_LAUNCHES C2 GEMVs; prints no JSON")
@@ -262,11 +409,16 @@ def main():
     from arf_amd import synth
     ctx = arf_amd.Context(0)
     if args.traffic_probe:
-        traffic_probe(ctx, args.copies)
+        traffic_probe(ctx, args.copies, args.only or "c2")
         ctx.close()
         return
     if args.gguf_reader:
         gguf_reader_bench(ctx)
+        ctx.close()
+        return
+
+    if args.only:
+        only_config(ctx, args)
         ctx.close()
         return
 
@@ -282,6 +434,18 @@ def main():
     configs = {}
     if not args.quick:
         steps2 = max(50, args.steps // 4)
+        # C2 again with ARFQ_OPT_GEMV_X16: x rounded to 16-bit fixed point per 32 elements
+        # and integer v_dot8 (faster, ~1e-4 rel err): not the reference's arithmetic
+        import arf_amd.arfq as _arfq
+        ctx.set_options(_arfq.OPT_GEMV_X16)
+        msx, _ = time_matmul(ctx, "q4_k", 1, n, k, steps2, 50, args.copies, seed=0xA7F00002)
+        ctx.set_options(0)
+        configs["c2_q4_k_gemv_m1_k5120_n17408_x16_option"] = {
+            "us_per_launch": round(msx * 1e3, 3), "GB/s": round(nbytes / msx / 1e6, 1),
+            "hbm_frac": round(nbytes / msx / 1e6 / HBM_PEAK_GBS, 4),
+            "dtype": "u4xi16->i32,f32", "note": "ARFQ_OPT_GEMV_X16: x in 16-bit fixed point per "
+            "32 elements (max rel err ~1e-4), integer dots; not the reference's f32 arithmetic"}
+        log(f"[bench] C2 x16 option: {msx * 1e3:.2f} us/launch")
         # C1 Q8_0 GEMV
         ms1, _ = time_matmul(ctx, "q8_0", 1, 2048, 2048, steps2, 50, 64, seed=0xA7F00001)
         b1 = algorithmic_bytes("q8_0", 1, 2048, 2048)
@@ -317,7 +481,7 @@ def main():
                 except arf_amd.ArfqError as e:
                     configs[key] = {"error": str(e)}
                     continue
-                bq = algorithmic_bytes(qt, mm, 17408, 5120)
+                bq = algorithmic_bytes(qt, mm, 17408, 5120, x_bytes=2 if mm == 2048 else 4)
                 configs[key] = {"us_per_launch": round(msq * 1e3, 3), "GB/s": round(bq / msq / 1e6, 1),
                                 "hbm_frac": round(bq / msq / 1e6 / HBM_PEAK_GBS, 4)}
                 if mm == 2048:
@@ -397,9 +561,15 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        log(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s)")
-        cpu = cpu_baseline_c2(args.cpu_seconds)
-        log(f"[bench] cpu: {cpu['value']} GB/s")
+        log(f"[bench] cpu baselines (~{2 * args.cpu_seconds:.0f} s)")
+        cpus = cpu_baselines(args.cpu_seconds)
+        cpu = cpus.pop("c2")
+        log(f"[bench] cpu C2: {cpu['value']} GB/s")
+        keys = {"c1": "c1_q8_0_gemv_m1_k2048_n2048", "c4": "c4_q4_k_gemm_m2048_k5120_n17408",
+                "c5": "c5_moe_q4_k_e128_top8_t512_h2048_i768"}
+        keys.update({f"c3_m{mm}": f"c3_q6_k_m{mm}_k17408_n5120" for mm in (1, 8, 32, 64)})
+        for ck, v in cpus.items():
+            configs.setdefault(keys[ck], {})["cpu_baseline"] = v
 
     ctx.close()
     out = {
@@ -413,12 +583,13 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u4xi16->i32,f32",
+        "dtype": "f32",
         "data": "synthetic (seeded Q4_K superblocks per BASELINE config 2, x ~ N(0,1) f32)",
         "config": {"workload": "c2_q4_k_gemv_m1_k5120_n17408", "m": m, "k": k, "n": n,
                    "weight_copies": args.copies, "parallelism": "single-gpu",
-                   "compute": "4-bit codes x 16-bit fixed-point activation digits on v_dot8 "
-                              "(exact int32 per sub-block), f32 scale and accumulate"},
+                   "compute": "f32 x times the exact 4-bit codes (v_fma_mix_f32 on f16-subnormal "
+                              "nibbles), f32 sums per 32-weight sub-block, then (d*sc)*code_sum - "
+                              "(dmin*m)*x_sum in f32, as matmul_nt_q4ks"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                      "traffic": load_traffic("q4k_gemv_c2_traffic.json")},

@@ -161,3 +161,34 @@ def moe_route_lcg_logits(count, state):
         s = (s * 6364136223846793005 + 1) & 0xFFFFFFFFFFFFFFFF
         out.append(np.float32(np.float32(s >> 40) / np.float32(1 << 23) - np.float32(0.5)))
     return np.array(out, np.float32), s
+
+
+def moe_dequant_reference(oracle, x, raw, E, hidden, inter, logits, top_k, norm):
+    """MoeMlp::forward (moe.rs:53-86) on every token from the oracle's routing
+    (top_k_softmax) and bit-exact dequant, the projections as float32 BLAS products over
+    each expert's tokens (quantized linear == dequant + f32 matmul, weight.rs:1693-1709),
+    SwiGLU (mlp.rs:20-24) in f32 and out[t] += w_j * y_j in top-k slot order."""
+    T = x.shape[0]
+    x = np.asarray(x, np.float32)
+    ids = np.zeros((T, top_k), np.int64)
+    wts = np.zeros((T, top_k), np.float32)
+    for t in range(T):
+        ids[t], wts[t] = oracle.top_k_softmax(logits[t], top_k, norm)
+    g_all, u_all, d_all = (r.reshape(E, -1) for r in raw)
+    ys = np.zeros((T, top_k, hidden), np.float32)
+    for e in range(E):
+        tt, jj = np.nonzero(ids == e)
+        if tt.size == 0:
+            continue
+        wg = oracle.dequant("q4_k", g_all[e], inter * hidden).reshape(inter, hidden)
+        wu = oracle.dequant("q4_k", u_all[e], inter * hidden).reshape(inter, hidden)
+        wd = oracle.dequant("q4_k", d_all[e], hidden * inter).reshape(hidden, inter)
+        xe = x[tt]
+        g, u = xe @ wg.T, xe @ wu.T
+        with np.errstate(over="ignore"):  # exp(-g) = inf for g << 0: silu -> 0, as in f32
+            h = (g / (np.float32(1) + np.exp(-g)) * u).astype(np.float32)
+        ys[tt, jj] = h @ wd.T
+    out = np.zeros((T, hidden), np.float32)
+    for j in range(top_k):
+        out += wts[:, j:j + 1] * ys[:, j]
+    return out

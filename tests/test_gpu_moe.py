@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from conftest import rel_err
-from formats import moe_route_lcg_logits
+from formats import moe_dequant_reference, moe_route_lcg_logits
 
 pytestmark = pytest.mark.gpu
 
@@ -250,7 +250,7 @@ def test_moe_shape_errors(gpu_ctx):
 
 
 def test_c5_moe_full(gpu_ctx, oracle):
-    # C5: 128 experts, top-8, T=512, hidden 2048, inter 768; oracle on 24 sampled tokens
+    # C5: 128 experts, top-8, T=512, hidden 2048, inter 768; every token checked
     from arf_amd import synth
     _say("case: C5 full")
     cfg = synth.CONFIGS["c5_moe"]
@@ -259,13 +259,15 @@ def test_c5_moe_full(gpu_ctx, oracle):
     x = synth.activations(T, hidden, seed=0xA7F00008, dtype=np.float16)
     logits = synth.router_logits(T, E, seed=0xA7F00009)
     got = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
-    rows = np.r_[0:8, 252:260, 504:512]
-    want = oracle.moe_forward(x[rows].astype(np.float32), raw[0], raw[1], raw[2], E, inter,
-                              logits[rows], k, True)
-    e = rel_err(got[rows], want)
-    _say("C5 rel err (24 sampled tokens)", e)
-    assert e <= TOL
     assert np.all(np.isfinite(got))
+    want = moe_dequant_reference(oracle, x, raw, E, hidden, inter, logits, k, True)
+    e = rel_err(got, want)
+    _say("C5 rel err (all 512 tokens)", e)
+    assert e <= TOL
+    # and a few tokens against the oracle's own MoeMlp::forward
+    rows = np.r_[0:2, 510:512]
+    assert rel_err(got[rows], oracle.moe_forward(x[rows].astype(np.float32), raw[0], raw[1], raw[2],
+                                                 E, inter, logits[rows], k, True)) <= TOL
 
 
 # ------------------------------------------------------------------- FFN ----

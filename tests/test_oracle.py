@@ -400,3 +400,20 @@ def test_moe_one_hot_router_is_the_expert(oracle):
     h = (g / (1 + np.exp(-g))) * u
     y = oracle.matmul_q("q4_k", h.astype(np.float32), db, hidden)
     assert rel_err(got, y) < 1e-6
+
+
+def test_moe_dequant_reference_equals_moe_forward(oracle):
+    # the full-size C5 GPU check computes MoeMlp::forward from the oracle's routing and
+    # dequant with BLAS products per expert; it must agree with the oracle's own
+    # restatement of moe.rs:53-86 (serial token loop, matmul_nt_q4ks per projection)
+    from arf_amd import synth
+    from formats import moe_dequant_reference
+    E, T, k, hidden, inter = 8, 24, 2, 512, 256
+    raw = [synth.weight("q4_k", inter, hidden, seed=70, experts=E),
+           synth.weight("q4_k", inter, hidden, seed=71, experts=E),
+           synth.weight("q4_k", hidden, inter, seed=72, experts=E)]
+    x = (synth.activations(T, hidden, seed=73) * np.float32(0.05)).astype(np.float32)
+    logits = synth.router_logits(T, E, seed=74)
+    want = oracle.moe_forward(x, raw[0], raw[1], raw[2], E, inter, logits, k, True)
+    got = moe_dequant_reference(oracle, x, raw, E, hidden, inter, logits, k, True)
+    assert rel_err(got, want) < 1e-5
