@@ -251,11 +251,16 @@ def cpu_baselines(budget_s):
     return out
 
 
-def load_traffic(name):
+def load_traffic(name, kernel):
+    """HBM bytes per dispatch of the kernel whose name contains `kernel`, from a
+    profiles/*_traffic.json summary of two rocprofv3 --pmc passes (FETCH_SIZE,
+    WRITE_SIZE), or None."""
     p = os.path.join(ROOT, "profiles", name)
     if os.path.exists(p):
         with open(p) as f:
-            return json.load(f).get("traffic_bytes_per_launch")
+            for kname, v in json.load(f).get("kernels", {}).items():
+                if kernel in kname:
+                    return v.get("traffic_bytes_per_launch")
     return None
 
 
@@ -592,7 +597,7 @@ def main():
                               "(dmin*m)*x_sum in f32, as matmul_nt_q4ks"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic("q4k_gemv_c2_traffic.json")},
+                     "traffic": load_traffic("q4k_gemv_c2_traffic.json", "gemv_q4k_f32")},
         "cpu_baseline": cpu,
         "configs": configs,
     }
