@@ -96,7 +96,8 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
                                                       const uint16_t *__restrict__ xs,
                                                       const float *__restrict__ rs,
                                                       float *__restrict__ y, float *__restrict__ part,
-                                                      uint32_t *__restrict__ tick, int M, int N, int K) {
+                                                      uint32_t *__restrict__ tick, int M, int N, int K,
+                                                      int rss) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     __shared__ int last;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -136,6 +137,16 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
                 if (m < M && n < N) y[(int64_t)m * N + n] = rs ? acc[0][t][i] * rs[m] : acc[0][t][i];
             }
         return;
+    }
+    // x scaled per K range (rs[sp * rss + row]): the partial back to true units
+    if (rs) {
+#pragma unroll
+        for (int t = 0; t < TA; t++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) {
+                const int m = sk_out_row(t, i);
+                acc[0][t][i] *= m < M ? rs[(int64_t)sp * rss + m] : 1.f;
+            }
     }
     // Split K.  Each wave stores its accumulators as they sit in registers:
     // float4 (row group gi = 4 t + g, lane) holds acc[t][4 g .. 4 g + 3], rows
@@ -204,7 +215,7 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
         const int row = 32 * t + 8 * g + 4 * (lane >> 5);
 #pragma unroll
         for (int c = 0; c < 4; c++)
-            if (row + c < M && n < N) y[(int64_t)(row + c) * N + n] = rs ? r[c] * rs[row + c] : r[c];
+            if (row + c < M && n < N) y[(int64_t)(row + c) * N + n] = r[c];
     }
 }
 
@@ -220,15 +231,33 @@ __global__ void splitk_reduce(const float *__restrict__ part, float *__restrict_
 }
 
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
-                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair) {
+                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair, int rs_splits) {
     if (m == 0 || (!xh && !xl && !xs)) return hipSuccess;
-    if (k % 32 || m > INT32_MAX || (pair && (!xh || xl != xh + m * k))) return hipErrorInvalidValue;
+    if (k % 32 || k > INT32_MAX || (pair && (!xh || xl != xh + m * k))) return hipErrorInvalidValue;
+    // segments: with rs, the skinny kernel's K ranges (whole 256-element
+    // blocks) or the whole row; otherwise up to XPREP_THREADS * XPREP_NJ * 8
+    // elements
+    int S, unit;
+    if (rs && rs_splits > 1) {
+        if (k % 256 || rs_splits > k / 256) return hipErrorInvalidValue;
+        S = rs_splits;
+        unit = 256;
+    } else if (rs) {
+        S = 1;
+        unit = 32;
+    } else {
+        unit = 32;
+        constexpr int per = XPREP_THREADS * XPREP_NJ * 8 / 32;  // 32-element units per segment
+        S = (int)((k / 32 + per - 1) / per);
+    }
+    if (m * S > INT32_MAX) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(m * S);
     if (x_dtype == ARFQ_F32)
-        xprep_kernel<float><<<(unsigned)m, XPREP_THREADS, 0, s>>>((const float *)x, m, (int)k, xh, xl, xs, rs,
-                                                                  pair ? 1 : 0);
+        xprep_kernel<float><<<grid, XPREP_THREADS, 0, s>>>((const float *)x, m, (int)k, xh, xl, xs, rs,
+                                                           pair ? 1 : 0, S, unit);
     else
-        xprep_kernel<_Float16><<<(unsigned)m, XPREP_THREADS, 0, s>>>((const _Float16 *)x, m, (int)k, xh, xl,
-                                                                     xs, nullptr, pair ? 1 : 0);
+        xprep_kernel<_Float16><<<grid, XPREP_THREADS, 0, s>>>((const _Float16 *)x, m, (int)k, xh, xl,
+                                                              xs, nullptr, pair ? 1 : 0, S, unit);
     return hipGetLastError();
 }
 
@@ -311,8 +340,8 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     o += p.xsplit ? al256((size_t)m * w->k * 2) : 0;
     p.off_xs = o;
     o += p.sums ? al256((size_t)(p.pair ? 2 : 1) * m * (w->k / 16) * 2) : 0;
-    p.off_rs = o;
-    o += p.convert ? al256((size_t)m * 4) : 0;
+    p.off_rs = o;  // skinny: one scale per row and split
+    o += p.convert ? al256((size_t)(p.skinny ? p.splits : 1) * m * 4) : 0;
     p.off_part = o;
     if (p.skinny)  // partials in register order: [split][column tile][wave][8-row group][lane] float4
         o += p.splits > 1 ? al256((size_t)p.splits * ((w->n + 127) / 128) * ((std::min<int64_t>(m, 64) + 7) / 8) * 4096)
@@ -325,7 +354,7 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
 
 template <class F, int TA, bool PAIR>
 static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
-                              const uint16_t *xs, const float *rs, float *y, float *part,
+                              const uint16_t *xs, const float *rs, int rss, float *y, float *part,
                               uint32_t *tick, int S, hipStream_t s) {
     constexpr size_t lds = sk_lds<F, TA, 1>();
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
@@ -333,25 +362,26 @@ static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, con
         return err;
     const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
     gemm_sk<F, TA, _Float16, PAIR><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
-                                                                 (int)w->n, (int)w->k);
+                                                                 (int)w->n, (int)w->k, rss);
     return hipGetLastError();
 }
 
 // S > 1 splits need S <= 16 and one zeroed counter per 128-column tile.  x is
-// f16 (an f32 x arrives prepared and row-scaled, rs its row scales); with pair
-// (m <= 16) it is [2m, K]: the hi rows, then the lo rows.
+// f16 (an f32 x arrives prepared and scaled, rs[split * rss + row] its scale
+// over each split's K range); with pair (m <= 32) it is [2m, K]: the hi rows,
+// then the lo rows.
 template <class F>
 static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
-                            const uint16_t *xs, const float *rs, float *y, float *part, uint32_t *tick,
-                            int ntick, int S, hipStream_t s, bool pair) {
+                            const uint16_t *xs, const float *rs, int rss, float *y, float *part,
+                            uint32_t *tick, int ntick, int S, hipStream_t s, bool pair) {
     if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;
     if (pair) {
         if (m > 32) return hipErrorInvalidValue;
-        return m <= 16 ? launch_sk_t<F, 1, true>(fmt, w, m, x, xs, rs, y, part, tick, S, s)
-                       : launch_sk_t<F, 2, true>(fmt, w, m, x, xs, rs, y, part, tick, S, s);
+        return m <= 16 ? launch_sk_t<F, 1, true>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
+                       : launch_sk_t<F, 2, true>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
     }
-    return m <= 32 ? launch_sk_t<F, 1, false>(fmt, w, m, x, xs, rs, y, part, tick, S, s)
-                   : launch_sk_t<F, 2, false>(fmt, w, m, x, xs, rs, y, part, tick, S, s);
+    return m <= 32 ? launch_sk_t<F, 1, false>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
+                   : launch_sk_t<F, 2, false>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
 }
 
 SkQ4K sk_q4k(const arfq_weight *w) {
@@ -377,12 +407,12 @@ template <class F>
 static hipError_t launch_sk_rows(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                                  const uint16_t *xs, const float *rs, float *y, float *part,
                                  uint32_t *tick, int ntick, int S, hipStream_t s, bool pair) {
-    if (pair) return launch_sk(fmt, w, m, x, xs, rs, y, part, tick, ntick, S, s, true);  // m <= 32
+    if (pair) return launch_sk(fmt, w, m, x, xs, rs, (int)m, y, part, tick, ntick, S, s, true);  // m <= 32
     for (int64_t r0 = 0; r0 < m; r0 += 64) {
         const int64_t mc = std::min<int64_t>(64, m - r0);
         if (hipError_t err = launch_sk(fmt, w, mc, x + r0 * w->k, xs ? xs + r0 * (w->k / 16) : nullptr,
-                                       rs ? rs + r0 : nullptr, y + r0 * w->n, part, tick, ntick, S, s,
-                                       false))
+                                       rs ? rs + r0 : nullptr, (int)m, y + r0 * w->n, part, tick, ntick,
+                                       S, s, false))
             return err;
     }
     return hipSuccess;
@@ -457,7 +487,8 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     uint16_t *xs = p.sums ? (uint16_t *)(sc + p.off_xs) : nullptr;
     float *rs = p.convert ? (float *)(sc + p.off_rs) : nullptr;  // row scales of an f32 x
     if (p.convert || p.sums) {
-        hipError_t err = launch_xprep(x, x_dtype, m, w->k, p.convert ? xh : nullptr, xl, xs, rs, s, p.pair);
+        hipError_t err = launch_xprep(x, x_dtype, m, w->k, p.convert ? xh : nullptr, xl, xs, rs, s, p.pair,
+                                      p.skinny ? p.splits : 1);
         if (err != hipSuccess) return err;
     }
     float *out = p.splits > 1 ? (float *)(sc + p.off_part) : y;
@@ -468,14 +499,14 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         const int64_t eb = (int64_t)e * w->n * (w->k / 256);
         switch (w->qtype) {
         case ARFQ_Q4_K:
-            return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets, ntickets,
+            return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
                              p.splits, s, p.pair);
         case ARFQ_Q6_K:
-            return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets, ntickets,
+            return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
                              p.splits, s, p.pair);
         case ARFQ_Q8_0:
             return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xs, rs,
-                             y, out, tickets, ntickets, p.splits, s, p.pair);
+                             (int)m, y, out, tickets, ntickets, p.splits, s, p.pair);
         case ARFQ_Q5_K:
             return launch_sk_rows(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets,
                                   ntickets, p.splits, s, p.pair);

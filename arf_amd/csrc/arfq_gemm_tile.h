@@ -560,26 +560,30 @@ __device__ __forceinline__ int tile_out_col(int b) {
 }
 
 // ---- activation preparation ------------------------------------------------
-// One workgroup per row of a row-major [M, K] activation (K a multiple of 32),
-// one thread per 8 consecutive elements in each pass, so a quad of lanes covers
-// a 32-element sub-block and every load and store is 16 bytes wide and
-// coalesced.  Writes x as f16 (and, when `xl` is set, the f16 remainder
-// x - hi) and, when `xs` is set, the sub-block sum X (of the values the MFMAs
-// will see: each lane's 8 in order, then the quad's four partial sums
-// pairwise) as bf16 hi + lo into xs[row][k / 256][j] and [8 + j] (j =
-// sub-block within block).
+// Row-major [M, K] activation (K a multiple of 32) in segments: workgroup b
+// takes segment sp = b % S of row b / S, the elements [e(sp), e(sp + 1)) with
+// e(j) = unit * floor(j * (K / unit) / S); one thread per 8 consecutive
+// elements, so a quad of lanes covers a 32-element sub-block and every load
+// and store is 16 bytes wide and coalesced.  A segment of at most
+// XPREP_THREADS * XPREP_NJ * 8 elements is read once, into registers.  Writes x as f16
+// (and, when `xl` is set, the f16 remainder x - hi) and, when `xs` is set, the
+// sub-block sum X (of the values the MFMAs will see: each lane's 8 in order,
+// then the quad's four partial sums pairwise) as bf16 hi + lo into
+// xs[row][k / 256][j] and [8 + j] (j = sub-block within block).
 // With `pair` set, xl must be xh + M * K: the lo remainders are stored as rows
 // M .. 2M - 1 after the hi rows, and xs holds the sums of each hi row at row r
 // and of each lo row at row M + r (xs then has 2M rows); otherwise the sums
 // are of hi + lo.
-// With `rs` set (f32 x), the row is first scanned for its max |x| and every
-// element is stored divided by rs[row] = 2^(e - 15), e the exponent of that
-// max (max in [2^(e-1), 2^e)): an exact power-of-two scaling that puts the
-// row's largest value in [2^14, 2^15), so no finite f32 x overflows f16 and
-// small rows do not fall into f16 subnormals.  The products' consumers
-// multiply their output rows by rs.  Rows whose max is 0 or not finite keep
+// With `rs` set (f32 x), each segment is first scanned for its max |x| and
+// its elements are stored divided by rs[sp * M + row] = 2^(e - 15), e the
+// exponent of that max (max in [2^(e-1), 2^e)): an exact power-of-two scaling
+// that puts the segment's largest value in [2^14, 2^15), so no finite f32 x
+// overflows f16 and small values do not fall into f16 subnormals.  The
+// consumers multiply their partial sums over the segment by its scale (with
+// S = 1: the output rows).  Segments whose max is 0 or not finite keep
 // rs = 1.
 constexpr int XPREP_THREADS = 512;
+constexpr int XPREP_NJ = 2;  // 8-element chunks per thread loaded together
 template <typename TIn>
 __device__ __forceinline__ void xprep_load8(const TIn *__restrict__ p, float v[8]) {
     if constexpr (sizeof(TIn) == 4) {
@@ -596,67 +600,90 @@ __device__ __forceinline__ void xprep_load8(const TIn *__restrict__ p, float v[8
 template <typename TIn>
 __global__ __launch_bounds__(XPREP_THREADS) void xprep_kernel(
     const TIn *__restrict__ x, int64_t M, int K, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
-    uint16_t *__restrict__ xs, float *__restrict__ rs, int pair) {
+    uint16_t *__restrict__ xs, float *__restrict__ rs, int pair, int S, int unit) {
     __shared__ float wmax[XPREP_THREADS / 64];
-    const int64_t row = blockIdx.x;
+    const int64_t row = blockIdx.x / S;
+    const int sp = blockIdx.x % S, tid = threadIdx.x;
+    const int nu = K / unit;
+    const int c0 = unit / 8 * (int)((int64_t)sp * nu / S);  // first and last + 1 8-element chunk
+    const int c1 = unit / 8 * (int)((int64_t)(sp + 1) * nu / S);
     const int nch = K / 8;
     const TIn *xr = x + row * K;
+    // up to XPREP_NJ chunks per thread are loaded together (all in flight), then
+    // processed; a longer segment is walked in rounds of that many (twice with rs)
+    constexpr int NJ = XPREP_NJ, STEP = XPREP_THREADS * NJ;
+    float v[NJ][8];
+    auto load_round = [&](int base) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+            const int ch = base + tid + XPREP_THREADS * j;
+            if (ch < c1) xprep_load8(xr + (int64_t)ch * 8, v[j]);
+        }
+    };
+    const bool once = c1 - c0 <= STEP;  // the segment in registers
+    if (once) load_round(c0);
     int sh = 0;  // elements are stored times 2^sh
     if (rs) {
         float amax = 0.f;
-        for (int ch = threadIdx.x; ch < nch; ch += XPREP_THREADS) {
-            float v[8];
-            xprep_load8(xr + (int64_t)ch * 8, v);
+        for (int base = c0; base < c1; base += STEP) {
+            if (!once) load_round(base);
 #pragma unroll
-            for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[i]));
+            for (int j = 0; j < NJ; j++)
+                if (base + tid + XPREP_THREADS * j < c1)
+#pragma unroll
+                    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(v[j][i]));
         }
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
-        if ((threadIdx.x & 63) == 0) wmax[threadIdx.x >> 6] = amax;
+        if ((tid & 63) == 0) wmax[tid >> 6] = amax;
         __syncthreads();
         amax = wmax[0];
 #pragma unroll
         for (int w = 1; w < XPREP_THREADS / 64; w++) amax = fmaxf(amax, wmax[w]);
         if (amax > 0.f && amax < INFINITY) sh = 15 - __builtin_amdgcn_frexp_expf(amax);
-        if (threadIdx.x == 0) rs[row] = ldexpf(1.f, -sh);
+        if (tid == 0) rs[(int64_t)sp * M + row] = ldexpf(1.f, -sh);
     }
-    // K % 32 == 0 and the stride is a multiple of 4: a quad's lanes run the
+    // c0 % 4 == 0 and the strides are multiples of 4: a quad's lanes run the
     // same iterations, so the quad DPP sums below see the whole sub-block
-    for (int ch = threadIdx.x; ch < nch; ch += XPREP_THREADS) {
-        const int64_t g = row * nch + ch;
-        float v[8];
-        xprep_load8(xr + (int64_t)ch * 8, v);
-        half8 hv, lv;
-        float sum = 0.f, suml = 0.f;
+    for (int base = c0; base < c1; base += STEP) {
+        if (!once) load_round(base);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float u = sh ? ldexpf(v[i], sh) : v[i];
-            hv[i] = (_Float16)u;
-            lv[i] = (_Float16)(u - (float)hv[i]);
-            sum += (xl && !pair) ? ((float)hv[i] + (float)lv[i]) : (float)hv[i];
-            suml += (float)lv[i];
-        }
-        if (xh) reinterpret_cast<half8 *>(xh)[g] = hv;
-        if (xl) reinterpret_cast<half8 *>(xl)[g] = lv;
-        if (xs) {
-            // (s0 + s1) + (s2 + s3) on every lane of the quad (quad_perm [1,0,3,2], then [2,3,0,1])
-            auto quad_sum = [](float t) {
-                t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, true));
-                return t + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, true));
-            };
-            sum = quad_sum(sum);
-            if (pair) suml = quad_sum(suml);
-            if ((ch & 3) == 0) {
-                const int sub = ch >> 2;
-                auto put = [&](int64_t r, float t) {
-                    const uint32_t hi = bf16_bits(t);
-                    const uint32_t lo = bf16_bits(t - bf16_to_f32(hi));
-                    uint16_t *d = xs + r * (K / 16) + (sub >> 3) * 16 + (sub & 7);
-                    d[0] = (uint16_t)hi;
-                    d[8] = (uint16_t)lo;
+        for (int j = 0; j < NJ; j++) {
+            const int ch = base + tid + XPREP_THREADS * j;
+            if (ch >= c1) break;
+            const int64_t g = row * nch + ch;
+            half8 hv, lv;
+            float sum = 0.f, suml = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float u = sh ? ldexpf(v[j][i], sh) : v[j][i];
+                hv[i] = (_Float16)u;
+                lv[i] = (_Float16)(u - (float)hv[i]);
+                sum += (xl && !pair) ? ((float)hv[i] + (float)lv[i]) : (float)hv[i];
+                suml += (float)lv[i];
+            }
+            if (xh) reinterpret_cast<half8 *>(xh)[g] = hv;
+            if (xl) reinterpret_cast<half8 *>(xl)[g] = lv;
+            if (xs) {
+                // (s0 + s1) + (s2 + s3) on every lane of the quad (quad_perm [1,0,3,2], then [2,3,0,1])
+                auto quad_sum = [](float t) {
+                    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, true));
+                    return t + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, true));
                 };
-                put(row, sum);
-                if (pair) put(M + row, suml);
+                sum = quad_sum(sum);
+                if (pair) suml = quad_sum(suml);
+                if ((ch & 3) == 0) {
+                    const int sub = ch >> 2;
+                    auto put = [&](int64_t r, float t) {
+                        const uint32_t hi = bf16_bits(t);
+                        const uint32_t lo = bf16_bits(t - bf16_to_f32(hi));
+                        uint16_t *d = xs + r * (K / 16) + (sub >> 3) * 16 + (sub & 7);
+                        d[0] = (uint16_t)hi;
+                        d[8] = (uint16_t)lo;
+                    };
+                    put(row, sum);
+                    if (pair) put(M + row, suml);
+                }
             }
         }
     }

@@ -1,16 +1,15 @@
-// arfq_gemv.hip -- decode GEMV kernels (m = 1..4 activation rows) for Q4_K,
-// Q8_0 and Q6_K weights.  HBM-bound: every weight byte is read exactly once,
-// with 128-bit loads, and unpacked in registers.
-//
-// Thread mapping (all three formats):
-//   * one workgroup = one wave64 = two half-waves; half-wave h owns R
-//     consecutive output rows;
-//   * lane ll (0..31) of a half-wave owns one fixed chunk position inside a
-//     block (Q4_K: 16 B of qs = 32 nibbles; Q8_0: 16 B = half a block; Q6_K:
-//     one 48-B chunk = 64 codes) and strides over blocks;
-//   * the lane loads the x values matching its chunk once per block and reuses
-//     them for its R rows (so x traffic is 1/R of the weight traffic through
-//     L1), keeps R partial sums, and the half-wave reduces them at the end.
+// arfq_gemv.hip -- decode GEMV kernels (m = 1..4 activation rows).  HBM bound:
+// every weight byte is read once, with 128-bit loads, and unpacked in
+// registers.
+//   * Q4_K, m = 1: gemv_q4k_f32 (f32 x times the exact codes; also the MoE
+//     decode pairs and the fused SwiGLU down GEMV); m = 2..4 and the
+//     ARFQ_OPT_GEMV_X16 option: gemv_q4k (x in 16-bit fixed point, integer
+//     dots).  16-lane groups walk (row, 4-block column) steps handed out from
+//     LDS counters.
+//   * Q6_K / Q5_K / IQ4_XS: gemv_dot<Fmt> (x in 16-bit fixed point, integer
+//     dots), the same step walk; gemv_q6k is the fallback for shapes it does
+//     not take.
+//   * Q8_0: gemv_q80w, one wave per row, f32.
 // Reference behaviour: matmul_vec_q4ks_msl.metal:46-165 (simdgroup strides
 // sub-blocks, s*sum(q*x) + lo*sum(x) per sub-block, simd_sum), and the oracle
 // dot_q4ks (crates/arf-ml/src/matmul.rs:327-358), matmul_nt_q8_0 (:174-204).
@@ -1238,53 +1237,99 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot(F fmt, const float 
 }
 
 // ------------------------------------------------------------------ Q8_0 ----
-// Lane chunk c (0..1) = codes [16c, 16c+16) of a 32-weight block.
-template <int R, int MX>
-__global__ __launch_bounds__(64) void gemv_q80(const uint4 *__restrict__ qs,
-                                               const uint16_t *__restrict__ dd,
-                                               const float *__restrict__ x, float *__restrict__ y,
-                                               int n, int nblk, int m) {
-    const int lane = threadIdx.x;
-    const int half = lane >> 5, ll = lane & 31;
-    const int c = ll & 1, bq = ll >> 1;
-    const int64_t row0 = ((int64_t)blockIdx.x * 2 + half) * R;
+// One wave per Q80_ROWS weight rows; lane l takes blocks l, l + 64, ... of
+// each: two 16-byte code loads and the block's f16 d per row, all the loads
+// of a 128-block round issued before the first use, so a row of up to 128
+// blocks costs one memory round trip.  Per block the lane forms
+// d * (sum of x * q over its 32 codes) in f32; the wave then adds its lanes.
+// x rows (f32, <= 4) are read per block from the L1/L2-resident vector, once
+// for the wave's rows.
+// Reference arithmetic: matmul_nt_q8_0 (crates/arf-ml/src/matmul.rs:174-204).
+constexpr int Q80_WAVES = 4, Q80_ROWS = 2;
+template <int MX>
+__global__ __launch_bounds__(64 * Q80_WAVES) void gemv_q80w(const uint4 *__restrict__ qs,
+                                                           const uint16_t *__restrict__ dd,
+                                                           const float *__restrict__ x,
+                                                           float *__restrict__ y, int n, int nblk,
+                                                           int m) {
+    constexpr int R = Q80_ROWS;
+    const int lane = threadIdx.x & 63;
+    const int64_t row0 = ((int64_t)blockIdx.x * Q80_WAVES + (threadIdx.x >> 6)) * R;
+    if (row0 >= n) return;  // the whole wave
     const int64_t k = (int64_t)nblk * 32;
+    const uint4 *qr[R];
+    const uint16_t *dr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int64_t row = min(row0 + r, (int64_t)n - 1);  // rows past n: computed, not stored
+        qr[r] = qs + row * nblk * 2;
+        dr[r] = dd + row * nblk;
+    }
     float acc[MX][R];
 #pragma unroll
     for (int mi = 0; mi < MX; mi++)
 #pragma unroll
         for (int r = 0; r < R; r++) acc[mi][r] = 0.f;
-
-    for (int b = bq; b < nblk; b += 16) {
-        uint4 qv[R];
-        float dv[R];
+    for (int b0 = 0; b0 < nblk; b0 += 128) {
+        const int nu = nblk - b0 > 64 ? 2 : 1;  // 64-block rounds in this pass (uniform)
+        uint4 q[2][R][2];
+        float dv[2][R];
+        int bc[2];
+        bool ok[2];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            int64_t row = row0 + r;
-            row = row < n ? row : n - 1;
-            const int64_t blk = row * nblk + b;
-            qv[r] = ld_nt(qs + blk * 2 + c);
-            dv[r] = h2f(dd[blk]);
+        for (int u = 0; u < 2; u++) {
+            const int b = b0 + 64 * u + lane;
+            ok[u] = b < nblk;
+            bc[u] = ok[u] ? b : nblk - 1;  // past the row: a valid block, its term dropped
+            if (u < nu) {
+#pragma unroll
+                for (int r = 0; r < R; r++) {
+                    q[u][r][0] = ld_nt(qr[r] + 2 * bc[u]);
+                    q[u][r][1] = ld_nt(qr[r] + 2 * bc[u] + 1);
+                    dv[u][r] = h2f(dr[r][bc[u]]);
+                }
+            }
         }
 #pragma unroll
         for (int mi = 0; mi < MX; mi++) {
             if (mi < m) {
-                float xv[16];
-                load16(x + mi * k + (int64_t)b * 32 + 16 * c, xv);
 #pragma unroll
-                for (int r = 0; r < R; r++) acc[mi][r] += dv[r] * dot16_i8(xv, qv[r]);
+                for (int u = 0; u < 2; u++) {
+                    if (u < nu) {
+                        float xv[32];
+                        load16(x + mi * k + (int64_t)bc[u] * 32, xv);
+                        load16(x + mi * k + (int64_t)bc[u] * 32 + 16, xv + 16);
+#pragma unroll
+                        for (int r = 0; r < R; r++) {
+                            const float t = dv[u][r] * (dot16_i8(xv, q[u][r][0]) + dot16_i8(xv + 16, q[u][r][1]));
+                            acc[mi][r] += ok[u] ? t : 0.f;
+                        }
+                    }
+                }
             }
         }
     }
 #pragma unroll
-    for (int mi = 0; mi < MX; mi++) {
+    for (int mi = 0; mi < MX; mi++)
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const float v = half_wave_sum(acc[mi][r]);
-            const int64_t row = row0 + r;
-            if (ll == 0 && mi < m && row < n) y[(int64_t)mi * n + row] = v;
+            const float hv = half_wave_sum_dpp(acc[mi][r]);
+            // every lane: .x = lane half 0's sum, .y = half 1's
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(hv), __float_as_uint(hv), false, false);
+            const float v = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+            if (lane == 0 && mi < m && row0 + r < n) y[(int64_t)mi * n + row0 + r] = v;
         }
-    }
+}
+
+template <int MX>
+static hipError_t launch_q80(const arfq_weight *w, int e, int m, const float *x, float *y, hipStream_t s) {
+    const int nblk = (int)(w->k / 32);
+    const int64_t eb = (int64_t)e * w->n * nblk;  // first block of expert e
+    const int64_t rows_per_wg = (int64_t)Q80_WAVES * Q80_ROWS;
+    const unsigned grid = (unsigned)((w->n + rows_per_wg - 1) / rows_per_wg);
+    gemv_q80w<MX><<<grid, 64 * Q80_WAVES, 0, s>>>((const uint4 *)w->s0 + eb * 2, (const uint16_t *)w->s1 + eb,
+                                                  x, y, (int)w->n, nblk, m);
+    return hipGetLastError();
 }
 
 // ------------------------------------------------------------------ Q6_K ----
@@ -1411,10 +1456,6 @@ static hipError_t launch_gemv_t(const arfq_weight *w, int e, int m, const float 
     switch (w->qtype) {
     case ARFQ_Q4_K:
         return hipErrorInvalidValue;  // handled by launch_gemv_q4k
-    case ARFQ_Q8_0:
-        gemv_q80<R, MX><<<grid, 64, 0, s>>>((const uint4 *)w->s0 + eb * 2,
-                                            (const uint16_t *)w->s1 + eb, x, y, n, nblk, m);
-        break;
     case ARFQ_Q6_K:
         gemv_q6k<R, MX><<<grid, 64, 0, s>>>((const uint4 *)w->s0 + eb * 12,
                                             (const uint32_t *)w->s1 + eb * 4,
@@ -1692,6 +1733,11 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
     if (w->qtype == ARFQ_Q6_K && dot_ok(w, m)) {
         const DotQ6K f = dot_q6k(w, e);
         return m == 1 ? launch_dot<DotQ6K, 1>(f, w, 1, x, y, s) : launch_dot<DotQ6K, 2>(f, w, 2, x, y, s);
+    }
+    if (w->qtype == ARFQ_Q8_0) {
+        if (m == 1) return launch_q80<1>(w, e, 1, x, y, s);
+        if (m == 2) return launch_q80<2>(w, e, 2, x, y, s);
+        return launch_q80<4>(w, e, (int)m, x, y, s);
     }
     if (m == 1) return launch_gemv_t<4, 1>(w, e, 1, x, y, s);
     if (m == 2) return launch_gemv_t<4, 2>(w, e, 2, x, y, s);

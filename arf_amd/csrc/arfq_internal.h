@@ -124,8 +124,11 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
 // multiplied back by rs[row].
 // With pair (xl == xh + m * k) the lo rows follow the hi rows and xs has the
 // hi rows' sums, then the lo rows' sums.
+// rs_splits: with rs, one scale per row and per K range of the skinny
+// kernel's split-K (rs[split * m + row]; 1: one per row)
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
-                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair = false);
+                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair = false,
+                        int rs_splits = 1);
 
 // ---- arfq_moe.hip ----
 // Routing: ids/weights [tokens, top_k] from logits [tokens, E] (E <= 1024, top_k <= 64).

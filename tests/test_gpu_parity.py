@@ -357,6 +357,36 @@ def test_gemm_split_k_is_deterministic(gpu_ctx, n, k, m):
     assert np.array_equal(y1.numpy().view(np.uint32), y2.numpy().view(np.uint32))
 
 
+@pytest.mark.parametrize("m,n,k,xdt", [(1024, 16896, 1024, np.float16), (256, 66048, 512, np.float32),
+                                        (512, 33280, 768, np.float16)])
+def test_gemm_q4k_prefill_split_tail(gpu_ctx, oracle, m, n, k, xdt):
+    # Q4_K prefill with more tiles than CUs and a remainder: the tiles past the
+    # last whole round are cut into K ranges whose partials are added in order
+    # (XCD tile order at m = 1024); every output is checked, and a repeat gives
+    # the same bits.  The f32 case holds f16 values times 2^20 (the prefill
+    # rounds f32 x to f16 after its per-row power-of-two scaling, which this x
+    # survives exactly), so it checks the row scales on the split tiles
+    _say("case: gemm q4k prefill split tail", m, n, k, xdt.__name__)
+    from arf_amd import QType, synth
+    raw = synth.weight("q4_k", n, k, seed=m + n)
+    x = synth.activations(m, k, seed=k + 7).astype(np.float16).astype(xdt)
+    if xdt == np.float32:
+        x *= np.float32(2.0 ** 20)
+    w = gpu_ctx.upload(QType.Q4_K, raw, n, k)
+    xd = gpu_ctx.to_device(x)
+    outs = []
+    for _ in range(2):
+        y = gpu_ctx.empty((m, n), np.float32)
+        gpu_ctx.matmul(w, xd, m, y)
+        outs.append(y.numpy())
+    e = rel_err(outs[0], _dequant_matmul(oracle, "q4_k", x.astype(np.float32), raw, n))
+    _say("rel err (all rows)", e)
+    assert e <= TOL
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    rows = np.array([0, m // 2, m - 1])
+    assert rel_err(outs[0][rows], oracle.matmul_q("q4_k", x[rows].astype(np.float32), raw, n)) <= TOL
+
+
 def test_skinny_split_counters_reset(gpu_ctx, oracle):
     # skinny products split over K sum their partials in the kernel, the last
     # workgroup of each column tile resetting that tile's arrival counter:
