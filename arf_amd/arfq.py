@@ -37,6 +37,9 @@ ARFQ_E_NOT_FOUND = -8
 
 # context options (include/arfq.h ARFQ_OPT_*)
 OPT_GEMV_X16 = 1
+# arfq_act: the FFN's gate activation (GateAct)
+ACT_SILU = 0
+ACT_GELU_TANH = 1
 
 
 class QType(enum.IntEnum):
@@ -84,6 +87,8 @@ _SIGS = {
     "arfq_moe_route": (_int, [_vp, _vp, _i64, _int, _int, _int, _vp, _vp]),
     "arfq_moe": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _int, _int, _vp, _int, _vp]),
     "arfq_moe_ids": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _int, _vp, _int, _vp]),
+    "arfq_moe_add": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _int, _int, _vp, _int, _vp]),
+    "arfq_moe_ids_add": (_int, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _int, _vp, _int, _vp]),
     "arfq_dev_malloc": (_int, [_vp, ctypes.c_size_t, ctypes.POINTER(_vp)]),
     "arfq_dev_free": (_int, [_vp, _vp]),
     "arfq_copy_h2d": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
@@ -93,6 +98,7 @@ _SIGS = {
     "arfq_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
     "arfq_matmul_repeat": (_int, [_vp, ctypes.POINTER(_vp), _int, _int, _i64, _vp, _int, _vp]),
     "arfq_ffn": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _vp]),
+    "arfq_ffn_act": (_int, [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _int]),
     "arfq_gguf_is_gguf": (_int, [ctypes.c_char_p]),
     "arfq_gguf_open": (_int, [ctypes.c_char_p, ctypes.POINTER(_vp)]),
     "arfq_gguf_close": (_int, [_vp]),
@@ -300,22 +306,29 @@ class Context:
             self.handle, logits.ptr, int(tokens), int(n_experts), int(top_k), int(bool(norm_topk)),
             ids.ptr, weights.ptr))
 
-    def ffn(self, gate, up, down, x, m, y):
-        """y[m, hidden] = down . (silu(gate . x) * (up . x)) (ffn_dispatch / Mlp::forward)."""
-        _check(self.handle, load_library().arfq_ffn(self.handle, gate.handle, up.handle, down.handle,
-                                                    int(m), x.ptr, y.ptr))
+    def ffn(self, gate, up, down, x, m, y, act=None):
+        """y[m, hidden] = down . (act(gate . x) * (up . x)) (ffn_dispatch / Mlp::forward);
+        act ACT_SILU (default: arfq_ffn) or ACT_GELU_TANH (arfq_ffn_act)."""
+        L = load_library()
+        if act is None:
+            _check(self.handle, L.arfq_ffn(self.handle, gate.handle, up.handle, down.handle, int(m), x.ptr,
+                                           y.ptr))
+        else:
+            _check(self.handle, L.arfq_ffn_act(self.handle, gate.handle, up.handle, down.handle, int(m),
+                                               x.ptr, y.ptr, int(act)))
 
-    def moe(self, gate, up, down, logits, tokens, top_k, norm_topk, x, y):
+    def moe(self, gate, up, down, logits, tokens, top_k, norm_topk, x, y, accumulate=False):
+        """MoE block into y (accumulate: added to y, which holds the shared experts' output)."""
         xd = DType.F16 if x.dtype == np.float16 else DType.F32
-        _check(self.handle, load_library().arfq_moe(
-            self.handle, gate.handle, up.handle, down.handle, logits.ptr, int(tokens), int(top_k),
-            int(bool(norm_topk)), x.ptr, int(xd), y.ptr))
+        fn = load_library().arfq_moe_add if accumulate else load_library().arfq_moe
+        _check(self.handle, fn(self.handle, gate.handle, up.handle, down.handle, logits.ptr, int(tokens),
+                               int(top_k), int(bool(norm_topk)), x.ptr, int(xd), y.ptr))
 
-    def moe_ids(self, gate, up, down, ids, weights, tokens, top_k, x, y):
+    def moe_ids(self, gate, up, down, ids, weights, tokens, top_k, x, y, accumulate=False):
         xd = DType.F16 if x.dtype == np.float16 else DType.F32
-        _check(self.handle, load_library().arfq_moe_ids(
-            self.handle, gate.handle, up.handle, down.handle, ids.ptr, weights.ptr, int(tokens),
-            int(top_k), x.ptr, int(xd), y.ptr))
+        fn = load_library().arfq_moe_ids_add if accumulate else load_library().arfq_moe_ids
+        _check(self.handle, fn(self.handle, gate.handle, up.handle, down.handle, ids.ptr, weights.ptr,
+                               int(tokens), int(top_k), x.ptr, int(xd), y.ptr))
 
     def copy_d2d(self, dst, src, nbytes=None):
         """Enqueue dst <- src (device arrays) on the context's stream."""

@@ -23,6 +23,8 @@
 #include <hip/hip_fp16.h>
 #include <stdint.h>
 
+#include "../../include/arfq.h"
+
 namespace arfq {
 
 constexpr int QK_K = 256;
@@ -120,6 +122,26 @@ __device__ __forceinline__ int q6k_code(const uint32_t *w, int t, int i) {
     const uint32_t lo = (t & 1) ? qlb : qla;
     const uint32_t nib = (t & 2) ? (lo >> 4) : (lo & 0xFu);
     return (int)(nib | (((qh >> (2 * t)) & 3u) << 4));
+}
+
+// ---- gated FFN activations: h = act(g) * u ---------------------------------
+// act 0, SwiGLU: silu(g) = g / (1 + exp(-g)) (crates/arf-ml/src/lib.rs:160-162,
+// mlp.rs:20-24).  act 1, GeGLU: gelu_tanh(g) = 0.5 g (1 + tanh(inner)),
+// inner = sqrt(2/pi) (g + 0.044715 g^3) clamped to [-15, 15] before the tanh
+// (shaders/metal/decode_ops_msl.metal:15-27; CPU oracle
+// gpu/metal/selftest.rs:6091-6095), the gate activation of GateAct::GeluTanh
+// models (crates/arf-core/src/config.rs:58).  Evaluated left to right without
+// contraction, as the reference writes them.
+constexpr int ACT_SILU = ARFQ_ACT_SILU, ACT_GELU_TANH = ARFQ_ACT_GELU_TANH;
+template <int ACT>
+__device__ __forceinline__ float glu(float g, float u) {
+#pragma clang fp contract(off)
+    if constexpr (ACT == ACT_GELU_TANH) {
+        const float inner = fminf(fmaxf(0.7978845608028654f * (g + 0.044715f * g * g * g), -15.0f), 15.0f);
+        return 0.5f * g * (1.0f + tanhf(inner)) * u;
+    } else {
+        return g / (1.0f + expf(-g)) * u;
+    }
 }
 
 }  // namespace arfq

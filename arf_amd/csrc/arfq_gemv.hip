@@ -147,10 +147,11 @@ __device__ __forceinline__ XqRound xq_load(const float *__restrict__ x, int item
     return r;
 }
 
-// x sources of gemv_q4k: a row-major f32 x (the plain GEMV), and for the MoE
-// decode path one row per (token, expert) pair: the token's f32 or f16 row, or
-// silu(g) * u of the pair's gate and up rows (crates/arf-ml/src/lib.rs:160-162;
-// the same expression as the grouped path's gate|up kernel).
+// x sources of gemv_q4k: a row-major f32 x (the plain GEMV), act(g) * u of the
+// FFN's gate and up outputs (XsGlu: the down GEMV with the gated activation
+// applied as it reads its x), and for the MoE decode path one row per (token,
+// expert) pair: the token's f32 or f16 row, or silu(g) * u of the pair's gate
+// and up rows (the same expression as the grouped path's gate|up kernel).
 struct XsF32 {
     const float *x;
     __device__ XqRound load(int items, int base) const { return xq_load(x, items, base); }
@@ -177,24 +178,25 @@ struct XsRowF16 {
         return r;
     }
 };
-struct XsSwiglu {
+template <int ACT>
+struct XsGlu {
     const float *g, *u;
     int64_t stride;
     __device__ void pair(int p) {
         g += (int64_t)p * stride;
         u += (int64_t)p * stride;
     }
-    __device__ static float silu_mul(float a, float b) { return a / (1.0f + expf(-a)) * b; }
     __device__ XqRound load(int items, int base) const {
         const XqRound a = xq_load(g, items, base), b = xq_load(u, items, base);
         XqRound r;
-        r.v0 = make_float4(silu_mul(a.v0.x, b.v0.x), silu_mul(a.v0.y, b.v0.y),
-                           silu_mul(a.v0.z, b.v0.z), silu_mul(a.v0.w, b.v0.w));
-        r.v1 = make_float4(silu_mul(a.v1.x, b.v1.x), silu_mul(a.v1.y, b.v1.y),
-                           silu_mul(a.v1.z, b.v1.z), silu_mul(a.v1.w, b.v1.w));
+        r.v0 = make_float4(glu<ACT>(a.v0.x, b.v0.x), glu<ACT>(a.v0.y, b.v0.y), glu<ACT>(a.v0.z, b.v0.z),
+                           glu<ACT>(a.v0.w, b.v0.w));
+        r.v1 = make_float4(glu<ACT>(a.v1.x, b.v1.x), glu<ACT>(a.v1.y, b.v1.y), glu<ACT>(a.v1.z, b.v1.z),
+                           glu<ACT>(a.v1.w, b.v1.w));
         return r;
     }
 };
+using XsSwiglu = XsGlu<ACT_SILU>;
 
 __device__ __forceinline__ void xq_process(const XqRound &r, int items, int base, int nsub,
                                            uint4 *dg, float2 *xs) {
@@ -512,13 +514,13 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k(
     gemv_q4k_body<MX, XR, PF>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n, nblk, m);
 }
 
-// The FFN's down GEMV: x = silu(g) * u over m row-major rows (g, u: [m][k]).
-template <int MX, int XR>
-__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_swiglu(
+// The FFN's down GEMV: x = act(g) * u over m row-major rows (g, u: [m][k]).
+template <int MX, int XR, int ACT>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_glu(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ g, const float *__restrict__ u,
     float *__restrict__ y, int n, int nblk, int m) {
-    gemv_q4k_body<MX, XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsSwiglu{g, u, 0}, y, n, nblk, m);
+    gemv_q4k_body<MX, XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y, n, nblk, m);
 }
 
 // ------------------------------------------------- Q4_K, f32 activations ----
@@ -762,13 +764,26 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32(
     gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n, nblk);
 }
 
-// The FFN's down GEMV at one x row: x = silu(g) * u, f32 arithmetic.
-template <int XR>
-__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_swiglu(
+// The FFN's down GEMV at one x row: x = act(g) * u, f32 arithmetic.
+template <int XR, int ACT>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_glu(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ g, const float *__restrict__ u,
     float *__restrict__ y, int n, int nblk) {
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsSwiglu{g, u, 0}, y, n, nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y, n, nblk);
+}
+
+// The FFN's gate and up GEMVs in one launch: blockIdx.y = 0 multiplies x by
+// the first weight into y0, 1 by the second into y1 (same shape), each
+// weight's rows split over gridDim.x workgroups; f32 arithmetic.
+template <int XR>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_dual(
+    const uint8_t *__restrict__ hdr0, const uint8_t *__restrict__ qs0, const uint8_t *__restrict__ hdr1,
+    const uint8_t *__restrict__ qs1, uint32_t hdr_bytes, uint32_t qs_bytes, const float *__restrict__ x,
+    float *__restrict__ y0, float *__restrict__ y1, int n, int nblk) {
+    const bool second = blockIdx.y != 0;  // uniform over the workgroup
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0, qs_bytes,
+                                       XsF32{x}, second ? y1 : y0, n, nblk);
 }
 
 // MoE decode: blockIdx.y = pair p, one x row each, the weight of expert ids[p]
@@ -1614,17 +1629,55 @@ static hipError_t launch_q4k_f32(const arfq_weight *w, int e, const float *x, fl
     default: return launch_q4k_f32_t<4>(w, e, x, y, s);
     }
 }
-template <int XR>
-static hipError_t launch_q4k_f32_swiglu_t(const arfq_weight *w, const float *g, const float *u, float *y,
-                                          hipStream_t s) {
+template <int XR, int ACT>
+static hipError_t launch_q4k_f32_glu_t(const arfq_weight *w, const float *g, const float *u, float *y,
+                                       hipStream_t s) {
     static std::atomic<uint64_t> lds_set{0};
-    if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_f32_swiglu<XR>, Q4K_F32_LDS_MAX, lds_set))
+    if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_f32_glu<XR, ACT>, Q4K_F32_LDS_MAX, lds_set))
         return err;
     const int64_t nb = w->n * (w->k / 256);
-    gemv_q4k_f32_swiglu<XR><<<(unsigned)q4k_f32_grid(w), Q4K_GEMV_THREADS, q4k_f32_lds(w), s>>>(
+    gemv_q4k_f32_glu<XR, ACT><<<(unsigned)q4k_f32_grid(w), Q4K_GEMV_THREADS, q4k_f32_lds(w), s>>>(
         (const uint8_t *)w->s0, (uint32_t)(nb * 16), (const uint8_t *)w->s1, (uint32_t)(nb * 128), g, u, y,
         (int)w->n, (int)(w->k / 256));
     return hipGetLastError();
+}
+template <int ACT>
+static hipError_t launch_q4k_f32_glu(const arfq_weight *w, const float *g, const float *u, float *y,
+                                     hipStream_t s) {
+    switch (q4k_f32_xr(w)) {
+    case 1: return launch_q4k_f32_glu_t<1, ACT>(w, g, u, y, s);
+    case 2: return launch_q4k_f32_glu_t<2, ACT>(w, g, u, y, s);
+    default: return launch_q4k_f32_glu_t<4, ACT>(w, g, u, y, s);
+    }
+}
+
+// gate and up in one launch: half the single GEMV's workgroups per weight
+static int64_t q4k_dual_grid(const arfq_weight *w) { return std::max<int64_t>(1, q4k_f32_grid(w) / 2); }
+bool gemv_dual_supports(const arfq_weight *a, const arfq_weight *b, int64_t m) {
+    return m == 1 && a->qtype == ARFQ_Q4_K && b->qtype == ARFQ_Q4_K && a->n == b->n && a->k == b->k &&
+           a->experts == 1 && b->experts == 1 && q4k_f32_ok(a) &&
+           q4k_f32_lds_rows(a, (a->n + q4k_dual_grid(a) - 1) / q4k_dual_grid(a)) <= Q4K_F32_LDS_MAX;
+}
+template <int XR>
+static hipError_t launch_dual_t(const arfq_weight *a, const arfq_weight *b, const float *x, float *ya, float *yb,
+                                hipStream_t s) {
+    static std::atomic<uint64_t> lds_set{0};
+    if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_f32_dual<XR>, Q4K_F32_LDS_MAX, lds_set))
+        return err;
+    const int64_t g = q4k_dual_grid(a), nb = a->n * (a->k / 256);
+    gemv_q4k_f32_dual<XR><<<dim3((unsigned)g, 2), Q4K_GEMV_THREADS, q4k_f32_lds_rows(a, (a->n + g - 1) / g), s>>>(
+        (const uint8_t *)a->s0, (const uint8_t *)a->s1, (const uint8_t *)b->s0, (const uint8_t *)b->s1,
+        (uint32_t)(nb * 16), (uint32_t)(nb * 128), x, ya, yb, (int)a->n, (int)(a->k / 256));
+    return hipGetLastError();
+}
+hipError_t launch_gemv_dual(const arfq_weight *a, const arfq_weight *b, const float *x, float *ya, float *yb,
+                            hipStream_t s) {
+    if (!gemv_dual_supports(a, b, 1)) return hipErrorInvalidValue;
+    switch (q4k_f32_xr(a)) {
+    case 1: return launch_dual_t<1>(a, b, x, ya, yb, s);
+    case 2: return launch_dual_t<2>(a, b, x, ya, yb, s);
+    default: return launch_dual_t<4>(a, b, x, ya, yb, s);
+    }
 }
 
 // LDS of gemv_q4k_pairs with g workgroups per pair.
@@ -1663,39 +1716,40 @@ static hipError_t launch_pairs_t(const arfq_weight *w, int64_t P, const int32_t 
     return hipGetLastError();
 }
 
-template <int MX, int XR>
-static hipError_t launch_swiglu_t(const arfq_weight *w, int m, const float *g, const float *u,
-                                  float *y, hipStream_t s) {
+template <int MX, int XR, int ACT>
+static hipError_t launch_glu_t(const arfq_weight *w, int m, const float *g, const float *u, float *y,
+                               hipStream_t s) {
     const int64_t nb = w->n * (w->k / 256);
-    gemv_q4k_swiglu<MX, XR><<<(unsigned)q4k_gemv_grid(w), Q4K_GEMV_THREADS, q4k_gemv_lds(w, MX), s>>>(
+    gemv_q4k_glu<MX, XR, ACT><<<(unsigned)q4k_gemv_grid(w), Q4K_GEMV_THREADS, q4k_gemv_lds(w, MX), s>>>(
         (const uint8_t *)w->s0, (uint32_t)(nb * 16), (const uint8_t *)w->s1, (uint32_t)(nb * 128), g, u,
         y, (int)w->n, (int)(w->k / 256), m);
     return hipGetLastError();
 }
-template <int MX>
-static hipError_t launch_swiglu_mx(const arfq_weight *w, int m, const float *g, const float *u,
-                                   float *y, hipStream_t s) {
+template <int MX, int ACT>
+static hipError_t launch_glu_mx(const arfq_weight *w, int m, const float *g, const float *u, float *y,
+                                hipStream_t s) {
     const int64_t rounds = ((int64_t)m * (w->k / 8) + Q4K_GEMV_THREADS - 1) / Q4K_GEMV_THREADS;
-    if (rounds <= 1) return launch_swiglu_t<MX, 1>(w, m, g, u, y, s);
-    if (rounds <= 2) return launch_swiglu_t<MX, 2>(w, m, g, u, y, s);
-    return launch_swiglu_t<MX, 4>(w, m, g, u, y, s);
+    if (rounds <= 1) return launch_glu_t<MX, 1, ACT>(w, m, g, u, y, s);
+    if (rounds <= 2) return launch_glu_t<MX, 2, ACT>(w, m, g, u, y, s);
+    return launch_glu_t<MX, 4, ACT>(w, m, g, u, y, s);
 }
-bool gemv_swiglu_supports(const arfq_weight *w, int64_t m) {
+template <int ACT>
+static hipError_t launch_gemv_glu_t(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y,
+                                    hipStream_t s, bool x16) {
+    if (m == 1 && !x16 && q4k_f32_ok(w)) return launch_q4k_f32_glu<ACT>(w, g, u, y, s);
+    if (m == 1) return launch_glu_mx<1, ACT>(w, 1, g, u, y, s);
+    if (m == 2) return launch_glu_mx<2, ACT>(w, 2, g, u, y, s);
+    return launch_glu_mx<4, ACT>(w, (int)m, g, u, y, s);
+}
+bool gemv_glu_supports(const arfq_weight *w, int64_t m) {
     return w->qtype == ARFQ_Q4_K && w->experts == 1 && gemv_supports(w, m);
 }
-hipError_t launch_gemv_swiglu(const arfq_weight *w, int64_t m, const float *g, const float *u,
-                              float *y, hipStream_t s, bool x16) {
-    if (!gemv_swiglu_supports(w, m)) return hipErrorInvalidValue;
-    if (m == 1 && !x16 && q4k_f32_ok(w)) {
-        switch (q4k_f32_xr(w)) {
-        case 1: return launch_q4k_f32_swiglu_t<1>(w, g, u, y, s);
-        case 2: return launch_q4k_f32_swiglu_t<2>(w, g, u, y, s);
-        default: return launch_q4k_f32_swiglu_t<4>(w, g, u, y, s);
-        }
-    }
-    if (m == 1) return launch_swiglu_mx<1>(w, 1, g, u, y, s);
-    if (m == 2) return launch_swiglu_mx<2>(w, 2, g, u, y, s);
-    return launch_swiglu_mx<4>(w, (int)m, g, u, y, s);
+hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y, int act,
+                           hipStream_t s, bool x16) {
+    if (!gemv_glu_supports(w, m)) return hipErrorInvalidValue;
+    if (act == ACT_GELU_TANH) return launch_gemv_glu_t<ACT_GELU_TANH>(w, m, g, u, y, s, x16);
+    if (act == ACT_SILU) return launch_gemv_glu_t<ACT_SILU>(w, m, g, u, y, s, x16);
+    return hipErrorInvalidValue;
 }
 
 hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,

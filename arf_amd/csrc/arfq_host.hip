@@ -435,7 +435,7 @@ static int check_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *
 static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
                        const arfq_weight *down, const float *logits, const int32_t *ids_in,
                        const float *wts_in, int64_t tokens, int top_k, int norm_topk,
-                       const void *x, int x_dtype, float *y) {
+                       const void *x, int x_dtype, float *y, bool accumulate) {
     if (tokens == 0) return ARFQ_OK;
     const int E = gate->experts;
     const int64_t hidden = gate->k, inter = gate->n, P = tokens * top_k;
@@ -470,7 +470,7 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
         if (e != hipSuccess) return hip_fail(ctx, e, "moe: gate/up GEMV launch");
         e = arfq::launch_gemv_pairs(down, P, ids, nullptr, ARFQ_F32, 1, g, u, ob, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "moe: down GEMV launch");
-        e = arfq::launch_moe_combine(ob, ids, wts, tokens, top_k, E, hidden, y, ctx->stream);
+        e = arfq::launch_moe_combine(ob, ids, wts, tokens, top_k, E, hidden, y, accumulate, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "moe: combine launch");
         return ARFQ_OK;
     }
@@ -532,28 +532,52 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     if (e != hipSuccess) return hip_fail(ctx, e, "moe: h preparation launch");
     e = arfq::launch_moe_down(down, h16, hs, rs, off, srt, tiles, nt, max_tiles, ob, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "moe: down launch");
-    e = arfq::launch_moe_combine(ob, ids, wts, tokens, top_k, E, hidden, y, ctx->stream);
+    e = arfq::launch_moe_combine(ob, ids, wts, tokens, top_k, E, hidden, y, accumulate, ctx->stream);
     if (e != hipSuccess) return hip_fail(ctx, e, "moe: combine launch");
     return ARFQ_OK;
+}
+
+static int moe_routed(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
+                      const float *router_logits, int64_t tokens, int top_k, int norm_topk, const void *x,
+                      int x_dtype, float *y, bool accumulate) {
+    if (int rc = check_moe(ctx, gate, up, down, tokens, top_k, x, x_dtype, y)) return rc;
+    if (tokens > 0 && !router_logits) return fail(ctx, ARFQ_E_INVALID, "moe: null router logits");
+    if (int rc = use_device(ctx)) return rc;
+    return moe_enqueue(ctx, gate, up, down, router_logits, nullptr, nullptr, tokens, top_k, norm_topk, x,
+                       x_dtype, y, accumulate);
+}
+
+static int moe_given(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
+                     const int32_t *ids, const float *weights, int64_t tokens, int top_k, const void *x,
+                     int x_dtype, float *y, bool accumulate) {
+    if (int rc = check_moe(ctx, gate, up, down, tokens, top_k, x, x_dtype, y)) return rc;
+    if (tokens > 0 && (!ids || !weights)) return fail(ctx, ARFQ_E_INVALID, "moe_ids: null ids or weights");
+    if (int rc = use_device(ctx)) return rc;
+    return moe_enqueue(ctx, gate, up, down, nullptr, ids, weights, tokens, top_k, 0, x, x_dtype, y, accumulate);
 }
 
 int arfq_moe(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
              const arfq_weight *down, const float *router_logits, int64_t tokens, int top_k,
              int norm_topk, const void *x, int x_dtype, float *y) {
-    if (int rc = check_moe(ctx, gate, up, down, tokens, top_k, x, x_dtype, y)) return rc;
-    if (tokens > 0 && !router_logits) return fail(ctx, ARFQ_E_INVALID, "moe: null router logits");
-    if (int rc = use_device(ctx)) return rc;
-    return moe_enqueue(ctx, gate, up, down, router_logits, nullptr, nullptr, tokens, top_k,
-                       norm_topk, x, x_dtype, y);
+    return moe_routed(ctx, gate, up, down, router_logits, tokens, top_k, norm_topk, x, x_dtype, y, false);
+}
+
+int arfq_moe_add(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                 const arfq_weight *down, const float *router_logits, int64_t tokens, int top_k,
+                 int norm_topk, const void *x, int x_dtype, float *y) {
+    return moe_routed(ctx, gate, up, down, router_logits, tokens, top_k, norm_topk, x, x_dtype, y, true);
 }
 
 int arfq_moe_ids(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
                  const arfq_weight *down, const int32_t *ids, const float *weights,
                  int64_t tokens, int top_k, const void *x, int x_dtype, float *y) {
-    if (int rc = check_moe(ctx, gate, up, down, tokens, top_k, x, x_dtype, y)) return rc;
-    if (tokens > 0 && (!ids || !weights)) return fail(ctx, ARFQ_E_INVALID, "moe_ids: null ids or weights");
-    if (int rc = use_device(ctx)) return rc;
-    return moe_enqueue(ctx, gate, up, down, nullptr, ids, weights, tokens, top_k, 0, x, x_dtype, y);
+    return moe_given(ctx, gate, up, down, ids, weights, tokens, top_k, x, x_dtype, y, false);
+}
+
+int arfq_moe_ids_add(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                     const arfq_weight *down, const int32_t *ids, const float *weights,
+                     int64_t tokens, int top_k, const void *x, int x_dtype, float *y) {
+    return moe_given(ctx, gate, up, down, ids, weights, tokens, top_k, x, x_dtype, y, true);
 }
 
 // -------------------------------------------------------------------- FFN ----
@@ -564,9 +588,10 @@ static size_t matmul_scratch(const arfq_weight *w, int64_t m) {
     return arfq::gemm_supports(w, m) ? arfq::gemm_plan(w, m, ARFQ_F32).scratch_bytes : 0;
 }
 
-int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
-             int64_t m, const float *x, float *y) {
+int arfq_ffn_act(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
+                 int64_t m, const float *x, float *y, int act) {
     if (!ctx) return ARFQ_E_INVALID;
+    if (act != ARFQ_ACT_SILU && act != ARFQ_ACT_GELU_TANH) return fail(ctx, ARFQ_E_INVALID, "ffn: unknown activation");
     if (!gate || !up || !down) return fail(ctx, ARFQ_E_INVALID, "ffn: null weight");
     if (m < 0) return fail(ctx, ARFQ_E_SHAPE, "ffn: m < 0");
     if (m > 0 && (!x || !y)) return fail(ctx, ARFQ_E_INVALID, "ffn: null x or y");
@@ -577,7 +602,11 @@ int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, cons
     if (m == 0) return ARFQ_OK;
     if (int rc = use_device(ctx)) return rc;
     const int64_t inter = gate->n;
-    const bool fused = arfq::gemv_swiglu_supports(down, m);
+    const bool x16 = (ctx->options & ARFQ_OPT_GEMV_X16) != 0;
+    // gate and up of one x row in one launch (Q4_K, f32 arithmetic)
+    const bool dual = !x16 && arfq::gemv_dual_supports(gate, up, m);
+    // the activation applied as the down GEMV reads its x (Q4_K, m <= 4)
+    const bool fused = arfq::gemv_glu_supports(down, m);
     // the GEMM plans use the scratch from offset 0; g, u (and h) sit above the largest
     size_t base = std::max({matmul_scratch(gate, m), matmul_scratch(up, m),
                             fused ? (size_t)0 : matmul_scratch(down, m)});
@@ -586,18 +615,27 @@ int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, cons
     if (int rc = ensure_scratch(ctx, base + (fused ? 2 : 3) * gb)) return rc;
     char *sc = (char *)ctx->scratch;
     float *g = (float *)(sc + base), *u = (float *)(sc + base + gb), *h = (float *)(sc + base + 2 * gb);
-    if (int rc = matmul_enqueue(ctx, gate, 0, m, x, ARFQ_F32, g)) return rc;
-    if (int rc = matmul_enqueue(ctx, up, 0, m, x, ARFQ_F32, u)) return rc;
     hipError_t e;
+    if (dual) {
+        e = arfq::launch_gemv_dual(gate, up, x, g, u, ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "ffn: gate/up GEMV launch");
+    } else {
+        if (int rc = matmul_enqueue(ctx, gate, 0, m, x, ARFQ_F32, g)) return rc;
+        if (int rc = matmul_enqueue(ctx, up, 0, m, x, ARFQ_F32, u)) return rc;
+    }
     if (fused) {
-        e = arfq::launch_gemv_swiglu(down, m, g, u, y, ctx->stream,
-                                     (ctx->options & ARFQ_OPT_GEMV_X16) != 0);
+        e = arfq::launch_gemv_glu(down, m, g, u, y, act, ctx->stream, x16);
         if (e != hipSuccess) return hip_fail(ctx, e, "ffn: down GEMV launch");
         return ARFQ_OK;
     }
-    e = arfq::launch_swiglu(g, u, h, m * inter, ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "ffn: swiglu launch");
+    e = arfq::launch_glu(g, u, h, m * inter, act, ctx->stream);
+    if (e != hipSuccess) return hip_fail(ctx, e, "ffn: activation launch");
     return matmul_enqueue(ctx, down, 0, m, h, ARFQ_F32, y);
+}
+
+int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
+             int64_t m, const float *x, float *y) {
+    return arfq_ffn_act(ctx, gate, up, down, m, x, y, ARFQ_ACT_SILU);
 }
 
 int arfq_dequant_f32(arfq_ctx *ctx, const arfq_weight *w, float *out) {

@@ -83,13 +83,18 @@ bool gemv_supports(const arfq_weight *w, int64_t m);
 // x_p, where x_p is row p / x_div of x (f32 or f16, [*, w->k]) or, when g is
 // set, silu(g[p]) * u[p] (g, u: [P, w->k] f32).  Pairs with an out-of-range id
 // are skipped.
-// The FFN's down projection: y[m, n] = W . (silu(g) * u), g and u [m, w->k] f32
-// (Q4_K, m <= 4).
-bool gemv_swiglu_supports(const arfq_weight *w, int64_t m);
-hipError_t launch_gemv_swiglu(const arfq_weight *w, int64_t m, const float *g, const float *u,
-                              float *y, hipStream_t s, bool x16 = false);
-// h = silu(g) * u elementwise (n floats)
-hipError_t launch_swiglu(const float *g, const float *u, float *h, int64_t n, hipStream_t s);
+// The FFN's down projection: y[m, n] = W . (act(g) * u), g and u [m, w->k] f32
+// (Q4_K, m <= 4); act ARFQ_ACT_SILU or ARFQ_ACT_GELU_TANH.
+bool gemv_glu_supports(const arfq_weight *w, int64_t m);
+hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y, int act,
+                           hipStream_t s, bool x16 = false);
+// The FFN's gate and up projections of one x row in one launch: ya = A . x,
+// yb = B . x (Q4_K, same shape, f32 arithmetic).
+bool gemv_dual_supports(const arfq_weight *a, const arfq_weight *b, int64_t m);
+hipError_t launch_gemv_dual(const arfq_weight *a, const arfq_weight *b, const float *x, float *ya, float *yb,
+                            hipStream_t s);
+// h = act(g) * u elementwise (n floats; act ARFQ_ACT_*)
+hipError_t launch_glu(const float *g, const float *u, float *h, int64_t n, int act, hipStream_t s);
 bool gemv_pairs_supports(const arfq_weight *w);
 hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,
                              int x_dtype, int x_div, const float *g, const float *u, float *y,
@@ -158,7 +163,7 @@ hipError_t launch_moe_down(const arfq_weight *down, const _Float16 *h, const uin
                            int64_t max_tiles, float *o, hipStream_t s);
 // y[t] = sum_j w[t, j] * o[t * top_k + j] in slot order.
 hipError_t launch_moe_combine(const float *o, const int32_t *ids, const float *wts, int64_t tokens,
-                              int top_k, int E, int64_t hidden, float *y, hipStream_t s);
+                              int top_k, int E, int64_t hidden, float *y, bool accumulate, hipStream_t s);
 constexpr int MOE_EXPERTS_MAX = 512;
 constexpr int MOE_ROUTE_EXPERTS_MAX = 1024;
 constexpr int MOE_TOPK_MAX = 64;

@@ -406,12 +406,14 @@ __global__ __launch_bounds__(SK_THREADS) void moe_down_kernel(
 // Grid: (hidden / 4 / 256 column blocks, tokens); 4 columns per thread.
 __global__ void moe_combine_kernel(const float *__restrict__ o, const int32_t *__restrict__ ids,
                                    const float *__restrict__ wts, int top_k, int E, int hidden,
-                                   float *__restrict__ y) {
+                                   float *__restrict__ y, int accumulate) {
 #pragma clang fp contract(off)
     const int64_t t = blockIdx.y;
     const int c4 = blockIdx.x * blockDim.x + threadIdx.x;
     if (4 * c4 >= hidden) return;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    // accumulate: y already holds the shared experts' sum, added first as in
+    // MoeMlp::forward (moe.rs:62-67: out = 0 + shared, then += w_j * y_j)
+    float4 acc = accumulate ? reinterpret_cast<const float4 *>(y + t * hidden)[c4] : make_float4(0.f, 0.f, 0.f, 0.f);
     for (int j = 0; j < top_k; j++) {
         const int e = ids[t * top_k + j];
         if (e < 0 || e >= E) continue;  // dropped pair: contributes nothing
@@ -425,18 +427,25 @@ __global__ void moe_combine_kernel(const float *__restrict__ o, const int32_t *_
     reinterpret_cast<float4 *>(y + t * hidden)[c4] = acc;
 }
 
-// ---- SwiGLU --------------------------------------------------------------------
-// h = silu(g) * u, silu(v) = v / (1 + exp(-v)) (crates/arf-ml/src/lib.rs:160-162;
-// the gate|up kernel's expression).
-__global__ void swiglu_kernel(const float *__restrict__ g, const float *__restrict__ u,
-                              float *__restrict__ h, int64_t n) {
+// ---- gated activation ------------------------------------------------------
+// h = act(g) * u: SwiGLU or GeGLU (glu<ACT>, arfq_common.h), the same
+// expressions as the fused down GEMVs and the gate|up kernel.
+template <int ACT>
+__global__ void glu_kernel(const float *__restrict__ g, const float *__restrict__ u, float *__restrict__ h,
+                           int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) h[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
+    if (i < n) h[i] = glu<ACT>(g[i], u[i]);
 }
 
-hipError_t launch_swiglu(const float *g, const float *u, float *h, int64_t n, hipStream_t s) {
+hipError_t launch_glu(const float *g, const float *u, float *h, int64_t n, int act, hipStream_t s) {
     if (n == 0) return hipSuccess;
-    swiglu_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(g, u, h, n);
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    if (act == ACT_GELU_TANH)
+        glu_kernel<ACT_GELU_TANH><<<grid, 256, 0, s>>>(g, u, h, n);
+    else if (act == ACT_SILU)
+        glu_kernel<ACT_SILU><<<grid, 256, 0, s>>>(g, u, h, n);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
@@ -554,10 +563,10 @@ hipError_t launch_moe_hprep(const float *h, int64_t P, int inter, _Float16 *h16,
 }
 
 hipError_t launch_moe_combine(const float *o, const int32_t *ids, const float *wts, int64_t tokens,
-                              int top_k, int E, int64_t hidden, float *y, hipStream_t s) {
+                              int top_k, int E, int64_t hidden, float *y, bool accumulate, hipStream_t s) {
     if (tokens == 0) return hipSuccess;
     const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
-    moe_combine_kernel<<<grid, 256, 0, s>>>(o, ids, wts, top_k, E, (int)hidden, y);
+    moe_combine_kernel<<<grid, 256, 0, s>>>(o, ids, wts, top_k, E, (int)hidden, y, accumulate ? 1 : 0);
     return hipGetLastError();
 }
 

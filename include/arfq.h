@@ -180,6 +180,19 @@ int arfq_moe_ids(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
                  const arfq_weight *down, const int32_t *ids, const float *weights,
                  int64_t tokens, int top_k, const void *x, int x_dtype, float *y);
 
+/* As arfq_moe / arfq_moe_ids, adding into y instead of overwriting it: y holds
+ * the shared experts' output on entry (e.g. from arfq_ffn on the same x), and
+ * each token's routed contributions are added to it in slot order,
+ * y[t] = ((y[t] + w_0 * y_0) + w_1 * y_1) + ...  That is MoeMlp::forward with
+ * shared experts (crates/arf-core/src/model/moe.rs:62-67: out starts at 0, the
+ * shared experts' outputs are added first, then the routed experts'). */
+int arfq_moe_add(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                 const arfq_weight *down, const float *router_logits, int64_t tokens, int top_k,
+                 int norm_topk, const void *x, int x_dtype, float *y);
+int arfq_moe_ids_add(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up,
+                     const arfq_weight *down, const int32_t *ids, const float *weights,
+                     int64_t tokens, int top_k, const void *x, int x_dtype, float *y);
+
 /* ---- device-memory and timing helpers -------------------------------------
  * For callers without their own HIP allocator (the FFI host, tests, the bench).
  * The reference's equivalents are GpuContext buffer init / readback
@@ -206,14 +219,26 @@ int arfq_timer_stop(arfq_ctx *ctx, float *ms);
 int arfq_matmul_repeat(arfq_ctx *ctx, const arfq_weight *const *ws, int n_ws, int iters,
                        int64_t m, const void *x, int x_dtype, float *y);
 
+/* Gate activation of the dense FFN (GateAct, crates/arf-core/src/config.rs:58):
+ * SwiGLU silu(g) * u (crates/arf-ml/src/lib.rs:160-162) or GeGLU
+ * gelu_tanh(g) * u with the tanh argument clamped to [-15, 15]
+ * (crates/arf-gpu/src/shaders/metal/decode_ops_msl.metal:15-27). */
+typedef enum { ARFQ_ACT_SILU = 0, ARFQ_ACT_GELU_TANH = 1 } arfq_act;
+
 /* The dense FFN of one decode/prefill step on already-normalised x (f32,
- * [m, hidden], device): y = down . (silu(gate . x) * (up . x)), f32 [m, hidden];
+ * [m, hidden], device): y = down . (act(gate . x) * (up . x)), f32 [m, hidden];
  * gate/up [inter, hidden], down [hidden, inter], single matrices of any qtype
- * the matmul takes.  Replaces the island's ffn_dispatch (gate GEMV, up GEMV,
- * the SwiGLU kernel, down GEMV on one queue;
- * crates/arf-gpu/src/gpu/metal/island.rs:13436-13529) and Mlp::forward
- * (crates/arf-core/src/model/mlp.rs:20-24).  With Q4_K down weights at m <= 4
- * the SwiGLU is applied as the down GEMV reads its x (no intermediate). */
+ * the matmul takes; act an arfq_act.  Replaces the island's ffn_dispatch (gate
+ * GEMV, up GEMV, the geglu kernel, down GEMV on one queue;
+ * crates/arf-gpu/src/gpu/metal/island.rs:13436-13529), its activation choice
+ * in the decode and batch paths (crates/arf-gpu/src/gpu/decode.rs:123,
+ * batch.rs:6953) and Mlp::forward (crates/arf-core/src/model/mlp.rs:20-24).
+ * At m = 1 with Q4_K gate and up of one shape, gate and up run as one launch;
+ * with Q4_K down weights at m <= 4 the activation is applied as the down GEMV
+ * reads its x (no intermediate). */
+int arfq_ffn_act(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
+                 int64_t m, const float *x, float *y, int act);
+/* arfq_ffn_act with ARFQ_ACT_SILU (Mlp::forward). */
 int arfq_ffn(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
              int64_t m, const float *x, float *y);
 

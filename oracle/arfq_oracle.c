@@ -546,6 +546,24 @@ void arfo_top_k_softmax(const float *logits, int n, int top_k, int norm_topk, in
 /* silu: crates/arf-ml/src/lib.rs:160-162  x / (1 + exp(-x)) */
 static float silu(float x) { return x / (1.0f + expf(-x)); }
 
+/* gelu_tanh with the inner clamp: crates/arf-gpu/src/shaders/metal/decode_ops_msl.metal:15-27,
+ * the same expression as its CPU oracle crates/arf-gpu/src/gpu/metal/selftest.rs:6091-6095
+ * (inner = (C * (x + 0.044715 x^3)).clamp(-15, 15), 0.5 x (1 + tanh(inner))).  Rust's
+ * f32::clamp keeps a NaN; so do the comparisons below. */
+static float gelu_tanh(float x) {
+    const float C = 0.7978845608028654f; /* sqrt(2/pi); the selftest's 0.797_884_6 is the same f32 */
+    float inner = C * (x + 0.044715f * x * x * x);
+    if (inner < -15.0f) inner = -15.0f;
+    if (inner > 15.0f) inner = 15.0f;
+    return 0.5f * x * (1.0f + tanhf(inner));
+}
+
+/* The gated FFN activation h = act(g) * u over n elements: act 0 SwiGLU
+ * (mlp.rs:20-24 with silu above), act 1 GeGLU (decode_ops_msl.metal:15-27). */
+void arfo_glu(const float *g, const float *u, int64_t n, int act, float *out) {
+    for (int64_t i = 0; i < n; i++) out[i] = (act ? gelu_tanh(g[i]) : silu(g[i])) * u[i];
+}
+
 /* ---- a11/a12: SwiGLU expert + MoE block.  crates/arf-core/src/model/mlp.rs:20-24,
  * crates/arf-core/src/model/moe.rs:53-86.  Experts are Q4_K (transcoded to
  * Q4_K_S, so every projection is matmul_nt_q4ks).  The router Linear is replaced
@@ -555,7 +573,8 @@ static float silu(float x) { return x / (1.0f + expf(-x)); }
  * rows][inter] Q4_K blocks. ---------------------------------------------------- */
 void arfo_moe_forward(const float *x, int64_t tokens, int64_t hidden, int64_t inter,
                       const uint8_t *gate, const uint8_t *up, const uint8_t *down,
-                      int n_experts, const float *logits, int top_k, int norm_topk, float *out) {
+                      int n_experts, const float *logits, int top_k, int norm_topk, int accumulate,
+                      float *out) {
     int64_t gu_bytes = inter * (hidden / QK_K) * 144;  /* one expert's gate (or up) */
     int64_t dn_bytes = hidden * (inter / QK_K) * 144;  /* one expert's down */
     float *g = (float *)malloc(sizeof(float) * (size_t)inter);
@@ -563,7 +582,9 @@ void arfo_moe_forward(const float *x, int64_t tokens, int64_t hidden, int64_t in
     float *y = (float *)malloc(sizeof(float) * (size_t)hidden);
     int32_t *ids = (int32_t *)malloc(sizeof(int32_t) * (size_t)top_k);
     float *wts = (float *)malloc(sizeof(float) * (size_t)top_k);
-    memset(out, 0, sizeof(float) * (size_t)(tokens * hidden));
+    /* out starts at 0; with accumulate it holds the shared experts' sum, which the
+     * reference adds first (moe.rs:62-67; 0 + s == s exactly) */
+    if (!accumulate) memset(out, 0, sizeof(float) * (size_t)(tokens * hidden));
     for (int64_t t = 0; t < tokens; t++) {
         arfo_top_k_softmax(logits + t * n_experts, n_experts, top_k, norm_topk, ids, wts);
         int k = top_k < n_experts ? top_k : n_experts;

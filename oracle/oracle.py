@@ -55,7 +55,8 @@ def lib():
         L.arfo_top_k_softmax.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                          _i32p, _f32p]
         L.arfo_moe_forward.argtypes = [_f32p, _i64, _i64, _i64, _u8p, _u8p, _u8p, ctypes.c_int,
-                                       _f32p, ctypes.c_int, ctypes.c_int, _f32p]
+                                       _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]
+        L.arfo_glu.argtypes = [_f32p, _f32p, _i64, ctypes.c_int, _f32p]
         L.arfo_set_threads.argtypes = [ctypes.c_int]
         L.arfo_threads.restype = ctypes.c_int
         _lib = L
@@ -201,10 +202,22 @@ def top_k_softmax(logits, top_k, norm_topk):
     return ids, w
 
 
-def moe_forward(x, gate, up, down, n_experts, inter, logits, top_k, norm_topk):
+def glu(g, u, act):
+    """h = act(g) * u elementwise: act 0 SwiGLU (mlp.rs:20-24), 1 GeGLU with the reference's
+    inner clamp (decode_ops_msl.metal:15-27, selftest.rs:6091-6095)."""
+    g = _c(g, np.float32).reshape(-1)
+    u = _c(u, np.float32).reshape(-1)
+    assert g.size == u.size
+    out = np.empty(g.size, np.float32)
+    lib().arfo_glu(_p(g, _f32p), _p(u, _f32p), g.size, int(act), _p(out, _f32p))
+    return out
+
+
+def moe_forward(x, gate, up, down, n_experts, inter, logits, top_k, norm_topk, init=None):
     """MoeMlp::forward with Q4_K SwiGLU experts (crates/arf-core/src/model/moe.rs:53-86,
     mlp.rs:20-24).  x [T, hidden] f32; gate/up: n_experts x [inter, hidden] Q4_K blocks;
-    down: n_experts x [hidden, inter] Q4_K blocks; logits [T, n_experts]."""
+    down: n_experts x [hidden, inter] Q4_K blocks; logits [T, n_experts].  init [T, hidden]:
+    the shared experts' output, which the routed contributions are added to (moe.rs:62-67)."""
     x = _c(x, np.float32)
     T, hidden = x.shape
     lg = _c(logits, np.float32)
@@ -214,8 +227,9 @@ def moe_forward(x, gate, up, down, n_experts, inter, logits, top_k, norm_topk):
     d = _c(down, np.uint8).reshape(-1)
     assert g.size == u.size == n_experts * inter * hidden // 256 * 144
     assert d.size == n_experts * hidden * inter // 256 * 144
-    out = np.empty((T, hidden), np.float32)
+    out = np.empty((T, hidden), np.float32) if init is None else np.array(init, np.float32, copy=True)
+    assert out.shape == (T, hidden)
     lib().arfo_moe_forward(_p(x, _f32p), T, hidden, inter, _p(g, _u8p), _p(u, _u8p),
                            _p(d, _u8p), int(n_experts), _p(lg, _f32p), int(top_k),
-                           int(bool(norm_topk)), _p(out, _f32p))
+                           int(bool(norm_topk)), int(init is not None), _p(out, _f32p))
     return out

@@ -53,6 +53,10 @@ def test_null_handles_are_rejected():
     assert L.arfq_moe(None, None, None, None, None, 1, 2, 1, None, 0, None) == arfq.ARFQ_E_INVALID
     assert L.arfq_ctx_create(0, None, None) == arfq.ARFQ_E_INVALID
     assert L.arfq_ctx_set_options(None, 0) == arfq.ARFQ_E_INVALID
+    assert L.arfq_moe_add(None, None, None, None, None, 1, 2, 1, None, 0, None) == arfq.ARFQ_E_INVALID
+    assert L.arfq_moe_ids_add(None, None, None, None, None, None, 1, 2, None, 0, None) == arfq.ARFQ_E_INVALID
+    assert L.arfq_ffn(None, None, None, None, 1, None, None) == arfq.ARFQ_E_INVALID
+    assert L.arfq_ffn_act(None, None, None, None, 1, None, None, arfq.ACT_GELU_TANH) == arfq.ARFQ_E_INVALID
 
 
 def test_no_gpu_here_fails_loudly():

@@ -166,10 +166,10 @@ def _h_f16(h):
 
 
 @pytest.mark.parametrize("qg,qd", [("q4_k", "q6_k"), ("q5_k", "q5_k"), ("iq4_xs", "iq4_xs"),
-                                   ("q5_k", "iq4_xs")])
+                                   ("q5_k", "iq4_xs"), ("q8_0", "q8_0"), ("q6_k", "q4_k")])
 def test_moe_expert_formats(gpu_ctx, oracle, qg, qd):
-    # down projection in Q6_K (as Q4_K_M GGUFs ship ffn_down_exps), and Q5_K / IQ4_XS
-    # experts through the grouped GEMMs; composed from oracle parts
+    # down projection in Q6_K (as Q4_K_M GGUFs ship ffn_down_exps), Q5_K / IQ4_XS / Q8_0
+    # experts and Q6_K gate|up through the grouped GEMMs; composed from oracle parts
     from arf_amd import synth
     _say("case: moe experts", qg, qd)
     T, E, k, hidden, inter = 9, 4, 2, 256, 512
@@ -187,7 +187,8 @@ def test_moe_expert_formats(gpu_ctx, oracle, qg, qd):
         for e, wt in zip(ids, w):
             g = oracle.matmul_q(qg, xf[t:t + 1], g_e[e], inter)
             u = oracle.matmul_q(qg, xf[t:t + 1], u_e[e], inter)
-            h = ((g / (1.0 + np.exp(-g))) * u).astype(np.float32)
+            with np.errstate(over="ignore"):  # exp(-g) = inf for g << 0: silu -> 0, as in f32
+                h = ((g / (1.0 + np.exp(-g))) * u).astype(np.float32)
             want[t] += wt * oracle.matmul_q(qd, _h_f16(h), d_e[e], hidden)[0]
     e = rel_err(got, want)
     _say("rel err", e)
@@ -318,3 +319,122 @@ def test_ffn_shape_errors(gpu_ctx):
     y = gpu_ctx.empty((1, 512), np.float32)
     with pytest.raises(ValueError):
         gpu_ctx.ffn(g, g, d, x, 1, y)
+
+
+# ------------------------------------------------------------ GeGLU FFN ----
+def _glu_oracle(oracle, x, raws, qts, inter, hidden, act):
+    g = oracle.matmul_q(qts[0], x, raws[0], inter)
+    u = oracle.matmul_q(qts[1], x, raws[1], inter)
+    h = oracle.glu(g, u, act).reshape(g.shape)
+    return oracle.matmul_q(qts[2], h, raws[2], hidden), g
+
+
+@pytest.mark.parametrize("qts,hidden,inter,m,xscale,x16", [
+    # m = 1, Q4_K: gate and up in one launch, GeGLU applied as the down GEMV reads its x
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 1, 0.02, False),
+    (("q4_k", "q4_k", "q4_k"), 5120, 17408, 1, 0.005, False),
+    # the 16-bit-x GEMV option (gate and up as two launches)
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 1, 0.02, True),
+    # m = 3: the integer-dot GEMV with GeGLU fused; m = 8: skinny GEMMs + the GeGLU kernel
+    (("q4_k", "q4_k", "q4_k"), 512, 768, 3, 0.02, False),
+    (("q4_k", "q4_k", "q6_k"), 512, 768, 8, 0.02, False),
+    (("q4_k", "q4_k", "q6_k"), 1024, 512, 1, 0.02, False)])
+def test_ffn_geglu_matches_reference(gpu_ctx, oracle, qts, hidden, inter, m, xscale, x16):
+    # ffn_dispatch's gate GEMV, up GEMV, geglu, down GEMV (island.rs:13436-13529,
+    # decode_ops_msl.metal:15-27); x scaled so that most g fall where gelu is curved
+    import arf_amd.arfq as A
+    from arf_amd import QType, synth
+    _say("case: ffn geglu", qts, hidden, inter, m, xscale, x16)
+    shapes = [(inter, hidden), (inter, hidden), (hidden, inter)]
+    raws = [synth.weight(q, n, k, seed=61 + i) for i, (q, (n, k)) in enumerate(zip(qts, shapes))]
+    ws = [gpu_ctx.upload(QType[q.upper()], r, n, k) for q, r, (n, k) in zip(qts, raws, shapes)]
+    x = (synth.activations(m, hidden, seed=67) * np.float32(xscale)).astype(np.float32)
+    y = gpu_ctx.empty((m, hidden), np.float32)
+    gpu_ctx.set_options(A.OPT_GEMV_X16 if x16 else 0)
+    try:
+        gpu_ctx.ffn(ws[0], ws[1], ws[2], gpu_ctx.to_device(x), m, y, act=A.ACT_GELU_TANH)
+    finally:
+        gpu_ctx.set_options(0)
+    want, g = _glu_oracle(oracle, x, raws, qts, inter, hidden, 1)
+    got = y.numpy()
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, want)
+    _say("rel err", e, "share of g in [-6, 6]", float(np.mean(np.abs(g) <= 6)))
+    assert np.mean(np.abs(g) <= 6) > 0.5
+    assert e <= TOL
+    # the same weights through SwiGLU differ (the activation is not cosmetic)
+    y2 = gpu_ctx.empty((m, hidden), np.float32)
+    gpu_ctx.ffn(ws[0], ws[1], ws[2], gpu_ctx.to_device(x), m, y2, act=A.ACT_SILU)
+    assert rel_err(y2.numpy(), want) > 10 * TOL
+
+
+def _q80_identity(n):
+    """Q8_0 blocks of the n x n identity: d = 1.0, one code 1 per row."""
+    nb = n // 32
+    blk = np.zeros((n, nb, 34), np.uint8)
+    blk[:, :, 0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    r = np.arange(n)
+    blk[r, r // 32, 2 + r % 32] = 1
+    return blk.reshape(-1)
+
+
+@pytest.mark.parametrize("act", [0, 1])
+@pytest.mark.parametrize("m", [1, 2])
+def test_ffn_activation_exact_through_identity(gpu_ctx, oracle, act, m):
+    # gate = up = down = the identity in Q8_0, whose f32 GEMV adds exactly one nonzero term
+    # per output: y = act(x) * x elementwise, so the GPU's activation is compared with the
+    # oracle's directly (to the last bits of exp / tanh), over the selftest's inputs
+    # (selftest.rs:6049-6052) including the clamp region and |x| >= 7
+    from arf_amd import QType
+    n = 256
+    raw = _q80_identity(n)
+    w = gpu_ctx.upload(QType.Q8_0, raw, n, n)
+    i = np.arange(m * n)
+    x = (((i % 29) - 14) * 0.3).astype(np.float32).reshape(m, n)
+    x[0, :6] = [7.0, -7.0, 20.0, -20.0, 0.0, 1.0]
+    y = gpu_ctx.empty((m, n), np.float32)
+    gpu_ctx.ffn(w, w, w, gpu_ctx.to_device(x), m, y, act=act)
+    got = y.numpy().reshape(-1).astype(np.float64)
+    want = oracle.glu(x, x, act).astype(np.float64)
+    # a few ulps of exp / tanh apart; for GeGLU at g < -3 the tanh's rounding is magnified
+    # by 1 + tanh(inner) ~ 0 (2^-21 of 0.5 |g u| bounds it)
+    xx = x.reshape(-1).astype(np.float64)
+    bound = 2e-6 * np.abs(want) + (2.0 ** -21 * 0.5 * xx * xx if act else 0.0) + 1e-30
+    _say("max err / bound", float(np.max(np.abs(got - want) / bound)))
+    assert np.all(np.abs(got - want) <= bound)
+
+
+# ---------------------------------------------------- MoE shared expert ----
+@pytest.mark.parametrize("T,E,k", [(2, 16, 4), (40, 16, 4)])
+def test_moe_add_onto_shared_expert(gpu_ctx, oracle, T, E, k):
+    # MoeMlp::forward with a shared expert (moe.rs:62-67): y = shared Mlp (arfq_ffn), then
+    # the routed block added on top (arfq_moe_add), on the decode path (8 pairs) and the
+    # grouped path (160 pairs); arfq_moe_add onto zeros gives arfq_moe's bits
+    from arf_amd import QType, synth
+    hidden, inter = 512, 256
+    _say("case: moe add", T, E, k)
+    raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=500 + T)
+    sh_raw = [synth.weight("q4_k", inter, hidden, seed=510), synth.weight("q4_k", inter, hidden, seed=511),
+              synth.weight("q4_k", hidden, inter, seed=512)]
+    sh = [gpu_ctx.upload(QType.Q4_K, sh_raw[0], inter, hidden), gpu_ctx.upload(QType.Q4_K, sh_raw[1], inter, hidden),
+          gpu_ctx.upload(QType.Q4_K, sh_raw[2], hidden, inter)]
+    x = (synth.activations(T, hidden, seed=T + 520) * np.float32(0.05)).astype(np.float16)
+    xf = x.astype(np.float32)
+    logits = synth.router_logits(T, E, seed=T + 521)
+    xd, lg = gpu_ctx.to_device(xf), gpu_ctx.to_device(logits)
+    y = gpu_ctx.empty((T, hidden), np.float32)
+    gpu_ctx.ffn(sh[0], sh[1], sh[2], xd, T, y)
+    s_gpu = y.numpy()
+    gpu_ctx.moe(ws[0], ws[1], ws[2], lg, T, k, True, gpu_ctx.to_device(x), y, accumulate=True)
+    got = y.numpy()
+    s_want, _ = _ffn_oracle(oracle, xf, sh_raw, ("q4_k",) * 3, inter, hidden)
+    assert rel_err(s_gpu, s_want) <= TOL
+    want = oracle.moe_forward(xf, raw[0], raw[1], raw[2], E, inter, logits, k, True, init=s_want)
+    e = rel_err(got, want)
+    _say("rel err", e)
+    assert e <= TOL
+    # accumulate onto zeros == overwrite
+    z = gpu_ctx.to_device(np.zeros((T, hidden), np.float32))
+    gpu_ctx.moe(ws[0], ws[1], ws[2], lg, T, k, True, gpu_ctx.to_device(x), z, accumulate=True)
+    plain = _moe_gpu(gpu_ctx, ws, x, logits, k, True)
+    assert np.array_equal(z.numpy().view(np.uint32), plain.view(np.uint32))

@@ -417,3 +417,79 @@ def test_moe_dequant_reference_equals_moe_forward(oracle):
     want = oracle.moe_forward(x, raw[0], raw[1], raw[2], E, inter, logits, k, True)
     got = moe_dequant_reference(oracle, x, raw, E, hidden, inter, logits, k, True)
     assert rel_err(got, want) < 1e-5
+
+
+def test_moe_forward_accumulates_onto_shared_output(oracle):
+    # MoeMlp::forward with a shared expert (moe.rs:62-67): out starts at 0, the shared
+    # output s is added first, then w_j * y_j per token in slot order.  init = 0 gives the
+    # plain block bit for bit; init = s gives s plus the routed sum (within f32 rounding),
+    # and each token's result is ((s + w0 y0) + w1 y1) exactly
+    from arf_amd import synth
+    E, hidden, inter, T, top_k = 4, 256, 256, 3, 2
+    gate = synth.weight("q4_k", inter, hidden, seed=51, experts=E)
+    up = synth.weight("q4_k", inter, hidden, seed=52, experts=E)
+    down = synth.weight("q4_k", hidden, inter, seed=53, experts=E)
+    x = (synth.activations(T, hidden, seed=54) * np.float32(0.05)).astype(np.float32)
+    logits = synth.router_logits(T, E, seed=55)
+    plain = oracle.moe_forward(x, gate, up, down, E, inter, logits, top_k, True)
+    zero = oracle.moe_forward(x, gate, up, down, E, inter, logits, top_k, True, init=np.zeros_like(plain))
+    assert np.array_equal(plain.view(np.uint32), zero.view(np.uint32))
+    s = synth.activations(T, hidden, seed=56)
+    got = oracle.moe_forward(x, gate, up, down, E, inter, logits, top_k, True, init=s)
+    assert rel_err(got, s.astype(np.float64) + plain) < 1e-5
+    # slot by slot: one-expert blocks (top_k = 1 of a one-hot router) added in order
+    for t in range(T):
+        ids, wts = oracle.top_k_softmax(logits[t], top_k, True)
+        acc = s[t].copy()
+        for e, w in zip(ids, wts):
+            oh = np.full((1, E), -1e4, np.float32)
+            oh[0, e] = 30.0
+            ye = oracle.moe_forward(x[t:t + 1], gate, up, down, E, inter, oh, 1, True)[0]
+            acc = (acc + np.float32(w) * ye).astype(np.float32)
+        assert np.array_equal(acc.view(np.uint32), got[t].view(np.uint32))
+
+
+def _gelu64(v):
+    v = np.asarray(v, np.float64)
+    inner = np.clip(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3), -15.0, 15.0)
+    return 0.5 * v * (1.0 + np.tanh(inner))
+
+
+def test_geglu_known_values_and_closed_forms(oracle):
+    # GeGLU (decode_ops_msl.metal:15-27, CPU oracle selftest.rs:6091-6095): gelu_tanh(g) * u
+    one = np.ones(1, np.float32)
+    f = lambda g: oracle.glu(np.array([g], np.float32), one, 1)[0]
+    assert f(0.0) == 0.0
+    # qwen_vision.rs:1205 gelu_tanh(1.0) = 0.841192 (to 1e-5): the erf form gives 0.8413447
+    # and dropping the cubic term 0.8317, both outside it
+    assert abs(f(1.0) - 0.841192) < 1e-5
+    # vision.rs:512-513
+    assert abs(f(0.0)) < 1e-6 and f(10.0) > 9.9 and abs(f(-10.0)) < 1e-3
+    # |g| >= 7: the (clamped) tanh is +-1 in f32, so gelu(g) = g and gelu(-g) = 0
+    for g in (7.0, 8.5, 34.0, 1e6, 1e20):
+        assert f(g) == np.float32(g)
+        assert f(-g) == 0.0
+    # oddness of tanh: gelu(g) - gelu(-g) = g
+    g = np.linspace(-6, 6, 1201, dtype=np.float32)
+    ones = np.ones_like(g)
+    d = oracle.glu(g, ones, 1).astype(np.float64) - oracle.glu(-g, ones, 1).astype(np.float64)
+    assert np.max(np.abs(d - g) / np.maximum(np.abs(g), 1e-3)) < 4e-7
+    # the selftest's inputs (gate spans the clamp region) against float64 of the same
+    # formula: within 1e-6 relative, plus the f32 rounding of tanh (2^-22 of 0.5 |g u|),
+    # which 1 + tanh(inner) magnifies where gelu is near 0 (g < -3)
+    i = np.arange(4096)
+    gs = (((i % 29) - 14) * 0.3).astype(np.float32)
+    us = (((i % 19) - 9) * 0.1).astype(np.float32)
+    got = oracle.glu(gs, us, 1).astype(np.float64)
+    want = _gelu64(gs) * us.astype(np.float64)
+    bound = 1e-6 * np.abs(want) + 2.0 ** -22 * 0.5 * np.abs(gs.astype(np.float64) * us)
+    assert np.all(np.abs(want - got) <= bound)
+
+
+def test_swiglu_act_matches_float64(oracle):
+    i = np.arange(4096)
+    gs = (((i % 29) - 14) * 0.3).astype(np.float32)
+    us = (((i % 19) - 9) * 0.1).astype(np.float32)
+    got = oracle.glu(gs, us, 0).astype(np.float64)
+    want = _silu64(gs.astype(np.float64)) * us.astype(np.float64)
+    assert np.max(np.abs(want - got) / np.maximum(np.abs(want), 1e-4)) < 2e-6
