@@ -91,7 +91,7 @@ __global__ __launch_bounds__(GM_THREADS) void gemm_q(
 // sums the S partials in split order into y, so the result does not depend on
 // the arrival order.
 // (held to 256 VGPRs: two workgroups per CU)
-template <class F, int TA, class XT, bool PAIR>
+template <class F, int TA, class XT, bool PAIR, int GM = 0xFF>
 __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__restrict__ x,
                                                       const uint16_t *__restrict__ xs,
                                                       const float *__restrict__ rs,
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
     for (int t = 0; t < TA; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    skinny_run<F, TA, 1, SK_THREADS, XT>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds, PAIR ? PO + M : M);
+    skinny_run<F, TA, 1, SK_THREADS, XT, false, GM>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds, PAIR ? PO + M : M);
     if constexpr (PAIR && TA == 1) {
         // rows r and r + 16 of a lane's accumulator are elements i and i + 8
 #pragma unroll
@@ -352,17 +352,22 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     return p;
 }
 
-template <class F, int TA, bool PAIR>
+template <class F, int TA, bool PAIR, int GM = 0xFF>
 static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                               const uint16_t *xs, const float *rs, int rss, float *y, float *part,
                               uint32_t *tick, int S, hipStream_t s) {
+    if constexpr (F::KIND == 4 && TA == 1 && GM == 0xFF) {
+        // at most 8 rows (8 hi + 8 lo with PAIR): the per-sub-block scaling
+        // touches only the accumulator groups that hold them
+        if (m <= 8) return launch_sk_t<F, 1, PAIR, PAIR ? 0x5 : 0x1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+    }
     constexpr size_t lds = sk_lds<F, TA, 1>();
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
-    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PAIR>, lds, lds_set))
+    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PAIR, GM>, lds, lds_set))
         return err;
     const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
-    gemm_sk<F, TA, _Float16, PAIR><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
-                                                                 (int)w->n, (int)w->k, rss);
+    gemm_sk<F, TA, _Float16, PAIR, GM><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
+                                                                     (int)w->n, (int)w->k, rss);
     return hipGetLastError();
 }
 

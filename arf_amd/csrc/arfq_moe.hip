@@ -387,7 +387,7 @@ __global__ __launch_bounds__(SK_THREADS) void moe_down_kernel(
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // (Q6_K: the second loop copy would not fit the registers)
-    skinny_run<F, 2, 1, SK_THREADS, _Float16, F::KIND != 1>(fm, wrow0, hidden, xr, h, hs, 0, K / 256,
+    skinny_run<F, 2, 1, SK_THREADS, _Float16, F::KIND != 4>(fm, wrow0, hidden, xr, h, hs, 0, K / 256,
                                                            acc, lds, rows);
     const int n = n0 + (lane & 31);
 #pragma unroll

@@ -12,14 +12,15 @@
 // the weights.  x is staged in LDS one block at a time and shared by the 4
 // waves (two barriers per block).
 //
-// The weight operand is exact: Q4_K lanes hold sc_j * q and Q6_K lanes
-// sc * (q - 32) as f16 integers; each block accumulates separately and is
-// scaled by the lane's own d at the block end (lane l's C column is its weight
-// row, so d is a register, not a broadcast).  Q4_K's min term
-// -dmin * sum_j m_j * X_j enters as two bf16 MFMAs against the x sub-block
-// sums X_j.  Q5_K is Q4_K with a 5-bit q.  IQ4_XS lanes hold the codebook
-// values and Q8_0 lanes the int8 codes; each MFMA covers one sub-block (one
-// Q8_0 block) and its result is scaled by that sub-block's d * (ls - 32) (d).
+// The weight operand is exact: Q4_K lanes hold sc_j * q as f16 integers;
+// each block accumulates separately and is scaled by the lane's own d at the
+// block end (lane l's C column is its weight row, so d is a register, not a
+// broadcast).  Q4_K's min term -dmin * sum_j m_j * X_j enters as two bf16
+// MFMAs against the x sub-block sums X_j.  Q5_K is Q4_K with a 5-bit q.
+// IQ4_XS lanes hold the codebook values, Q8_0 lanes the int8 codes and Q6_K
+// lanes q - 32; each MFMA (two for IQ4_XS) covers one sub-block (one Q8_0
+// block) and its result is scaled by that sub-block's d * (ls - 32) (d,
+// d * sc) in f32.
 //
 // K-slot map of step p (64 elements) of block b: lane half h and MFMA kk use
 // elements a_off(p, kk, h) + 0..7 of the block; the x operand is read from LDS
@@ -114,7 +115,10 @@ struct SkQ4K {
 // positions 8h .. 8h + 7 of the 4 quadrants; MFMA kk = quadrant kk:
 // element 128 n2 + 16 isub + 32 kk + 8 h + i.
 struct SkQ6K {
-    static constexpr int KIND = 1, RB = 192;
+    // exact operands: the codes q - 32 as f16; MFMA kk of step p covers one
+    // 16-element sub-block, whose product is scaled by its own d * sc in f32
+    // (KIND 4)
+    static constexpr int KIND = 4, RB = 192;
     struct Blk {
         u32x4 sc;  // the 16 i8 scales
         uint32_t d;
@@ -136,14 +140,21 @@ struct SkQ6K {
         return {ldv(sc16 + row * nblk + b), dd[row * nblk + b]};
     }
     __device__ static float2 scale(const Blk &k) { return make_float2(h2f(k.d), 0.f); }
-    // sc * (q - 32): q as the f16 1024 + q (v_perm inserts 0x64 above each code
-    // byte; the 2 qh bits go to bits 4-5), minus 1056, times sc.
-    __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
+    // d * sc of the sub-block MFMA kk of step p covers (dequant_q6_k's
+    // d * sc * (q - 32), crates/arf-core/src/model/gguf.rs:2092-2131, with the
+    // product d * sc formed first as there)
+    __device__ static float sub_scale(const Blk &k, int p, int kk) {
+        const int si = 8 * (p >> 1) + (p & 1) + 2 * kk;
+        const uint32_t scw[4] = {k.sc.x, k.sc.y, k.sc.z, k.sc.w};
+        return h2f(k.d) * (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
+    }
+    // q - 32: q as the f16 1024 + q (v_perm inserts 0x64 above each code
+    // byte; the 2 qh bits go to bits 4-5), minus 1056, exact
+    __device__ static void frag(const uint8_t *srow, const Blk &, int p, int h, half8 f[4]) {
         const uint8_t *ch = srow + 48 * p;  // ql_a[16] | ql_b[16] | qh[16]
         const u32x2 qa = *reinterpret_cast<const u32x2 *>(ch + 8 * h);
         const u32x2 qb = *reinterpret_cast<const u32x2 *>(ch + 16 + 8 * h);
         const u32x2 qh = *reinterpret_cast<const u32x2 *>(ch + 32 + 8 * h);
-        const uint32_t scw[4] = {k.sc.x, k.sc.y, k.sc.z, k.sc.w};
         const half2v m1056 = h2splat(-1056.f);
         // qh bytes of positions (4hh + 2pr, +1) spread into the two halves
         uint32_t hp[2][2];
@@ -154,8 +165,6 @@ struct SkQ6K {
                 hp[hh][pr] = __builtin_amdgcn_perm(0u, hh ? qh.y : qh.x, pr ? 0x0c030c02u : 0x0c010c00u);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const int si = 8 * (p >> 1) + (p & 1) + 2 * t;  // scale index
-            const half2v sv = h2splat((float)(int8_t)(scw[si >> 2] >> (8 * (si & 3))));
             const u32x2 ql = (t & 1) ? qb : qa;
             uint32_t o[4];
 #pragma unroll
@@ -166,7 +175,7 @@ struct SkQ6K {
                     const uint32_t lp = __builtin_amdgcn_perm(0x64646464u, l, pr ? 0x04030402u : 0x04010400u);
                     const uint32_t top = 2 * t <= 4 ? (hp[hh][pr] << (4 - 2 * t)) : (hp[hh][pr] >> (2 * t - 4));
                     const uint32_t q = (lp & 0x640F640Fu) | (top & 0x00300030u);
-                    o[2 * hh + pr] = as_u((as_h2(q) + m1056) * sv);
+                    o[2 * hh + pr] = as_u(as_h2(q) + m1056);
                 }
             }
             f[t] = u4_to_h8(o[0], o[1], o[2], o[3]);
@@ -368,7 +377,9 @@ constexpr size_t sk_lds() {
 // 256-element blocks [b0, b1) for the wave's 32 weight rows wrow0[w] ..
 // wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
 // The block loop of skinny_run for the first TU (<= TA) x tiles.
-template <class F, int TA, int TU, int NW, int NT, class XT>
+// GM: the 8-row accumulator groups (bit 4 t + g: rows 32 t + 8 g .. + 7) that
+// hold real rows; KIND 4 scales only those (the others stay 0).
+template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF>
 __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                             int64_t nrows, const SkRows<TA, NT> &rows,
                                             const XT *__restrict__ x,
@@ -498,7 +509,17 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                     for (int t = 0; t < TU; t++) {
                         const half8 af = *reinterpret_cast<const half8 *>(
                             xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
-                        if constexpr (KIND == 3) {
+                        if constexpr (KIND == 4) {
+                            // one sub-block per MFMA, times its d * sc
+                            floatx16 z;
+#pragma unroll
+                            for (int i = 0; i < 16; i++) z[i] = 0.f;
+                            const floatx16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], z, 0, 0, 0);
+                            const float ss = F::sub_scale(wb[w], p, kk);
+#pragma unroll
+                            for (int i = 0; i < 16; i++)
+                                if ((GM >> (4 * t + (i >> 2))) & 1) acc[w][t][i] = fmaf(ss, c[i], acc[w][t][i]);
+                        } else if constexpr (KIND == 3) {
                             floatx16 &c = kk < 2 ? cb[w][t] : cq[w][t];
                             if (kk % 2 == 0) {
                                 floatx16 z;
@@ -574,7 +595,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 // second x tile is neither staged nor multiplied (acc[w][1] is left as it
 // is).  All threads of the workgroup call it with the same block range and
 // xrows.
-template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false>
+template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
                                            const XT *__restrict__ x,
@@ -582,11 +603,11 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
                                            floatx16 (&acc)[NW][TA], _Float16 *lds, int xrows) {
     if constexpr (TA == 2 && SHORT) {
         if (xrows <= 32) {
-            skinny_loop<F, TA, 1, NW, NT, XT>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+            skinny_loop<F, TA, 1, NW, NT, XT, GM>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
             return;
         }
     }
-    skinny_loop<F, TA, TA, NW, NT, XT>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+    skinny_loop<F, TA, TA, NW, NT, XT, GM>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
 }
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.

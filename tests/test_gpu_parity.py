@@ -231,9 +231,12 @@ def test_next_formats_skinny_and_chunked(gpu_ctx, oracle, qtype, m, n, k, x16):
 
 @pytest.mark.parametrize("m", [1, 8, 64, 130])
 def test_q6_k_full_range_scales(gpu_ctx, oracle, m):
-    # quantizers put each block's largest sub-block scale near +-127, where the MFMA
-    # paths' f16 operand sc * (q - 32) passes 2048 and rounds (relative error <= 2^-12);
-    # the synthetic blocks keep scales in [-32, 31], so this test draws them from all of i8
+    # quantizers put each block's largest sub-block scale near +-127, where sc * (q - 32)
+    # passes 2048 and would round in f16; the skinny kernel (m = 5..64) multiplies the exact
+    # codes q - 32 and scales each sub-block's product by d * sc in f32, the prefill tile
+    # (m = 130) holds d * sc * (q - 32) rounded to f16 (relative error <= 2^-11).  The
+    # synthetic blocks keep scales in [-32, 31], so this test draws them from all of i8;
+    # at m = 8 (x as f16 hi + lo, about 22 bits) the skinny result is held to 2e-5
     from arf_amd import QType, synth
     _say("case: q6_k full-range scales", m)
     n, k = 384, 4096
@@ -247,7 +250,7 @@ def test_q6_k_full_range_scales(gpu_ctx, oracle, m):
     gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)
     e = rel_err(y.numpy(), oracle.matmul_q("q6_k", x, raw, n))
     _say("rel err", e)
-    assert e <= TOL
+    assert e <= (2e-5 if m == 8 else TOL)
 
 
 @pytest.mark.parametrize("qtype", ["q6_k", "q8_0"])
