@@ -943,6 +943,10 @@ struct DotQ6K {
         (void)B;
         return A * (xsc * (float)sdot - 32.f * xsum);
     }
+    __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
+        (void)B;
+        return A * (xsc * dot - 32.f * xsum);
+    }
 };
 
 // Q5_K: streams hdr (d, dmin, the 12 scale bytes: 16 B per block) and q
@@ -1014,6 +1018,9 @@ struct DotQ5K {
     }
     __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
         return A * (xsc * (float)sdot) - B * xsum;
+    }
+    __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
+        return A * (xsc * dot) - B * xsum;
     }
 };
 
@@ -1251,6 +1258,183 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot(F fmt, const float 
     }
 }
 
+// ----------------------------------------------- Q6_K / Q5_K at f32 x (m = 1) ----
+// The dot GEMV's work split and lane map with f32 arithmetic: x is kept in LDS
+// as f32, each 32 elements scaled by 2^s (s = min(24, 100 - e), |x| < 2^e, so
+// no product overflows), with the true-unit sum of every 16 elements and
+// 2^(24 - s) per 32.  A quadrant's 16 codes (q < 64) go into v_fma_mix_f32 as
+// the f16 subnormals q * 2^-24, so each product x * 2^s * q * 2^-24 is exact
+// in f32 and the quadrant adds F::term(A, B, 2^(24 - s), sum(x * q), sum(x)):
+// for Q6_K (d * sc) * (sum(x * q) - 32 * sum(x)), the oracle's
+// (d * sc) * (q - 32) per weight (gguf.rs:2120-2123) times f32 x, factorised.
+namespace {
+
+__device__ __forceinline__ void xf16_process(const XqRound &r, int items, int base, float4 *xf,
+                                             float *s16, float *xe) {
+    const int it = base + (int)threadIdx.x;
+    const float4 v0 = r.v0, v1 = r.v1;
+    float amax = fmaxf(fmaxf(fmaxf(fabsf(v0.x), fabsf(v0.y)), fmaxf(fabsf(v0.z), fabsf(v0.w))),
+                       fmaxf(fmaxf(fabsf(v1.x), fabsf(v1.y)), fmaxf(fabsf(v1.z), fabsf(v1.w))));
+    float sum = ((v0.x + v0.y) + (v0.z + v0.w)) + ((v1.x + v1.y) + (v1.z + v1.w));
+    amax = fmaxf(amax, quad_perm<QP_XOR1>(amax));
+    sum += quad_perm<QP_XOR1>(sum);  // 16 elements (items 2i, 2i + 1)
+    amax = fmaxf(amax, quad_perm<QP_XOR2>(amax));
+    const int ex = (amax > 0.f) ? __builtin_amdgcn_frexp_expf(amax) : 0;
+    const int sh = min(24, 100 - ex);
+    if (it < items) {
+        xf[2 * it] = make_float4(ldexpf(v0.x, sh), ldexpf(v0.y, sh), ldexpf(v0.z, sh), ldexpf(v0.w, sh));
+        xf[2 * it + 1] = make_float4(ldexpf(v1.x, sh), ldexpf(v1.y, sh), ldexpf(v1.z, sh), ldexpf(v1.w, sh));
+        if ((it & 1) == 0) s16[it >> 1] = sum;
+        if ((it & 3) == 0) xe[it >> 2] = ldexpf(1.f, 24 - sh);
+    }
+}
+
+// sum of x * q over 16 codes (one byte each in cw[4], element order), x scaled
+__device__ __forceinline__ float codes16_fdot(const uint32_t cw[4], const float *X) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t A = cw[j] & 0x00FF00FFu, B = (cw[j] >> 8) & 0x00FF00FFu;
+        acc = fmix<0>(X[4 * j], A, acc);
+        acc = fmix<1>(X[4 * j + 2], A, acc);
+        acc = fmix<0>(X[4 * j + 1], B, acc);
+        acc = fmix<1>(X[4 * j + 3], B, acc);
+    }
+    return acc;
+}
+
+}  // namespace
+
+template <class F, int XR>
+__global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const float *__restrict__ x,
+                                                                float *__restrict__ y, int n, int nblk) {
+    constexpr int C = Q6K_GEMV_CHUNK, PF = F::PF;
+    static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
+    extern __shared__ uint4 smem4[];
+    __shared__ int next_chunk;
+    const int k = nblk * 256;
+    float *xfl = reinterpret_cast<float *>(smem4);  // [k], scaled
+    float *s16 = xfl + k;                           // [k / 16]
+    float *xe = s16 + k / 16;                       // [k / 32]
+    float *part = xe + k / 32;                      // [R][spr]
+
+    const typename F::Res res = fmt.res();
+    const int tid = threadIdx.x;
+    const int l16 = tid & 15, grp = tid >> 4;
+    const int bq = l16 >> 2, c = l16 & 3;
+
+    const int G = gridDim.x;
+    const int r0 = (int)((int64_t)blockIdx.x * n / G);
+    const int r1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
+    const int R = r1 - r0;
+    const int spr = (nblk + 3) >> 2;
+    const int cpc = (R + C - 1) / C;
+    const int nchunks = cpc * spr;
+
+    int icol = 0, irow = 0;
+    auto start_chunk = [&](int kc) {
+        icol = kc < nchunks ? kc / cpc : spr;
+        irow = (kc - icol * cpc) * C;
+    };
+    typename F::Lane ld[PF];
+    int srow[PF], scol[PF];
+    auto issue = [&](int u, bool first) {
+        if (u % C == 0) {
+            int kc = grp;
+            if (!first) {
+                if (l16 == 0) kc = atomicAdd(&next_chunk, 1);
+                kc = __builtin_amdgcn_ds_swizzle(kc, 0x10);  // lane 0 of each 16-lane group
+            }
+            start_chunk(kc);
+        } else {
+            irow++;
+        }
+        const int b = 4 * icol + bq;
+        const bool live = icol < spr && irow < R && b < nblk;
+        const uint32_t blk = (uint32_t)(r0 + irow) * (uint32_t)nblk + (uint32_t)b;
+        F::load(res, ld[u], blk, live, c);
+        srow[u] = irow;
+        scol[u] = icol;
+    };
+
+    if (tid == 0) next_chunk = Q6K_GEMV_GROUPS;
+    // x loads, then (after every wave has issued them) the first weights, then
+    // x is scaled into LDS; the barrier after it orders LDS only, so the
+    // weight loads stay in flight across it
+    const int xitems = k / 8;
+    XqRound xr[XR];
+#pragma unroll
+    for (int r = 0; r < XR; r++) xr[r] = xq_load(x, xitems, r * Q6K_GEMV_THREADS);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int u = 0; u < PF; u++) issue(u, u < C);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int r = 0; r < XR; r++)
+        xf16_process(xr[r], xitems, r * Q6K_GEMV_THREADS, reinterpret_cast<float4 *>(xfl), s16, xe);
+    for (int base = XR * Q6K_GEMV_THREADS; base < xitems; base += Q6K_GEMV_THREADS)
+        xf16_process(xq_load(x, xitems, base), xitems, base, reinterpret_cast<float4 *>(xfl), s16, xe);
+    lds_barrier();
+
+    // scaled x of the column being consumed: the lane's 4 quadrants
+    int xcol = -1;
+    float X[4][16], XS[4], XE[4];
+    auto load_x = [&](int col) {
+        xcol = col;
+        const int xb = F::xbase(min(4 * col + bq, nblk - 1), c);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int eo = xb + F::XSTEP * t;
+            const float4 *src = reinterpret_cast<const float4 *>(xfl + eo);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = src[i];
+                X[t][4 * i] = v.x;
+                X[t][4 * i + 1] = v.y;
+                X[t][4 * i + 2] = v.z;
+                X[t][4 * i + 3] = v.w;
+            }
+            XS[t] = s16[eo >> 4];
+            XE[t] = xe[eo >> 5];
+        }
+    };
+
+    auto consume = [&](int u) {
+        const int col = scol[u], row = srow[u];
+        const bool live = col < spr && row < R;
+        if (live && col != xcol) load_x(col);
+        F::expand(ld[u]);  // DPP: every lane, live or not
+        float A[4], B[4];
+        F::scales(ld[u], c, A, B);
+        float v = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            uint32_t cw[4];
+            F::codes(ld[u], c, t, cw);
+            v += F::fterm(A[t], B[t], XE[t], codes16_fdot(cw, X[t]), XS[t]);
+        }
+        v = row16_sum(v);
+        if (l16 == 0 && live) part[(size_t)row * spr + col] = v;
+    };
+
+    while (scol[0] < spr) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            consume(u);
+            issue(u, false);
+        }
+    }
+    lds_barrier();
+
+    for (int t = tid; t < R; t += Q6K_GEMV_THREADS) {
+        const float *pr = part + (size_t)t * spr;
+        float v = 0.f;
+        for (int cc = 0; cc < spr; cc++) v += pr[cc];
+        y[r0 + t] = v;
+    }
+}
+
 // ------------------------------------------------------------------ Q8_0 ----
 // One wave per Q80_ROWS weight rows; lane l takes blocks l, l + 64, ... of
 // each: two 16-byte code loads and the block's f16 d per row, all the loads
@@ -1435,6 +1619,7 @@ constexpr int GEMV_MAX_M = 4;
 static size_t q4k_gemv_lds(const arfq_weight *w, int mx);
 static bool q4k_f32_ok(const arfq_weight *w);
 static size_t dot_lds(const arfq_weight *w, int mx);
+static bool dot_f32_ok(const arfq_weight *w);
 // the byte-code dot GEMV: Q6_K at m <= 2, Q5_K at m <= 4, while x fits in LDS and
 // one expert's streams fit 31-bit buffer offsets
 static int dot_mx(int64_t m) { return m <= 2 ? (int)m : 4; }
@@ -1456,6 +1641,7 @@ bool gemv_supports(const arfq_weight *w, int64_t m) {
     if (w->qtype == ARFQ_Q4_K)
         return q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
                w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
+    if (w->qtype == ARFQ_Q5_K && m == 1 && dot_f32_ok(w)) return true;
     if (w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS) return dot_ok(w, m);
     return w->qtype == ARFQ_Q8_0 || w->qtype == ARFQ_Q6_K;
 }
@@ -1539,6 +1725,46 @@ static hipError_t launch_dot_t(const F &fmt, const arfq_weight *w, int m, const 
         fmt, x, y, (int)w->n, (int)(w->k / 256), m);
     return hipGetLastError();
 }
+// f32-x dot GEMV (m = 1): one workgroup per CU (its 137 VGPRs leave room for
+// one; held to 128 for two, it spilled and ran 31.7 us instead of 23.9 at C3)
+constexpr size_t DOT_F32_LDS_MAX = 159 * 1024;
+static size_t dot_f32_lds_rows(const arfq_weight *w, int64_t rows) {
+    const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
+    return (size_t)w->k * 4 + (size_t)(w->k / 16) * 4 + (size_t)(w->k / 32) * 4 + (size_t)rows * spr * 4;
+}
+static int64_t dot_f32_grid(const arfq_weight *w) {
+    const int nblk = (int)(w->k / 256);
+    const int64_t steps = w->n * ((nblk + 3) / 4);
+    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
+    return std::max<int64_t>(1, std::min<int64_t>({(int64_t)cus, w->n,
+                                                   (steps + 2 * Q6K_GEMV_GROUPS - 1) / (2 * Q6K_GEMV_GROUPS)}));
+}
+static size_t dot_f32_lds(const arfq_weight *w) {
+    const int64_t g = dot_f32_grid(w);
+    return dot_f32_lds_rows(w, (w->n + g - 1) / g);
+}
+static bool dot_f32_ok(const arfq_weight *w) {
+    const int64_t nb = w->n * (w->k / 256);
+    const int64_t bpb = w->qtype == ARFQ_Q6_K ? 192 : w->qtype == ARFQ_Q5_K ? 160 : 0;
+    return bpb && w->k % 256 == 0 && dot_f32_lds(w) <= DOT_F32_LDS_MAX && nb * bpb < (int64_t)Q4K_OOB;
+}
+template <class F, int XR>
+static hipError_t launch_dot_f32_t(const F &fmt, const arfq_weight *w, const float *x, float *y, hipStream_t s) {
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)gemv_dot_f32<F, XR>, DOT_F32_LDS_MAX, lds_set))
+        return err;
+    gemv_dot_f32<F, XR><<<(unsigned)dot_f32_grid(w), Q6K_GEMV_THREADS, dot_f32_lds(w), s>>>(
+        fmt, x, y, (int)w->n, (int)(w->k / 256));
+    return hipGetLastError();
+}
+template <class F>
+static hipError_t launch_dot_f32(const F &fmt, const arfq_weight *w, const float *x, float *y, hipStream_t s) {
+    const int64_t rounds = (w->k / 8 + Q6K_GEMV_THREADS - 1) / Q6K_GEMV_THREADS;
+    if (rounds <= 1) return launch_dot_f32_t<F, 1>(fmt, w, x, y, s);
+    if (rounds <= 2) return launch_dot_f32_t<F, 2>(fmt, w, x, y, s);
+    return launch_dot_f32_t<F, 4>(fmt, w, x, y, s);
+}
+
 template <class F, int MX>
 static hipError_t launch_dot(const F &fmt, const arfq_weight *w, int m, const float *x, float *y,
                              hipStream_t s) {
@@ -1774,6 +2000,7 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
     }
     if (w->qtype == ARFQ_Q5_K) {
         const DotQ5K f = dot_q5k(w, e);
+        if (m == 1 && !x16 && dot_f32_ok(w)) return launch_dot_f32(f, w, x, y, s);
         if (m == 1) return launch_dot<DotQ5K, 1>(f, w, 1, x, y, s);
         if (m == 2) return launch_dot<DotQ5K, 2>(f, w, 2, x, y, s);
         return launch_dot<DotQ5K, 4>(f, w, (int)m, x, y, s);
@@ -1784,6 +2011,7 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
         if (m == 2) return launch_dot<DotIQ4XS, 2>(f, w, 2, x, y, s);
         return launch_dot<DotIQ4XS, 4>(f, w, (int)m, x, y, s);
     }
+    if (w->qtype == ARFQ_Q6_K && m == 1 && !x16 && dot_f32_ok(w)) return launch_dot_f32(dot_q6k(w, e), w, x, y, s);
     if (w->qtype == ARFQ_Q6_K && dot_ok(w, m)) {
         const DotQ6K f = dot_q6k(w, e);
         return m == 1 ? launch_dot<DotQ6K, 1>(f, w, 1, x, y, s) : launch_dot<DotQ6K, 2>(f, w, 2, x, y, s);

@@ -371,9 +371,15 @@ def only_config(ctx, args):
     elif c == "c1":
         ms, _ = time_matmul(ctx, "q8_0", 1, 2048, 2048, args.steps, args.warmup, 64, 0xA7F00001)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q8_0", 1, 2048, 2048) / ms / 1e6}
+    elif c == "q5km1":
+        ms, _ = time_matmul(ctx, "q5_k", 1, 17408, 5120, args.steps, args.warmup, 6, 0xA7F00005)
+        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q5_k", 1, 17408, 5120) / ms / 1e6}
     elif c.startswith("c3"):
-        mm = int(c[3:])
+        if c.endswith("x16"):
+            ctx.set_options(_arfq.OPT_GEMV_X16)
+        mm = int(c[3:].replace("x16", ""))
         ms, _ = time_matmul(ctx, "q6_k", mm, 5120, 17408, args.steps, args.warmup, 6, 0xA7F00003)
+        ctx.set_options(0)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q6_k", mm, 5120, 17408) / ms / 1e6}
     elif c == "c4":
         ms, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, args.steps, args.warmup, 2, 0xA7F00004,
@@ -399,7 +405,8 @@ def main():
                     help="time the GGUF reader instead: open a synthetic model file (C5's expert "
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
-    ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m8", "c3m32", "c3m64", "c4", "c5"],
+    ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c4",
+                                       "c5", "q5km1"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "

@@ -196,11 +196,57 @@ def test_q4k_gemv_f32_dynamic_range(gpu_ctx, oracle, case):
 
 
 def test_c3_q6_k_gemv_m1_full(gpu_ctx, oracle):
+    # C3 at m = 1: the f32-x GEMV (exact products), held to the f32 bound
     _say("case: C3 m=1 full")
     got, raw, x = _matmul(gpu_ctx, "q6_k", 5120, 17408, 1, seed=0xA7F00003)
     e = rel_err(got, oracle.matmul_q("q6_k", x, raw, 5120))
     _say("C3 m=1 rel err", e)
+    assert e <= F32_TOL
+
+
+def test_c3_q6_k_gemv_x16_option(gpu_ctx, oracle):
+    # ARFQ_OPT_GEMV_X16 at C3 m = 1: the integer-dot kernel (x in 16-bit fixed point)
+    import arf_amd
+    _say("case: C3 m=1, x16 option")
+    gpu_ctx.set_options(arf_amd.arfq.OPT_GEMV_X16)
+    try:
+        got, raw, x = _matmul(gpu_ctx, "q6_k", 5120, 17408, 1, seed=0xA7F00003)
+    finally:
+        gpu_ctx.set_options(0)
+    e = rel_err(got, oracle.matmul_q("q6_k", x, raw, 5120))
+    _say("C3 x16 rel err", e)
     assert e <= TOL
+
+
+def _dyadic_blocks(qtype, n, k, seed):
+    """Q6_K blocks with d = 2^-4, Q5_K blocks with d = 2^-4 and dmin = 2^-5 (random
+    codes and scales): every weight is a multiple of 2^-5 below 256."""
+    from arf_amd import synth
+    bb = {"q6_k": 210, "q5_k": 176}[qtype]
+    raw = synth.weight(qtype, n, k, seed=seed).reshape(-1, bb)
+    if qtype == "q6_k":
+        raw[:, 208:210] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)
+    else:
+        raw[:, 0:2] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)
+        raw[:, 2:4] = np.frombuffer(np.float16(2.0 ** -5).tobytes(), np.uint8)
+    return raw.reshape(-1)
+
+
+@pytest.mark.parametrize("qtype,n,k", [("q6_k", 512, 4096), ("q6_k", 300, 256), ("q5_k", 512, 4096),
+                                       ("q5_k", 64, 2048)])
+def test_dot_gemv_f32_exact_on_integer_x(gpu_ctx, oracle, qtype, n, k):
+    # the f32-x Q6_K / Q5_K GEMV (m = 1): integer x in [-8, 8] and dyadic weights keep
+    # every product and sum exact in f32 in any order, so the result equals the
+    # oracle's bit for bit -- any rounding of x or of the codes would show
+    _say("case: dot f32 exact", qtype, n, k)
+    from arf_amd import QType
+    raw = _dyadic_blocks(qtype, n, k, seed=n + k)
+    rng = np.random.default_rng(k + 1)
+    x = rng.integers(-8, 9, size=(1, k)).astype(np.float32)
+    w = gpu_ctx.upload(QType[qtype.upper()], raw, n, k)
+    y = gpu_ctx.empty((1, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), 1, y)
+    assert np.array_equal(y.numpy(), oracle.matmul_q(qtype, x, raw, n))
 
 
 @pytest.mark.parametrize("qtype", ["q5_k", "iq4_xs"])
@@ -210,7 +256,7 @@ def test_next_formats_gemv_c2_shape(gpu_ctx, oracle, qtype):
     got, raw, x = _matmul(gpu_ctx, qtype, 17408, 5120, 1, seed=0xA7F00005)
     e = rel_err(got, oracle.matmul_q(qtype, x, raw, 17408))
     _say(qtype, "rel err", e)
-    assert e <= TOL
+    assert e <= (F32_TOL if qtype == "q5_k" else TOL)  # Q5_K at m = 1: the f32-x GEMV
 
 
 @pytest.mark.parametrize("qtype", ["q5_k", "iq4_xs"])
