@@ -6,9 +6,10 @@
 //     ARFQ_OPT_GEMV_X16 option: gemv_q4k (x in 16-bit fixed point, integer
 //     dots).  16-lane groups walk (row, 4-block column) steps handed out from
 //     LDS counters.
-//   * Q6_K / Q5_K / IQ4_XS: gemv_dot<Fmt> (x in 16-bit fixed point, integer
-//     dots), the same step walk; gemv_q6k is the fallback for shapes it does
-//     not take.
+//   * Q6_K / Q5_K / IQ4_XS: m = 1: gemv_dot_f32<Fmt> (f32 x times the exact
+//     codes); m = 2..4 and ARFQ_OPT_GEMV_X16: gemv_dot<Fmt> (x in 16-bit fixed
+//     point, integer dots); the same step walk; gemv_q6k is the fallback for
+//     shapes neither takes.
 //   * Q8_0: gemv_q80w, one wave per row, f32.
 // Reference behaviour: matmul_vec_q4ks_msl.metal:46-165 (simdgroup strides
 // sub-blocks, s*sum(q*x) + lo*sum(x) per sub-block, simd_sum), and the oracle
@@ -943,6 +944,8 @@ struct DotQ6K {
         (void)B;
         return A * (xsc * (float)sdot - 32.f * xsum);
     }
+    // the f32-x kernel's codes are the bytes xor FXOR (unsigned), its quadrant term
+    static constexpr uint32_t FXOR = 0u;
     __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
         (void)B;
         return A * (xsc * dot - 32.f * xsum);
@@ -1019,6 +1022,7 @@ struct DotQ5K {
     __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
         return A * (xsc * (float)sdot) - B * xsum;
     }
+    static constexpr uint32_t FXOR = 0u;
     __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
         return A * (xsc * dot) - B * xsum;
     }
@@ -1103,6 +1107,12 @@ struct DotIQ4XS {
     __device__ static float term(float A, float B, float xsc, int sdot, float xsum) {
         (void)B, (void)xsum;
         return A * (xsc * (float)sdot);
+    }
+    // f32 x: the unsigned codes kv + 128 (kv xor 0x80), less 128 * sum(x)
+    static constexpr uint32_t FXOR = 0x80808080u;
+    __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
+        (void)B;
+        return A * (xsc * dot - 128.f * xsum);
     }
 };
 
@@ -1262,11 +1272,12 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot(F fmt, const float 
 // The dot GEMV's work split and lane map with f32 arithmetic: x is kept in LDS
 // as f32, each 32 elements scaled by 2^s (s = min(24, 100 - e), |x| < 2^e, so
 // no product overflows), with the true-unit sum of every 16 elements and
-// 2^(24 - s) per 32.  A quadrant's 16 codes (q < 64) go into v_fma_mix_f32 as
-// the f16 subnormals q * 2^-24, so each product x * 2^s * q * 2^-24 is exact
-// in f32 and the quadrant adds F::term(A, B, 2^(24 - s), sum(x * q), sum(x)):
-// for Q6_K (d * sc) * (sum(x * q) - 32 * sum(x)), the oracle's
-// (d * sc) * (q - 32) per weight (gguf.rs:2120-2123) times f32 x, factorised.
+// 2^(24 - s) per 32.  A quadrant's 16 codes (unsigned bytes: Q6_K q < 64,
+// Q5_K q < 32, IQ4_XS kv + 128) go into v_fma_mix_f32 as the f16 subnormals
+// q * 2^-24, so each product x * 2^s * q * 2^-24 is exact in f32 and the
+// quadrant adds F::fterm(A, B, 2^(24 - s), sum(x * q), sum(x)): for Q6_K
+// (d * sc) * (sum(x * q) - 32 * sum(x)), the oracle's (d * sc) * (q - 32) per
+// weight (gguf.rs:2120-2123) times f32 x, factorised.
 namespace {
 
 __device__ __forceinline__ void xf16_process(const XqRound &r, int items, int base, float4 *xf,
@@ -1412,6 +1423,8 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
         for (int t = 0; t < 4; t++) {
             uint32_t cw[4];
             F::codes(ld[u], c, t, cw);
+#pragma unroll
+            for (int j = 0; j < 4; j++) cw[j] ^= F::FXOR;
             v += F::fterm(A[t], B[t], XE[t], codes16_fdot(cw, X[t]), XS[t]);
         }
         v = row16_sum(v);
@@ -1641,7 +1654,7 @@ bool gemv_supports(const arfq_weight *w, int64_t m) {
     if (w->qtype == ARFQ_Q4_K)
         return q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
                w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
-    if (w->qtype == ARFQ_Q5_K && m == 1 && dot_f32_ok(w)) return true;
+    if ((w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS) && m == 1 && dot_f32_ok(w)) return true;
     if (w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS) return dot_ok(w, m);
     return w->qtype == ARFQ_Q8_0 || w->qtype == ARFQ_Q6_K;
 }
@@ -1745,7 +1758,7 @@ static size_t dot_f32_lds(const arfq_weight *w) {
 }
 static bool dot_f32_ok(const arfq_weight *w) {
     const int64_t nb = w->n * (w->k / 256);
-    const int64_t bpb = w->qtype == ARFQ_Q6_K ? 192 : w->qtype == ARFQ_Q5_K ? 160 : 0;
+    const int64_t bpb = w->qtype == ARFQ_Q6_K ? 192 : w->qtype == ARFQ_Q5_K ? 160 : w->qtype == ARFQ_IQ4_XS ? 128 : 0;
     return bpb && w->k % 256 == 0 && dot_f32_lds(w) <= DOT_F32_LDS_MAX && nb * bpb < (int64_t)Q4K_OOB;
 }
 template <class F, int XR>
@@ -2007,6 +2020,7 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
     }
     if (w->qtype == ARFQ_IQ4_XS) {
         const DotIQ4XS f = dot_iq4xs(w, e);
+        if (m == 1 && !x16 && dot_f32_ok(w)) return launch_dot_f32(f, w, x, y, s);
         if (m == 1) return launch_dot<DotIQ4XS, 1>(f, w, 1, x, y, s);
         if (m == 2) return launch_dot<DotIQ4XS, 2>(f, w, 2, x, y, s);
         return launch_dot<DotIQ4XS, 4>(f, w, (int)m, x, y, s);

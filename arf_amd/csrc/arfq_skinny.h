@@ -378,15 +378,18 @@ constexpr size_t sk_lds() {
 // wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
 // The block loop of skinny_run for the first TU (<= TA) x tiles.
 // GM: the 8-row accumulator groups (bit 4 t + g: rows 32 t + 8 g .. + 7) that
-// hold real rows; KIND 4 scales only those (the others stay 0).
-template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF>
+// hold real rows; KIND 4 scales only those (the others stay 0).  MERGE: x tile
+// 1 holds the low halves of tile 0's rows (f32 x as f16 hi + lo), so its
+// products go into tile 0's accumulators (acc[w][1] is left as it is).
+template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF, bool MERGE = false>
 __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                             int64_t nrows, const SkRows<TA, NT> &rows,
                                             const XT *__restrict__ x,
                                             const uint16_t *__restrict__ xs, int b0, int b1,
                                             floatx16 (&acc)[NW][TA], _Float16 *lds) {
     constexpr int KIND = F::KIND;
-    constexpr int XR = 32 * TA;  // x rows staged
+    constexpr int XR = 32 * TA;       // x rows staged
+    constexpr int TO = MERGE ? 1 : TU;  // accumulator tiles written
     constexpr int XC = SkRows<TA, NT>::XC;
     constexpr int RL = F::RB / 16;          // lanes per weight row in a coalesced load
     constexpr int NI = 32 * F::RB / 1024;   // 16-byte loads per lane per block
@@ -478,7 +481,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
         for (int w = 0; w < NW; w++)
 #pragma unroll
-            for (int t = 0; t < TA; t++)
+            for (int t = 0; t < TO; t++)
 #pragma unroll
                 for (int i = 0; i < 16; i++) cmin[w][t][i] = 0.f;
     }
@@ -505,39 +508,45 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                 F::frag(slab + (w * 32 + lr) * SL, wb[w], p, h, bf);
 #pragma unroll
                 for (int kk = 0; kk < 4; kk++) {
+                    if constexpr (KIND == 4) {
+                        // one sub-block per MFMA (both x tiles with MERGE), times its d * sc
+                        floatx16 c[TO], z;
 #pragma unroll
-                    for (int t = 0; t < TU; t++) {
-                        const half8 af = *reinterpret_cast<const half8 *>(
-                            xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
-                        if constexpr (KIND == 4) {
-                            // one sub-block per MFMA, times its d * sc
-                            floatx16 z;
+                        for (int i = 0; i < 16; i++) z[i] = 0.f;
 #pragma unroll
-                            for (int i = 0; i < 16; i++) z[i] = 0.f;
-                            const floatx16 c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], z, 0, 0, 0);
-                            const float ss = F::sub_scale(wb[w], p, kk);
+                        for (int t = 0; t < TU; t++) {
+                            const half8 af = *reinterpret_cast<const half8 *>(
+                                xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
+                            const int ti = MERGE ? 0 : t;
+                            c[ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], MERGE && t > 0 ? c[0] : z,
+                                                                           0, 0, 0);
+                        }
+                        const float ss = F::sub_scale(wb[w], p, kk);
+#pragma unroll
+                        for (int ti = 0; ti < TO; ti++)
 #pragma unroll
                             for (int i = 0; i < 16; i++)
-                                if ((GM >> (4 * t + (i >> 2))) & 1) acc[w][t][i] = fmaf(ss, c[i], acc[w][t][i]);
-                        } else if constexpr (KIND == 3) {
-                            floatx16 &c = kk < 2 ? cb[w][t] : cq[w][t];
-                            if (kk % 2 == 0) {
-                                floatx16 z;
+                                if ((GM >> (4 * ti + (i >> 2))) & 1) acc[w][ti][i] = fmaf(ss, c[ti][i], acc[w][ti][i]);
+                    } else {
 #pragma unroll
-                                for (int i = 0; i < 16; i++) z[i] = 0.f;
-                                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], z, 0, 0, 0);
-                            } else {
-                                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], c, 0, 0, 0);
-                            }
-                        } else if (KIND != 0 && p == 0 && kk == 0) {
+                        for (int t = 0; t < TU; t++) {
+                            const half8 af = *reinterpret_cast<const half8 *>(
+                                xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
+                            const int ti = MERGE ? 0 : t;
+                            const bool cont = MERGE && t > 0;  // tile 1 adds onto tile 0's chain
                             floatx16 z;
 #pragma unroll
                             for (int i = 0; i < 16; i++) z[i] = 0.f;
-                            cb[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], z, 0, 0, 0);
-                        } else if (KIND != 0) {
-                            cb[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], cb[w][t], 0, 0, 0);
-                        } else {
-                            acc[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], acc[w][t], 0, 0, 0);
+                            if constexpr (KIND == 3) {
+                                floatx16 &c = kk < 2 ? cb[w][ti] : cq[w][ti];
+                                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], kk % 2 == 0 && !cont ? z : c,
+                                                                           0, 0, 0);
+                            } else if constexpr (KIND != 0) {
+                                cb[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                    af, bf[kk], p == 0 && kk == 0 && !cont ? z : cb[w][ti], 0, 0, 0);
+                            } else {
+                                acc[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], acc[w][ti], 0, 0, 0);
+                            }
                         }
                     }
                 }
@@ -545,10 +554,10 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                     // the step's two sub-blocks, each times its own d * (ls - 32)
                     const float2 ss = F::sub_scales(wb[w], p);
 #pragma unroll
-                    for (int t = 0; t < TU; t++)
+                    for (int ti = 0; ti < TO; ti++)
 #pragma unroll
                         for (int i = 0; i < 16; i++)
-                            acc[w][t][i] = fmaf(ss.y, cq[w][t][i], fmaf(ss.x, cb[w][t][i], acc[w][t][i]));
+                            acc[w][ti][i] = fmaf(ss.y, cq[w][ti][i], fmaf(ss.x, cb[w][ti][i], acc[w][ti][i]));
                 }
             }
         }
@@ -564,14 +573,15 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
                     for (int t = 0; t < TU; t++) {
                         const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sl + (32 * t + lr) * 16 + 8 * h);
-                        cmin[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][t], 0, 0, 0);
-                        cmin[w][t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][t], 0, 0, 0);
+                        const int ti = MERGE ? 0 : t;
+                        cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][ti], 0, 0, 0);
+                        cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][ti], 0, 0, 0);
                     }
                 }
 #pragma unroll
-                for (int t = 0; t < TU; t++)
+                for (int ti = 0; ti < TO; ti++)
 #pragma unroll
-                    for (int i = 0; i < 16; i++) acc[w][t][i] = fmaf(dd.x, cb[w][t][i], acc[w][t][i]);
+                    for (int i = 0; i < 16; i++) acc[w][ti][i] = fmaf(dd.x, cb[w][ti][i], acc[w][ti][i]);
             }
         }
 #pragma unroll
@@ -584,9 +594,9 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
         for (int w = 0; w < NW; w++)
 #pragma unroll
-            for (int t = 0; t < TU; t++)
+            for (int ti = 0; ti < TO; ti++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) acc[w][t][i] += cmin[w][t][i];
+                for (int i = 0; i < 16; i++) acc[w][ti][i] += cmin[w][ti][i];
     }
 }
 
@@ -595,7 +605,8 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 // second x tile is neither staged nor multiplied (acc[w][1] is left as it
 // is).  All threads of the workgroup call it with the same block range and
 // xrows.
-template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF>
+template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF,
+          bool MERGE = false>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
                                            const XT *__restrict__ x,
@@ -607,7 +618,7 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
             return;
         }
     }
-    skinny_loop<F, TA, TA, NW, NT, XT, GM>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
 }
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.

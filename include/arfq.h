@@ -85,13 +85,13 @@ const char *arfq_last_error(const arfq_ctx *ctx);
 int arfq_ctx_sync(arfq_ctx *ctx);
 
 /* Context options (bit set; default 0).
- * ARFQ_OPT_GEMV_X16: the Q4_K, Q5_K and Q6_K decode GEMVs at m = 1
+ * ARFQ_OPT_GEMV_X16: the Q4_K, Q5_K, Q6_K and IQ4_XS decode GEMVs at m = 1
  *   (arfq_matmul, arfq_ffn_act) round each 32-element block of f32 x to 16-bit
  *   fixed point (relative to the block's max |x|) and take exact integer dots;
- *   faster for Q4_K, max relative error ~1e-4 of the output's rms.  By default
+ *   faster, max relative error ~1e-4 of the output's rms.  By default
  *   they multiply f32 x by the exact weights in f32, as the reference GEMVs do
  *   (crates/arf-gpu/src/shaders/metal/matmul_vec_q4ks_msl.metal:46-165).
- *   (m = 2..4 and IQ4_XS always use the 16-bit form.)
+ *   (m = 2..4 always use the 16-bit form.)
  * No counterpart in the reference (which has only the f32 form). */
 #define ARFQ_OPT_GEMV_X16 1u
 int arfq_ctx_set_options(arfq_ctx *ctx, unsigned options);

@@ -219,13 +219,15 @@ def test_c3_q6_k_gemv_x16_option(gpu_ctx, oracle):
 
 
 def _dyadic_blocks(qtype, n, k, seed):
-    """Q6_K blocks with d = 2^-4, Q5_K blocks with d = 2^-4 and dmin = 2^-5 (random
-    codes and scales): every weight is a multiple of 2^-5 below 256."""
+    """Q6_K and IQ4_XS blocks with d = 2^-4, Q5_K blocks with d = 2^-4 and dmin = 2^-5
+    (random codes and scales): every weight is a multiple of 2^-5 below 256."""
     from arf_amd import synth
-    bb = {"q6_k": 210, "q5_k": 176}[qtype]
+    bb = {"q6_k": 210, "q5_k": 176, "iq4_xs": 136}[qtype]
     raw = synth.weight(qtype, n, k, seed=seed).reshape(-1, bb)
     if qtype == "q6_k":
         raw[:, 208:210] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)
+    elif qtype == "iq4_xs":
+        raw[:, 0:2] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)
     else:
         raw[:, 0:2] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)
         raw[:, 2:4] = np.frombuffer(np.float16(2.0 ** -5).tobytes(), np.uint8)
@@ -233,9 +235,9 @@ def _dyadic_blocks(qtype, n, k, seed):
 
 
 @pytest.mark.parametrize("qtype,n,k", [("q6_k", 512, 4096), ("q6_k", 300, 256), ("q5_k", 512, 4096),
-                                       ("q5_k", 64, 2048)])
+                                       ("q5_k", 64, 2048), ("iq4_xs", 512, 4096), ("iq4_xs", 70, 1024)])
 def test_dot_gemv_f32_exact_on_integer_x(gpu_ctx, oracle, qtype, n, k):
-    # the f32-x Q6_K / Q5_K GEMV (m = 1): integer x in [-8, 8] and dyadic weights keep
+    # the f32-x Q6_K / Q5_K / IQ4_XS GEMV (m = 1): integer x in [-8, 8] and dyadic weights keep
     # every product and sum exact in f32 in any order, so the result equals the
     # oracle's bit for bit -- any rounding of x or of the codes would show
     _say("case: dot f32 exact", qtype, n, k)
@@ -256,7 +258,7 @@ def test_next_formats_gemv_c2_shape(gpu_ctx, oracle, qtype):
     got, raw, x = _matmul(gpu_ctx, qtype, 17408, 5120, 1, seed=0xA7F00005)
     e = rel_err(got, oracle.matmul_q(qtype, x, raw, 17408))
     _say(qtype, "rel err", e)
-    assert e <= (F32_TOL if qtype == "q5_k" else TOL)  # Q5_K at m = 1: the f32-x GEMV
+    assert e <= F32_TOL  # m = 1: the f32-x GEMV
 
 
 @pytest.mark.parametrize("qtype", ["q5_k", "iq4_xs"])
