@@ -233,8 +233,11 @@ struct FmtQ6K {
 
 // Q4_K and Q6_K with the weights rounded to f16 (KIND 0): the prefill tiles
 // (m > 64), where MFMA throughput, not bytes, is the bound and the register
-// file holds no room for per-block accumulators.  One rounding per weight,
-// as the reference's half tiles (matmul_mm_q4ks.metal:166).
+// file holds no room for per-block accumulators.  One rounding per weight
+// (relative error <= 2^-11).  The reference's dense prefill tile holds f32
+// weights by default and f16 only under MM_HALF_FRAG
+// (matmul_mm_q4ks.metal:161-171); its MoE tiles are f16
+// (moe_mm_id_q4ks.metal:34-46).
 struct FmtQ4KR : FmtQ4K {
     static constexpr int KIND = 0;
     __host__ __device__ FmtQ4KR shifted(int64_t nb) const { return {FmtQ4K::shifted(nb)}; }

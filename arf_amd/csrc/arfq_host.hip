@@ -496,8 +496,9 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     if (int rc = ensure_scratch(ctx, o)) return rc;
     char *sc = (char *)ctx->scratch;
     hipError_t e;
-    // the grouped GEMMs read f16 activation tiles (as the reference's half mm_id
-    // tiles) and, for Q4_K and Q5_K, the x sub-block sums
+    // the grouped GEMMs read f16 activation tiles (as the reference's mm_id
+    // kernel stages half tiles, moe_mm_id_q4ks.metal:34-46) and, for Q4_K and
+    // Q5_K, the x sub-block sums
     const _Float16 *xh = x_dtype == ARFQ_F32 ? (const _Float16 *)(sc + o_x) : (const _Float16 *)x;
     uint16_t *xs = gsums ? (uint16_t *)(sc + o_xs) : nullptr;
     // an f32 x is stored row-scaled into f16 range; gate|up multiply back

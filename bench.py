@@ -122,16 +122,25 @@ def time_moe(ctx, steps, warmup, copies, tokens=None):
 
 
 def cpu_model():
-    """The host CPU's model name (from /proc/cpuinfo) and logical CPU count."""
+    """The host CPU's model name with its family / model / stepping numbers (from
+    /proc/cpuinfo, which a virtual machine may report generically) and the logical
+    CPU count."""
     name = platform.processor() or platform.machine()
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    name = line.split(":", 1)[1].strip()
-                    break
+                if not line.strip():
+                    break  # the first processor's block
+                k, _, v = line.partition(":")
+                fields[k.strip()] = v.strip()
     except OSError:
         pass
+    if "model name" in fields:
+        name = fields["model name"]
+        ids = [f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields]
+        if ids:
+            name += " (" + ", ".join(ids) + ")"
     return name, os.cpu_count() or 1
 
 
@@ -368,6 +377,10 @@ def only_config(ctx, args):
         ms, _ = time_matmul(ctx, "q4_k", 1, 17408, 5120, args.steps, args.warmup, args.copies, 0xA7F00002)
         ctx.set_options(0)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q4_k", 1, 17408, 5120) / ms / 1e6}
+    elif c == "c1n8":
+        # one workgroup's worth of C1 (8 rows): the per-launch floor C1 sits on
+        ms, _ = time_matmul(ctx, "q8_0", 1, 8, 2048, args.steps, args.warmup, 64, 0xA7F00001)
+        res = {"us_per_launch": ms * 1e3}
     elif c == "c1":
         ms, _ = time_matmul(ctx, "q8_0", 1, 2048, 2048, args.steps, args.warmup, 64, 0xA7F00001)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q8_0", 1, 2048, 2048) / ms / 1e6}
@@ -406,7 +419,7 @@ def main():
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
     ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c4",
-                                       "c5", "q5km1"],
+                                       "c5", "q5km1", "c1n8"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
