@@ -475,7 +475,7 @@ static hipError_t launch_bd_q4k(const arfq_weight *w, int e, int64_t m, const _F
         (int)w->n, (int)w->k, mt, xcd, p.bd_full, p.bd_chunks);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !nsplit) return err;
-    bd_reduce_kernel<<<dim3(BD_BM * BD_BN / 256, (unsigned)nsplit), 256, 0, s>>>(
+    bd_reduce_kernel<<<dim3(BD_BM * BD_BN / 1024, (unsigned)nsplit), 256, 0, s>>>(
         part, rs, y, (int)m, (int)w->n, mt, p.bd_full, p.bd_chunks);
     return hipGetLastError();
 }

@@ -393,21 +393,43 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
 }
 
 // y of the split tiles: the chunks' partial tiles added in chunk order.
-// One thread per output; grid (BD_BM * BD_BN / 256, split tiles).
+// A thread per 4 consecutive outputs of a tile row (16-byte partial loads,
+// up to 8 chunks' loads in flight at once); grid (BD_BM * BD_BN / 1024, split
+// tiles).
 __global__ __launch_bounds__(256) void bd_reduce_kernel(const float *__restrict__ part,
                                                         const float *__restrict__ rs,
                                                         float *__restrict__ y, int m, int n,
                                                         int mt, int full, int chunks) {
     const int lt = blockIdx.y;
-    const int e = blockIdx.x * 256 + threadIdx.x;
+    const int e = (blockIdx.x * 256 + threadIdx.x) * 4;
     const int rl = e / BD_BN, cl = e - rl * BD_BN;
     const int tile = full + lt;
     const int r = (tile % mt) * BD_BM + rl, c = (tile / mt) * BD_BN + cl;
     if (r >= m || c >= n) return;
-    const float *pp = part + (size_t)lt * chunks * BD_BM * BD_BN + e;
-    float v = 0.f;
-    for (int j = 0; j < chunks; j++) v += pp[(size_t)j * BD_BM * BD_BN];
-    y[(int64_t)r * n + c] = rs ? v * rs[r] : v;
+    const float4 *pp = reinterpret_cast<const float4 *>(part + (size_t)lt * chunks * BD_BM * BD_BN + e);
+    constexpr size_t CS = (size_t)BD_BM * BD_BN / 4;  // one chunk's tile, in float4
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j0 = 0; j0 < chunks; j0 += 8) {
+        float4 t[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (j0 + j < chunks) t[j] = pp[(size_t)(j0 + j) * CS];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            if (j0 + j < chunks) {
+                v.x += t[j].x;
+                v.y += t[j].y;
+                v.z += t[j].z;
+                v.w += t[j].w;
+            }
+        }
+    }
+    const float sr = rs ? rs[r] : 1.f;
+    float *yr = y + (int64_t)r * n + c;
+    const float o[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        if (c + i < n) yr[i] = rs ? o[i] * sr : o[i];
 }
 
 }  // namespace arfq
