@@ -213,11 +213,15 @@ __global__ __launch_bounds__(1024) void moe_group_kernel(const int32_t *__restri
 // tile of up to MOE_BM = 64 (token, slot) rows.
 constexpr int MOE_BM = 64;
 
-// gate|up: workgroup = one tile x 128 columns of inter, 8 waves: wave w < 4
-// streams gate rows n0 + 32 w, wave w + 4 the same rows of up (one weight per
-// wave keeps two waves per SIMD).  After the loop the up waves hand their
-// accumulators to the gate waves through LDS, and the gate waves write
-// h = silu(g) * u in f32 (its range can exceed f16's; moe_hprep scales it).
+// gate|up: a work item is one tile x 128 columns of inter, taken by a
+// workgroup of 8 waves: wave w < 4 streams gate rows n0 + 32 w, wave w + 4 the
+// same rows of up (one weight per wave keeps two waves per SIMD).  After the
+// loop the up waves hand their accumulators to the gate waves through LDS, and
+// the gate waves write h = silu(g) * u in f32 (its range can exceed f16's;
+// moe_hprep scales it).  The grid holds as many workgroups as fit on the
+// device at once and each walks the items with a stride of the grid, so the
+// item count (known only on the device) never leaves a part-filled last round
+// of workgroups.
 constexpr int MOE_GU_THREADS = 512;
 template <class F>
 __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
@@ -226,53 +230,58 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     const int32_t *__restrict__ off, const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ h) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-    if ((int)blockIdx.x >= *ntiles) return;  // uniform over the workgroup
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
-    const int wq = wave & 3;
-    const bool is_up = wave >= 4;
-    const int2 tile = tiles[blockIdx.x];
-    const int e = tile.x, row0 = tile.y;
-    const int rows = min(MOE_BM, off[e + 1] - row0);
-    const int n0 = blockIdx.y * 128 + 32 * wq;
-    const SkRows<2, MOE_GU_THREADS> xr =
-        sk_rows<2, MOE_GU_THREADS>(rows, K, [&](int r) { return sorted[row0 + r] / top_k; });
-    const F fm[1] = {(is_up ? up : gate).shifted((int64_t)e * expert_blocks)};
-    const int64_t wrow0[1] = {n0};
-    floatx16 acc[1][2];
-#pragma unroll
-    for (int t = 0; t < 2; t++)
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    skinny_run<F, 2, 1, MOE_GU_THREADS, _Float16, true>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc,
-                                                        lds, rows);
-    // the loop ends with a barrier after its last LDS use: hand up to gate
-    float *ex = reinterpret_cast<float *>(lds);  // [4 waves][2 tiles][16][64 lanes]
-    if (is_up) {
+    const int ncol = (inter + 127) / 128;
+    const int items = *ntiles * ncol;
+    for (int it = blockIdx.x; it < items; it += gridDim.x) {  // uniform over the workgroup
+        const int tid = sk_tid(), lane = tid & 63;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
+        const int wq = wave & 3;
+        const bool is_up = wave >= 4;
+        const int ti = it / ncol;
+        const int2 tile = tiles[ti];
+        const int e = tile.x, row0 = tile.y;
+        const int rows = min(MOE_BM, off[e + 1] - row0);
+        const int n0 = (it - ti * ncol) * 128 + 32 * wq;
+        const SkRows<2, MOE_GU_THREADS> xr =
+            sk_rows<2, MOE_GU_THREADS>(rows, K, [&](int r) { return sorted[row0 + r] / top_k; });
+        const F fm[1] = {(is_up ? up : gate).shifted((int64_t)e * expert_blocks)};
+        const int64_t wrow0[1] = {n0};
+        floatx16 acc[1][2];
 #pragma unroll
         for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) ex[((wq * 2 + t) * 16 + i) * 64 + lane] = acc[0][t][i];
-    }
-    __syncthreads();
-    if (!is_up) {
-        const int n = n0 + (lane & 31);
+            for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
+        skinny_run<F, 2, 1, MOE_GU_THREADS, _Float16, true>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc,
+                                                            lds, rows);
+        // the loop ends with a barrier after its last LDS use: hand up to gate
+        float *ex = reinterpret_cast<float *>(lds);  // [4 waves][2 tiles][16][64 lanes]
+        if (is_up) {
 #pragma unroll
-        for (int t = 0; t < 2; t++)
+            for (int t = 0; t < 2; t++)
 #pragma unroll
-            for (int i = 0; i < 16; i++) {
-                const int r = sk_out_row(t, i);
-                if (r < rows && n < inter) {
-                    float g = acc[0][t][i], u = ex[((wq * 2 + t) * 16 + i) * 64 + lane];
-                    if (xrs) {  // the token row was stored divided by xrs (exact)
-                        const float sc = xrs[sorted[row0 + r] / top_k];
-                        g *= sc;
-                        u *= sc;
+                for (int i = 0; i < 16; i++) ex[((wq * 2 + t) * 16 + i) * 64 + lane] = acc[0][t][i];
+        }
+        __syncthreads();
+        if (!is_up) {
+            const int n = n0 + (lane & 31);
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    const int r = sk_out_row(t, i);
+                    if (r < rows && n < inter) {
+                        float g = acc[0][t][i], u = ex[((wq * 2 + t) * 16 + i) * 64 + lane];
+                        if (xrs) {  // the token row was stored divided by xrs (exact)
+                            const float sc = xrs[sorted[row0 + r] / top_k];
+                            g *= sc;
+                            u *= sc;
+                        }
+                        const float sg = g / (1.0f + expf(-g));
+                        h[(int64_t)(row0 + r) * inter + n] = sg * u;
                     }
-                    const float sg = g / (1.0f + expf(-g));
-                    h[(int64_t)(row0 + r) * inter + n] = sg * u;
                 }
-            }
+        }
+        __syncthreads();  // the hand-off area is the next item's x staging
     }
 }
 
@@ -362,17 +371,20 @@ __global__ __launch_bounds__(256) void moe_hprep_kernel(const float *__restrict_
     }
 }
 
-// down: workgroup = one tile x 128 columns of hidden; rows are stored to
-// o[pair index], scaled back by the row's h scale, so the combine can read
-// each token's slots in order.
+// down: workgroup = one tile x 128 columns of hidden, two workgroups per CU
+// (at most 256 registers per lane); rows are stored to o[pair index], scaled
+// back by the row's h scale, so the combine can read each token's slots in
+// order.  A plain grid here: its items differ in cost (one or two x tiles) and
+// the dispatcher's dynamic placement beat a grid-stride loop (64 vs 76 us at
+// 128 experts, top-8, 512 tokens).
 template <class F>
-__global__ __launch_bounds__(SK_THREADS) void moe_down_kernel(
+__global__ __launch_bounds__(SK_THREADS, 2) void moe_down_kernel(
     F down, int64_t expert_blocks, const _Float16 *__restrict__ h, const uint16_t *__restrict__ hs,
     const float *__restrict__ rs, int K, int hidden, const int32_t *__restrict__ off,
     const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles,
     const int32_t *__restrict__ ntiles, float *__restrict__ o) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-    if ((int)blockIdx.x >= *ntiles) return;
+    if ((int)blockIdx.x >= *ntiles) return;  // uniform over the workgroup
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int2 tile = tiles[blockIdx.x];
     const int e = tile.x, row0 = tile.y;
@@ -474,6 +486,22 @@ hipError_t launch_moe_group(const int32_t *ids, int64_t P, int E, int32_t *off, 
 
 int64_t moe_max_tiles(int64_t P, int E) { return (P + MOE_BM - 1) / MOE_BM + E; }
 
+// Workgroups of a grid-stride grouped GEMM: as many as fit on the device at
+// once (workgroups per CU from the occupancy query, cached per kernel in
+// `fit`), never more than the items can use.
+static unsigned moe_grid(const void *fn, int threads, size_t lds, std::atomic<int> &fit,
+                         const arfq_weight *w, int64_t max_items) {
+    int per_cu = fit.load(std::memory_order_relaxed);
+    if (per_cu == 0) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, threads, lds) != hipSuccess ||
+            per_cu < 1)
+            per_cu = 1;
+        fit.store(per_cu, std::memory_order_relaxed);
+    }
+    const int64_t cus = w->ctx && w->ctx->cus > 0 ? w->ctx->cus : 1;
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(max_items, per_cu * cus));
+}
+
 template <class F>
 static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const _Float16 *x,
                            const uint16_t *xs, const float *xrs, int top_k, const int32_t *off,
@@ -484,7 +512,9 @@ static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const 
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)moe_gateup_kernel<F>, lds, lds_set)) return err;
     const int64_t eb = gw->n * g.nblk;
-    const dim3 grid((unsigned)max_tiles, (unsigned)((gw->n + 127) / 128));
+    static std::atomic<int> fit{0};
+    const unsigned grid = moe_grid((const void *)moe_gateup_kernel<F>, MOE_GU_THREADS, lds, fit, gw,
+                                   max_tiles * ((gw->n + 127) / 128));
     moe_gateup_kernel<F><<<grid, MOE_GU_THREADS, lds, s>>>(g, u, eb, x, xs, xrs, (int)gw->k,
                                                        (int)gw->n, top_k, off, sorted,
                                                        (const int2 *)tiles, ntiles, h);

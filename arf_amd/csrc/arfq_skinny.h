@@ -39,6 +39,16 @@ constexpr int SK_THREADS = 256;
 constexpr int SK_XLD = 256 + 8;  // halves per x row in LDS (16 bytes of padding)
 
 
+// threadIdx.x behind an empty asm: values derived from it are computed where
+// it is read, so in a kernel that loops over work items they are not hoisted
+// out of that loop (where they would stay live across the whole loop body and
+// crowd the tile loop's registers).
+__device__ __forceinline__ int sk_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 __device__ __forceinline__ half8 u4_to_h8(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     return __builtin_bit_cast(half8, u32x4{a, b, c, d});
 }
@@ -394,7 +404,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
     constexpr int RL = F::RB / 16;          // lanes per weight row in a coalesced load
     constexpr int NI = 32 * F::RB / 1024;   // 16-byte loads per lane per block
     constexpr int SL = F::RB + 16;          // slab row stride (bytes)
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = sk_tid(), lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, lr = lane & 31;
     _Float16 *xl = lds;                                              // [XR][SK_XLD]
     uint16_t *sl = reinterpret_cast<uint16_t *>(lds + XR * SK_XLD);  // [XR][16]
@@ -625,7 +635,7 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
 template <int TA, int NT = SK_THREADS, class RowOf>
 __device__ __forceinline__ SkRows<TA, NT> sk_rows(int n, int K, RowOf row_of) {
     SkRows<TA, NT> r;
-    const int tid = threadIdx.x;
+    const int tid = sk_tid();
 #pragma unroll
     for (int i = 0; i < SkRows<TA, NT>::XC; i++)
         r.x[i] = (int64_t)row_of(min((tid >> 5) + (NT / 32) * i, n - 1)) * K;
