@@ -1,5 +1,6 @@
 // arfq_gemm.hip -- dense dequant-into-LDS MFMA GEMM for prefill and batched
-// decode: y[m, n] (f32) = x[m, k] . W[n, k]^T with W in Q4_K, Q6_K or Q8_0.
+// decode: y[m, n] (f32) = x[m, k] . W[n, k]^T with W in Q4_K, Q6_K, Q8_0, Q5_K
+// or IQ4_XS.
 // The tile loop (LDS staging, dequant, MFMA) is in arfq_gemm_tile.h.
 //
 // Skinny shapes use split-K: grid.y splits the K steps, each split writes its
@@ -11,7 +12,7 @@
 //
 // Reference behaviour: matmul_mm_q4ks.metal:65-290; oracles matmul_nt_q4ks /
 // matmul_nt_q8_0 (crates/arf-ml/src/matmul.rs:174-204, 363-400) and
-// dequant_q6_k + matmul_nt for Q6_K.
+// dequant_q6_k / dequant_q5_k / dequant_iq4_xs + matmul_nt for the others.
 #include "arfq_gemm_tile.h"
 #include "arfq_internal.h"
 #include "arfq_skinny.h"
@@ -22,7 +23,7 @@
 namespace arfq {
 
 template <class F, int BM, bool XSPLIT>
-__global__ __launch_bounds__(GM_THREADS) void gemm_q(
+__global__ __launch_bounds__(GM_THREADS, F::WG_PER_CU) void gemm_q(
     F fmt, const _Float16 *__restrict__ xh, const _Float16 *__restrict__ xl,
     const uint16_t *__restrict__ xs, const float *__restrict__ rs, float *__restrict__ y, int M,
     int N, int K, int mt, int xcd_order) {
@@ -276,16 +277,16 @@ static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     GemmPlan p;
     const int cus = w->ctx && w->ctx->cus > 0 ? w->ctx->cus : 256;
-    // Q5_K and IQ4_XS have only the skinny kernel: above 64 rows it runs once
-    // per 64-row chunk of x
-    const bool chunked = w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS;
     const bool kind2 = w->qtype == ARFQ_Q4_K || w->qtype == ARFQ_Q5_K;  // min term: x sums
-    p.skinny = (m <= 64 || chunked) && w->k % 256 == 0;
+    p.skinny = m <= 64 && w->k % 256 == 0;
     p.bm = m > 64 ? 128 : 64;
-    // f32 x: scaled per row by a power of two into f16 range and rounded to f16
-    // for the skinny kernel and for prefill shapes (m > 64), split into f16 hi +
-    // lo otherwise; the output rows are multiplied back by the scale
-    p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && m <= 64;
+    // f32 x: scaled per row by a power of two into f16 range, then rounded to
+    // f16 for the skinny kernel and the prefill shapes (m > 64), or split into
+    // f16 hi + lo for the tile loop at m <= 64 and for the Q5_K and IQ4_XS
+    // prefill tiles (their weights are rounded to f16: this way only one of the
+    // two operands is); the output rows are multiplied back by the scale
+    const bool next = w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS;
+    p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && (m <= 64 || next);
     p.convert = x_dtype == ARFQ_F32;
     // skinny kernel, f32 x, m <= 32: x as f16 hi + lo (about 22 bits, as close
     // to the reference's f32 batched GEMV as the f16 MFMA gets): at m <= 16 the
@@ -403,24 +404,6 @@ SkIQ4XS sk_iq4xs(const arfq_weight *w) {
     return {(const uint2 *)w->s0, (const uint4 *)w->s1, (int)(w->k / 256)};
 }
 
-// The skinny kernel over x rows in chunks of 64 (one launch per chunk; m <= 64
-// is one launch).  Chunks run in stream order and reuse the partials and
-// counters.
-template <class F>
-static hipError_t launch_sk_rows(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
-                                 const uint16_t *xs, const float *rs, float *y, float *part,
-                                 uint32_t *tick, int ntick, int S, hipStream_t s, bool pair) {
-    if (pair) return launch_sk(fmt, w, m, x, xs, rs, (int)m, y, part, tick, ntick, S, s, true);  // m <= 32
-    for (int64_t r0 = 0; r0 < m; r0 += 64) {
-        const int64_t mc = std::min<int64_t>(64, m - r0);
-        if (hipError_t err = launch_sk(fmt, w, mc, x + r0 * w->k, xs ? xs + r0 * (w->k / 16) : nullptr,
-                                       rs ? rs + r0 : nullptr, (int)m, y + r0 * w->n, part, tick, ntick,
-                                       S, s, false))
-            return err;
-    }
-    return hipSuccess;
-}
-
 template <class F, int BM, bool XS>
 static hipError_t launch_gemm_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *xh,
                                 const _Float16 *xl, const uint16_t *xs, const float *rs, float *out,
@@ -511,11 +494,11 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
             return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xs, rs,
                              (int)m, y, out, tickets, ntickets, p.splits, s, p.pair);
         case ARFQ_Q5_K:
-            return launch_sk_rows(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets,
-                                  ntickets, p.splits, s, p.pair);
+            return launch_sk(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
+                             p.splits, s, p.pair);
         case ARFQ_IQ4_XS:
-            return launch_sk_rows(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, y, out, tickets,
-                                  ntickets, p.splits, s, p.pair);
+            return launch_sk(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
+                             p.splits, s, p.pair);
         default:
             return hipErrorInvalidValue;
         }
@@ -537,6 +520,25 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     case ARFQ_Q8_0: {
         const FmtQ80 f = fmt_q80(w).shifted((int64_t)e * w->n * (w->k / 32));
         err = launch_fmt(f, w, m, xh, xl, xs, p.splits == 1 ? rs : nullptr, out, p, s);
+        break;
+    }
+    // Q5_K and IQ4_XS reach the tile loop only above 64 rows (128-row tiles)
+    case ARFQ_Q5_K: {
+        if (p.bm != 128) return hipErrorInvalidValue;
+        const FmtQ5KR f = FmtQ5KR{(const uint4 *)w->s0, (const uint8_t *)w->s1, (int)(w->k / 256)}.shifted(
+            (int64_t)e * w->n * (w->k / 256));
+        const float *r1 = p.splits == 1 ? rs : nullptr;
+        err = p.xsplit ? launch_gemm_t<FmtQ5KR, 128, true>(f, w, m, xh, xl, xs, r1, out, p.splits, s)
+                       : launch_gemm_t<FmtQ5KR, 128, false>(f, w, m, xh, xl, xs, r1, out, p.splits, s);
+        break;
+    }
+    case ARFQ_IQ4_XS: {
+        if (p.bm != 128) return hipErrorInvalidValue;
+        const FmtIQ4XSR f = FmtIQ4XSR{(const uint2 *)w->s0, (const uint4 *)w->s1, (int)(w->k / 256)}.shifted(
+            (int64_t)e * w->n * (w->k / 256));
+        const float *r1 = p.splits == 1 ? rs : nullptr;
+        err = p.xsplit ? launch_gemm_t<FmtIQ4XSR, 128, true>(f, w, m, xh, xl, xs, r1, out, p.splits, s)
+                       : launch_gemm_t<FmtIQ4XSR, 128, false>(f, w, m, xh, xl, xs, r1, out, p.splits, s);
         break;
     }
     default:

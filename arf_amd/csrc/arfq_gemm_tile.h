@@ -99,6 +99,7 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t b) { return __uint_as_floa
 struct FmtQ4K {
     static constexpr int KIND = 2;
     static constexpr bool PHASED = true;  // deq depends on st % 4
+    static constexpr int WG_PER_CU = 1;   // the tile kernel's launch bound (workgroups per CU)
     struct Raw {
         u32x4 c, h;
     };
@@ -171,6 +172,7 @@ struct FmtQ4K {
 struct FmtQ6K {
     static constexpr int KIND = 1;
     static constexpr bool PHASED = true;
+    static constexpr int WG_PER_CU = 1;
     struct Raw {
         u32x2 qa, qb, qh, sc;
         uint32_t d;
@@ -292,11 +294,120 @@ struct FmtQ6KR : FmtQ6K {
     }
 };
 
+// Q5_K with the weights rounded to f16 (KIND 0, prefill): Q4_K's step map
+// (step st = sub-blocks 2p, 2p + 1, p = st % 4; half ws = sub-block 2p + ws,
+// slots 32 ws + e = element e of that sub-block) over ggml's block layout
+// qh[32] | qs[128] after the 16-byte header.  Element e of sub-block s is the
+// low (s even) or high nibble of qs[32 (s / 2) + e] plus bit s of qh[e] as
+// bit 4; its weight (d * sc) * q - dmin * m (dequant_q5_k,
+// crates/arf-core/src/model/gguf.rs:2053-2090) is formed in f32 and rounded
+// once to f16.
+struct FmtQ5KR {
+    static constexpr int KIND = 0;
+    static constexpr bool PHASED = true;
+    static constexpr int WG_PER_CU = 2;  // within 256 registers (one per CU took 268)
+    struct Raw {
+        u32x4 q0, q1, h0, h1, hd;
+    };
+    const uint4 *hdr;
+    const uint8_t *q;  // qh | qs, 160 bytes per block
+    int nblk;
+    __host__ __device__ FmtQ5KR shifted(int64_t nb) const { return {hdr + nb, q + nb * 160, nblk}; }
+    __device__ static int xk(int st, int qd) { return (st >> 2) * 256 + 64 * (st & 3) + 8 * qd; }
+    __device__ static int run_off(int ws, int r) { return 32 * ws + 8 * r; }
+    __device__ Raw load(int64_t row, int st, int, int) const {
+        const int64_t blk = row * nblk + (st >> 2);
+        const uint4 *b = reinterpret_cast<const uint4 *>(q + blk * 160);
+        Raw r;
+        r.h0 = ldv(b);
+        r.h1 = ldv(b + 1);
+        r.q0 = ldv(b + 2 + 2 * (st & 3));
+        r.q1 = ldv(b + 3 + 2 * (st & 3));
+        r.hd = ldv(hdr + blk);
+        return r;
+    }
+    __device__ static void deq(const Raw &r, int ph, int ws, uint32_t o[16]) {
+        const int s = 2 * ph + ws;
+        uint32_t sc, mm;
+        q4k_scale_min(r.hd.y, r.hd.z, r.hd.w, s, sc, mm);
+        const float d1 = h2f(r.hd.x) * (float)sc;
+        const float m1 = h2f(r.hd.x >> 16) * (float)mm;
+        const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+        const uint32_t hw[8] = {r.h0.x, r.h0.y, r.h0.z, r.h0.w, r.h1.x, r.h1.y, r.h1.z, r.h1.w};
+#pragma unroll
+        for (int w = 0; w < 8; w++) {
+            // elements 4w .. 4w + 3, one per byte
+            const uint32_t v = ((qw[w] >> (4 * ws)) & 0x0F0F0F0Fu) | (((hw[w] >> s) & 0x01010101u) << 4);
+            o[2 * w] = pack2h(fmaf(d1, (float)(v & 0xffu), -m1), fmaf(d1, (float)((v >> 8) & 0xffu), -m1));
+            o[2 * w + 1] = pack2h(fmaf(d1, (float)((v >> 16) & 0xffu), -m1), fmaf(d1, (float)(v >> 24), -m1));
+        }
+    }
+    __device__ static float2 scale(const Raw &) { return make_float2(1.f, 0.f); }
+    __device__ static void mins(const Raw &, uint32_t m[4]) { m[0] = m[1] = m[2] = m[3] = 0; }
+};
+
+// IQ4_XS with the weights rounded to f16 (KIND 0, prefill): the same step map
+// (half ws = sub-block 2p + ws); the 16 code bytes of sub-block s hold its
+// elements 0..15 in the low nibbles and 16..31 in the high ones.  Weight
+// (d * (ls - 32)) * kvalues[code] in f32 (dequant_iq4_xs,
+// crates/arf-core/src/model/gguf.rs:1937-1976), rounded once to f16.
+struct FmtIQ4XSR {
+    static constexpr int KIND = 0;
+    static constexpr bool PHASED = true;
+    static constexpr int WG_PER_CU = 2;
+    struct Raw {
+        u32x4 c;
+        u32x2 h;  // d | scales_h << 16, scales_l
+    };
+    const uint2 *hdr;
+    const uint4 *qs;
+    int nblk;
+    __host__ __device__ FmtIQ4XSR shifted(int64_t nb) const { return {hdr + nb, qs + nb * 8, nblk}; }
+    __device__ static int xk(int st, int qd) { return (st >> 2) * 256 + 64 * (st & 3) + 8 * qd; }
+    __device__ static int run_off(int ws, int r) { return 32 * ws + 8 * r; }
+    __device__ Raw load(int64_t row, int st, int ws, int) const {
+        const int64_t blk = row * nblk + (st >> 2);
+        Raw r;
+        r.c = ldv(qs + blk * 8 + 2 * (st & 3) + ws);
+        r.h = ldv(hdr + blk);
+        return r;
+    }
+    __device__ static void deq(const Raw &r, int ph, int ws, uint32_t o[16]) {
+        const int s = 2 * ph + ws;
+        const int ls = (int)(((r.h.y >> (4 * s)) & 0xFu) | (((r.h.x >> (16 + 2 * s)) & 3u) << 4));
+        const float dl = h2f(r.h.x) * (float)(ls - 32);
+        const float m128 = -128.f * dl;  // exact
+        // kvalues_iq4nl + 128 as bytes: entries 0..7 and 8..15, little-endian
+        constexpr uint32_t T0lo = 0xBFAD9881u ^ 0x80808080u, T0hi = 0xF6EADDCFu ^ 0x80808080u;
+        constexpr uint32_t T1lo = 0x26190D01u ^ 0x80808080u, T1hi = 0x71594535u ^ 0x80808080u;
+        const uint32_t cw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
+#pragma unroll
+        for (int nib = 0; nib < 2; nib++)
+#pragma unroll
+            for (int w = 0; w < 4; w++) {
+                // elements 16 nib + 4w .. + 3: kv + 128 per byte
+                const uint32_t sel = (cw[w] >> (4 * nib)) & 0x0F0F0F0Fu;
+                const uint32_t s7 = sel & 0x07070707u;
+                const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
+                const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
+                const uint32_t hi = (sel >> 3) & 0x01010101u;
+                const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
+                const uint32_t v = (v1 & mask) | (v0 & ~mask);
+                // (kv + 128) * dl - 128 dl = kv * dl, one rounding
+                o[8 * nib + 2 * w] = pack2h(fmaf(dl, (float)(v & 0xffu), m128), fmaf(dl, (float)((v >> 8) & 0xffu), m128));
+                o[8 * nib + 2 * w + 1] = pack2h(fmaf(dl, (float)((v >> 16) & 0xffu), m128), fmaf(dl, (float)(v >> 24), m128));
+            }
+    }
+    __device__ static float2 scale(const Raw &) { return make_float2(1.f, 0.f); }
+    __device__ static void mins(const Raw &, uint32_t m[4]) { m[0] = m[1] = m[2] = m[3] = 0; }
+};
+
 // Q8_0: step st = blocks 2st, 2st+1; half ws = block 2st + ws.  Weights d*q
 // rounded to f16.
 struct FmtQ80 {
     static constexpr int KIND = 0;
     static constexpr bool PHASED = false;
+    static constexpr int WG_PER_CU = 1;
     struct Raw {
         u32x4 a, b;
         uint32_t d;

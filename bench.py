@@ -492,7 +492,7 @@ def main():
             log(f"[bench] C3 m={mm}: {ms3 * 1e3:.2f} us/launch")
         # Q5_K and IQ4_XS at C2's shape: the survey's next row (no benchmark config): the
         # decode GEMV (m = 1), the skinny MFMA kernel (m = 8, 64) and, at m = 2048 (f16 x),
-        # the skinny kernel per 64-row chunk
+        # the rounded-weight prefill tile
         for qt, seed in (("q5_k", 0xA7F00005), ("iq4_xs", 0xA7F00006)):
             for mm in (1, 8, 64, 2048):
                 key = f"{qt}_gemv_m1_k5120_n17408" if mm == 1 else f"{qt}_m{mm}_k5120_n17408"

@@ -266,9 +266,9 @@ def test_next_formats_gemv_c2_shape(gpu_ctx, oracle, qtype):
                                        (8, 37, 2816, True), (32, 200, 5120, False),
                                        (33, 130, 1024, False), (64, 256, 2816, True),
                                        (100, 130, 1024, False), (130, 64, 512, True)])
-def test_next_formats_skinny_and_chunked(gpu_ctx, oracle, qtype, m, n, k, x16):
-    # Q5_K / IQ4_XS beyond the decode GEMV: the skinny MFMA kernel (m <= 64, f16 x
-    # at any m), run per 64-row chunk above 64 rows; f16 x is what the oracle sees
+def test_next_formats_skinny_and_prefill(gpu_ctx, oracle, qtype, m, n, k, x16):
+    # Q5_K / IQ4_XS beyond the decode GEMV: the skinny MFMA kernel (m <= 64) and the
+    # rounded-weight prefill tile above 64 rows; f16 x is what the oracle sees
     _say("case: next-format skinny", qtype, m, n, k, "f16" if x16 else "f32")
     dt = np.float16 if x16 else np.float32
     got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=11 * m + n, x_dtype=dt)
@@ -510,6 +510,22 @@ def test_c4_q4_k_gemm_full(gpu_ctx, oracle):
     assert e <= TOL
     rows = np.r_[0:4, 2044:2048]
     assert rel_err(got[rows], oracle.matmul_q("q4_k", x[rows].astype(np.float32), raw, n)) <= TOL
+
+
+@pytest.mark.parametrize("qtype", ["q5_k", "iq4_xs", "q6_k", "q8_0"])
+def test_prefill_tile_full(gpu_ctx, oracle, qtype):
+    # the rounded-weight prefill tile (m > 64) at 2048 f16 x rows: every output against the
+    # oracle's exact dequant + BLAS; the tile holds each weight rounded once to f16
+    # (2^-11), which the k-sums average down
+    _say("case: prefill tile full", qtype)
+    m, n, k = 2048, 640, 5120
+    got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=0xA7F00010 + len(qtype), x_dtype=np.float16)
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, _dequant_matmul(oracle, qtype, x.astype(np.float32), raw, n))
+    _say("rel err (all rows)", e)
+    assert e <= TOL
+    rows = np.r_[0:2, 2046:2048]
+    assert rel_err(got[rows], oracle.matmul_q(qtype, x[rows].astype(np.float32), raw, n)) <= TOL
 
 
 # ------------------------------------------------------ edge cases ----
