@@ -807,6 +807,25 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
                                        y + (int64_t)p * n, n, nblk);
 }
 
+// MoE decode, gate and up in one launch: blockIdx.z = 0 multiplies pair p's x
+// by expert ids[p]'s first weight into y0 row p, 1 by its second weight (same
+// shape) into y1.
+template <int XR, class XSRC>
+__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs_dual(
+    const uint8_t *__restrict__ hdr0, const uint8_t *__restrict__ qs0, const uint8_t *__restrict__ hdr1,
+    const uint8_t *__restrict__ qs1, uint32_t e_hdr_bytes, uint32_t e_qs_bytes, XSRC xsrc,
+    float *__restrict__ y0, float *__restrict__ y1, int n, int nblk, const int32_t *__restrict__ ids,
+    int E) {
+    const int p = blockIdx.y;
+    const int e = ids[p];
+    if (e < 0 || e >= E) return;  // uniform over the workgroup
+    const bool second = blockIdx.z != 0;
+    xsrc.pair(p);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>((second ? hdr1 : hdr0) + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+                                       (second ? qs1 : qs0) + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
+                                       (second ? y1 : y0) + (int64_t)p * n, n, nblk);
+}
+
 // --------------------------------------------- Q6_K / Q5_K / IQ4_XS (dot) ----
 // Integer-dot GEMV for up to four x rows (gemv_dot<Format, MX, XR>; the
 // formats are below).  x is quantized per 32-element
@@ -1989,6 +2008,42 @@ hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, cons
     if (act == ACT_GELU_TANH) return launch_gemv_glu_t<ACT_GELU_TANH>(w, m, g, u, y, s, x16);
     if (act == ACT_SILU) return launch_gemv_glu_t<ACT_SILU>(w, m, g, u, y, s, x16);
     return hipErrorInvalidValue;
+}
+
+template <class XS>
+static hipError_t launch_pairs_dual_t(const arfq_weight *w0, const arfq_weight *w1, int64_t P,
+                                      const int32_t *ids, const XS &xs, float *y0, float *y1, hipStream_t s) {
+    const int cus = w0->ctx->cus > 0 ? w0->ctx->cus : 256;
+    // about two workgroups per CU over both weights' pairs, >= 4 rows per workgroup
+    const int64_t g = std::max<int64_t>(1, std::min<int64_t>((2 * (int64_t)cus + 2 * P - 1) / (2 * P), w0->n / 4));
+    const int64_t nb = w0->n * (w0->k / 256);
+    const dim3 grid((unsigned)g, (unsigned)P, 2);
+    const size_t lds = q4k_pairs_lds(w0, g);
+    auto go = [&](auto kern) -> hipError_t {
+        static std::atomic<uint64_t> lds_set{0};
+        if (hipError_t err = set_max_lds_once((const void *)kern, Q4K_F32_LDS_MAX, lds_set)) return err;
+        kern<<<grid, Q4K_GEMV_THREADS, lds, s>>>((const uint8_t *)w0->s0, (const uint8_t *)w0->s1,
+                                                 (const uint8_t *)w1->s0, (const uint8_t *)w1->s1,
+                                                 (uint32_t)(nb * 16), (uint32_t)(nb * 128), xs, y0, y1,
+                                                 (int)w0->n, (int)(w0->k / 256), ids, w0->experts);
+        return hipGetLastError();
+    };
+    if ((int)(w0->k / 32) * 4 <= Q4K_GEMV_THREADS) return go(gemv_q4k_pairs_dual<1, XS>);
+    return go(gemv_q4k_pairs_dual<2, XS>);
+}
+
+bool gemv_pairs_dual_supports(const arfq_weight *w0, const arfq_weight *w1) {
+    return gemv_pairs_supports(w0) && gemv_pairs_supports(w1) && w1->qtype == w0->qtype &&
+           w1->n == w0->n && w1->k == w0->k && w1->experts == w0->experts;
+}
+
+hipError_t launch_gemv_pairs_dual(const arfq_weight *w0, const arfq_weight *w1, int64_t P, const int32_t *ids,
+                                  const void *x, int x_dtype, int x_div, float *y0, float *y1, hipStream_t s) {
+    if (P == 0) return hipSuccess;
+    if (!gemv_pairs_dual_supports(w0, w1) || P > 65535) return hipErrorInvalidValue;
+    if (x_dtype == ARFQ_F16)
+        return launch_pairs_dual_t(w0, w1, P, ids, XsRowF16{(const _Float16 *)x, w0->k, x_div}, y0, y1, s);
+    return launch_pairs_dual_t(w0, w1, P, ids, XsRowF32{(const float *)x, w0->k, x_div}, y0, y1, s);
 }
 
 hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,

@@ -464,9 +464,13 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
             wts = (const float *)(sc + o_w);
         }
         float *g = (float *)(sc + o_g), *u = (float *)(sc + o_u), *ob = (float *)(sc + o_o);
-        e = arfq::launch_gemv_pairs(gate, P, ids, x, x_dtype, top_k, nullptr, nullptr, g, ctx->stream);
-        if (e == hipSuccess)
-            e = arfq::launch_gemv_pairs(up, P, ids, x, x_dtype, top_k, nullptr, nullptr, u, ctx->stream);
+        if (arfq::gemv_pairs_dual_supports(gate, up)) {
+            e = arfq::launch_gemv_pairs_dual(gate, up, P, ids, x, x_dtype, top_k, g, u, ctx->stream);
+        } else {
+            e = arfq::launch_gemv_pairs(gate, P, ids, x, x_dtype, top_k, nullptr, nullptr, g, ctx->stream);
+            if (e == hipSuccess)
+                e = arfq::launch_gemv_pairs(up, P, ids, x, x_dtype, top_k, nullptr, nullptr, u, ctx->stream);
+        }
         if (e != hipSuccess) return hip_fail(ctx, e, "moe: gate/up GEMV launch");
         e = arfq::launch_gemv_pairs(down, P, ids, nullptr, ARFQ_F32, 1, g, u, ob, ctx->stream);
         if (e != hipSuccess) return hip_fail(ctx, e, "moe: down GEMV launch");

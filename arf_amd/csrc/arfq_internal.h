@@ -99,6 +99,10 @@ bool gemv_pairs_supports(const arfq_weight *w);
 hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids, const void *x,
                              int x_dtype, int x_div, const float *g, const float *u, float *y,
                              hipStream_t s);
+// MoE decode gate and up in one launch (same qtype, shape and expert count).
+bool gemv_pairs_dual_supports(const arfq_weight *w0, const arfq_weight *w1);
+hipError_t launch_gemv_pairs_dual(const arfq_weight *w0, const arfq_weight *w1, int64_t P, const int32_t *ids,
+                                  const void *x, int x_dtype, int x_div, float *y0, float *y1, hipStream_t s);
 
 // ---- arfq_gemm.hip ----
 // Launch shape and scratch layout of the dequant-into-LDS MFMA GEMM.
