@@ -121,7 +121,14 @@ int arfq_weight_info(const arfq_weight *w, int *qtype, int64_t *n_rows, int64_t 
 /* y[m, n_rows] (f32) = x[m, k_cols] . W^T for expert `expert` of `w` (0 for a
  * plain matrix).  x is f32 or f16 per `x_dtype`.  The library picks the kernel
  * by (qtype, m): wave-per-rows GEMV for small m, dequant-into-LDS MFMA GEMM
- * otherwise.  Replaces add_matmul_m / add_matmul
+ * otherwise.  Arithmetic: at m = 1 f32 x times the exact weights in f32; at
+ * m >= 5 f16 MFMAs with f32 sums.  There an f32 x is first scaled per row (and
+ * per K range) by a power of two that puts the row's max |x| in [2^14, 2^15),
+ * so every finite x stays finite, and the output is scaled back; it then
+ * enters as f16 hi + lo (~22 bits) at m <= 32 and for Q5_K / IQ4_XS above 64
+ * rows, as f16 otherwise.  The weights are exact up to 64 rows; above 64 rows
+ * Q6_K, Q8_0, Q5_K and IQ4_XS use the dequant rounded once to f16.
+ * Replaces add_matmul_m / add_matmul
  * (crates/arf-gpu/src/gpu/dispatch.rs:169-202, Q4KS arms :517-630) and the
  * island's gemv_q4ks / gemv_q4ks_batch / matmul_mm_q4ks selection
  * (crates/arf-gpu/src/gpu/metal/island.rs:4289-4333). */
