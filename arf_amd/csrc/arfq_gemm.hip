@@ -120,7 +120,7 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // PAIR with two tiles: the lo tile's products go into tile 0's accumulators
-    skinny_run<F, TA, 1, SK_THREADS, XT, false, GM, PAIR && TA == 2>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
+    skinny_run<F, TA, 1, SK_THREADS, XT, false, GM, PAIR && TA == 2, true>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
                                                                     PAIR ? PO + M : M);
     if constexpr (PAIR && TA == 1) {
         // rows r and r + 16 of a lane's accumulator are elements i and i + 8

@@ -390,8 +390,13 @@ constexpr size_t sk_lds() {
 // GM: the 8-row accumulator groups (bit 4 t + g: rows 32 t + 8 g .. + 7) that
 // hold real rows; KIND 4 scales only those (the others stay 0).  MERGE: x tile
 // 1 holds the low halves of tile 0's rows (f32 x as f16 hi + lo), so its
-// products go into tile 0's accumulators (acc[w][1] is left as it is).
-template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF, bool MERGE = false>
+// products go into tile 0's accumulators (acc[w][1] is left as it is).  PIN:
+// with two accumulator tiles, hold the scheduler to one step's operands at a
+// time (left free, it hoists all four steps' operand builds and x reads; the
+// dense skinny GEMM at C3 m = 64 ran 57.6 -> 53.0 us with the step boundary
+// held, the MoE tiles 1 % slower).
+template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF, bool MERGE = false,
+          bool PIN = false>
 __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                             int64_t nrows, const SkRows<TA, NT> &rows,
                                             const XT *__restrict__ x,
@@ -512,6 +517,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int p = 0; p < 4; p++) {
+            if constexpr (PIN && TO == 2) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int w = 0; w < NW; w++) {
                 half8 bf[4];
@@ -616,7 +622,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 // is).  All threads of the workgroup call it with the same block range and
 // xrows.
 template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF,
-          bool MERGE = false>
+          bool MERGE = false, bool PIN = false>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
                                            const XT *__restrict__ x,
@@ -628,7 +634,7 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
             return;
         }
     }
-    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE, PIN>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
 }
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.
