@@ -13,9 +13,12 @@
 // 16-byte load of that sub-block's codes per group gives the B operands of
 // the step's 4 MFMA groups (group kk uses dword kk: block elements
 // 64 p + 32 (l/32) + 8 kk .. + 7), and the A operands read the x tile with
-// the same element map.  Code loads run two steps ahead; the operand
-// registers of the next MFMA group are refilled while the current group's
-// MFMAs issue (the schedule is pinned with sched_barrier).
+// the same element map.  Code loads run two steps ahead.  The B operands
+// are software-pipelined against the MFMAs: the g = 1 operand of a group is
+// built between that group's four g = 0 MFMAs, and the next group's g = 0
+// operand between its four g = 1 MFMAs (one MFMA, then three VALU, pinned with
+// sched_group_barrier), so a wave's own dequant issues while its MFMAs run
+// instead of in a burst after them (C4: 427 -> 414 us).
 //
 // The B operands are exact: sc_j * q (<= 63 * 15) as f16 integers, made from
 // the code bits with v_perm (each nibble under the f16 bit pattern of 1024)
@@ -273,18 +276,19 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
         const _Float16 *xt0 = sx + ((size_t)buf * BD_BM + col) * BD_LD + 32 * h;
 
         // 16 MFMA groups per block: group i = (step p = i / 4, dword kk = i % 4)
-        // of 8 MFMAs, g-major.  The operand registers of group i + 1 are
-        // refilled as soon as group i's last use of them has issued: b[0]
-        // (dequantized codes) after the four g = 0 MFMAs, a[mg] (x from LDS)
-        // after MFMA (mg, g = 1), b[1] after the last MFMA.  Around them:
+        // of 8 MFMAs, g-major.  Operand registers are refilled as soon as their
+        // last use has issued: b[1] (dequantized codes) between group i's four
+        // g = 0 MFMAs, b[0] of group i + 1 between its four g = 1 MFMAs, a[mg]
+        // (x from LDS) after MFMA (mg, g = 1).  Around them:
         //  - the accumulators move into this block's unit: g = 1 here, g = 0
         //    at the end of the previous block (behind its last MFMAs);
         //  - groups 0, 1 work out the min-term operands and group 2 adds the
         //    min term -dmin * sum_j m_j X_j (units of d: two bf16 MFMAs per
         //    tile against the x sub-block sums, lane half h reading the hi /
         //    lo half of row (32 mg + l % 32)'s 16);
-        //  - group 12 takes the next block's headers (scales, ratio) and
-        //    issues the loads of the one after.
+        //  - group 13 takes the next block's headers (scales, ratio; the last
+        //    read of this block's scales is group 12's b[1]) and issues the
+        //    loads of the one after.
         half8 a[4], b[2];
         BdScale ks[2];
         bf16x8 bh[2], bl[2], am[4];
@@ -300,7 +304,6 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
 #pragma unroll
         for (int mg = 0; mg < 4; mg++) xread(0, mg);
         deq(0, 0);
-        deq(0, 1);
 #pragma unroll
         for (int mg = 0; mg < 4; mg++)
 #pragma unroll
@@ -315,7 +318,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
                 xsload(nb);
             }
             if (i == 9) xload(nb, 1);
-            if (i == 12) {
+            if (i == 13) {
                 block_scales();  // the next block's (scd of this one is used up)
                 hload(blk + 2);
             }
@@ -335,9 +338,17 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
                         acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bl[g], acc[mg][g], 0, 0, 0);
                     }
                 }
-                __builtin_amdgcn_sched_barrier(0);
+                if (i == 2) __builtin_amdgcn_sched_barrier(0);
             }
-            if (more) deq(i + 1, 0);
+            deq(i, 1);  // this group's second B operand, under its first four MFMAs
+            if (i != 2) {
+#pragma unroll
+                for (int mg = 0; mg < 4; mg++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
             if (i == 15) {
                 // group 0's accumulators into the next block's unit (the last
                 // block keeps its unit)
@@ -351,10 +362,16 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
             for (int mg = 0; mg < 4; mg++) {
                 acc[mg][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[1], acc[mg][1], 0, 0, 0);
                 if (more) xread(i + 1, mg);
-                __builtin_amdgcn_sched_barrier(0);
             }
+            if (more) deq(i + 1, 0);  // the next group's first B operand, under these MFMAs
+#pragma unroll
+            for (int mg = 0; mg < 4; mg++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // its x read
+                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
             if (kk == 3) cload(p & 1, 4 * blk + p + 2);  // the slot is free: step + 2
-            if (more) deq(i + 1, 1);
             if (i == 8) {
                 xstore(buf ^ 1, 0);
                 xsstore(buf ^ 1);
