@@ -460,9 +460,11 @@ struct TileShape {
 // For formats whose decode depends on st % 4 (PHASED: Q4_K, Q6_K) st0 and st1
 // are multiples of 4 (whole 256-element blocks); Q8_0 ranges are arbitrary.
 // Global loads run D steps ahead of the MFMAs in a register ring (D = 4 for
-// 64-row tiles, which stream weights, 2 when x comes as hi + lo; 1 for
-// 128-row tiles, whose registers are spent on accumulators); a load past st1 re-reads step st1 - 1 (a cache
-// hit), which keeps the ring free of branches.
+// 64-row tiles, which stream weights, 2 when x comes as hi + lo; 2 for
+// 128-row tiles, 1 with hi + lo x, whose registers go to the second A tile;
+// at C4's shape D = 2 against 1 took Q6_K 811 -> 767 us, IQ4_XS 732 -> 713,
+// Q5_K 766 -> 752, Q8_0 701 -> 694, and D = 4 no further); a load past st1
+// re-reads step st1 - 1 (a cache hit), which keeps the ring free of branches.
 // The caller zeroes acc and owns `lds` (gm_lds(BM, XSPLIT) bytes).
 template <class F, int BM, bool XSPLIT>
 __device__ __forceinline__ void gemm_tile_run(const F &fmt, int64_t wrow,
@@ -475,7 +477,7 @@ __device__ __forceinline__ void gemm_tile_run(const F &fmt, int64_t wrow,
     using S = TileShape<BM, XSPLIT>;
     constexpr int TA = S::TA, XI = S::XI, NA = S::NA, ATILE = S::ATILE, STAGE = S::STAGE;
     constexpr int KIND = F::KIND;
-    constexpr int D = BM == 64 ? (XSPLIT ? 2 : 4) : 1;  // prefetch depth (steps), divides 4
+    constexpr int D = BM == 64 ? (XSPLIT ? 2 : 4) : (XSPLIT ? 1 : 2);  // prefetch depth (steps), divides 4
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave & 1, wn = wave >> 1;
