@@ -233,6 +233,11 @@ hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float
                         _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair, int rs_splits) {
     if (m == 0 || (!xh && !xl && !xs)) return hipSuccess;
     if (k % 32 || k > INT32_MAX || (pair && (!xh || xl != xh + m * k))) return hipErrorInvalidValue;
+    if (x_dtype != ARFQ_F32 && !xh && !xl && !rs) {  // the sums of an f16 x alone
+        xsums_kernel<XSUM_WAVES><<<(unsigned)((m + XSUM_WAVES - 1) / XSUM_WAVES), 64 * XSUM_WAVES, 0, s>>>(
+            (const _Float16 *)x, m, (int)k, xs);
+        return hipGetLastError();
+    }
     // segments: with rs, the skinny kernel's K ranges (whole 256-element
     // blocks) or the whole row; otherwise up to XPREP_THREADS * XPREP_NJ * 8
     // elements

@@ -713,6 +713,50 @@ __device__ __forceinline__ void xprep_load8(const TIn *__restrict__ p, float v[8
         for (int i = 0; i < 8; i++) v[i] = (float)a[i];
     }
 }
+// The sub-block sums alone, for an f16 x (no copy, split or scale): one wave
+// per row, lane l taking the 32-element sub-blocks l, l + 64, ... with the
+// loads of four sub-blocks in flight at once.  Each sum is the one
+// xprep_kernel forms for the same input, in the same order: the four 8-element
+// runs each summed left to right, then (r0 + r1) + (r2 + r3).
+constexpr int XSUM_WAVES = 4;
+template <int NW>  // rows (waves) per workgroup
+__global__ __launch_bounds__(64 * NW) void xsums_kernel(const _Float16 *__restrict__ x, int64_t M, int K,
+                                                       uint16_t *__restrict__ xs) {
+    const int64_t row = (int64_t)blockIdx.x * NW + (threadIdx.x >> 6);
+    if (row >= M) return;  // whole waves
+    const int lane = threadIdx.x & 63, nsb = K / 32;
+    const half8 *src = reinterpret_cast<const half8 *>(x + row * K);
+    uint16_t *dst = xs + row * (K / 16);
+    for (int s0 = 0; s0 < nsb; s0 += 64 * 4) {
+        half8 v[4][4];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int sb = min(s0 + lane + 64 * q, nsb - 1);  // past the end: a re-read, not stored
+#pragma unroll
+            for (int c = 0; c < 4; c++) v[q][c] = src[4 * sb + c];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const int sb = s0 + lane + 64 * q;
+            float r[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                float t = 0.f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) t += (float)v[q][c][i];
+                r[c] = t;
+            }
+            const float sum = (r[0] + r[1]) + (r[2] + r[3]);
+            if (sb < nsb) {
+                const uint32_t hi = bf16_bits(sum);
+                uint16_t *d = dst + (sb >> 3) * 16 + (sb & 7);
+                d[0] = (uint16_t)hi;
+                d[8] = (uint16_t)bf16_bits(sum - bf16_to_f32(hi));
+            }
+        }
+    }
+}
+
 template <typename TIn>
 __global__ __launch_bounds__(XPREP_THREADS) void xprep_kernel(
     const TIn *__restrict__ x, int64_t M, int K, _Float16 *__restrict__ xh, _Float16 *__restrict__ xl,
