@@ -719,11 +719,9 @@ __device__ __forceinline__ void xprep_load8(const TIn *__restrict__ p, float v[8
 // xprep_kernel forms for the same input, in the same order: the four 8-element
 // runs each summed left to right, then (r0 + r1) + (r2 + r3).
 constexpr int XSUM_WAVES = 4;
-template <int NW>  // rows (waves) per workgroup
-__global__ __launch_bounds__(64 * NW) void xsums_kernel(const _Float16 *__restrict__ x, int64_t M, int K,
-                                                       uint16_t *__restrict__ xs) {
-    const int64_t row = (int64_t)blockIdx.x * NW + (threadIdx.x >> 6);
-    if (row >= M) return;  // whole waves
+// One wave: the sums of row `row` (row < M) into xs.
+__device__ __forceinline__ void xsums_row(const _Float16 *__restrict__ x, int K, uint16_t *__restrict__ xs,
+                                          int64_t row) {
     const int lane = threadIdx.x & 63, nsb = K / 32;
     const half8 *src = reinterpret_cast<const half8 *>(x + row * K);
     uint16_t *dst = xs + row * (K / 16);
@@ -755,6 +753,13 @@ __global__ __launch_bounds__(64 * NW) void xsums_kernel(const _Float16 *__restri
             }
         }
     }
+}
+template <int NW>  // rows (waves) per workgroup
+__global__ __launch_bounds__(64 * NW) void xsums_kernel(const _Float16 *__restrict__ x, int64_t M, int K,
+                                                       uint16_t *__restrict__ xs) {
+    const int64_t row = (int64_t)blockIdx.x * NW + (threadIdx.x >> 6);
+    if (row >= M) return;  // whole waves
+    xsums_row(x, K, xs, row);
 }
 
 template <typename TIn>

@@ -507,15 +507,20 @@ static int moe_enqueue(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight
     uint16_t *xs = gsums ? (uint16_t *)(sc + o_xs) : nullptr;
     // an f32 x is stored row-scaled into f16 range; gate|up multiply back
     float *xrs = x_dtype == ARFQ_F32 ? (float *)(sc + o_xrs) : nullptr;
-    e = arfq::launch_xprep(x, x_dtype, tokens, hidden,
-                           x_dtype == ARFQ_F32 ? (_Float16 *)(sc + o_x) : nullptr, nullptr, xs, xrs,
-                           ctx->stream);
-    if (e != hipSuccess) return hip_fail(ctx, e, "moe: x preparation launch");
+    // an f16 x needing only its sums gets them from the routing launch
+    const bool sums_in_route = !ids_in && x_dtype != ARFQ_F32 && xs;
+    if (!sums_in_route) {
+        e = arfq::launch_xprep(x, x_dtype, tokens, hidden,
+                               x_dtype == ARFQ_F32 ? (_Float16 *)(sc + o_x) : nullptr, nullptr, xs, xrs,
+                               ctx->stream);
+        if (e != hipSuccess) return hip_fail(ctx, e, "moe: x preparation launch");
+    }
     const int32_t *ids = ids_in;
     const float *wts = wts_in;
     if (!ids_in) {
-        e = arfq::launch_moe_route(logits, tokens, E, top_k, norm_topk ? 1 : 0,
-                                   (int32_t *)(sc + o_ids), (float *)(sc + o_w), ctx->stream);
+        e = arfq::launch_moe_route(logits, tokens, E, top_k, norm_topk ? 1 : 0, (int32_t *)(sc + o_ids),
+                                   (float *)(sc + o_w), ctx->stream, sums_in_route ? xh : nullptr, hidden,
+                                   sums_in_route ? xs : nullptr);
         if (e != hipSuccess) return hip_fail(ctx, e, "moe: route launch");
         ids = (const int32_t *)(sc + o_ids);
         wts = (const float *)(sc + o_w);

@@ -141,8 +141,11 @@ hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float
 
 // ---- arfq_moe.hip ----
 // Routing: ids/weights [tokens, top_k] from logits [tokens, E] (E <= 1024, top_k <= 64).
+// With xs, the same launch also writes the bf16 sub-block sums of the f16 x
+// [tokens, k] (what launch_xprep writes for an f16 x and xs alone).
 hipError_t launch_moe_route(const float *logits, int64_t tokens, int E, int top_k, int norm,
-                            int32_t *ids, float *wts, hipStream_t s);
+                            int32_t *ids, float *wts, hipStream_t s, const _Float16 *x = nullptr,
+                            int64_t k = 0, uint16_t *xs = nullptr);
 // Grouping of P = tokens * top_k pairs by expert (E <= MOE_MAX_EXPERTS): off[E + 1],
 // sorted[P] (pair indices), tiles[moe_max_tiles] (int2 expert, first row), *ntiles.
 hipError_t launch_moe_group(const int32_t *ids, int64_t P, int E, int32_t *off, int32_t *sorted,

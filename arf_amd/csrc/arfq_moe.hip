@@ -57,12 +57,22 @@ __device__ __forceinline__ int route_wave_min(int v) {
     return route_wave_reduce(v, [](int a, int b) { return min(a, b); });
 }
 
+// The workgroups past the routing ones (blockIdx.x >= rblocks) form the x
+// sub-block sums of an f16 x [tokens, K] for the grouped GEMMs instead (no
+// dependence between the two, so one launch serves both).
 template <int PL>
 __global__ __launch_bounds__(256) void moe_route_kernel(const float *__restrict__ logits,
                                                         int64_t tokens, int E, int top_k,
                                                         int norm, int32_t *__restrict__ ids,
-                                                        float *__restrict__ wts) {
+                                                        float *__restrict__ wts, int rblocks,
+                                                        const _Float16 *__restrict__ x, int K,
+                                                        uint16_t *__restrict__ xs) {
     const int lane = threadIdx.x & 63;
+    if ((int)blockIdx.x >= rblocks) {  // uniform over the workgroup
+        const int64_t row = (int64_t)(blockIdx.x - rblocks) * 4 + (threadIdx.x >> 6);
+        if (row < tokens) xsums_row(x, K, xs, row);
+        return;
+    }
     const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (t >= tokens) return;  // whole waves: every lane of a running wave is active
     const float *lg = logits + t * E;
@@ -464,17 +474,21 @@ hipError_t launch_glu(const float *g, const float *u, float *h, int64_t n, int a
 // ---- launchers -----------------------------------------------------------------
 
 hipError_t launch_moe_route(const float *logits, int64_t tokens, int E, int top_k, int norm,
-                            int32_t *ids, float *wts, hipStream_t s) {
+                            int32_t *ids, float *wts, hipStream_t s, const _Float16 *x, int64_t k,
+                            uint16_t *xs) {
     if (tokens == 0) return hipSuccess;
-    const unsigned grid = (unsigned)((tokens + 3) / 4);
+    if (xs && (k % 32 || k > INT32_MAX)) return hipErrorInvalidValue;
+    const unsigned rb = (unsigned)((tokens + 3) / 4);
+    const unsigned grid = xs ? 2 * rb : rb;
     if (E <= 64)
-        moe_route_kernel<1><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
+        moe_route_kernel<1><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts, rb, x, (int)k, xs);
     else if (E <= 128)
-        moe_route_kernel<2><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
+        moe_route_kernel<2><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts, rb, x, (int)k, xs);
     else if (E <= 256)
-        moe_route_kernel<4><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
+        moe_route_kernel<4><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts, rb, x, (int)k, xs);
     else
-        moe_route_kernel<MOE_ROUTE_PL><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts);
+        moe_route_kernel<MOE_ROUTE_PL><<<grid, 256, 0, s>>>(logits, tokens, E, top_k, norm, ids, wts, rb, x,
+                                                            (int)k, xs);
     return hipGetLastError();
 }
 
