@@ -277,6 +277,22 @@ bool gemm_supports(const arfq_weight *w, int64_t m) {
     }
 }
 
+// weight bytes per 256-element block of the direct-operand formats' largest
+// stream (0: no such kernel); the buffer loads take 32-bit offsets
+static int64_t bd_stream_bytes(int qtype) {
+    switch (qtype) {
+    case ARFQ_Q4_K:
+    case ARFQ_IQ4_XS:
+        return 128;
+    case ARFQ_Q6_K:
+        return 192;
+    case ARFQ_Q8_0:
+        return 256;
+    default:
+        return 0;
+    }
+}
+
 static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
@@ -298,9 +314,12 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     // lo rows fill the other half of the 32-row x tile staged anyway (no extra
     // MFMAs), at m <= 32 a second tile (twice the MFMAs)
     p.pair = p.skinny && x_dtype == ARFQ_F32 && m <= 32;
-    // Q4_K prefill: the direct-operand kernel (one launch, no split-K)
-    p.bd = !p.skinny && w->qtype == ARFQ_Q4_K && m > 64 &&
-           w->n * (w->k / 2) < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
+    // prefill: the direct-operand kernel (one launch, no split-K) for Q4_K,
+    // Q6_K and Q8_0, and for IQ4_XS at f16 x (an f32 x keeps its hi + lo
+    // split in the tile loop, since these weights are rounded to f16)
+    const int64_t bdb = bd_stream_bytes(w->qtype);
+    p.bd = !p.skinny && m > 64 && bdb && w->k % 256 == 0 && !(w->qtype == ARFQ_IQ4_XS && x_dtype == ARFQ_F32) &&
+           w->n * (w->k / 256) * bdb < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
     // the exact Q4_K paths read x sub-block sums (min term)
     p.sums = (p.skinny || p.bd) && kind2;
     int64_t S;
@@ -445,27 +464,47 @@ FmtQ80 fmt_q80(const arfq_weight *w) {
     return {(const uint4 *)w->s0, (const uint16_t *)w->s1, (int)(w->k / 32)};
 }
 
-// Q4_K prefill: weights straight into the MFMA operands (arfq_gemm_bd.h)
-static hipError_t launch_bd_q4k(const arfq_weight *w, int e, int64_t m, const _Float16 *x,
-                                const uint16_t *xs, const float *rs, float *y, float *part,
-                                const GemmPlan &p, hipStream_t s) {
-    const int64_t nblk = w->k / 256;
-    const int64_t eb = (int64_t)e * w->n * nblk;
+// Prefill: weights straight into the MFMA operands (arfq_gemm_bd.h)
+template <class F>
+static hipError_t launch_bd_t(const F &f, const arfq_weight *w, int64_t m, const _Float16 *x,
+                              const uint16_t *xs, const float *rs, float *y, float *part,
+                              const GemmPlan &p, hipStream_t s) {
     const int mt = (int)((m + BD_BM - 1) / BD_BM), nt = (int)((w->n + BD_BN - 1) / BD_BN);
     const int tiles = mt * nt, nsplit = tiles - p.bd_full;
     const int xcd = (mt % 8 == 0 && p.bd_full % mt == 0) ? 1 : 0;
     if (nsplit && !part) return hipErrorInvalidValue;
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
-    if (hipError_t err = set_max_lds_once((const void *)gemm_bd_q4k, bd_lds(), lds_set)) return err;
+    if (hipError_t err = set_max_lds_once((const void *)gemm_bd<F>, bd_lds(), lds_set)) return err;
     const unsigned items = (unsigned)(p.bd_full + nsplit * p.bd_chunks);
-    gemm_bd_q4k<<<items, BD_THREADS, bd_lds(), s>>>(
-        (const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8, x, xs, rs, y, part, (int)m,
-        (int)w->n, (int)w->k, mt, xcd, p.bd_full, p.bd_chunks);
+    gemm_bd<F><<<items, BD_THREADS, bd_lds(), s>>>(f, x, xs, rs, y, part, (int)m, (int)w->n, (int)w->k, mt, xcd,
+                                                   p.bd_full, p.bd_chunks);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !nsplit) return err;
     bd_reduce_kernel<<<dim3(BD_BM * BD_BN / 1024, (unsigned)nsplit), 256, 0, s>>>(
         part, rs, y, (int)m, (int)w->n, mt, p.bd_full, p.bd_chunks);
     return hipGetLastError();
+}
+
+static hipError_t launch_bd(const arfq_weight *w, int e, int64_t m, const _Float16 *x, const uint16_t *xs,
+                            const float *rs, float *y, float *part, const GemmPlan &p, hipStream_t s) {
+    const int64_t eb = (int64_t)e * w->n * (w->k / 256);
+    switch (w->qtype) {
+    case ARFQ_Q4_K:
+        return launch_bd_t(BdQ4K{(const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8}, w, m, x, xs, rs, y,
+                           part, p, s);
+    case ARFQ_IQ4_XS:
+        return launch_bd_t(BdIQ4XS{(const uint2 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8}, w, m, x, xs, rs,
+                           y, part, p, s);
+    case ARFQ_Q6_K:
+        return launch_bd_t(BdQ6K{(const uint2 *)w->s0 + eb * 24, (const uint4 *)w->s1 + eb,
+                                 (const uint16_t *)w->s2 + eb},
+                           w, m, x, xs, rs, y, part, p, s);
+    case ARFQ_Q8_0:
+        return launch_bd_t(BdQ80{(const uint4 *)w->s0 + eb * 16, (const uint16_t *)w->s1 + eb * 8}, w, m, x, xs,
+                           rs, y, part, p, s);
+    default:
+        return hipErrorInvalidValue;
+    }
 }
 
 hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
@@ -507,12 +546,10 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         default:
             return hipErrorInvalidValue;
         }
+    } else if (p.bd) {
+        return launch_bd(w, e, m, xh, xs, rs, y, (float *)(sc + p.off_part), p, s);
     } else switch (w->qtype) {
     case ARFQ_Q4_K: {
-        if (p.bd) {
-            err = launch_bd_q4k(w, e, m, xh, xs, rs, out, (float *)(sc + p.off_part), p, s);
-            break;
-        }
         const FmtQ4KR f{fmt_q4k(w).shifted((int64_t)e * w->n * (w->k / 256))};
         err = launch_fmt(f, w, m, xh, xl, xs, p.splits == 1 ? rs : nullptr, out, p, s);
         break;

@@ -117,15 +117,299 @@ __device__ __forceinline__ void bd_mins(const u32x4 hd, float inv_su, int h, bf1
     lo = __builtin_bit_cast(bf16x8, u32x4{l0[0], l1[0], l0[1], l1[1]});
 }
 
+// ---- formats ------------------------------------------------------------------
+// A direct-operand format gives, per lane, the codes of one step (its weight
+// row's 32 elements of that step, loaded straight into registers) and, per
+// block, the row's header; from those it builds the step's B operands in units
+// of the block scale su (UNITS: su = the block's d, so the accumulators are
+// moved into each block's unit; otherwise su = 1 and the operands carry their
+// whole scale).  MIN: the Q4_K min term (x sub-block sums).  VPM: VALU slots
+// per MFMA in the pinned schedule (about a quarter of one operand's build).
+// a_off(p, kk, h): the block elements a lane's 8 k-slots of MFMA group kk of
+// step p hold (the x tile is read with the same map).
+// Buffer loads: per-lane 32-bit offsets fixed for the work item plus a
+// uniform (SGPR) offset per block and step; the launcher keeps every stream
+// below 2 GiB.
+
+// Q4_K (exact): step p, lane half h = sub-block 2p + h; group kk = code dword
+// kk (elements 8kk .. 8kk + 7, sigma nibble order).  Operands sc_j * q.
+struct BdQ4K {
+    static constexpr bool UNITS = true, MIN = true, STEP_KK = false;
+    static constexpr int VPM = 3;
+    using Code = u32x4;
+    using Head = u32x4;
+    using Blk = uint32_t;  // sc of sub-blocks 2p + h, byte p
+    using Step = BdScale;
+    const uint4 *hdr, *qs;
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    struct Lanes {
+        __amdgpu_buffer_rsrc_t q, hd;
+        uint32_t qv[2], hv[2];
+        __device__ Code code(int g, int st) const {
+            return __builtin_amdgcn_raw_buffer_load_b128(q, qv[g], (st >> 2) * 128 + 32 * (st & 3), 0);
+        }
+        __device__ Head head(int g, int blk) const {
+            return __builtin_amdgcn_raw_buffer_load_b128(hd, hv[g], blk * 16, 0);
+        }
+    };
+    __device__ Lanes lanes(int n, int nblk, uint32_t wr0, uint32_t wr1, int h) const {
+        Lanes l;
+        l.q = __builtin_amdgcn_make_buffer_rsrc((void *)qs, (short)0, (int)((uint32_t)n * nblk * 128), 0x00020000);
+        l.hd = __builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)((uint32_t)n * nblk * 16), 0x00020000);
+        l.qv[0] = wr0 * nblk * 128 + 16 * h;
+        l.qv[1] = wr1 * nblk * 128 + 16 * h;
+        l.hv[0] = wr0 * nblk * 16;
+        l.hv[1] = wr1 * nblk * 16;
+        return l;
+    }
+    __device__ static float unit(const Head &hd) { return h2f(hd.x); }
+    __device__ static Blk block(const Head &hd, int h) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            uint32_t sc, mm;
+            q4k_scale_min(hd.y, hd.z, hd.w, 2 * p + h, sc, mm);
+            packed |= sc << (8 * p);
+        }
+        return packed;
+    }
+    __device__ static Blk dead() { return 0u; }
+    __device__ static Step step(Blk b, int p, int) { return bd_scale((b >> (8 * p)) & 0xffu); }
+    __device__ static half8 deq(const Code &c, const Step &k, int kk) {
+        return bd_dequant(kk == 0 ? c.x : kk == 1 ? c.y : kk == 2 ? c.z : c.w, k);
+    }
+};
+
+// IQ4_XS (weights rounded to f16): step p, lane half h = sub-block 2p + h,
+// whose 16 code bytes hold elements 0..15 in the low nibbles and 16..31 in the
+// high ones; group kk = elements 8kk .. 8kk + 7 (nibble kk / 2 of bytes
+// 8 (kk % 2) .. + 7).  Operands (ls - 32) * kv in units of d, rounded once to
+// f16 (exact while |(ls - 32) kv| <= 2048); kv from the codebook with two
+// v_perm.  (dequant_iq4_xs, crates/arf-core/src/model/gguf.rs:1937-1976)
+struct BdIQ4XS {
+    static constexpr bool UNITS = true, MIN = false, STEP_KK = false;
+    static constexpr int VPM = 6;
+    using Code = u32x4;
+    using Head = u32x2;    // d | scales_h << 16, scales_l
+    using Blk = uint32_t;  // ls - 32 of sub-blocks 2p + h as int8, byte p
+    struct Step {
+        half2v s, c;
+    };
+    const uint2 *hdr;
+    const uint4 *qs;
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    struct Lanes {
+        __amdgpu_buffer_rsrc_t q, hd;
+        uint32_t qv[2], hv[2];
+        __device__ Code code(int g, int st) const {
+            return __builtin_amdgcn_raw_buffer_load_b128(q, qv[g], (st >> 2) * 128 + 32 * (st & 3), 0);
+        }
+        __device__ Head head(int g, int blk) const {
+            return __builtin_amdgcn_raw_buffer_load_b64(hd, hv[g], blk * 8, 0);
+        }
+    };
+    __device__ Lanes lanes(int n, int nblk, uint32_t wr0, uint32_t wr1, int h) const {
+        Lanes l;
+        l.q = __builtin_amdgcn_make_buffer_rsrc((void *)qs, (short)0, (int)((uint32_t)n * nblk * 128), 0x00020000);
+        l.hd = __builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)((uint32_t)n * nblk * 8), 0x00020000);
+        l.qv[0] = wr0 * nblk * 128 + 16 * h;
+        l.qv[1] = wr1 * nblk * 128 + 16 * h;
+        l.hv[0] = wr0 * nblk * 8;
+        l.hv[1] = wr1 * nblk * 8;
+        return l;
+    }
+    __device__ static float unit(const Head &hd) { return h2f(hd.x); }
+    __device__ static Blk block(const Head &hd, int h) {
+        uint32_t packed = 0;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const int s = 2 * p + h;
+            const uint32_t ls = ((hd.y >> (4 * s)) & 0xFu) | (((hd.x >> (16 + 2 * s)) & 3u) << 4);
+            packed |= ((ls - 32u) & 0xffu) << (8 * p);
+        }
+        return packed;
+    }
+    __device__ static Blk dead() { return 0u; }
+    __device__ static Step step(Blk b, int p, int) {
+        const half2v s = h2splat((float)(int8_t)(b >> (8 * p)));
+        return {s, s * (half2v){-1152.f, -1152.f}};  // 1152 |ls - 32| <= 36864: exact
+    }
+    __device__ static half8 deq(const Code &c, const Step &k, int kk) {
+        // kvalues_iq4nl + 128 as bytes: entries 0..7 and 8..15, little-endian
+        constexpr uint32_t T0lo = 0xBFAD9881u ^ 0x80808080u, T0hi = 0xF6EADDCFu ^ 0x80808080u;
+        constexpr uint32_t T1lo = 0x26190D01u ^ 0x80808080u, T1hi = 0x71594535u ^ 0x80808080u;
+        const uint32_t w[2] = {(kk & 1) ? c.z : c.x, (kk & 1) ? c.w : c.y};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t sel = (kk >> 1) ? (w[j] >> 4) & 0x0F0F0F0Fu : w[j] & 0x0F0F0F0Fu;
+            const uint32_t s7 = sel & 0x07070707u;
+            const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
+            const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
+            const uint32_t hi = (sel >> 3) & 0x01010101u;
+            const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
+            const uint32_t v = (v1 & mask) | (v0 & ~mask);
+            // (1024 + kv + 128) * s - 1152 s = s * kv, one rounding
+            o[2 * j] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), k.s, k.c);
+            o[2 * j + 1] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u), k.s, k.c);
+        }
+        return bd_h8(o[0], o[1], o[2], o[3]);
+    }
+};
+
+// Q8_0 (weights d * q rounded to f16, true units): step p of block b, lane
+// half h = Q8_0 block 8b + 2p + h (its 32 codes, 32 bytes); group kk =
+// elements 8kk .. 8kk + 7.  The header is the 8 block scales d of the 256
+// elements.  (dequant_q8_0, crates/arf-core/src/model/gguf.rs)
+struct BdQ80 {
+    static constexpr bool UNITS = false, MIN = false, STEP_KK = false;
+    static constexpr int VPM = 4;
+    struct Code {
+        u32x4 a, b;
+    };
+    using Head = u32x4;  // d of the 8 Q8_0 blocks
+    using Blk = u32x2;   // this lane's d of blocks 2p + h: half p % 2 of dword p / 2
+    using Step = half2v;
+    const uint4 *qs;
+    const uint16_t *dd;
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    struct Lanes {
+        __amdgpu_buffer_rsrc_t q, hd;
+        uint32_t qv[2], hv[2];
+        __device__ Code code(int g, int st) const {
+            const int so = (st >> 2) * 256 + 64 * (st & 3);
+            return {__builtin_amdgcn_raw_buffer_load_b128(q, qv[g], so, 0),
+                    __builtin_amdgcn_raw_buffer_load_b128(q, qv[g] + 16, so, 0)};
+        }
+        __device__ Head head(int g, int blk) const {
+            return __builtin_amdgcn_raw_buffer_load_b128(hd, hv[g], blk * 16, 0);
+        }
+    };
+    __device__ Lanes lanes(int n, int nblk, uint32_t wr0, uint32_t wr1, int h) const {
+        Lanes l;
+        l.q = __builtin_amdgcn_make_buffer_rsrc((void *)qs, (short)0, (int)((uint32_t)n * nblk * 256), 0x00020000);
+        l.hd = __builtin_amdgcn_make_buffer_rsrc((void *)dd, (short)0, (int)((uint32_t)n * nblk * 16), 0x00020000);
+        l.qv[0] = wr0 * nblk * 256 + 32 * h;
+        l.qv[1] = wr1 * nblk * 256 + 32 * h;
+        l.hv[0] = wr0 * nblk * 16;
+        l.hv[1] = wr1 * nblk * 16;
+        return l;
+    }
+    __device__ static float unit(const Head &) { return 1.f; }
+    __device__ static Blk block(const Head &hd, int h) {
+        const uint32_t sel = h ? 0x07060302u : 0x05040100u;
+        return {__builtin_amdgcn_perm(hd.y, hd.x, sel), __builtin_amdgcn_perm(hd.w, hd.z, sel)};
+    }
+    __device__ static Blk dead() { return {0u, 0u}; }
+    __device__ static Step step(const Blk &b, int p, int) {
+        return as_h2(__builtin_amdgcn_perm(0u, (p >> 1) ? b.y : b.x, (p & 1) ? 0x03020302u : 0x01000100u));
+    }
+    __device__ static half8 deq(const Code &c, const Step &d, int kk) {
+        const uint32_t w[2] = {kk == 0 ? c.a.x : kk == 1 ? c.a.z : kk == 2 ? c.b.x : c.b.z,
+                               kk == 0 ? c.a.y : kk == 1 ? c.a.w : kk == 2 ? c.b.y : c.b.w};
+        const half2v m1152 = {-1152.f, -1152.f};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const uint32_t u = w[j] ^ 0x80808080u;  // q + 128 per byte
+            // (1024 + q + 128) - 1152 = q exactly, then one rounding of d * q
+            o[2 * j] = as_u((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + m1152) * d);
+            o[2 * j + 1] = as_u((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + m1152) * d);
+        }
+        return bd_h8(o[0], o[1], o[2], o[3]);
+    }
+};
+
+// Q6_K (weights rounded to f16): step p = 48-byte chunk p of the block
+// (ql_a[16] | ql_b[16] | qh[16]); lane half h takes bytes 8h .. 8h + 7 of
+// each; group kk = quadrant kk: elements 128 (p / 2) + 16 (p % 2) + 32 kk +
+// 8h + 0..7, one 16-element sub-block.  Operands sc * (q - 32) in units of d,
+// rounded once to f16 (exact while |sc| <= 64).
+// (dequant_q6_k, crates/arf-core/src/model/gguf.rs:2092-2131)
+struct BdQ6K {
+    static constexpr bool UNITS = true, MIN = false, STEP_KK = true;
+    static constexpr int VPM = 7;
+    struct Code {
+        u32x2 a, b, qh;
+    };
+    struct Head {
+        u32x4 sc;
+        uint32_t d;
+    };
+    using Blk = u32x4;  // the 16 int8 sub-block scales
+    using Step = half2v;
+    const uint2 *qb8;
+    const uint4 *sc16;
+    const uint16_t *dd;
+    __device__ static int a_off(int p, int kk, int h) { return 128 * (p >> 1) + 16 * (p & 1) + 32 * kk + 8 * h; }
+    struct Lanes {
+        __amdgpu_buffer_rsrc_t q, s, d;
+        uint32_t qv[2], sv[2], dv[2];
+        __device__ Code code(int g, int st) const {
+            const int so = (st >> 2) * 192 + 48 * (st & 3);
+            return {__builtin_amdgcn_raw_buffer_load_b64(q, qv[g], so, 0),
+                    __builtin_amdgcn_raw_buffer_load_b64(q, qv[g] + 16, so, 0),
+                    __builtin_amdgcn_raw_buffer_load_b64(q, qv[g] + 32, so, 0)};
+        }
+        __device__ Head head(int g, int blk) const {
+            return {__builtin_amdgcn_raw_buffer_load_b128(s, sv[g], blk * 16, 0),
+                    (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(d, dv[g], blk * 2, 0)};
+        }
+    };
+    __device__ Lanes lanes(int n, int nblk, uint32_t wr0, uint32_t wr1, int h) const {
+        Lanes l;
+        l.q = __builtin_amdgcn_make_buffer_rsrc((void *)qb8, (short)0, (int)((uint32_t)n * nblk * 192), 0x00020000);
+        l.s = __builtin_amdgcn_make_buffer_rsrc((void *)sc16, (short)0, (int)((uint32_t)n * nblk * 16), 0x00020000);
+        l.d = __builtin_amdgcn_make_buffer_rsrc((void *)dd, (short)0, (int)((uint32_t)n * nblk * 2), 0x00020000);
+        l.qv[0] = wr0 * nblk * 192 + 8 * h;
+        l.qv[1] = wr1 * nblk * 192 + 8 * h;
+        l.sv[0] = wr0 * nblk * 16;
+        l.sv[1] = wr1 * nblk * 16;
+        l.dv[0] = wr0 * nblk * 2;
+        l.dv[1] = wr1 * nblk * 2;
+        return l;
+    }
+    __device__ static float unit(const Head &hd) { return h2f(hd.d); }
+    __device__ static Blk block(const Head &hd, int) { return hd.sc; }
+    __device__ static Blk dead() { return {0u, 0u, 0u, 0u}; }
+    __device__ static Step step(const Blk &b, int p, int kk) {
+        const int si = 8 * (p >> 1) + (p & 1) + 2 * kk;
+        const uint32_t w = (si >> 2) == 0 ? b.x : (si >> 2) == 1 ? b.y : (si >> 2) == 2 ? b.z : b.w;
+        return h2splat((float)(int8_t)(w >> (8 * (si & 3))));
+    }
+    // q as the f16 1024 + q (v_perm puts 0x64 above each code byte; the two
+    // qh bits go to bits 4-5), minus 1056 (exact), times sc (one rounding)
+    __device__ static half8 deq(const Code &c, const Step &sc, int kk) {
+        const half2v m1056 = {-1056.f, -1056.f};
+        const u32x2 ql = (kk & 1) ? c.b : c.a;
+        uint32_t o[4];
+#pragma unroll
+        for (int hh = 0; hh < 2; hh++) {
+            const uint32_t l = (kk & 2) ? ((hh ? ql.y : ql.x) >> 4) : (hh ? ql.y : ql.x);
+            const uint32_t qw = hh ? c.qh.y : c.qh.x;
+#pragma unroll
+            for (int pr = 0; pr < 2; pr++) {
+                const uint32_t lp = __builtin_amdgcn_perm(0x64646464u, l, pr ? 0x04030402u : 0x04010400u);
+                const uint32_t hp = __builtin_amdgcn_perm(0u, qw, pr ? 0x0c030c02u : 0x0c010c00u);
+                const uint32_t top = 2 * kk <= 4 ? (hp << (4 - 2 * kk)) : (hp >> (2 * kk - 4));
+                const uint32_t q = (lp & 0x640F640Fu) | (top & 0x00300030u);
+                o[2 * hh + pr] = as_u((as_h2(q) + m1056) * sc);
+            }
+        }
+        return bd_h8(o[0], o[1], o[2], o[3]);
+    }
+};
+
 // Work items: the first `full` items are whole tiles (in XCD order when
 // xcd_order); the remaining tiles are each split into `chunks` K ranges of
 // whole blocks, one item per range, whose partial tiles go to part[item -
 // full][BD_BM][BD_BN] and are added in chunk order by bd_reduce_kernel.  This
 // fills the last round of workgroups when the tiles do not divide the CUs.
-__global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
-    const uint4 *__restrict__ hdr, const uint4 *__restrict__ qs, const _Float16 *__restrict__ x,
-    const uint16_t *__restrict__ xs, const float *__restrict__ rs, float *__restrict__ y,
-    float *__restrict__ part, int m, int n, int k, int mt, int xcd_order, int full, int chunks) {
+template <class F>
+__global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
+    F fmt, const _Float16 *__restrict__ x, const uint16_t *__restrict__ xs, const float *__restrict__ rs,
+    float *__restrict__ y, float *__restrict__ part, int m, int n, int k, int mt, int xcd_order, int full,
+    int chunks) {
     extern __shared__ __attribute__((aligned(16))) _Float16 sx[];  // [2][BD_BM][BD_LD]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nblk = k / 256;
@@ -155,13 +439,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
 
     const int col = lane & 31, h = lane >> 5;
     const uint32_t wr0 = min(n0 + col, n - 1), wr1 = min(n0 + 32 + col, n - 1);
-    // buffer loads: a per-lane 32-bit offset fixed for the whole item plus a
-    // uniform (SGPR) offset per block and step, so no per-load address math
-    // (the launcher keeps every stream below 2 GiB)
-    const __amdgpu_buffer_rsrc_t qrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)qs, (short)0, (int)((uint32_t)n * nblk * 128), 0x00020000);
-    const __amdgpu_buffer_rsrc_t hrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)hdr, (short)0, (int)((uint32_t)n * nblk * 16), 0x00020000);
+    const typename F::Lanes ld = fmt.lanes(n, nblk, wr0, wr1, h);
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
         (void *)x, (short)0, (int)((uint32_t)m * k * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
@@ -181,13 +459,17 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
         xa[2] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 128, so, 0);  // + 64 halves
         xa[3] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 144, so, 0);
     };
-    // x sub-block sums of the next block: thread t moves 4 of row t / 4's 16
+    // x sub-block sums of the next block (min term): thread t moves 4 of row
+    // t / 4's 16
     const uint32_t sv = (uint32_t)min(m0 + xr, m - 1) * (k / 16) * 2 + (tid & 3) * 8;  // bytes
     uint16_t *sxs = reinterpret_cast<uint16_t *>(sx + 2 * BD_BM * BD_LD);  // [2][BD_BM][16]
     u32x2 xsa;
-    auto xsload = [&](int blk) { xsa = __builtin_amdgcn_raw_buffer_load_b64(srs, sv, blk * 32, 0); };
+    auto xsload = [&](int blk) {
+        if constexpr (F::MIN) xsa = __builtin_amdgcn_raw_buffer_load_b64(srs, sv, blk * 32, 0);
+    };
     auto xsstore = [&](int buf) {
-        *reinterpret_cast<u32x2 *>(sxs + ((size_t)buf * BD_BM + xr) * 16 + (tid & 3) * 4) = xsa;
+        if constexpr (F::MIN)
+            *reinterpret_cast<u32x2 *>(sxs + ((size_t)buf * BD_BM + xr) * 16 + (tid & 3) * 4) = xsa;
     };
     auto xstore = [&](int buf, int half) {
         u32x4 *dst = reinterpret_cast<u32x4 *>(sx + ((size_t)buf * BD_BM + xr) * BD_LD + 128 * half + xo);
@@ -197,25 +479,20 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
         dst[9] = xa[3];
     };
 
-    const uint32_t qv0 = wr0 * nblk * 128 + 16 * h, qv1 = wr1 * nblk * 128 + 16 * h;
-    const uint32_t hv0 = wr0 * nblk * 16, hv1 = wr1 * nblk * 16;
-    // code ring: slot s % 2 holds step s (the two groups' 16-byte sub-block
-    // loads); it is refilled with step s + 2 as soon as its last dword is
-    // dequantized
-    u32x4 cq[2][2];
+    // code ring: slot s % 2 holds step s (both groups' codes); it is refilled
+    // with step s + 2 as soon as its last operand is built
+    typename F::Code cq[2][2];
     auto cload = [&](int u, int st) {
         st = min(st, st1 - 1);  // past the end: reload the last step (unused)
-        const int blk = st >> 2;
-        const int so = blk * 128 + 32 * (st & 3);  // + 16 h in the lane offsets
-        cq[u][0] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qv0, so, 0);
-        cq[u][1] = __builtin_amdgcn_raw_buffer_load_b128(qrs, qv1, so, 0);
+        cq[u][0] = ld.code(0, st);
+        cq[u][1] = ld.code(1, st);
     };
     // block headers of the two rows, one block ahead
-    u32x4 hdn[2];
+    typename F::Head hdn[2];
     auto hload = [&](int blk) {
         blk = min(blk, kb1 - 1);
-        hdn[0] = __builtin_amdgcn_raw_buffer_load_b128(hrs, hv0, blk * 16, 0);
-        hdn[1] = __builtin_amdgcn_raw_buffer_load_b128(hrs, hv1, blk * 16, 0);
+        hdn[0] = ld.head(0, blk);
+        hdn[1] = ld.head(1, blk);
     };
 
     floatx16 acc[4][2];
@@ -239,29 +516,22 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
     for (int u = 0; u < 2; u++) cload(u, st0 + u);
     bd_barrier();
 
-    // block scale state of the current block: scd (integer scales of the
-    // sub-blocks 2p + h, byte p), inv = 1 / su and ratio = su_prev / su, the
-    // factor that moves the accumulators into this block's unit su (= d, or 1
-    // when d = 0); hdc holds the block's headers for the min term
-    uint32_t scd[2];
+    // block scale state of the current block: scd (the step scales), inv =
+    // 1 / su and ratio = su_prev / su, the factor that moves the accumulators
+    // into this block's unit su (= d, or 1 when d = 0: zero weights); hdc
+    // holds the block's headers for the min term
+    typename F::Blk scd[2];
     float inv[2], ratio[2], sprev[2] = {1.f, 1.f};
-    u32x4 hdc[2];
+    typename F::Head hdc[2];
     auto block_scales = [&]() {
 #pragma unroll
         for (int g = 0; g < 2; g++) {
             hdc[g] = hdn[g];
-            const u32x4 hd = hdc[g];
-            const float d = h2f(hd.x);
+            const float d = F::unit(hdc[g]);
             const bool live = d != 0.f;
             const float su = live ? d : 1.f;
-            uint32_t packed = 0;
-#pragma unroll
-            for (int p = 0; p < 4; p++) {
-                uint32_t sc, mm;
-                q4k_scale_min(hd.y, hd.z, hd.w, 2 * p + h, sc, mm);
-                packed |= sc << (8 * p);
-            }
-            scd[g] = live ? packed : 0u;
+            scd[g] = F::block(hdc[g], h);
+            if (!live) scd[g] = F::dead();
             inv[g] = __builtin_amdgcn_rcpf(su);
             ratio[g] = sprev[g] * inv[g];
             sprev[g] = su;
@@ -273,83 +543,92 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
     for (int blk = kb0; blk < kb1; blk++) {
         const int buf = (blk - kb0) & 1;
         const int nb = min(blk + 1, kb1 - 1);  // next block (past the end: unused copy)
-        const _Float16 *xt0 = sx + ((size_t)buf * BD_BM + col) * BD_LD + 32 * h;
+        const _Float16 *xt0 = sx + ((size_t)buf * BD_BM + col) * BD_LD;
 
-        // 16 MFMA groups per block: group i = (step p = i / 4, dword kk = i % 4)
-        // of 8 MFMAs, g-major.  Operand registers are refilled as soon as their
-        // last use has issued: b[1] (dequantized codes) between group i's four
-        // g = 0 MFMAs, b[0] of group i + 1 between its four g = 1 MFMAs, a[mg]
-        // (x from LDS) after MFMA (mg, g = 1).  Around them:
+        // 16 MFMA groups per block: group i = (step p = i / 4, kk = i % 4) of
+        // 8 MFMAs, g-major.  Operand registers are refilled as soon as their
+        // last use has issued: b[1] between group i's four g = 0 MFMAs, b[0] of
+        // group i + 1 between its four g = 1 MFMAs, a[mg] (x from LDS) after
+        // MFMA (mg, g = 1).  Around them:
         //  - the accumulators move into this block's unit: g = 1 here, g = 0
         //    at the end of the previous block (behind its last MFMAs);
-        //  - groups 0, 1 work out the min-term operands and group 2 adds the
-        //    min term -dmin * sum_j m_j X_j (units of d: two bf16 MFMAs per
-        //    tile against the x sub-block sums, lane half h reading the hi /
-        //    lo half of row (32 mg + l % 32)'s 16);
+        //  - min term: groups 0, 1 work out its operands and group 2 adds
+        //    -dmin * sum_j m_j X_j (units of d: two bf16 MFMAs per tile
+        //    against the x sub-block sums, lane half h reading the hi / lo
+        //    half of row (32 mg + l % 32)'s 16);
         //  - group 13 takes the next block's headers (scales, ratio; the last
         //    read of this block's scales is group 12's b[1]) and issues the
-        //    loads of the one after.
+        //    loads of the one after; with a scale per group (STEP_KK), group 15
+        //    does, after its b[1].
         half8 a[4], b[2];
-        BdScale ks[2];
+        typename F::Step ks[2];
         bf16x8 bh[2], bl[2], am[4];
         auto xread = [&](int i, int mg) {
-            a[mg] = *reinterpret_cast<const half8 *>(xt0 + (size_t)mg * 32 * BD_LD + 64 * (i >> 2) + 8 * (i & 3));
+            a[mg] = *reinterpret_cast<const half8 *>(xt0 + (size_t)mg * 32 * BD_LD + F::a_off(i >> 2, i & 3, h));
         };
         auto deq = [&](int i, int g) {
             const int p = i >> 2, kk = i & 3;
-            if (kk == 0) ks[g] = bd_scale((scd[g] >> (8 * p)) & 0xffu);
-            const uint32_t cw = kk == 0 ? cq[p & 1][g].x : kk == 1 ? cq[p & 1][g].y : kk == 2 ? cq[p & 1][g].z : cq[p & 1][g].w;
-            b[g] = bd_dequant(cw, ks[g]);
+            if (F::STEP_KK || kk == 0) ks[g] = F::step(scd[g], p, kk);
+            b[g] = F::deq(cq[p & 1][g], ks[g], kk);
         };
 #pragma unroll
         for (int mg = 0; mg < 4; mg++) xread(0, mg);
         deq(0, 0);
+        if constexpr (F::UNITS) {
 #pragma unroll
-        for (int mg = 0; mg < 4; mg++)
+            for (int mg = 0; mg < 4; mg++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) acc[mg][1][e] *= ratio[1];
+                for (int e = 0; e < 16; e++) acc[mg][1][e] *= ratio[1];
+        }
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int p = i >> 2, kk = i & 3;
             const bool more = i < 15;
+            const bool mgroup = F::MIN && i == 2;  // the min-term group
             __builtin_amdgcn_sched_barrier(0);
             if (i == 3) {
                 xload(nb, 0);
                 xsload(nb);
             }
             if (i == 9) xload(nb, 1);
-            if (i == 13) {
+            if (!F::STEP_KK && i == 13) {
                 block_scales();  // the next block's (scd of this one is used up)
                 hload(blk + 2);
             }
-            if (i < 2) bd_mins(hdc[i], inv[i], h, bh[i], bl[i]);
-            if (i == 1) {
+            if constexpr (F::MIN) {
+                if (i < 2) bd_mins(hdc[i], inv[i], h, bh[i], bl[i]);
+                if (i == 1) {
 #pragma unroll
-                for (int mg = 0; mg < 4; mg++)
-                    am[mg] = *reinterpret_cast<const bf16x8 *>(sxs + ((size_t)buf * BD_BM + 32 * mg + col) * 16 + 8 * h);
+                    for (int mg = 0; mg < 4; mg++)
+                        am[mg] = *reinterpret_cast<const bf16x8 *>(sxs + ((size_t)buf * BD_BM + 32 * mg + col) * 16 + 8 * h);
+                }
             }
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
                 acc[mg][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[0], acc[mg][0], 0, 0, 0);
-                if (i == 2) {
+                if (mgroup) {
 #pragma unroll
                     for (int g = 0; g < 2; g++) {
                         acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bh[g], acc[mg][g], 0, 0, 0);
                         acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bl[g], acc[mg][g], 0, 0, 0);
                     }
+                    __builtin_amdgcn_sched_barrier(0);
                 }
-                if (i == 2) __builtin_amdgcn_sched_barrier(0);
             }
             deq(i, 1);  // this group's second B operand, under its first four MFMAs
-            if (i != 2) {
+            if (!mgroup) {
 #pragma unroll
                 for (int mg = 0; mg < 4; mg++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
+                    __builtin_amdgcn_sched_group_barrier(0x002, F::VPM, 0);  // VALU
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (i == 15) {
+            if (F::STEP_KK && i == 15) {
+                block_scales();  // scales read per group: the last one is read above
+                hload(blk + 2);
+            }
+            if (F::UNITS && i == 15) {
                 // group 0's accumulators into the next block's unit (the last
                 // block keeps its unit)
                 const float r0 = blk + 1 < kb1 ? ratio[0] : 1.f;
@@ -366,9 +645,9 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
             if (more) deq(i + 1, 0);  // the next group's first B operand, under these MFMAs
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // its x read
-                __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // its x read
+                __builtin_amdgcn_sched_group_barrier(0x002, F::VPM, 0);  // VALU
             }
             __builtin_amdgcn_sched_barrier(0);
             if (kk == 3) cload(p & 1, 4 * blk + p + 2);  // the slot is free: step + 2
@@ -380,13 +659,15 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd_q4k(
         }
         bd_barrier();
     }
-    // back to true units
+    if constexpr (F::UNITS) {
+        // back to true units
 #pragma unroll
-    for (int g = 0; g < 2; g++)
+        for (int g = 0; g < 2; g++)
 #pragma unroll
-        for (int mg = 0; mg < 4; mg++)
+            for (int mg = 0; mg < 4; mg++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) acc[mg][g][e] *= sprev[g];
+                for (int e = 0; e < 16; e++) acc[mg][g][e] *= sprev[g];
+    }
 
     // C layout of a 32x32 tile: lane l, value i -> row 8 (i/4) + 4 (l/32) + i%4, column l % 32
     float *pt = split ? part + (size_t)(item - full) * BD_BM * BD_BN : nullptr;

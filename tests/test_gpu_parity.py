@@ -528,6 +528,57 @@ def test_prefill_tile_full(gpu_ctx, oracle, qtype):
     assert rel_err(got[rows], oracle.matmul_q(qtype, x[rows].astype(np.float32), raw, n)) <= TOL
 
 
+# (bytes per block, offset of the f16 block scale d) of the direct-operand prefill formats,
+# and their elements per block
+_D_FIELD = {"q4_k": (144, 0), "q6_k": (210, 208), "q8_0": (34, 0), "iq4_xs": (136, 0)}
+QK_OF = {"q4_k": 256, "q6_k": 256, "q8_0": 32, "iq4_xs": 256}
+
+
+@pytest.mark.parametrize("qtype", ["q4_k", "q6_k", "q8_0", "iq4_xs"])
+def test_prefill_direct_operand_block_units(gpu_ctx, oracle, qtype):
+    # the direct-operand prefill kernel with work items that run the whole K range (136
+    # tiles of 128 x 512 rows: no split) over weight blocks whose d spans 2^-4 .. 2^2 of
+    # the generator's, every 5th one dead (d = 0): the accumulators change unit at every
+    # block, and the per-block (Q4_K, IQ4_XS, Q8_0) and per-group (Q6_K) scales must belong
+    # to the block being multiplied.  Every output against BLAS on the weights the
+    # operands hold, where only the f32 sums differ: the oracle's exact dequant for Q4_K;
+    # for the formats whose operands are rounded to f16, that dequant rounded the same way
+    # (Q8_0: d * q rounded; Q6_K, IQ4_XS: the dequant at d = 1, sc * (q - 32) and
+    # (ls - 32) * kv, rounded, times d).  (Against the exact dequant their error is the
+    # weights' rounding, 2^-11 each, which the uniform-d prefill test holds to 2e-3.)
+    from arf_amd import QType, synth
+    m, n, k = 1024, 8704, 1024
+    _say("case: direct-operand block units", qtype)
+    rng = np.random.default_rng(0xB10C + len(qtype))
+    raw = synth.weight(qtype, n, k, seed=0xB10D).copy()
+    bb, off = _D_FIELD[qtype]
+    blocks = raw.reshape(-1, bb)
+    d = np.ascontiguousarray(blocks[:, off:off + 2]).view(np.float16).astype(np.float32).reshape(-1)
+    d *= np.exp2(rng.integers(-4, 3, size=d.shape)).astype(np.float32)
+    d[::5] = 0.0
+    dh = d.astype(np.float16)
+    blocks[:, off:off + 2] = dh.reshape(-1, 1).view(np.uint8)
+    x = synth.activations(m, k, seed=0xB10E).astype(np.float16)
+    if qtype == "q4_k":
+        wref = oracle.dequant(qtype, raw, n * k).reshape(n, k)
+    elif qtype == "q8_0":
+        wref = oracle.dequant(qtype, raw, n * k).reshape(n, k).astype(np.float16).astype(np.float32)
+    else:
+        one = raw.copy()
+        one.reshape(-1, bb)[:, off:off + 2] = np.full((1, 1), 1.0, np.float16).view(np.uint8)
+        unit = oracle.dequant(qtype, one, n * k).reshape(-1, QK_OF[qtype])
+        wref = (unit.astype(np.float16).astype(np.float32) * dh.astype(np.float32)[:, None]).reshape(n, k)
+    w = gpu_ctx.upload(QType[qtype.upper()], raw, n, k)
+    y = gpu_ctx.empty((m, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)
+    got = y.numpy()
+    w.free()
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, x.astype(np.float32) @ wref.T)
+    _say("rel err against the operands' weights (all rows)", e)
+    assert e <= 1e-4
+
+
 # ------------------------------------------------------ edge cases ----
 def _run(ctx, qtype, raw, x, n):
     from arf_amd import QType
