@@ -284,6 +284,8 @@ static int64_t bd_stream_bytes(int qtype) {
     case ARFQ_Q4_K:
     case ARFQ_IQ4_XS:
         return 128;
+    case ARFQ_Q5_K:
+        return 160;
     case ARFQ_Q6_K:
         return 192;
     case ARFQ_Q8_0:
@@ -301,25 +303,24 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     const bool kind2 = w->qtype == ARFQ_Q4_K || w->qtype == ARFQ_Q5_K;  // min term: x sums
     p.skinny = m <= 64 && w->k % 256 == 0;
     p.bm = m > 64 ? 128 : 64;
+    // prefill: the direct-operand kernel (one launch, no split-K) for every
+    // format but IQ4_XS at f32 x (its weights are rounded to f16, so its x
+    // keeps the hi + lo split of the tile loop below)
+    const int64_t bdb = bd_stream_bytes(w->qtype);
+    p.bd = !p.skinny && m > 64 && bdb && w->k % 256 == 0 && !(w->qtype == ARFQ_IQ4_XS && x_dtype == ARFQ_F32) &&
+           w->n * (w->k / 256) * bdb < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
     // f32 x: scaled per row by a power of two into f16 range, then rounded to
-    // f16 for the skinny kernel and the prefill shapes (m > 64), or split into
-    // f16 hi + lo for the tile loop at m <= 64 and for the Q5_K and IQ4_XS
-    // prefill tiles (their weights are rounded to f16: this way only one of the
-    // two operands is); the output rows are multiplied back by the scale
-    const bool next = w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS;
-    p.xsplit = !p.skinny && x_dtype == ARFQ_F32 && (m <= 64 || next);
+    // f16 for the skinny kernel and the direct-operand prefill, or split into
+    // f16 hi + lo for the tile loop (at m <= 64, and IQ4_XS prefill, whose
+    // weights are rounded to f16: this way only one of the two operands is);
+    // the output rows are multiplied back by the scale
+    p.xsplit = !p.skinny && !p.bd && x_dtype == ARFQ_F32;
     p.convert = x_dtype == ARFQ_F32;
     // skinny kernel, f32 x, m <= 32: x as f16 hi + lo (about 22 bits, as close
     // to the reference's f32 batched GEMV as the f16 MFMA gets): at m <= 16 the
     // lo rows fill the other half of the 32-row x tile staged anyway (no extra
     // MFMAs), at m <= 32 a second tile (twice the MFMAs)
     p.pair = p.skinny && x_dtype == ARFQ_F32 && m <= 32;
-    // prefill: the direct-operand kernel (one launch, no split-K) for Q4_K,
-    // Q6_K and Q8_0, and for IQ4_XS at f16 x (an f32 x keeps its hi + lo
-    // split in the tile loop, since these weights are rounded to f16)
-    const int64_t bdb = bd_stream_bytes(w->qtype);
-    p.bd = !p.skinny && m > 64 && bdb && w->k % 256 == 0 && !(w->qtype == ARFQ_IQ4_XS && x_dtype == ARFQ_F32) &&
-           w->n * (w->k / 256) * bdb < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
     // the exact Q4_K paths read x sub-block sums (min term)
     p.sums = (p.skinny || p.bd) && kind2;
     int64_t S;
@@ -474,9 +475,9 @@ static hipError_t launch_bd_t(const F &f, const arfq_weight *w, int64_t m, const
     const int xcd = (mt % 8 == 0 && p.bd_full % mt == 0) ? 1 : 0;
     if (nsplit && !part) return hipErrorInvalidValue;
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
-    if (hipError_t err = set_max_lds_once((const void *)gemm_bd<F>, bd_lds(), lds_set)) return err;
+    if (hipError_t err = set_max_lds_once((const void *)gemm_bd<F>, bd_lds<F>(), lds_set)) return err;
     const unsigned items = (unsigned)(p.bd_full + nsplit * p.bd_chunks);
-    gemm_bd<F><<<items, BD_THREADS, bd_lds(), s>>>(f, x, xs, rs, y, part, (int)m, (int)w->n, (int)w->k, mt, xcd,
+    gemm_bd<F><<<items, BD_THREADS, bd_lds<F>(), s>>>(f, x, xs, rs, y, part, (int)m, (int)w->n, (int)w->k, mt, xcd,
                                                    p.bd_full, p.bd_chunks);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !nsplit) return err;
@@ -492,6 +493,9 @@ static hipError_t launch_bd(const arfq_weight *w, int e, int64_t m, const _Float
     case ARFQ_Q4_K:
         return launch_bd_t(BdQ4K{(const uint4 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8}, w, m, x, xs, rs, y,
                            part, p, s);
+    case ARFQ_Q5_K:
+        return launch_bd_t(BdQ5K{(const uint4 *)w->s0 + eb, (const uint8_t *)w->s1 + eb * 160}, w, m, x, xs, rs,
+                           y, part, p, s);
     case ARFQ_IQ4_XS:
         return launch_bd_t(BdIQ4XS{(const uint2 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8}, w, m, x, xs, rs,
                            y, part, p, s);

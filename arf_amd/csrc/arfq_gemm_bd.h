@@ -48,9 +48,13 @@ constexpr int BD_BN = BD_NW * BD_WN;  // weight rows per workgroup
 constexpr int BD_THREADS = 64 * BD_NW;
 constexpr int BD_LD = 256 + 8;     // halves per LDS x row: one block, 16-byte pad
 
-// LDS: x tiles [2][BD_BM][BD_LD] halves, then the x sub-block sums [2][BD_BM][16] bf16
+// LDS: x tiles [2][BD_BM][BD_LD] halves, then the x sub-block sums [2][BD_BM][16] bf16,
+// then (formats with EXTRA block data) a dword per wave, group, MFMA kk and lane
+constexpr size_t BD_EXTRA_DWORDS = (size_t)BD_NW * 2 * 4 * 64;
+template <class F>
 __host__ __device__ constexpr size_t bd_lds() {
-    return (size_t)2 * BD_BM * BD_LD * sizeof(_Float16) + (size_t)2 * BD_BM * 16 * sizeof(uint16_t);
+    return (size_t)2 * BD_BM * BD_LD * sizeof(_Float16) + (size_t)2 * BD_BM * 16 * sizeof(uint16_t) +
+           (F::EXTRA ? BD_EXTRA_DWORDS * 4 : 0);
 }
 
 // workgroup barrier for the x tile: this wave's LDS writes are complete, no
@@ -123,7 +127,11 @@ __device__ __forceinline__ void bd_mins(const u32x4 hd, float inv_su, int h, bf1
 // block, the row's header; from those it builds the step's B operands in units
 // of the block scale su (UNITS: su = the block's d, so the accumulators are
 // moved into each block's unit; otherwise su = 1 and the operands carry their
-// whole scale).  MIN: the Q4_K min term (x sub-block sums).  VPM: VALU slots
+// whole scale).  MIN: the Q4_K min term (x sub-block sums).  STEP_KK: a
+// scale per group, not per step.  LATE: every group reads the block data
+// (Blk), so the next block's replaces it only after group 15.  EXTRA: block
+// data loaded at group 9 for the next block (LATE formats).  XPERM: the x
+// tile is staged in the format's slot order.  VPM: VALU slots
 // per MFMA in the pinned schedule (about a quarter of one operand's build).
 // a_off(p, kk, h): the block elements a lane's 8 k-slots of MFMA group kk of
 // step p hold (the x tile is read with the same map).
@@ -134,6 +142,10 @@ __device__ __forceinline__ void bd_mins(const u32x4 hd, float inv_su, int h, bf1
 // Q4_K (exact): step p, lane half h = sub-block 2p + h; group kk = code dword
 // kk (elements 8kk .. 8kk + 7, sigma nibble order).  Operands sc_j * q.
 struct BdQ4K {
+    static constexpr int XPARTS = 2;
+    static constexpr bool EXTRA = false;
+    struct Extra {};
+    static constexpr bool XPERM = false, LATE = false;
     static constexpr bool UNITS = true, MIN = true, STEP_KK = false;
     static constexpr int VPM = 3;
     using Code = u32x4;
@@ -163,7 +175,7 @@ struct BdQ4K {
         return l;
     }
     __device__ static float unit(const Head &hd) { return h2f(hd.x); }
-    __device__ static Blk block(const Head &hd, int h) {
+    __device__ static Blk block(const Head &hd, const Extra &, int h, uint32_t *) {
         uint32_t packed = 0;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
@@ -173,10 +185,106 @@ struct BdQ4K {
         }
         return packed;
     }
-    __device__ static Blk dead() { return 0u; }
+    __device__ static void kill(Blk &b) { b = 0u; }
     __device__ static Step step(Blk b, int p, int) { return bd_scale((b >> (8 * p)) & 0xffu); }
-    __device__ static half8 deq(const Code &c, const Step &k, int kk) {
+    __device__ static half8 deq(const Code &c, const Step &k, Blk, int, int kk) {
         return bd_dequant(kk == 0 ? c.x : kk == 1 ? c.y : kk == 2 ? c.z : c.w, k);
+    }
+    __device__ static void mins(const Head &hd, float inv_su, int h, bf16x8 &hi, bf16x8 &lo) {
+        bd_mins(hd, inv_su, h, hi, lo);
+    }
+};
+
+// Q5_K (exact): ggml's qs pairs sub-blocks 2p (low nibbles) and 2p + 1 (high
+// nibbles) byte by byte, so step p, lane half h takes elements 16h .. 16h + 15
+// of both: 16 code bytes, and group kk = elements 16h + 4kk .. + 3 of each
+// (slots 0..3 sub-block 2p, 4..7 sub-block 2p + 1; the x tile is staged in
+// that slot order, XPERM).  The fifth bit of element l of sub-block j is bit j
+// of qh[l]: the lane's 16 qh bytes come with the block header.  Operands
+// sc_j * q (<= 63 * 31, exact) as Q4_K's, with the fifth bit put into the
+// f16 pattern (bit 4 of 1024 + q, bit 8 of 1024 + 16 q).  Same header and
+// min term as Q4_K.  (dequant_q5_k, crates/arf-core/src/model/gguf.rs:2053-2090)
+struct BdQ5K {
+    static constexpr int XPARTS = 4;
+    static constexpr bool EXTRA = true;  // the qh bytes come separately, late
+    static constexpr bool XPERM = true, LATE = true;
+    static constexpr bool UNITS = true, MIN = true, STEP_KK = false;
+    static constexpr int VPM = 5;
+    using Code = u32x4;
+    using Head = u32x4;
+    using Extra = u32x4;  // the lane's 16 qh bytes
+    struct Blk {
+        uint32_t lo, hi;     // sc of sub-blocks 2p, 2p + 1, byte p
+        const uint32_t *qh;  // the lane's qh dword of MFMA kk at qh[64 kk] (LDS)
+    };
+    using Step = BdScale;
+    const uint4 *hdr;
+    const uint8_t *q;  // qh[32] | qs[128] per block
+    __device__ static int a_off(int p, int kk, int h) { return 64 * p + 32 * h + 8 * kk; }
+    struct Lanes {
+        __amdgpu_buffer_rsrc_t q, hd;
+        uint32_t qv[2], hv[2];
+        __device__ Code code(int g, int st) const {
+            return __builtin_amdgcn_raw_buffer_load_b128(q, qv[g], (st >> 2) * 160 + 32 + 32 * (st & 3), 0);
+        }
+        __device__ Head head(int g, int blk) const {
+            return __builtin_amdgcn_raw_buffer_load_b128(hd, hv[g], blk * 16, 0);
+        }
+        __device__ Extra extra(int g, int blk) const {
+            return __builtin_amdgcn_raw_buffer_load_b128(q, qv[g], blk * 160, 0);
+        }
+    };
+    __device__ Lanes lanes(int n, int nblk, uint32_t wr0, uint32_t wr1, int h) const {
+        Lanes l;
+        l.q = __builtin_amdgcn_make_buffer_rsrc((void *)q, (short)0, (int)((uint32_t)n * nblk * 160), 0x00020000);
+        l.hd = __builtin_amdgcn_make_buffer_rsrc((void *)hdr, (short)0, (int)((uint32_t)n * nblk * 16), 0x00020000);
+        l.qv[0] = wr0 * nblk * 160 + 16 * h;
+        l.qv[1] = wr1 * nblk * 160 + 16 * h;
+        l.hv[0] = wr0 * nblk * 16;
+        l.hv[1] = wr1 * nblk * 16;
+        return l;
+    }
+    __device__ static float unit(const Head &hd) { return h2f(hd.x); }
+    __device__ static Blk block(const Head &hd, const Extra &qh, int, uint32_t *xl) {
+        xl[0] = qh.x;
+        xl[64] = qh.y;
+        xl[128] = qh.z;
+        xl[192] = qh.w;
+        Blk b{0u, 0u, xl};
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            uint32_t sc, mm;
+            q4k_scale_min(hd.y, hd.z, hd.w, 2 * p, sc, mm);
+            b.lo |= sc << (8 * p);
+            q4k_scale_min(hd.y, hd.z, hd.w, 2 * p + 1, sc, mm);
+            b.hi |= sc << (8 * p);
+        }
+        return b;
+    }
+    __device__ static void kill(Blk &b) { b.lo = b.hi = 0u; }
+    __device__ static Step step(const Blk &b, int p, int) {
+        const half2v s1 = h2splat((float)((b.lo >> (8 * p)) & 0xffu));
+        const half2v s2 = h2splat((float)((b.hi >> (8 * p)) & 0xffu));
+        return {s1, s1 * (half2v){-1024.f, -1024.f}, s2 * (half2v){0.0625f, 0.0625f}, s2 * (half2v){-64.f, -64.f}};
+    }
+    __device__ static half8 deq(const Code &c, const Step &k, const Blk &b, int p, int kk) {
+        const uint32_t w = kk == 0 ? c.x : kk == 1 ? c.y : kk == 2 ? c.z : c.w;
+        const uint32_t H = b.qh[64 * kk];
+        const uint32_t t01 = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);  // b0 64 b1 64
+        const uint32_t t23 = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);  // b2 64 b3 64
+        const uint32_t u01 = __builtin_amdgcn_perm(0u, H, 0x0c010c00u);           // qh b0 0 b1 0
+        const uint32_t u23 = __builtin_amdgcn_perm(0u, H, 0x0c030c02u);
+        // bit 2p of a qh byte -> bit 4 of the half (+16 on 1024 + q); bit 2p + 1
+        // -> bit 8 (+256 on 1024 + 16 q)
+        auto lob = [&](uint32_t u) { return (p < 2 ? u << (4 - 2 * p) : u >> (2 * p - 4)) & 0x00100010u; };
+        auto hib = [&](uint32_t u) { return (u << (7 - 2 * p)) & 0x01000100u; };
+        return bd_h8(pk_fma((t01 & 0x640F640Fu) | lob(u01), k.s1, k.c1),
+                     pk_fma((t23 & 0x640F640Fu) | lob(u23), k.s1, k.c1),
+                     pk_fma((t01 & 0x64F064F0u) | hib(u01), k.s16, k.c16),
+                     pk_fma((t23 & 0x64F064F0u) | hib(u23), k.s16, k.c16));
+    }
+    __device__ static void mins(const Head &hd, float inv_su, int h, bf16x8 &hi, bf16x8 &lo) {
+        bd_mins(hd, inv_su, h, hi, lo);
     }
 };
 
@@ -187,6 +295,10 @@ struct BdQ4K {
 // f16 (exact while |(ls - 32) kv| <= 2048); kv from the codebook with two
 // v_perm.  (dequant_iq4_xs, crates/arf-core/src/model/gguf.rs:1937-1976)
 struct BdIQ4XS {
+    static constexpr int XPARTS = 2;
+    static constexpr bool EXTRA = false;
+    struct Extra {};
+    static constexpr bool XPERM = false, LATE = false;
     static constexpr bool UNITS = true, MIN = false, STEP_KK = false;
     static constexpr int VPM = 6;
     using Code = u32x4;
@@ -219,7 +331,7 @@ struct BdIQ4XS {
         return l;
     }
     __device__ static float unit(const Head &hd) { return h2f(hd.x); }
-    __device__ static Blk block(const Head &hd, int h) {
+    __device__ static Blk block(const Head &hd, const Extra &, int h, uint32_t *) {
         uint32_t packed = 0;
 #pragma unroll
         for (int p = 0; p < 4; p++) {
@@ -229,12 +341,12 @@ struct BdIQ4XS {
         }
         return packed;
     }
-    __device__ static Blk dead() { return 0u; }
+    __device__ static void kill(Blk &b) { b = 0u; }
     __device__ static Step step(Blk b, int p, int) {
         const half2v s = h2splat((float)(int8_t)(b >> (8 * p)));
         return {s, s * (half2v){-1152.f, -1152.f}};  // 1152 |ls - 32| <= 36864: exact
     }
-    __device__ static half8 deq(const Code &c, const Step &k, int kk) {
+    __device__ static half8 deq(const Code &c, const Step &k, Blk, int, int kk) {
         // kvalues_iq4nl + 128 as bytes: entries 0..7 and 8..15, little-endian
         constexpr uint32_t T0lo = 0xBFAD9881u ^ 0x80808080u, T0hi = 0xF6EADDCFu ^ 0x80808080u;
         constexpr uint32_t T1lo = 0x26190D01u ^ 0x80808080u, T1hi = 0x71594535u ^ 0x80808080u;
@@ -262,6 +374,10 @@ struct BdIQ4XS {
 // elements 8kk .. 8kk + 7.  The header is the 8 block scales d of the 256
 // elements.  (dequant_q8_0, crates/arf-core/src/model/gguf.rs)
 struct BdQ80 {
+    static constexpr int XPARTS = 2;
+    static constexpr bool EXTRA = false;
+    struct Extra {};
+    static constexpr bool XPERM = false, LATE = false;
     static constexpr bool UNITS = false, MIN = false, STEP_KK = false;
     static constexpr int VPM = 4;
     struct Code {
@@ -296,15 +412,15 @@ struct BdQ80 {
         return l;
     }
     __device__ static float unit(const Head &) { return 1.f; }
-    __device__ static Blk block(const Head &hd, int h) {
+    __device__ static Blk block(const Head &hd, const Extra &, int h, uint32_t *) {
         const uint32_t sel = h ? 0x07060302u : 0x05040100u;
         return {__builtin_amdgcn_perm(hd.y, hd.x, sel), __builtin_amdgcn_perm(hd.w, hd.z, sel)};
     }
-    __device__ static Blk dead() { return {0u, 0u}; }
+    __device__ static void kill(Blk &b) { b = u32x2{0u, 0u}; }
     __device__ static Step step(const Blk &b, int p, int) {
         return as_h2(__builtin_amdgcn_perm(0u, (p >> 1) ? b.y : b.x, (p & 1) ? 0x03020302u : 0x01000100u));
     }
-    __device__ static half8 deq(const Code &c, const Step &d, int kk) {
+    __device__ static half8 deq(const Code &c, const Step &d, const Blk &, int, int kk) {
         const uint32_t w[2] = {kk == 0 ? c.a.x : kk == 1 ? c.a.z : kk == 2 ? c.b.x : c.b.z,
                                kk == 0 ? c.a.y : kk == 1 ? c.a.w : kk == 2 ? c.b.y : c.b.w};
         const half2v m1152 = {-1152.f, -1152.f};
@@ -327,6 +443,10 @@ struct BdQ80 {
 // rounded once to f16 (exact while |sc| <= 64).
 // (dequant_q6_k, crates/arf-core/src/model/gguf.rs:2092-2131)
 struct BdQ6K {
+    static constexpr int XPARTS = 2;
+    static constexpr bool EXTRA = false;
+    struct Extra {};
+    static constexpr bool XPERM = false, LATE = true;
     static constexpr bool UNITS = true, MIN = false, STEP_KK = true;
     static constexpr int VPM = 7;
     struct Code {
@@ -370,8 +490,8 @@ struct BdQ6K {
         return l;
     }
     __device__ static float unit(const Head &hd) { return h2f(hd.d); }
-    __device__ static Blk block(const Head &hd, int) { return hd.sc; }
-    __device__ static Blk dead() { return {0u, 0u, 0u, 0u}; }
+    __device__ static Blk block(const Head &hd, const Extra &, int, uint32_t *) { return hd.sc; }
+    __device__ static void kill(Blk &b) { b = u32x4{0u, 0u, 0u, 0u}; }
     __device__ static Step step(const Blk &b, int p, int kk) {
         const int si = 8 * (p >> 1) + (p & 1) + 2 * kk;
         const uint32_t w = (si >> 2) == 0 ? b.x : (si >> 2) == 1 ? b.y : (si >> 2) == 2 ? b.z : b.w;
@@ -379,7 +499,7 @@ struct BdQ6K {
     }
     // q as the f16 1024 + q (v_perm puts 0x64 above each code byte; the two
     // qh bits go to bits 4-5), minus 1056 (exact), times sc (one rounding)
-    __device__ static half8 deq(const Code &c, const Step &sc, int kk) {
+    __device__ static half8 deq(const Code &c, const Step &sc, const Blk &, int, int kk) {
         const half2v m1056 = {-1056.f, -1056.f};
         const u32x2 ql = (kk & 1) ? c.b : c.a;
         uint32_t o[4];
@@ -446,23 +566,28 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         (void *)xs, (short)0, (int)((uint32_t)m * (k / 16) * 2), 0x00020000);
 
     // x tile staging: thread t copies row t / 4.  The next block's x moves in
-    // two halves (halves 0..127 of the row, then 128..255), each loaded at
-    // the start of one half of the current block and stored into the other
-    // buffer near its end: thread (t % 4) takes 2 x 16 bytes per 64 halves.
+    // XP parts of 256 / XP halves of the row (two or four; fewer registers
+    // held with four), each loaded during the current block and stored into
+    // the other buffer a few groups later: thread (t % 4) takes 2 x 16 bytes
+    // per 64 halves.
+    constexpr int XP = F::XPARTS, XS = 4 / XP;  // parts, steps per part
     const int xr = tid >> 2, xo = (tid & 3) * 16;
     const uint32_t xv = (uint32_t)min(m0 + xr, m - 1) * k * 2 + xo * 2;  // bytes
-    u32x4 xa[4];
-    auto xload = [&](int blk, int half) {
-        const int so = blk * 512 + 256 * half;
-        xa[0] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv, so, 0);
-        xa[1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 16, so, 0);
-        xa[2] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 128, so, 0);  // + 64 halves
-        xa[3] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 144, so, 0);
+    u32x4 xa[2 * XS];
+    auto xload = [&](int blk, int part) {
+#pragma unroll
+        for (int j = 0; j < XS; j++) {
+            const int so = blk * 512 + 128 * (XS * part + j);
+            xa[2 * j] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv, so, 0);
+            xa[2 * j + 1] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xv + 16, so, 0);
+        }
     };
     // x sub-block sums of the next block (min term): thread t moves 4 of row
     // t / 4's 16
     const uint32_t sv = (uint32_t)min(m0 + xr, m - 1) * (k / 16) * 2 + (tid & 3) * 8;  // bytes
     uint16_t *sxs = reinterpret_cast<uint16_t *>(sx + 2 * BD_BM * BD_LD);  // [2][BD_BM][16]
+    // EXTRA block data: this wave's [2][4][64] dwords, at this lane
+    uint32_t *exl = reinterpret_cast<uint32_t *>(sxs + 2 * BD_BM * 16) + (size_t)wave * 512 + lane;
     u32x2 xsa;
     auto xsload = [&](int blk) {
         if constexpr (F::MIN) xsa = __builtin_amdgcn_raw_buffer_load_b64(srs, sv, blk * 32, 0);
@@ -471,13 +596,32 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         if constexpr (F::MIN)
             *reinterpret_cast<u32x2 *>(sxs + ((size_t)buf * BD_BM + xr) * 16 + (tid & 3) * 4) = xsa;
     };
-    auto xstore = [&](int buf, int half) {
-        u32x4 *dst = reinterpret_cast<u32x4 *>(sx + ((size_t)buf * BD_BM + xr) * BD_LD + 128 * half + xo);
-        dst[0] = xa[0];
-        dst[1] = xa[1];
-        dst[8] = xa[2];
-        dst[9] = xa[3];
+    auto xstore = [&](int buf, int part) {
+#pragma unroll
+        for (int j = 0; j < XS; j++) {
+            _Float16 *row = sx + ((size_t)buf * BD_BM + xr) * BD_LD + 64 * (XS * part + j);
+            if constexpr (F::XPERM) {
+                // element e = 32 s + 16 hh + 4 kk + i of a step goes to slot
+                // 32 hh + 8 kk + 4 s + i (s = sub-block parity); this thread's
+                // 16 elements of each step have s = (t % 4) / 2, hh = t % 2
+                const int base = 32 * (tid & 1) + 4 * ((tid >> 1) & 1);
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    const u32x4 &v = xa[2 * j + (kk >> 1)];
+                    *reinterpret_cast<u32x2 *>(row + base + 8 * kk) = (kk & 1) ? u32x2{v.z, v.w} : u32x2{v.x, v.y};
+                }
+            } else {
+                u32x4 *dst = reinterpret_cast<u32x4 *>(row + xo);
+                dst[0] = xa[2 * j];
+                dst[1] = xa[2 * j + 1];
+            }
+        }
     };
+    // the groups that load and store x part q of the next block
+    // (loads at the top of a group, stores at its end; with four parts one
+    // part's registers are reused by the next)
+    auto xload_at = [](int i, int q) { return XP == 2 ? i == 3 + 6 * q : i == 4 * q + 1; };
+    auto xstore_at = [](int i, int q) { return XP == 2 ? i == (q == 0 ? 8 : 15) : i == (q == 3 ? 15 : 4 * q + 4); };
 
     // code ring: slot s % 2 holds step s (both groups' codes); it is refilled
     // with step s + 2 as soon as its last operand is built
@@ -487,12 +631,21 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         cq[u][0] = ld.code(0, st);
         cq[u][1] = ld.code(1, st);
     };
-    // block headers of the two rows, one block ahead
+    // block headers of the two rows, one block ahead; a format's EXTRA block
+    // data, from group 9 of the block before
     typename F::Head hdn[2];
     auto hload = [&](int blk) {
         blk = min(blk, kb1 - 1);
         hdn[0] = ld.head(0, blk);
         hdn[1] = ld.head(1, blk);
+    };
+    typename F::Extra ext[2];
+    auto eload = [&](int blk) {
+        if constexpr (F::EXTRA) {
+            blk = min(blk, kb1 - 1);
+            ext[0] = ld.extra(0, blk);
+            ext[1] = ld.extra(1, blk);
+        }
     };
 
     floatx16 acc[4][2];
@@ -505,13 +658,14 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
 
     // prologue: the first block's x tile, the first headers and code steps
 #pragma unroll
-    for (int hf = 0; hf < 2; hf++) {
-        xload(kb0, hf);
-        xstore(0, hf);
+    for (int q = 0; q < XP; q++) {
+        xload(kb0, q);
+        xstore(0, q);
     }
     xsload(kb0);
     xsstore(0);
     hload(kb0);
+    eload(kb0);
 #pragma unroll
     for (int u = 0; u < 2; u++) cload(u, st0 + u);
     bd_barrier();
@@ -530,8 +684,8 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
             const float d = F::unit(hdc[g]);
             const bool live = d != 0.f;
             const float su = live ? d : 1.f;
-            scd[g] = F::block(hdc[g], h);
-            if (!live) scd[g] = F::dead();
+            scd[g] = F::block(hdc[g], ext[g], h, exl + 256 * g);
+            if (!live) F::kill(scd[g]);
             inv[g] = __builtin_amdgcn_rcpf(su);
             ratio[g] = sprev[g] * inv[g];
             sprev[g] = su;
@@ -558,8 +712,8 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         //    half of row (32 mg + l % 32)'s 16);
         //  - group 13 takes the next block's headers (scales, ratio; the last
         //    read of this block's scales is group 12's b[1]) and issues the
-        //    loads of the one after; with a scale per group (STEP_KK), group 15
-        //    does, after its b[1].
+        //    loads of the one after; where every group's operands read the
+        //    block data (LATE), group 15 does, after its b[1].
         half8 a[4], b[2];
         typename F::Step ks[2];
         bf16x8 bh[2], bl[2], am[4];
@@ -569,7 +723,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         auto deq = [&](int i, int g) {
             const int p = i >> 2, kk = i & 3;
             if (F::STEP_KK || kk == 0) ks[g] = F::step(scd[g], p, kk);
-            b[g] = F::deq(cq[p & 1][g], ks[g], kk);
+            b[g] = F::deq(cq[p & 1][g], ks[g], scd[g], p, kk);
         };
 #pragma unroll
         for (int mg = 0; mg < 4; mg++) xread(0, mg);
@@ -586,17 +740,17 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
             const bool more = i < 15;
             const bool mgroup = F::MIN && i == 2;  // the min-term group
             __builtin_amdgcn_sched_barrier(0);
-            if (i == 3) {
-                xload(nb, 0);
-                xsload(nb);
-            }
-            if (i == 9) xload(nb, 1);
-            if (!F::STEP_KK && i == 13) {
+#pragma unroll
+            for (int q = 0; q < XP; q++)
+                if (xload_at(i, q)) xload(nb, q);
+            if (i == 3) xsload(nb);
+            if (i == 9) eload(blk + 1);
+            if (!F::LATE && i == 13) {
                 block_scales();  // the next block's (scd of this one is used up)
                 hload(blk + 2);
             }
             if constexpr (F::MIN) {
-                if (i < 2) bd_mins(hdc[i], inv[i], h, bh[i], bl[i]);
+                if (i < 2) F::mins(hdc[i], inv[i], h, bh[i], bl[i]);
                 if (i == 1) {
 #pragma unroll
                     for (int mg = 0; mg < 4; mg++)
@@ -624,8 +778,8 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
-            if (F::STEP_KK && i == 15) {
-                block_scales();  // scales read per group: the last one is read above
+            if (F::LATE && i == 15) {
+                block_scales();  // block data read by every group: the last read is above
                 hload(blk + 2);
             }
             if (F::UNITS && i == 15) {
@@ -651,11 +805,10 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
             }
             __builtin_amdgcn_sched_barrier(0);
             if (kk == 3) cload(p & 1, 4 * blk + p + 2);  // the slot is free: step + 2
-            if (i == 8) {
-                xstore(buf ^ 1, 0);
-                xsstore(buf ^ 1);
-            }
-            if (i == 15) xstore(buf ^ 1, 1);
+#pragma unroll
+            for (int q = 0; q < XP; q++)
+                if (xstore_at(i, q)) xstore(buf ^ 1, q);
+            if (i == 8) xsstore(buf ^ 1);
         }
         bd_barrier();
     }

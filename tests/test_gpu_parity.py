@@ -530,18 +530,19 @@ def test_prefill_tile_full(gpu_ctx, oracle, qtype):
 
 # (bytes per block, offset of the f16 block scale d) of the direct-operand prefill formats,
 # and their elements per block
-_D_FIELD = {"q4_k": (144, 0), "q6_k": (210, 208), "q8_0": (34, 0), "iq4_xs": (136, 0)}
-QK_OF = {"q4_k": 256, "q6_k": 256, "q8_0": 32, "iq4_xs": 256}
+_D_FIELD = {"q4_k": (144, 0), "q5_k": (176, 0), "q6_k": (210, 208), "q8_0": (34, 0), "iq4_xs": (136, 0)}
+QK_OF = {"q4_k": 256, "q5_k": 256, "q6_k": 256, "q8_0": 32, "iq4_xs": 256}
 
 
-@pytest.mark.parametrize("qtype", ["q4_k", "q6_k", "q8_0", "iq4_xs"])
+@pytest.mark.parametrize("qtype", ["q4_k", "q5_k", "q6_k", "q8_0", "iq4_xs"])
 def test_prefill_direct_operand_block_units(gpu_ctx, oracle, qtype):
     # the direct-operand prefill kernel with work items that run the whole K range (136
     # tiles of 128 x 512 rows: no split) over weight blocks whose d spans 2^-4 .. 2^2 of
     # the generator's, every 5th one dead (d = 0): the accumulators change unit at every
     # block, and the per-block (Q4_K, IQ4_XS, Q8_0) and per-group (Q6_K) scales must belong
     # to the block being multiplied.  Every output against BLAS on the weights the
-    # operands hold, where only the f32 sums differ: the oracle's exact dequant for Q4_K;
+    # operands hold, where only the f32 sums differ: the oracle's exact dequant for Q4_K
+    # and Q5_K;
     # for the formats whose operands are rounded to f16, that dequant rounded the same way
     # (Q8_0: d * q rounded; Q6_K, IQ4_XS: the dequant at d = 1, sc * (q - 32) and
     # (ls - 32) * kv, rounded, times d).  (Against the exact dequant their error is the
@@ -559,7 +560,7 @@ def test_prefill_direct_operand_block_units(gpu_ctx, oracle, qtype):
     dh = d.astype(np.float16)
     blocks[:, off:off + 2] = dh.reshape(-1, 1).view(np.uint8)
     x = synth.activations(m, k, seed=0xB10E).astype(np.float16)
-    if qtype == "q4_k":
+    if qtype in ("q4_k", "q5_k"):
         wref = oracle.dequant(qtype, raw, n * k).reshape(n, k)
     elif qtype == "q8_0":
         wref = oracle.dequant(qtype, raw, n * k).reshape(n, k).astype(np.float16).astype(np.float32)
