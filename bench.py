@@ -7,7 +7,9 @@ exact weights in f32 (the reference's arithmetic) -- one step is one GEMV launch
 activation vector.  Weights are 8 distinct seeded
 copies (8 x 50 MB, above the 256 MB MALL) used round-robin so the timed loop
 streams from HBM.  Timing: HIP events recorded on the library's stream around
-exactly K back-to-back launches, after one set-up launch per weight copy, W warm-up
+exactly K back-to-back launches, after one set-up launch per weight copy, a clock
+settle phase (launches for SETTLE_S of wall time: the GPU's clock ramps up over the
+first ~10-20 ms of sustained load, which moved C4 from 430 to 387 us), W warm-up
 launches and a stream sync.
 Secondary configs are measured the same way and reported under "configs".
 
@@ -29,6 +31,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0         # MI355X HBM3E
+SETTLE_S = 0.05               # untimed launches before each config's warm-up (clock ramp)
 FP16_MFMA_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 
 
@@ -42,7 +45,18 @@ def algorithmic_bytes(qtype, m, n, k, x_bytes=4):
     return wb + m * k * x_bytes + m * n * 4
 
 
-def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.float32):
+def settle(ctx, launch, seconds=SETTLE_S):
+    """Untimed launches (`launch(i)` issues some) until `seconds` of wall time have passed,
+    so the timed region starts at the clock the GPU holds under sustained load."""
+    t0, i = time.time(), 0
+    while time.time() - t0 < seconds:
+        for _ in range(16):  # host syncs only between batches: the GPU stays busy
+            launch(i)
+            i += 1
+        ctx.sync()
+
+
+def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.float32, settle_s=SETTLE_S):
     """Average ms per launch of arfq_matmul over `steps` launches rotating `copies` weights.
     Set-up runs one untimed launch per weight copy (so no copy is first touched inside the
     timed region, whatever `warmup` is), then the `warmup` launches."""
@@ -53,6 +67,7 @@ def time_matmul(ctx, qtype, m, n, k, steps, warmup, copies, seed, x_dtype=np.flo
     x = ctx.to_device(synth.activations(m, k, seed=seed + 1).astype(x_dtype))
     y = ctx.empty((m, n), np.float32)
     ctx.matmul_repeat(ws, copies, m, x, y)  # set-up: each copy once
+    settle(ctx, lambda i: ctx.matmul_repeat(ws, 4 * copies, m, x, y), settle_s)
     ctx.matmul_repeat(ws, warmup, m, x, y)
     ctx.sync()
     ctx.timer_start()
@@ -72,6 +87,7 @@ def time_ffn(ctx, qts, hidden, inter, m, steps, warmup, copies):
              for i, (q, (n, k)) in enumerate(zip(qts, shapes))] for c in range(copies)]
     x = ctx.to_device(synth.activations(m, hidden, seed=0xA7F0000F))
     y = ctx.empty((m, hidden), np.float32)
+    settle(ctx, lambda i: ctx.ffn(*sets[i % copies], x, m, y))
     for i in range(warmup):
         ctx.ffn(*sets[i % copies], x, m, y)
     ctx.sync()
@@ -86,7 +102,7 @@ def time_ffn(ctx, qts, hidden, inter, m, steps, warmup, copies):
     return ms / steps
 
 
-def time_moe(ctx, steps, warmup, copies, tokens=None):
+def time_moe(ctx, steps, warmup, copies, tokens=None, settle_s=SETTLE_S):
     """Average ms per arfq_moe call (C5's experts; `tokens` defaults to C5's 512) rotating
     `copies` weight sets, after `warmup` calls."""
     from arf_amd import QType, synth
@@ -105,6 +121,7 @@ def time_moe(ctx, steps, warmup, copies, tokens=None):
     x = ctx.to_device(synth.activations(T, hdim, seed=0xA7F00008, dtype=np.float16))
     lg = ctx.to_device(synth.router_logits(T, E, seed=0xA7F00009))
     y = ctx.empty((T, hdim), np.float32)
+    settle(ctx, lambda i: ctx.moe(*sets[i % copies], lg, T, k, True, x, y), settle_s)
     for i in range(warmup):
         g, u, d = sets[i % copies]
         ctx.moe(g, u, d, lg, T, k, True, x, y)
@@ -296,11 +313,11 @@ def traffic_probe(ctx, copies, config="c2"):
              "c3m32": ("q6_k", 32, 5120, 17408), "c3m64": ("q6_k", 64, 5120, 17408),
              "c4": ("q4_k", 2048, 17408, 5120)}
     if config == "c5":
-        time_moe(ctx, TRAFFIC_PROBE_LAUNCHES, 0, copies)
+        time_moe(ctx, TRAFFIC_PROBE_LAUNCHES, 0, copies, settle_s=0)
     else:
         qt, m, n, k = shape[config]
         time_matmul(ctx, qt, m, n, k, TRAFFIC_PROBE_LAUNCHES, 0, copies, 0xA7F00002,
-                    x_dtype=np.float16 if m == 2048 else np.float32)
+                    x_dtype=np.float16 if m == 2048 else np.float32, settle_s=0)
     ctx.sync()
     log(f"[probe] {COPY_PROBE_LAUNCHES} copies of {COPY_PROBE_BYTES} B, then {config}: "
         f"{copies} set-up + {TRAFFIC_PROBE_LAUNCHES} launches over {copies} weight copies")
