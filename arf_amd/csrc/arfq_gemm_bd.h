@@ -1,5 +1,6 @@
-// arfq_gemm_bd.h -- prefill GEMM for Q4_K weights with the weights going
-// straight from memory into the MFMA B operands (no LDS for weights).
+// arfq_gemm_bd.h -- prefill GEMM with the weights going straight from memory
+// into the MFMA B operands (no LDS for weights).  Q4_K is described here; the
+// Bd* format policies below give Q5_K, Q6_K, Q8_0 and IQ4_XS the same tile.
 //
 // A workgroup of 8 waves computes 128 x rows by 512 weight rows; wave w owns
 // the 64 weight rows [n0 + 64 w, n0 + 64 w + 64) for all 128 x rows, as 4 x 2
