@@ -351,8 +351,9 @@ def test_gemm_q4k_f16_small(gpu_ctx, oracle, m, n, k):
 @pytest.mark.parametrize("qtype,n,k", [("q4_k", 96, 2048), ("q6_k", 130, 1792), ("q8_0", 77, 1216),
                                        ("q8_0", 100, 2048)])
 def test_gemm_f32_x(gpu_ctx, oracle, qtype, n, k, m):
-    # m > 4 goes through the MFMA kernels: f32 x scaled per row into f16 range and
-    # rounded to f16 (split into an f16 hi + lo pair on the tiled kernel at m <= 64)
+    # m > 4 goes through the MFMA kernels: f32 x scaled per row into f16 range, then
+    # split into an f16 hi + lo pair on the skinny kernel at m <= 32 and on the tiled
+    # kernel (Q8_0 with k not a multiple of 256) at m <= 64, rounded to f16 otherwise
     _say("case: gemm f32 x", qtype, n, k, m)
     got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=91 + m + n)
     e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
