@@ -1948,12 +1948,18 @@ bool gemv_pairs_supports(const arfq_weight *w) {
            q4k_pairs_lds(w, 1) <= Q4K_F32_LDS_MAX;
 }
 
+// Workgroups per CU of the decode-pair GEMVs: two, or one for up to 8 pairs (one token's
+// top-8: C5's experts at T = 1 ran 21.9 us against 23.2 with two, while at T = 4 and 16
+// one per CU was 9 % and 13 % slower).
+static int pairs_per_cu(int64_t P) { return P <= 8 ? 1 : 2; }
+
 template <class XS>
 static hipError_t launch_pairs_t(const arfq_weight *w, int64_t P, const int32_t *ids, const XS &xs,
                                  float *y, hipStream_t s) {
     const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
-    // about two workgroups per CU over all pairs, >= 4 rows per workgroup
-    const int64_t g = std::max<int64_t>(1, std::min<int64_t>((2 * (int64_t)cus + P - 1) / P, w->n / 4));
+    // about two workgroups per CU over all pairs (one at a single token's pairs), >= 4 rows
+    // per workgroup
+    const int64_t g = std::max<int64_t>(1, std::min<int64_t>((pairs_per_cu(P) * (int64_t)cus + P - 1) / P, w->n / 4));
     const int64_t nb = w->n * (w->k / 256);
     const dim3 grid((unsigned)g, (unsigned)P);
     const int nsub = (int)(w->k / 32);
@@ -2016,8 +2022,10 @@ template <class XS>
 static hipError_t launch_pairs_dual_t(const arfq_weight *w0, const arfq_weight *w1, int64_t P,
                                       const int32_t *ids, const XS &xs, float *y0, float *y1, hipStream_t s) {
     const int cus = w0->ctx->cus > 0 ? w0->ctx->cus : 256;
-    // about two workgroups per CU over both weights' pairs, >= 4 rows per workgroup
-    const int64_t g = std::max<int64_t>(1, std::min<int64_t>((2 * (int64_t)cus + 2 * P - 1) / (2 * P), w0->n / 4));
+    // about two workgroups per CU over both weights' pairs (one at a single token's pairs),
+    // >= 4 rows per workgroup
+    const int64_t g = std::max<int64_t>(
+        1, std::min<int64_t>((pairs_per_cu(P) * (int64_t)cus + 2 * P - 1) / (2 * P), w0->n / 4));
     const int64_t nb = w0->n * (w0->k / 256);
     const dim3 grid((unsigned)g, (unsigned)P, 2);
     const size_t lds = q4k_pairs_lds(w0, g);
