@@ -233,6 +233,9 @@ constexpr int MOE_BM = 64;
 // item count (known only on the device) never leaves a part-filled last round
 // of workgroups.
 constexpr int MOE_GU_THREADS = 512;
+// Two x buffers (one barrier per block instead of two): C5 183.2 -> 182.4 us;
+// the workgroup holds a CU by its registers, so the LDS costs no occupancy.
+constexpr int MOE_GU_XB = 2;
 template <class F>
 __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     F gate, F up, int64_t expert_blocks, const _Float16 *__restrict__ x,
@@ -261,8 +264,8 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-        skinny_run<F, 2, 1, MOE_GU_THREADS, _Float16, true>(fm, wrow0, inter, xr, x, xs, 0, K / 256, acc,
-                                                            lds, rows);
+        skinny_run<F, 2, 1, MOE_GU_THREADS, _Float16, true, 0xFF, false, false, MOE_GU_XB>(
+            fm, wrow0, inter, xr, x, xs, 0, K / 256, acc, lds, rows);
         // the loop ends with a barrier after its last LDS use: hand up to gate
         float *ex = reinterpret_cast<float *>(lds);  // [4 waves][2 tiles][16][64 lanes]
         if (is_up) {
@@ -521,7 +524,7 @@ static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const 
                            const uint16_t *xs, const float *xrs, int top_k, const int32_t *off,
                            const int32_t *sorted, const void *tiles, const int32_t *ntiles,
                            int64_t max_tiles, float *h, hipStream_t s) {
-    constexpr size_t lds = sk_lds<F, 2, 1, MOE_GU_THREADS>();
+    constexpr size_t lds = sk_lds<F, 2, 1, MOE_GU_THREADS, MOE_GU_XB>();
     static_assert(lds >= (size_t)4 * 2 * 16 * 64 * 4, "room for the up -> gate hand-off");
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)moe_gateup_kernel<F>, lds, lds_set)) return err;

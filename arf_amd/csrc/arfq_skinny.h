@@ -376,11 +376,11 @@ struct SkRows {
     int64_t s;      // element offset (row * K / 16) of row min(tid >> 1, XR - 1)
 };
 
-// LDS of the loop: the x block of XR rows (+ its sub-block sums) and one weight
-// slab [32][RB + 16] per wave and weight.
-template <class F, int TA, int NW, int NT = SK_THREADS>
+// LDS of the loop: XB buffers of the x block of XR rows (+ its sub-block sums)
+// and one weight slab [32][RB + 16] per wave and weight.
+template <class F, int TA, int NW, int NT = SK_THREADS, int XB = 1>
 constexpr size_t sk_lds() {
-    return (size_t)32 * TA * SK_XLD * 2 + (size_t)32 * TA * 32 + (size_t)(NT / 64) * NW * 32 * (F::RB + 16);
+    return (size_t)XB * (32 * TA * SK_XLD * 2 + 32 * TA * 32) + (size_t)(NT / 64) * NW * 32 * (F::RB + 16);
 }
 
 // Accumulates acc[w][t] (w < NW weights, t < TA 32-row x tiles) over the
@@ -394,9 +394,11 @@ constexpr size_t sk_lds() {
 // with two accumulator tiles, hold the scheduler to one step's operands at a
 // time (left free, it hoists all four steps' operand builds and x reads; the
 // dense skinny GEMM at C3 m = 64 ran 57.6 -> 53.0 us with the step boundary
-// held, the MoE tiles 1 % slower).
+// held, the MoE tiles 1 % slower).  XB = 2: two x buffers; the next block's x
+// goes into the one not being read, which leaves one barrier per block
+// instead of two, for a second x buffer of LDS.
 template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF, bool MERGE = false,
-          bool PIN = false>
+          bool PIN = false, int XB = 1>
 __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                             int64_t nrows, const SkRows<TA, NT> &rows,
                                             const XT *__restrict__ x,
@@ -411,9 +413,11 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
     constexpr int SL = F::RB + 16;          // slab row stride (bytes)
     const int tid = sk_tid(), lane = tid & 63, wave = tid >> 6;
     const int h = lane >> 5, lr = lane & 31;
-    _Float16 *xl = lds;                                              // [XR][SK_XLD]
-    uint16_t *sl = reinterpret_cast<uint16_t *>(lds + XR * SK_XLD);  // [XR][16]
-    uint8_t *slab = reinterpret_cast<uint8_t *>(sl + XR * 16) + (size_t)wave * NW * 32 * SL;
+    static_assert(XB == 1 || XB == 2, "one or two x buffers");
+    _Float16 *xl = lds;                                                   // [XB][XR][SK_XLD]
+    uint16_t *sl = reinterpret_cast<uint16_t *>(lds + XB * XR * SK_XLD);  // [XB][XR][16]
+    uint8_t *slab = reinterpret_cast<uint8_t *>(sl + XB * XR * 16) + (size_t)wave * NW * 32 * SL;
+    int xb = 0;  // the x buffer this block reads
 
     // x chunks of 8 elements: one 16-byte load of f16, two of f32 (rounded to
     // f16 when stored to LDS)
@@ -435,7 +439,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
             if (tid < 64 * TU) sv = *reinterpret_cast<const u32x4 *>(xs + rows.s + 16 * b + 8 * (tid & 1));
         }
     };
-    auto xstore = [&]() {
+    auto xstore = [&](int to) {
 #pragma unroll
         for (int i = 0; i < XU; i++) {
             u32x4 v;
@@ -448,10 +452,10 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                     v[j] = pack_f16x2(__uint_as_float(f[2 * (j & 1)]), __uint_as_float(f[2 * (j & 1) + 1]));
                 }
             }
-            *reinterpret_cast<u32x4 *>(xl + ((tid >> 5) + (NT / 32) * i) * SK_XLD + 8 * (tid & 31)) = v;
+            *reinterpret_cast<u32x4 *>(xl + (to * XR + (tid >> 5) + (NT / 32) * i) * SK_XLD + 8 * (tid & 31)) = v;
         }
         if constexpr (KIND == 2) {
-            if (tid < 64 * TU) *reinterpret_cast<u32x4 *>(sl + (tid >> 1) * 16 + 8 * (tid & 1)) = sv;
+            if (tid < 64 * TU) *reinterpret_cast<u32x4 *>(sl + (to * XR + (tid >> 1)) * 16 + 8 * (tid & 1)) = sv;
         }
     };
 
@@ -487,7 +491,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
     for (int w = 0; w < NW; w++) wb[w] = fmt[w].load_blk(myrow[w], b0);
     wload(b0);
     xload(b0);
-    xstore();
+    xstore(0);
     __syncthreads();
 
     // KIND 3: cb holds the step's first sub-block (MFMAs 0, 1), cq its second
@@ -532,7 +536,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
                         for (int t = 0; t < TU; t++) {
                             const half8 af = *reinterpret_cast<const half8 *>(
-                                xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
+                                xl + (xb * XR + 32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
                             const int ti = MERGE ? 0 : t;
                             c[ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], MERGE && t > 0 ? c[0] : z,
                                                                            0, 0, 0);
@@ -547,7 +551,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
                         for (int t = 0; t < TU; t++) {
                             const half8 af = *reinterpret_cast<const half8 *>(
-                                xl + (32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
+                                xl + (xb * XR + 32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
                             const int ti = MERGE ? 0 : t;
                             const bool cont = MERGE && t > 0;  // tile 1 adds onto tile 0's chain
                             floatx16 z;
@@ -588,7 +592,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                     F::minsb(wb[w], bh, bl);
 #pragma unroll
                     for (int t = 0; t < TU; t++) {
-                        const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sl + (32 * t + lr) * 16 + 8 * h);
+                        const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sl + (xb * XR + 32 * t + lr) * 16 + 8 * h);
                         const int ti = MERGE ? 0 : t;
                         cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][ti], 0, 0, 0);
                         cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][ti], 0, 0, 0);
@@ -602,9 +606,15 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
         }
 #pragma unroll
         for (int w = 0; w < NW; w++) wb[w] = wbn[w];
-        __syncthreads();  // every wave is done with this block's x
-        xstore();
-        __syncthreads();
+        if constexpr (XB == 2) {
+            xstore(xb ^ 1);  // nobody reads that buffer: its block ended at the last barrier
+            xb ^= 1;
+            __syncthreads();
+        } else {
+            __syncthreads();  // every wave is done with this block's x
+            xstore(0);
+            __syncthreads();
+        }
     }
     if constexpr (KIND == 2) {
 #pragma unroll
@@ -622,7 +632,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 // is).  All threads of the workgroup call it with the same block range and
 // xrows.
 template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF,
-          bool MERGE = false, bool PIN = false>
+          bool MERGE = false, bool PIN = false, int XB = 1>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
                                            const XT *__restrict__ x,
@@ -630,11 +640,11 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
                                            floatx16 (&acc)[NW][TA], _Float16 *lds, int xrows) {
     if constexpr (TA == 2 && SHORT) {
         if (xrows <= 32) {
-            skinny_loop<F, TA, 1, NW, NT, XT, GM>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+            skinny_loop<F, TA, 1, NW, NT, XT, GM, false, false, XB>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
             return;
         }
     }
-    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE, PIN>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE, PIN, XB>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
 }
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.
