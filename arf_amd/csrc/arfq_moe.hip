@@ -236,6 +236,11 @@ constexpr int MOE_GU_THREADS = 512;
 // Two x buffers (one barrier per block instead of two): C5 183.2 -> 182.4 us;
 // the workgroup holds a CU by its registers, so the LDS costs no occupancy.
 constexpr int MOE_GU_XB = 2;
+// LDS of gate|up: the loop's, then the tile rows' x scales [MOE_BM] floats.
+template <class F>
+__host__ __device__ constexpr size_t gu_scale_off() {
+    return sk_lds<F, 2, 1, MOE_GU_THREADS, MOE_GU_XB>();
+}
 template <class F>
 __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     F gate, F up, int64_t expert_blocks, const _Float16 *__restrict__ x,
@@ -259,6 +264,11 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
             sk_rows<2, MOE_GU_THREADS>(rows, K, [&](int r) { return sorted[row0 + r] / top_k; });
         const F fm[1] = {(is_up ? up : gate).shifted((int64_t)e * expert_blocks)};
         const int64_t wrow0[1] = {n0};
+        // the tile rows' x scales, by up wave 0 into LDS past the loop's own:
+        // one division and one dependent load pair per row, not per output,
+        // and before the loop rather than after it
+        float *exs = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + gu_scale_off<F>());
+        if (xrs && wave == 4 && lane < rows) exs[lane] = xrs[sorted[row0 + lane] / top_k];
         floatx16 acc[1][2];
 #pragma unroll
         for (int t = 0; t < 2; t++)
@@ -285,7 +295,7 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
                     if (r < rows && n < inter) {
                         float g = acc[0][t][i], u = ex[((wq * 2 + t) * 16 + i) * 64 + lane];
                         if (xrs) {  // the token row was stored divided by xrs (exact)
-                            const float sc = xrs[sorted[row0 + r] / top_k];
+                            const float sc = reinterpret_cast<const float4 *>(exs)[r >> 2][i & 3];
                             g *= sc;
                             u *= sc;
                         }
@@ -404,6 +414,14 @@ __global__ __launch_bounds__(SK_THREADS, 2) void moe_down_kernel(
     const int rows = min(MOE_BM, off[e + 1] - row0);
     const int n0 = blockIdx.y * 128 + 32 * wave;
     const SkRows<2> xr = sk_rows<2>(rows, K, [&](int r) { return row0 + r; });
+    // the output row and h scale of tile row `tid`, loaded before the loop and
+    // handed over through LDS after it (not two loads per output at the end)
+    int orow = 0;
+    float ors = 0.f;
+    if (tid < rows) {
+        orow = sorted[row0 + tid];
+        ors = rs[row0 + tid];
+    }
     const F fm[1] = {down.shifted((int64_t)e * expert_blocks)};
     const int64_t wrow0[1] = {n0};
     floatx16 acc[1][2];
@@ -414,14 +432,21 @@ __global__ __launch_bounds__(SK_THREADS, 2) void moe_down_kernel(
     // (Q6_K: the second loop copy would not fit the registers)
     skinny_run<F, 2, 1, SK_THREADS, _Float16, F::KIND != 4>(fm, wrow0, hidden, xr, h, hs, 0, K / 256,
                                                            acc, lds, rows);
+    // the loop ends with a barrier after its last LDS use
+    int *lrow = reinterpret_cast<int *>(lds);                // [64]
+    float *lrs = reinterpret_cast<float *>(lds) + MOE_BM;    // [64]
+    if (tid < MOE_BM) {
+        lrow[tid] = orow;
+        lrs[tid] = ors;
+    }
+    __syncthreads();
     const int n = n0 + (lane & 31);
 #pragma unroll
     for (int t = 0; t < 2; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
             const int r = sk_out_row(t, i);
-            if (r < rows && n < hidden)
-                o[(int64_t)sorted[row0 + r] * hidden + n] = acc[0][t][i] * rs[row0 + r];
+            if (r < rows && n < hidden) o[(int64_t)lrow[r] * hidden + n] = acc[0][t][i] * lrs[r];
         }
 }
 
@@ -524,8 +549,9 @@ static hipError_t gateup_t(const F &g, const F &u, const arfq_weight *gw, const 
                            const uint16_t *xs, const float *xrs, int top_k, const int32_t *off,
                            const int32_t *sorted, const void *tiles, const int32_t *ntiles,
                            int64_t max_tiles, float *h, hipStream_t s) {
-    constexpr size_t lds = sk_lds<F, 2, 1, MOE_GU_THREADS, MOE_GU_XB>();
-    static_assert(lds >= (size_t)4 * 2 * 16 * 64 * 4, "room for the up -> gate hand-off");
+    constexpr size_t lds = gu_scale_off<F>() + MOE_BM * 4;
+    static_assert(gu_scale_off<F>() >= (size_t)4 * 2 * 16 * 64 * 4, "room for the up -> gate hand-off");
+    static_assert(gu_scale_off<F>() % 4 == 0, "aligned x scales");
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)moe_gateup_kernel<F>, lds, lds_set)) return err;
     const int64_t eb = gw->n * g.nblk;
