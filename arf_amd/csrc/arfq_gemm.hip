@@ -112,6 +112,10 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
         PAIR ? sk_rows<TA>(PO + M, K, [M](int r) { return r < M ? r : r >= PO ? M + r - PO : 0; })
              : sk_rows<TA>(M, K, [](int r) { return r; });
     const int n = n0 + 32 * wave + (lane & 31);
+    // the x rows' scales of this K range into LDS past the loop's own, before
+    // the loop: the epilogue reads them there instead of loading per output
+    float *lrs = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + sk_lds<F, TA, 1>());
+    if (rs && tid < 32 * TA) lrs[tid] = tid < M ? rs[(int64_t)sp * rss + tid] : 1.f;
     const F fm[1] = {fmt};
     const int64_t wrow0[1] = {n0 + 32 * wave};
     floatx16 acc[1][TA];
@@ -133,7 +137,10 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int m = sk_out_row(t, i);
-                if (m < M && n < N) y[(int64_t)m * N + n] = rs ? acc[0][t][i] * rs[m] : acc[0][t][i];
+                // (m & 3 == i & 3: one 16-byte LDS read serves four rows)
+                if (m < M && n < N)
+                    y[(int64_t)m * N + n] =
+                        rs ? acc[0][t][i] * reinterpret_cast<const float4 *>(lrs)[m >> 2][i & 3] : acc[0][t][i];
             }
         return;
     }
@@ -144,7 +151,7 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
 #pragma unroll
             for (int i = 0; i < 16; i++) {
                 const int m = sk_out_row(t, i);
-                acc[0][t][i] *= m < M ? rs[(int64_t)sp * rss + m] : 1.f;
+                acc[0][t][i] *= reinterpret_cast<const float4 *>(lrs)[m >> 2][i & 3];  // 1 past M
             }
     }
     // Split K.  Each wave stores its accumulators as they sit in registers:
@@ -385,7 +392,7 @@ static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, con
         // touches only the accumulator groups that hold them
         if (m <= 8) return launch_sk_t<F, 1, PAIR, PAIR ? 0x5 : 0x1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
     }
-    constexpr size_t lds = sk_lds<F, TA, 1>();
+    constexpr size_t lds = sk_lds<F, TA, 1>() + 32 * TA * 4;  // + the x rows' scales
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PAIR, GM>, lds, lds_set))
         return err;
