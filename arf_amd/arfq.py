@@ -94,6 +94,10 @@ _SIGS = {
     "arfq_copy_h2d": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
     "arfq_copy_d2h": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
     "arfq_copy_d2d": (_int, [_vp, _vp, _vp, ctypes.c_size_t]),
+    "arfq_stream_read": (_int, [_vp, _vp, ctypes.c_size_t, _vp, _int]),
+    "arfq_ctx_device_info": (_int, [_vp, ctypes.POINTER(_int), ctypes.POINTER(_int), ctypes.POINTER(_int)]),
+    "arfq_ctx_memory": (_int, [_vp, ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t),
+                               ctypes.POINTER(ctypes.c_size_t)]),
     "arfq_timer_start": (_int, [_vp]),
     "arfq_timer_stop": (_int, [_vp, ctypes.POINTER(ctypes.c_float)]),
     "arfq_matmul_repeat": (_int, [_vp, ctypes.POINTER(_vp), _int, _int, _i64, _vp, _int, _vp]),
@@ -336,6 +340,31 @@ class Context:
         if nb > dst.nbytes or nb > src.nbytes:
             raise ValueError("copy_d2d: size")
         _check(self.handle, load_library().arfq_copy_d2d(self.handle, dst.ptr, src.ptr, nb))
+
+    def stream_read(self, src, nbytes=None, stamps=None):
+        """Enqueue one read-only pass over nbytes of src (arfq_stream_read); `stamps`
+        (a uint64 device array of 4 * g entries) receives workgroup g's
+        (realtime, clock) at start and end for the first g workgroups."""
+        nb = src.nbytes if nbytes is None else int(nbytes)
+        if nb > src.nbytes:
+            raise ValueError("stream_read: size")
+        ns = 0 if stamps is None else stamps.nbytes // 32
+        _check(self.handle, load_library().arfq_stream_read(
+            self.handle, src.ptr, nb, None if stamps is None else stamps.ptr, ns))
+
+    def device_info(self):
+        """(compute units, peak shader clock kHz, s_memrealtime frequency kHz)."""
+        cus, sclk, wclk = _int(), _int(), _int()
+        _check(self.handle, load_library().arfq_ctx_device_info(
+            self.handle, ctypes.byref(cus), ctypes.byref(sclk), ctypes.byref(wclk)))
+        return cus.value, sclk.value, wclk.value
+
+    def memory(self):
+        """(context scratch bytes, device free bytes, device total bytes)."""
+        sb, fr, tot = ctypes.c_size_t(), ctypes.c_size_t(), ctypes.c_size_t()
+        _check(self.handle, load_library().arfq_ctx_memory(
+            self.handle, ctypes.byref(sb), ctypes.byref(fr), ctypes.byref(tot)))
+        return sb.value, fr.value, tot.value
 
     # -- timing --
     def timer_start(self):

@@ -92,7 +92,7 @@ __global__ __launch_bounds__(GM_THREADS, F::WG_PER_CU) void gemm_q(
 // sums the S partials in split order into y, so the result does not depend on
 // the arrival order.
 // (held to 256 VGPRs: two workgroups per CU)
-template <class F, int TA, class XT, bool PAIR, int GM = 0xFF>
+template <class F, int TA, class XT, int PARTS, int GM = 0xFF>
 __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__restrict__ x,
                                                       const uint16_t *__restrict__ xs,
                                                       const float *__restrict__ rs,
@@ -105,12 +105,21 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
     const int n0 = blockIdx.x * 128;
     const int nb = K / 256, S = gridDim.y, sp = blockIdx.y;
     const int b0 = (int)((int64_t)sp * nb / S), b1 = (int)((int64_t)(sp + 1) * nb / S);
-    // PAIR (M <= 16 TA): x row r < M stages hi row r of x, row PO + r its lo row
-    // M + r (PO = 16 in one 32-row tile, 32 = the second tile with two)
-    constexpr int PO = 16 * TA;
+    // PARTS 2 (M <= 16 TA): x row r < M stages hi row r of x, row PO + r its lo
+    // row M + r (PO = 16 in one 32-row tile, 32 = the second tile with two).
+    // PARTS 3 (M <= 8, one tile): rows r, 8 + r and 16 + r stage the hi, mid and
+    // lo rows r, M + r and 2M + r; a lane's accumulator holds rows r, r + 8 and
+    // r + 16 of its column as elements i, i + 4 and i + 8.  Rows that stage
+    // nothing read row 0 (their products land in rows never stored).
+    constexpr bool PAIR = PARTS == 2;
+    constexpr int PO = PARTS == 3 ? 8 : 16 * TA;
+    static_assert(PARTS != 3 || TA == 1, "three parts fit one tile");
     const SkRows<TA> rows =
-        PAIR ? sk_rows<TA>(PO + M, K, [M](int r) { return r < M ? r : r >= PO ? M + r - PO : 0; })
-             : sk_rows<TA>(M, K, [](int r) { return r; });
+        PARTS == 3 ? sk_rows<TA>(16 + M, K, [M](int r) {
+            return r < M ? r : r < 8 ? 0 : r < 8 + M ? M + r - 8 : r < 16 ? 0 : 2 * M + r - 16;
+        })
+        : PAIR ? sk_rows<TA>(PO + M, K, [M](int r) { return r < M ? r : r >= PO ? M + r - PO : 0; })
+               : sk_rows<TA>(M, K, [](int r) { return r; });
     const int n = n0 + 32 * wave + (lane & 31);
     // the x rows' scales of this K range into LDS past the loop's own, before
     // the loop: the epilogue reads them there instead of loading per output
@@ -125,11 +134,15 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // PAIR with two tiles: the lo tile's products go into tile 0's accumulators
     skinny_run<F, TA, 1, SK_THREADS, XT, false, GM, PAIR && TA == 2, true>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
-                                                                    PAIR ? PO + M : M);
+                                                                    PARTS == 3 ? 16 + M : PAIR ? PO + M : M);
     if constexpr (PAIR && TA == 1) {
         // rows r and r + 16 of a lane's accumulator are elements i and i + 8
 #pragma unroll
         for (int i = 0; i < 8; i++) acc[0][0][i] += acc[0][0][i + 8];
+    }
+    if constexpr (PARTS == 3) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[0][0][i] = (acc[0][0][i] + acc[0][0][i + 4]) + acc[0][0][i + 8];
     }
     if (S == 1) {
 #pragma unroll
@@ -237,9 +250,10 @@ __global__ void splitk_reduce(const float *__restrict__ part, float *__restrict_
 }
 
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
-                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair, int rs_splits) {
+                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, int parts, int rs_splits) {
     if (m == 0 || (!xh && !xl && !xs)) return hipSuccess;
-    if (k % 32 || k > INT32_MAX || (pair && (!xh || xl != xh + m * k))) return hipErrorInvalidValue;
+    if (parts < 1 || parts > 3 || (parts == 3 && x_dtype != ARFQ_F32)) return hipErrorInvalidValue;
+    if (k % 32 || k > INT32_MAX || (parts > 1 && (!xh || xl != xh + m * k))) return hipErrorInvalidValue;
     if (x_dtype != ARFQ_F32 && !xh && !xl && !rs) {  // the sums of an f16 x alone
         xsums_kernel<XSUM_WAVES><<<(unsigned)((m + XSUM_WAVES - 1) / XSUM_WAVES), 64 * XSUM_WAVES, 0, s>>>(
             (const _Float16 *)x, m, (int)k, xs);
@@ -265,10 +279,10 @@ hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float
     const unsigned grid = (unsigned)(m * S);
     if (x_dtype == ARFQ_F32)
         xprep_kernel<float><<<grid, XPREP_THREADS, 0, s>>>((const float *)x, m, (int)k, xh, xl, xs, rs,
-                                                           pair ? 1 : 0, S, unit);
+                                                           parts - 1, S, unit);
     else
         xprep_kernel<_Float16><<<grid, XPREP_THREADS, 0, s>>>((const _Float16 *)x, m, (int)k, xh, xl,
-                                                              xs, nullptr, pair ? 1 : 0, S, unit);
+                                                              xs, nullptr, parts - 1, S, unit);
     return hipGetLastError();
 }
 
@@ -327,7 +341,8 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     // to the reference's f32 batched GEMV as the f16 MFMA gets): at m <= 16 the
     // lo rows fill the other half of the 32-row x tile staged anyway (no extra
     // MFMAs), at m <= 32 a second tile (twice the MFMAs)
-    p.pair = p.skinny && x_dtype == ARFQ_F32 && m <= 32;
+    // m <= 8 (one 32-row tile holds three row blocks of 8): hi + mid + lo, exact
+    p.parts = p.skinny && x_dtype == ARFQ_F32 ? (m <= 8 ? 3 : m <= 32 ? 2 : 1) : 1;
     // the exact Q4_K paths read x sub-block sums (min term)
     p.sums = (p.skinny || p.bd) && kind2;
     int64_t S;
@@ -366,11 +381,11 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     p.splits = (int)std::min<int64_t>(S, 16);
     size_t o = 0;
     p.off_xh = o;
-    o += p.convert ? al256((size_t)(p.pair ? 2 : 1) * m * w->k * 2) : 0;  // pair: lo rows follow
+    o += p.convert ? al256((size_t)p.parts * m * w->k * 2) : 0;  // the lo (mid, lo) rows follow
     p.off_xl = o;
     o += p.xsplit ? al256((size_t)m * w->k * 2) : 0;
     p.off_xs = o;
-    o += p.sums ? al256((size_t)(p.pair ? 2 : 1) * m * (w->k / 16) * 2) : 0;
+    o += p.sums ? al256((size_t)p.parts * m * (w->k / 16) * 2) : 0;
     p.off_rs = o;  // skinny: one scale per row and split
     o += p.convert ? al256((size_t)(p.skinny ? p.splits : 1) * m * 4) : 0;
     p.off_part = o;
@@ -383,41 +398,47 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     return p;
 }
 
-template <class F, int TA, bool PAIR, int GM = 0xFF>
+template <class F, int TA, int PARTS, int GM = 0xFF>
 static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                               const uint16_t *xs, const float *rs, int rss, float *y, float *part,
                               uint32_t *tick, int S, hipStream_t s) {
     if constexpr (F::KIND == 4 && TA == 1 && GM == 0xFF) {
-        // at most 8 rows (8 hi + 8 lo with PAIR): the per-sub-block scaling
-        // touches only the accumulator groups that hold them
-        if (m <= 8) return launch_sk_t<F, 1, PAIR, PAIR ? 0x5 : 0x1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+        // at most 8 rows (8 hi + 8 lo with two parts, + 8 mid with three): the
+        // per-sub-block scaling touches only the accumulator groups that hold them
+        if (m <= 8)
+            return launch_sk_t<F, 1, PARTS, PARTS == 3 ? 0x7 : PARTS == 2 ? 0x5 : 0x1>(fmt, w, m, x, xs, rs, rss, y,
+                                                                                      part, tick, S, s);
     }
     constexpr size_t lds = sk_lds<F, TA, 1>() + 32 * TA * 4;  // + the x rows' scales
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
-    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PAIR, GM>, lds, lds_set))
+    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PARTS, GM>, lds, lds_set))
         return err;
     const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
-    gemm_sk<F, TA, _Float16, PAIR, GM><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
+    gemm_sk<F, TA, _Float16, PARTS, GM><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
                                                                      (int)w->n, (int)w->k, rss);
     return hipGetLastError();
 }
 
 // S > 1 splits need S <= 16 and one zeroed counter per 128-column tile.  x is
 // f16 (an f32 x arrives prepared and scaled, rs[split * rss + row] its scale
-// over each split's K range); with pair (m <= 32) it is [2m, K]: the hi rows,
-// then the lo rows.
+// over each split's K range); with parts 2 (m <= 32) it is [2m, K]: the hi
+// rows, then the lo rows; with parts 3 (m <= 8) [3m, K]: hi, mid, lo rows.
 template <class F>
 static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                             const uint16_t *xs, const float *rs, int rss, float *y, float *part,
-                            uint32_t *tick, int ntick, int S, hipStream_t s, bool pair) {
+                            uint32_t *tick, int ntick, int S, hipStream_t s, int parts) {
     if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;
-    if (pair) {
-        if (m > 32) return hipErrorInvalidValue;
-        return m <= 16 ? launch_sk_t<F, 1, true>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
-                       : launch_sk_t<F, 2, true>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+    if (parts == 3) {
+        if (m > 8) return hipErrorInvalidValue;
+        return launch_sk_t<F, 1, 3>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
     }
-    return m <= 32 ? launch_sk_t<F, 1, false>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
-                   : launch_sk_t<F, 2, false>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+    if (parts == 2) {
+        if (m > 32) return hipErrorInvalidValue;
+        return m <= 16 ? launch_sk_t<F, 1, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
+                       : launch_sk_t<F, 2, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+    }
+    return m <= 32 ? launch_sk_t<F, 1, 1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
+                   : launch_sk_t<F, 2, 1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
 }
 
 SkQ4K sk_q4k(const arfq_weight *w) {
@@ -524,11 +545,11 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     char *sc = (char *)scratch;
     if (p.scratch_bytes && !sc) return hipErrorInvalidValue;
     _Float16 *xh = p.convert ? (_Float16 *)(sc + p.off_xh) : (_Float16 *)x;
-    _Float16 *xl = p.xsplit ? (_Float16 *)(sc + p.off_xl) : p.pair ? xh + m * w->k : nullptr;
+    _Float16 *xl = p.xsplit ? (_Float16 *)(sc + p.off_xl) : p.parts > 1 ? xh + m * w->k : nullptr;
     uint16_t *xs = p.sums ? (uint16_t *)(sc + p.off_xs) : nullptr;
     float *rs = p.convert ? (float *)(sc + p.off_rs) : nullptr;  // row scales of an f32 x
     if (p.convert || p.sums) {
-        hipError_t err = launch_xprep(x, x_dtype, m, w->k, p.convert ? xh : nullptr, xl, xs, rs, s, p.pair,
+        hipError_t err = launch_xprep(x, x_dtype, m, w->k, p.convert ? xh : nullptr, xl, xs, rs, s, p.parts,
                                       p.skinny ? p.splits : 1);
         if (err != hipSuccess) return err;
     }
@@ -541,19 +562,19 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         switch (w->qtype) {
         case ARFQ_Q4_K:
             return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.pair);
+                             p.splits, s, p.parts);
         case ARFQ_Q6_K:
             return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.pair);
+                             p.splits, s, p.parts);
         case ARFQ_Q8_0:
             return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xs, rs,
-                             (int)m, y, out, tickets, ntickets, p.splits, s, p.pair);
+                             (int)m, y, out, tickets, ntickets, p.splits, s, p.parts);
         case ARFQ_Q5_K:
             return launch_sk(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.pair);
+                             p.splits, s, p.parts);
         case ARFQ_IQ4_XS:
             return launch_sk(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.pair);
+                             p.splits, s, p.parts);
         default:
             return hipErrorInvalidValue;
         }

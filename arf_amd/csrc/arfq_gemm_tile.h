@@ -686,10 +686,12 @@ __device__ __forceinline__ int tile_out_col(int b) {
 // sub-block sum X (of the values the MFMAs will see: each lane's 8 in order,
 // then the quad's four partial sums pairwise) as bf16 hi + lo into
 // xs[row][k / 256][j] and [8 + j] (j = sub-block within block).
-// With `pair` set, xl must be xh + M * K: the lo remainders are stored as rows
-// M .. 2M - 1 after the hi rows, and xs holds the sums of each hi row at row r
-// and of each lo row at row M + r (xs then has 2M rows); otherwise the sums
-// are of hi + lo.
+// With `pair` set (1: two parts, 2: three), xl must be xh + M * K: the lo
+// remainders x - hi (with three parts rounded to f16 as the mid part, whose
+// remainder x - hi - mid follows as rows 2M .. 3M - 1) are stored as rows
+// M .. 2M - 1 after the hi rows, and xs holds the sums of each hi row at row
+// r, of each lo (mid) row at row M + r and of each third-part row at 2M + r;
+// otherwise the sums are of hi + lo.
 // With `rs` set (f32 x), each segment is first scanned for its max |x| and
 // its elements are stored divided by rs[sp * M + row] = 2^(e - 15), e the
 // exponent of that max (max in [2^(e-1), 2^e)): an exact power-of-two scaling
@@ -817,18 +819,24 @@ __global__ __launch_bounds__(XPREP_THREADS) void xprep_kernel(
             const int ch = base + tid + XPREP_THREADS * j;
             if (ch >= c1) break;
             const int64_t g = row * nch + ch;
-            half8 hv, lv;
-            float sum = 0.f, suml = 0.f;
+            half8 hv, lv, ov;  // hi, lo (the mid part with three parts), lo of three
+            float sum = 0.f, suml = 0.f, sumo = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 const float u = sh ? ldexpf(v[j][i], sh) : v[j][i];
                 hv[i] = (_Float16)u;
-                lv[i] = (_Float16)(u - (float)hv[i]);
+                const float r1 = u - (float)hv[i];  // exact
+                lv[i] = (_Float16)r1;
                 sum += (xl && !pair) ? ((float)hv[i] + (float)lv[i]) : (float)hv[i];
                 suml += (float)lv[i];
+                if (pair == 2) {
+                    ov[i] = (_Float16)(r1 - (float)lv[i]);  // r1 - lo exact; two bits or fewer
+                    sumo += (float)ov[i];
+                }
             }
             if (xh) reinterpret_cast<half8 *>(xh)[g] = hv;
             if (xl) reinterpret_cast<half8 *>(xl)[g] = lv;
+            if (pair == 2) reinterpret_cast<half8 *>(xl)[g + M * nch] = ov;
             if (xs) {
                 // (s0 + s1) + (s2 + s3) on every lane of the quad (quad_perm [1,0,3,2], then [2,3,0,1])
                 auto quad_sum = [](float t) {
@@ -837,6 +845,7 @@ __global__ __launch_bounds__(XPREP_THREADS) void xprep_kernel(
                 };
                 sum = quad_sum(sum);
                 if (pair) suml = quad_sum(suml);
+                if (pair == 2) sumo = quad_sum(sumo);
                 if ((ch & 3) == 0) {
                     const int sub = ch >> 2;
                     auto put = [&](int64_t r, float t) {
@@ -848,6 +857,7 @@ __global__ __launch_bounds__(XPREP_THREADS) void xprep_kernel(
                     };
                     put(row, sum);
                     if (pair) put(M + row, suml);
+                    if (pair == 2) put(2 * M + row, sumo);
                 }
             }
         }

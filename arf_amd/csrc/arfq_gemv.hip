@@ -1668,16 +1668,38 @@ static bool dot_ok(const arfq_weight *w, int64_t m) {
     return false;
 }
 
-bool gemv_supports(const arfq_weight *w, int64_t m) {
+// The 16-bit fixed-point x kernels (gemv_q4k / gemv_dot): only under
+// ARFQ_OPT_GEMV_X16, and only where their LDS fits the default 64 KiB (they are
+// launched without raising the limit) and one expert's code stream fits the
+// 31-bit buffer offsets.
+static bool q4k_x16_ok(const arfq_weight *w, int64_t m) {
+    return w->qtype == ARFQ_Q4_K && m >= 1 && m <= GEMV_MAX_M && q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
+           w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
+}
+
+// Which (qtype, m) the GEMV family takes.  Without x16 every path multiplies
+// f32 x in f32: Q4_K / Q5_K / IQ4_XS / Q6_K at m = 1 (the exact-code f32
+// kernels, while their LDS fits), Q6_K at m = 2..4 (gemv_q6k) and Q8_0 at
+// m <= 4 (gemv_q80w).  Q4_K / Q5_K / IQ4_XS at m = 2..4, and m = 1 shapes too
+// long for the f32 kernels' LDS, go to the skinny MFMA GEMM (x as f16 hi + lo).
+// With x16 the 16-bit kernels take the shapes they fit; the rest keep the
+// f32 path.
+bool gemv_supports(const arfq_weight *w, int64_t m, bool x16) {
     if (m < 1 || m > GEMV_MAX_M) return false;
-    // the buffer loads address one expert's code stream with 32-bit offsets
-    if (w->qtype == ARFQ_Q4_K && m == 1 && q4k_f32_ok(w)) return true;
-    if (w->qtype == ARFQ_Q4_K)
-        return q4k_gemv_lds(w, m <= 2 ? (int)m : 4) <= 64 * 1024 &&
-               w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
-    if ((w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS) && m == 1 && dot_f32_ok(w)) return true;
-    if (w->qtype == ARFQ_Q5_K || w->qtype == ARFQ_IQ4_XS) return dot_ok(w, m);
-    return w->qtype == ARFQ_Q8_0 || w->qtype == ARFQ_Q6_K;
+    switch (w->qtype) {
+    case ARFQ_Q4_K:
+        if (x16 && q4k_x16_ok(w, m)) return true;
+        return m == 1 && q4k_f32_ok(w);
+    case ARFQ_Q5_K:
+    case ARFQ_IQ4_XS:
+        if (x16 && dot_ok(w, m)) return true;
+        return m == 1 && dot_f32_ok(w);
+    case ARFQ_Q6_K:  // gemv_q6k takes what the dot kernels do not
+    case ARFQ_Q8_0:
+        return true;
+    default:
+        return false;
+    }
 }
 
 template <int R, int MX>
@@ -2002,17 +2024,19 @@ static hipError_t launch_glu_mx(const arfq_weight *w, int m, const float *g, con
 template <int ACT>
 static hipError_t launch_gemv_glu_t(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y,
                                     hipStream_t s, bool x16) {
-    if (m == 1 && !x16 && q4k_f32_ok(w)) return launch_q4k_f32_glu<ACT>(w, g, u, y, s);
-    if (m == 1) return launch_glu_mx<1, ACT>(w, 1, g, u, y, s);
-    if (m == 2) return launch_glu_mx<2, ACT>(w, 2, g, u, y, s);
-    return launch_glu_mx<4, ACT>(w, (int)m, g, u, y, s);
+    if (x16 && q4k_x16_ok(w, m)) {
+        if (m == 1) return launch_glu_mx<1, ACT>(w, 1, g, u, y, s);
+        if (m == 2) return launch_glu_mx<2, ACT>(w, 2, g, u, y, s);
+        return launch_glu_mx<4, ACT>(w, (int)m, g, u, y, s);
+    }
+    return launch_q4k_f32_glu<ACT>(w, g, u, y, s);  // m == 1, q4k_f32_ok
 }
-bool gemv_glu_supports(const arfq_weight *w, int64_t m) {
-    return w->qtype == ARFQ_Q4_K && w->experts == 1 && gemv_supports(w, m);
+bool gemv_glu_supports(const arfq_weight *w, int64_t m, bool x16) {
+    return w->qtype == ARFQ_Q4_K && w->experts == 1 && gemv_supports(w, m, x16);
 }
 hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y, int act,
                            hipStream_t s, bool x16) {
-    if (!gemv_glu_supports(w, m)) return hipErrorInvalidValue;
+    if (!gemv_glu_supports(w, m, x16)) return hipErrorInvalidValue;
     if (act == ACT_GELU_TANH) return launch_gemv_glu_t<ACT_GELU_TANH>(w, m, g, u, y, s, x16);
     if (act == ACT_SILU) return launch_gemv_glu_t<ACT_SILU>(w, m, g, u, y, s, x16);
     return hipErrorInvalidValue;
@@ -2069,37 +2093,46 @@ hipError_t launch_gemv_pairs(const arfq_weight *w, int64_t P, const int32_t *ids
 
 hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, float *y,
                        hipStream_t s, bool x16) {
-    if (!gemv_supports(w, m)) return hipErrorInvalidValue;
+    if (!gemv_supports(w, m, x16)) return hipErrorInvalidValue;
     if (w->qtype == ARFQ_Q4_K) {
-        if (m == 1 && !x16 && q4k_f32_ok(w)) return launch_q4k_f32(w, e, x, y, s);
-        if (m == 1) return launch_gemv_q4k<1>(w, e, 1, x, y, s);
-        if (m == 2) return launch_gemv_q4k<2>(w, e, 2, x, y, s);
-        return launch_gemv_q4k<4>(w, e, (int)m, x, y, s);
+        if (x16 && q4k_x16_ok(w, m)) {
+            if (m == 1) return launch_gemv_q4k<1>(w, e, 1, x, y, s);
+            if (m == 2) return launch_gemv_q4k<2>(w, e, 2, x, y, s);
+            return launch_gemv_q4k<4>(w, e, (int)m, x, y, s);
+        }
+        return launch_q4k_f32(w, e, x, y, s);  // m == 1, q4k_f32_ok
     }
     if (w->qtype == ARFQ_Q5_K) {
         const DotQ5K f = dot_q5k(w, e);
-        if (m == 1 && !x16 && dot_f32_ok(w)) return launch_dot_f32(f, w, x, y, s);
-        if (m == 1) return launch_dot<DotQ5K, 1>(f, w, 1, x, y, s);
-        if (m == 2) return launch_dot<DotQ5K, 2>(f, w, 2, x, y, s);
-        return launch_dot<DotQ5K, 4>(f, w, (int)m, x, y, s);
+        if (x16 && dot_ok(w, m)) {
+            if (m == 1) return launch_dot<DotQ5K, 1>(f, w, 1, x, y, s);
+            if (m == 2) return launch_dot<DotQ5K, 2>(f, w, 2, x, y, s);
+            return launch_dot<DotQ5K, 4>(f, w, (int)m, x, y, s);
+        }
+        return launch_dot_f32(f, w, x, y, s);  // m == 1, dot_f32_ok
     }
     if (w->qtype == ARFQ_IQ4_XS) {
         const DotIQ4XS f = dot_iq4xs(w, e);
-        if (m == 1 && !x16 && dot_f32_ok(w)) return launch_dot_f32(f, w, x, y, s);
-        if (m == 1) return launch_dot<DotIQ4XS, 1>(f, w, 1, x, y, s);
-        if (m == 2) return launch_dot<DotIQ4XS, 2>(f, w, 2, x, y, s);
-        return launch_dot<DotIQ4XS, 4>(f, w, (int)m, x, y, s);
+        if (x16 && dot_ok(w, m)) {
+            if (m == 1) return launch_dot<DotIQ4XS, 1>(f, w, 1, x, y, s);
+            if (m == 2) return launch_dot<DotIQ4XS, 2>(f, w, 2, x, y, s);
+            return launch_dot<DotIQ4XS, 4>(f, w, (int)m, x, y, s);
+        }
+        return launch_dot_f32(f, w, x, y, s);  // m == 1, dot_f32_ok
     }
-    if (w->qtype == ARFQ_Q6_K && m == 1 && !x16 && dot_f32_ok(w)) return launch_dot_f32(dot_q6k(w, e), w, x, y, s);
-    if (w->qtype == ARFQ_Q6_K && dot_ok(w, m)) {
-        const DotQ6K f = dot_q6k(w, e);
-        return m == 1 ? launch_dot<DotQ6K, 1>(f, w, 1, x, y, s) : launch_dot<DotQ6K, 2>(f, w, 2, x, y, s);
+    if (w->qtype == ARFQ_Q6_K) {
+        if (x16 && dot_ok(w, m)) {
+            const DotQ6K f = dot_q6k(w, e);
+            return m == 1 ? launch_dot<DotQ6K, 1>(f, w, 1, x, y, s) : launch_dot<DotQ6K, 2>(f, w, 2, x, y, s);
+        }
+        if (m == 1 && dot_f32_ok(w)) return launch_dot_f32(dot_q6k(w, e), w, x, y, s);
     }
     if (w->qtype == ARFQ_Q8_0) {
         if (m == 1) return launch_q80<1>(w, e, 1, x, y, s);
         if (m == 2) return launch_q80<2>(w, e, 2, x, y, s);
         return launch_q80<4>(w, e, (int)m, x, y, s);
     }
+    // Q6_K, f32: gemv_q6k
     if (m == 1) return launch_gemv_t<4, 1>(w, e, 1, x, y, s);
     if (m == 2) return launch_gemv_t<4, 2>(w, e, 2, x, y, s);
     return launch_gemv_t<2, 4>(w, e, (int)m, x, y, s);

@@ -7,6 +7,7 @@
 #include <new>
 #include <string>
 
+#include "arfq_common.h"
 #include "arfq_internal.h"
 
 #include <algorithm>
@@ -120,11 +121,13 @@ int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_stop);
     if (e == hipSuccess) {
+        // the split-K counters, then STREAM_SINK_WORDS words of arfq_stream_read's sink
         ctx->ntickets = std::max(1024, 2 * ctx->cus);
-        e = hipMalloc(&ctx->tickets, (size_t)ctx->ntickets * sizeof(uint32_t));
+        e = hipMalloc(&ctx->tickets, ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS) * sizeof(uint32_t));
     }
     if (e == hipSuccess)
-        e = hipMemsetAsync(ctx->tickets, 0, (size_t)ctx->ntickets * sizeof(uint32_t), ctx->stream);
+        e = hipMemsetAsync(ctx->tickets, 0, ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS) * sizeof(uint32_t),
+                           ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
         g_create_err = std::string("arfq_ctx_create: ") + hipGetErrorString(e);
@@ -313,9 +316,9 @@ static int ensure_scratch(arfq_ctx *ctx, size_t bytes) {
 static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t m,
                           const void *x, int x_dtype, float *y) {
     hipError_t e;
-    if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
-        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream,
-                              (ctx->options & ARFQ_OPT_GEMV_X16) != 0);
+    const bool x16 = (ctx->options & ARFQ_OPT_GEMV_X16) != 0;
+    if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m, x16)) {
+        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream, x16);
     } else if (arfq::gemm_supports(w, m)) {
         const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
         if (int rc = ensure_scratch(ctx, plan.scratch_bytes)) return rc;
@@ -343,10 +346,10 @@ int arfq_matmul_noalloc(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t
     if (int rc = use_device(ctx)) return rc;
     if (!ctx->noalloc_scratch) return fail(ctx, ARFQ_E_DEVICE, "matmul_noalloc: no scratch on this device");
     hipError_t e;
-    if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m)) {
+    const bool x16 = (ctx->options & ARFQ_OPT_GEMV_X16) != 0;
+    if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m, x16)) {
         // the decode GEMVs use no scratch
-        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream,
-                              (ctx->options & ARFQ_OPT_GEMV_X16) != 0);
+        e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream, x16);
     } else if (arfq::gemm_supports(w, m)) {
         const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
         if (plan.scratch_bytes > ARFQ_NOALLOC_SCRATCH_BYTES)
@@ -593,8 +596,8 @@ int arfq_moe_ids_add(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *
 // -------------------------------------------------------------------- FFN ----
 
 // Scratch bytes a matmul of w at m rows needs (GEMM plans; the GEMV needs none).
-static size_t matmul_scratch(const arfq_weight *w, int64_t m) {
-    if (arfq::gemv_supports(w, m)) return 0;
+static size_t matmul_scratch(const arfq_weight *w, int64_t m, bool x16) {
+    if (arfq::gemv_supports(w, m, x16)) return 0;
     return arfq::gemm_supports(w, m) ? arfq::gemm_plan(w, m, ARFQ_F32).scratch_bytes : 0;
 }
 
@@ -616,10 +619,10 @@ int arfq_ffn_act(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, 
     // gate and up of one x row in one launch (Q4_K, f32 arithmetic)
     const bool dual = !x16 && arfq::gemv_dual_supports(gate, up, m);
     // the activation applied as the down GEMV reads its x (Q4_K, m <= 4)
-    const bool fused = arfq::gemv_glu_supports(down, m);
+    const bool fused = arfq::gemv_glu_supports(down, m, x16);
     // the GEMM plans use the scratch from offset 0; g, u (and h) sit above the largest
-    size_t base = std::max({matmul_scratch(gate, m), matmul_scratch(up, m),
-                            fused ? (size_t)0 : matmul_scratch(down, m)});
+    size_t base = std::max({matmul_scratch(gate, m, x16), matmul_scratch(up, m, x16),
+                            fused ? (size_t)0 : matmul_scratch(down, m, x16)});
     base = align256(base);
     const size_t gb = align256((size_t)m * inter * 4);
     if (int rc = ensure_scratch(ctx, base + (fused ? 2 : 3) * gb)) return rc;
@@ -709,6 +712,71 @@ int arfq_copy_d2d(arfq_ctx *ctx, void *dst, const void *src, size_t bytes) {
         HIP_TRY(ctx, hipGetLastError());
     } else {
         HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    }
+    return ARFQ_OK;
+}
+
+// Read-only stream: grid-stride 16-byte loads, folded into one word per lane
+// that is stored only if it holds an unlikely value (so the loads cannot be
+// dropped).  Wave 0 of workgroups < nstamps records (s_memrealtime,
+// s_memtime) at its start and end.
+__global__ __launch_bounds__(256) void read_stream_kernel(const uint4 *__restrict__ src, int64_t n,
+                                                          uint32_t *__restrict__ sink, uint64_t *__restrict__ stamps,
+                                                          int nstamps) {
+    const uint64_t r0 = __builtin_amdgcn_s_memrealtime(), c0 = __builtin_readcyclecounter();
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) {
+        const uint4 a = arfq::ld_nt(src + i);
+        acc ^= a.x ^ a.y ^ a.z ^ a.w;
+    }
+    if (acc == 0x9E3779B9u) sink[threadIdx.x] = acc;
+    if (stamps && threadIdx.x == 0 && (int)blockIdx.x < nstamps) {
+        const uint64_t r1 = __builtin_amdgcn_s_memrealtime(), c1 = __builtin_readcyclecounter();
+        uint64_t *o = stamps + 4 * (int64_t)blockIdx.x;
+        o[0] = r0;
+        o[1] = c0;
+        o[2] = r1;
+        o[3] = c1;
+    }
+}
+
+int arfq_stream_read(arfq_ctx *ctx, const void *src, size_t bytes, uint64_t *stamps, int nstamps) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (!src || (((uintptr_t)src | bytes) & 15)) return fail(ctx, ARFQ_E_INVALID, "stream_read: need 16-byte alignment");
+    if (nstamps < 0 || (nstamps > 0 && !stamps)) return fail(ctx, ARFQ_E_INVALID, "stream_read: bad stamps");
+    if (int rc = use_device(ctx)) return rc;
+    if (bytes == 0) return ARFQ_OK;
+    // the sink (a word per thread of a workgroup) sits past the split-K counters
+    // in the same allocation; nothing reads it
+    if (!ctx->tickets) return fail(ctx, ARFQ_E_DEVICE, "stream_read: no sink");
+    const int64_t n = (int64_t)(bytes / 16);
+    // eight 256-thread workgroups per CU (fewer for a short stream: a load per lane at least)
+    const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, (int64_t)std::max(ctx->cus, 1) * 8);
+    read_stream_kernel<<<grid, 256, 0, ctx->stream>>>((const uint4 *)src, n, ctx->tickets + ctx->ntickets,
+                                                       stamps, nstamps);
+    HIP_TRY(ctx, hipGetLastError());
+    return ARFQ_OK;
+}
+
+int arfq_ctx_device_info(arfq_ctx *ctx, int *cus, int *shader_clock_khz, int *wall_clock_khz) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (cus) *cus = ctx->cus;
+    if (shader_clock_khz) HIP_TRY(ctx, hipDeviceGetAttribute(shader_clock_khz, hipDeviceAttributeClockRate, ctx->device));
+    if (wall_clock_khz)
+        HIP_TRY(ctx, hipDeviceGetAttribute(wall_clock_khz, hipDeviceAttributeWallClockRate, ctx->device));
+    return ARFQ_OK;
+}
+
+int arfq_ctx_memory(arfq_ctx *ctx, size_t *scratch_bytes, size_t *device_free, size_t *device_total) {
+    if (!ctx) return ARFQ_E_INVALID;
+    if (scratch_bytes) *scratch_bytes = ctx->scratch_bytes;
+    if (device_free || device_total) {
+        if (int rc = use_device(ctx)) return rc;
+        size_t f = 0, t = 0;
+        HIP_TRY(ctx, hipMemGetInfo(&f, &t));
+        if (device_free) *device_free = f;
+        if (device_total) *device_total = t;
     }
     return ARFQ_OK;
 }

@@ -44,6 +44,10 @@ struct arfq_weight {
 
 namespace arfq {
 
+// words past the split-K counters (arfq_ctx::tickets) that arfq_stream_read's
+// kernel may store to (one per thread of a 256-thread workgroup)
+constexpr int STREAM_SINK_WORDS = 256;
+
 // hipFuncSetAttribute(MaxDynamicSharedMemorySize) for `fn` on the current
 // device, once per device: `done` (one per kernel, zero-initialised static)
 // holds a bit per device index already set.
@@ -78,14 +82,14 @@ hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s);
 // (ARFQ_OPT_GEMV_X16).
 hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, float *y,
                        hipStream_t s, bool x16 = false);
-bool gemv_supports(const arfq_weight *w, int64_t m);
+bool gemv_supports(const arfq_weight *w, int64_t m, bool x16 = false);
 // MoE decode GEMVs over P (token, expert) pairs, Q4_K: y[p] (w->n floats) = W_ids[p] .
 // x_p, where x_p is row p / x_div of x (f32 or f16, [*, w->k]) or, when g is
 // set, silu(g[p]) * u[p] (g, u: [P, w->k] f32).  Pairs with an out-of-range id
 // are skipped.
 // The FFN's down projection: y[m, n] = W . (act(g) * u), g and u [m, w->k] f32
 // (Q4_K, m <= 4); act ARFQ_ACT_SILU or ARFQ_ACT_GELU_TANH.
-bool gemv_glu_supports(const arfq_weight *w, int64_t m);
+bool gemv_glu_supports(const arfq_weight *w, int64_t m, bool x16 = false);
 hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y, int act,
                            hipStream_t s, bool x16 = false);
 // The FFN's gate and up projections of one x row in one launch: ya = A . x,
@@ -114,7 +118,10 @@ struct GemmPlan {
     bool sums = false;     // the format needs x sub-block sums (Q4_K)
     bool skinny = false;   // m <= 64: the weight-streaming kernel (arfq_skinny.h)
     bool bd = false;       // Q4_K prefill: weights straight into MFMA operands (arfq_gemm_bd.h)
-    bool pair = false;     // skinny, m <= 16, f32 x: x as f16 hi rows + lo rows in one x tile
+    // skinny, f32 x: the f16 parts x enters as (1: x rounded to f16; 2: hi + lo,
+    // ~22 bits, m <= 32; 3: hi + mid + lo, m <= 8, which represents every f32 x
+    // within 2^17 of its row's max exactly), stored as row blocks [parts][m][k]
+    int parts = 1;
     int bd_full = 0;       // bd: whole tiles; the rest are split into bd_chunks K ranges
     int bd_chunks = 1;
     size_t off_xh = 0, off_xl = 0, off_xs = 0, off_rs = 0, off_part = 0, scratch_bytes = 0;
@@ -131,12 +138,13 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
 // skipped.  With rs (f32 x only) each row is stored divided by a power of two
 // rs[row] that puts its max |x| in [2^14, 2^15); products of it must be
 // multiplied back by rs[row].
-// With pair (xl == xh + m * k) the lo rows follow the hi rows and xs has the
-// hi rows' sums, then the lo rows' sums.
+// With parts = 2 or 3 (xl == xh + m * k) the lo rows (parts 2: x - hi; parts
+// 3: the mid rows, then the lo rows x - hi - mid) follow the hi rows, and xs
+// holds each part's row sums in the same row order.
 // rs_splits: with rs, one scale per row and per K range of the skinny
 // kernel's split-K (rs[split * m + row]; 1: one per row)
 hipError_t launch_xprep(const void *x, int x_dtype, int64_t m, int64_t k, _Float16 *xh,
-                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, bool pair = false,
+                        _Float16 *xl, uint16_t *xs, float *rs, hipStream_t s, int parts = 1,
                         int rs_splits = 1);
 
 // ---- arfq_moe.hip ----

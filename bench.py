@@ -383,6 +383,61 @@ def gguf_reader_bench(ctx):
     print(json.dumps(out), flush=True)
 
 
+STREAM_BYTES = 512 << 20   # above the 256 MB MALL
+STREAM_STAMP_WGS = 256
+
+
+def stream_ceiling(ctx, c2_launches, copies):
+    """The practical HBM read ceiling, measured in this run with a plain read-only
+    kernel (arfq_stream_read: 16-byte loads, four in flight per lane):
+      - stream_gbs: one pass over a STREAM_BYTES buffer (best of 5 timed passes);
+      - stream_c2_gbs: back-to-back passes over `copies` rotating buffers of C2's
+        weight bytes (50,135,040 B each), timed like the C2 loop, so the figure
+        carries the same per-launch gap the GEMV pays;
+      - clock_mhz: the shader clock while the big pass ran, from s_memtime against
+        s_memrealtime in the first STREAM_STAMP_WGS workgroups."""
+    cus, sclk_khz, wclk_khz = ctx.device_info()
+    big = ctx.empty((STREAM_BYTES,), np.uint8)
+    stamps = ctx.empty((STREAM_STAMP_WGS * 4,), np.uint64)
+    for _ in range(3):
+        ctx.stream_read(big)
+    ctx.sync()
+    best = None
+    for _ in range(5):
+        ctx.timer_start()
+        ctx.stream_read(big, stamps=stamps)
+        ms = ctx.timer_stop()
+        best = ms if best is None else min(best, ms)
+    st = stamps.numpy().reshape(-1, 4).astype(np.float64)
+    dr, dc = st[:, 2] - st[:, 0], st[:, 3] - st[:, 1]
+    ok = dr > 0
+    clock = float(dc[ok].sum() / dr[ok].sum() * wclk_khz / 1e3) if ok.any() and wclk_khz > 0 else None
+    big.free()
+    stamps.free()
+    c2b = 50135040
+    bufs = [ctx.empty((c2b,), np.uint8) for _ in range(copies)]
+    for b in bufs:
+        ctx.stream_read(b)
+    t0 = time.time()
+    while time.time() - t0 < SETTLE_S:
+        for b in bufs:
+            ctx.stream_read(b)
+        ctx.sync()
+    ctx.timer_start()
+    for i in range(c2_launches):
+        ctx.stream_read(bufs[i % copies])
+    ms_c2 = ctx.timer_stop() / c2_launches
+    for b in bufs:
+        b.free()
+    out = {"stream_gbs": round(STREAM_BYTES / best / 1e6, 1),
+           "stream_c2_gbs": round(c2b / ms_c2 / 1e6, 1),
+           "stream_c2_us_per_launch": round(ms_c2 * 1e3, 3),
+           "clock_mhz": round(clock, 0) if clock else None,
+           "clock_peak_mhz": round(sclk_khz / 1e3, 0), "cus": cus}
+    log(f"[bench] stream ceiling: {out}")
+    return out
+
+
 def only_config(ctx, args):
     """One config, timed as in the full run (args.steps launches after args.warmup)."""
     from arf_amd import synth
@@ -472,6 +527,7 @@ def main():
     nbytes = algorithmic_bytes("q4_k", m, n, k)
     gbs = nbytes / (ms * 1e-3) / 1e9
     log(f"[bench] C2: {ms * 1e3:.2f} us/launch, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM)")
+    ceiling = stream_ceiling(ctx, max(200, args.steps), args.copies)
 
     configs = {}
     if not args.quick:
@@ -634,7 +690,15 @@ def main():
                               "(dmin*m)*x_sum in f32, as matmul_nt_q4ks"},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": load_traffic("q4k_gemv_c2_traffic.json", "gemv_q4k_f32")},
+                     "traffic": load_traffic("q4k_gemv_c2_traffic.json", "gemv_q4k_f32"),
+                     "stream_gbs": ceiling["stream_gbs"], "stream_c2_gbs": ceiling["stream_c2_gbs"],
+                     "frac_of_stream_c2": round(gbs / ceiling["stream_c2_gbs"], 4),
+                     "clock_mhz": ceiling["clock_mhz"], "clock_peak_mhz": ceiling["clock_peak_mhz"],
+                     "stream_note": "stream_gbs: a plain read-only kernel over 512 MB; stream_c2_gbs: the "
+                                    "same kernel over C2's 50,135,040 weight bytes, rotating the same number "
+                                    "of buffers back to back like the GEMV loop (launch gaps included); "
+                                    "clock_mhz: shader clock during the 512 MB pass (s_memtime vs "
+                                    "s_memrealtime)"},
         "cpu_baseline": cpu,
         "configs": configs,
     }

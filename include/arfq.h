@@ -85,13 +85,15 @@ const char *arfq_last_error(const arfq_ctx *ctx);
 int arfq_ctx_sync(arfq_ctx *ctx);
 
 /* Context options (bit set; default 0).
- * ARFQ_OPT_GEMV_X16: the Q4_K, Q5_K, Q6_K and IQ4_XS decode GEMVs at m = 1
- *   (arfq_matmul, arfq_ffn_act) round each 32-element block of f32 x to 16-bit
- *   fixed point (relative to the block's max |x|) and take exact integer dots;
- *   faster, max relative error ~1e-4 of the output's rms.  By default
- *   they multiply f32 x by the exact weights in f32, as the reference GEMVs do
- *   (crates/arf-gpu/src/shaders/metal/matmul_vec_q4ks_msl.metal:46-165).
- *   (m = 2..4 always use the 16-bit form.)
+ * ARFQ_OPT_GEMV_X16: the Q4_K, Q5_K, Q6_K and IQ4_XS decode GEMVs at m <= 4
+ *   (Q6_K at m <= 2; arfq_matmul, arfq_ffn_act) round each 32-element block
+ *   of f32 x to 16-bit fixed point (relative to the block's max |x|) and take
+ *   exact integer dots; faster, max relative error ~1e-4 of the output's rms.
+ *   Only where those kernels' LDS fits 64 KiB: longer x keeps the default
+ *   path.  By default every GEMV multiplies f32 x by the exact weights in f32,
+ *   as the reference GEMVs do
+ *   (crates/arf-gpu/src/shaders/metal/matmul_vec_q4ks_msl.metal:46-165,
+ *   matmul_vec_q4ks_batch_msl.metal:104-288).
  * No counterpart in the reference (which has only the f32 form). */
 #define ARFQ_OPT_GEMV_X16 1u
 int arfq_ctx_set_options(arfq_ctx *ctx, unsigned options);
@@ -121,12 +123,20 @@ int arfq_weight_info(const arfq_weight *w, int *qtype, int64_t *n_rows, int64_t 
 /* y[m, n_rows] (f32) = x[m, k_cols] . W^T for expert `expert` of `w` (0 for a
  * plain matrix).  x is f32 or f16 per `x_dtype`.  The library picks the kernel
  * by (qtype, m): wave-per-rows GEMV for small m, dequant-into-LDS MFMA GEMM
- * otherwise.  Arithmetic: at m = 1 f32 x times the exact weights in f32; at
- * m >= 5 f16 MFMAs with f32 sums.  There an f32 x is first scaled per row (and
- * per K range) by a power of two that puts the row's max |x| in [2^14, 2^15),
- * so every finite x stays finite, and the output is scaled back; it then
- * enters as f16 hi + lo (~22 bits) at m <= 32 and for Q5_K / IQ4_XS above 64
- * rows, as f16 otherwise.  The weights are exact up to 64 rows; above 64 rows
+ * otherwise.  Arithmetic, f32 x:
+ *   - m = 1: f32 x times the exact weights in f32 (Q4_K, Q5_K, IQ4_XS and Q6_K
+ *     while x fits the kernels' LDS: k up to about 37K for Q4_K and 38K for the
+ *     others; longer x takes the m <= 8 path below).
+ *   - m <= 4: Q6_K and Q8_0 GEMVs in f32.
+ *   - m <= 8 (Q4_K / Q5_K / IQ4_XS from m = 2, Q6_K / Q8_0 from m = 5): the
+ *     skinny MFMA kernel with x as three f16 parts (hi + mid + lo) of x scaled
+ *     per row (and per K range) by a power of two that puts the row's max |x|
+ *     in [2^14, 2^15), so every x within 2^15 of that max is represented
+ *     exactly; exact codes, f32 sums, the output scaled back.
+ *   - m = 9..32: the same with two parts (hi + lo, ~22 bits).
+ *   - m = 33..64: one f16 part.  Above 64 rows: one part (the Q5_K / IQ4_XS
+ *     tile loop keeps hi + lo).
+ * f16 x enters as is.  The weights are exact up to 64 rows; above 64 rows
  * Q6_K, Q8_0, Q5_K and IQ4_XS use the dequant rounded once to f16.
  * Replaces add_matmul_m / add_matmul
  * (crates/arf-gpu/src/gpu/dispatch.rs:169-202, Q4KS arms :517-630) and the
@@ -217,6 +227,28 @@ int arfq_copy_d2h(arfq_ctx *ctx, void *dst, const void *src, size_t bytes);
  * known-size reference for HBM byte counters.  No counterpart in the
  * reference (its buffers are copied by the wgpu/Metal runtime). */
 int arfq_copy_d2d(arfq_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Enqueue one read-only pass over `bytes` (a multiple of 16, 16-byte aligned)
+ * of device memory at `src`: grid-stride 16-byte loads, eight 256-thread
+ * workgroups per CU.  The practical HBM read ceiling the
+ * GEMV roofline is judged against (the bench times it beside the datasheet
+ * peak).  When `stamps` is not NULL (device memory, room for 4 * `nstamps`
+ * uint64), the first wave of each of the first `nstamps` workgroups writes
+ * (s_memrealtime, s_memtime) at its start and at its end there; their ratio
+ * against the device's wall-clock rate (hipDeviceAttributeWallClockRate) is
+ * the shader clock while the stream ran.  No counterpart in the reference
+ * (its roofline probe reads through a wgpu kernel,
+ * crates/arf-gpu/examples/gemv_roofline_probe.rs:15-45). */
+int arfq_stream_read(arfq_ctx *ctx, const void *src, size_t bytes, uint64_t *stamps, int nstamps);
+/* The context device's compute units, peak shader clock and the frequency of
+ * s_memrealtime (both kHz, hipDeviceAttributeClockRate and
+ * hipDeviceAttributeWallClockRate); any pointer may be NULL.  No counterpart
+ * in the reference (its adapter info comes from wgpu). */
+int arfq_ctx_device_info(arfq_ctx *ctx, int *cus, int *shader_clock_khz, int *wall_clock_khz);
+/* The device scratch the context holds (grown on demand by arfq_matmul,
+ * arfq_moe* and arfq_ffn*; never by arfq_matmul_noalloc) and the device's free
+ * and total memory (hipMemGetInfo); any pointer may be NULL.  No counterpart
+ * in the reference. */
+int arfq_ctx_memory(arfq_ctx *ctx, size_t *scratch_bytes, size_t *device_free, size_t *device_total);
 /* Record a start event / a stop event on the context's stream; elapsed time in
  * ms between the last start and stop (waits for the stop event). */
 int arfq_timer_start(arfq_ctx *ctx);

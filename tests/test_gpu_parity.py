@@ -321,6 +321,85 @@ def test_vocab_wide_lm_head_gemv(gpu_ctx, oracle, qtype):
         assert rel_err(got[:, r0:r0 + 2048], part) <= TOL
 
 
+# ---- f32 x over the small-batch decode range ----
+# m = 2..8 multiply f32 x in f32 terms: Q4_K / Q5_K / IQ4_XS on the skinny MFMA kernel
+# with x as three f16 parts (hi + mid + lo, which represent every f32 value within 2^15 of
+# its row's max |x| exactly; the exact codes times each part, f32 sums), Q6_K on the f32
+# GEMV at m <= 4, Q8_0 on its f32 GEMV at m <= 4.  Held to 2e-5 against the oracle.
+SMALL_M_TOL = 2e-5
+
+
+@pytest.mark.parametrize("qtype,n,k", [("q4_k", 200, 2048), ("q5_k", 200, 2048), ("iq4_xs", 200, 2048),
+                                       ("q6_k", 200, 2048), ("q8_0", 200, 2048), ("q4_k", 17408, 5120)])
+@pytest.mark.parametrize("m", [2, 3, 4, 5, 8])
+def test_small_m_f32_x(gpu_ctx, oracle, qtype, n, k, m):
+    if n == 17408 and m not in (2, 4):
+        pytest.skip("C2's shape at m = 2 and 4 only")
+    _say("case: small-m f32 x", qtype, n, k, m)
+    got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=13 * m + n + k)
+    e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
+    _say("rel err", e)
+    assert e <= SMALL_M_TOL
+
+
+@pytest.mark.parametrize("qtype,n,k", [("q4_k", 300, 2048), ("q4_k", 17408, 5120), ("q5_k", 300, 2048),
+                                       ("iq4_xs", 300, 2048), ("q6_k", 300, 2048)])
+@pytest.mark.parametrize("m", [2, 3, 4])
+def test_small_m_exact_on_integer_x(gpu_ctx, oracle, qtype, n, k, m):
+    # integer x in [-8, 8] and dyadic weights: every product and sum is exact in f32 in
+    # any order, so m = 2..4 must equal the oracle bit for bit, as m = 1 does
+    _say("case: small-m exact", qtype, n, k, m)
+    from arf_amd import QType
+    raw = _q4k_dyadic_blocks(n, k, seed=n + k + m) if qtype == "q4_k" else _dyadic_blocks(qtype, n, k, seed=n + k + m)
+    rng = np.random.default_rng(k + m)
+    x = rng.integers(-8, 9, size=(m, k)).astype(np.float32)
+    w = gpu_ctx.upload(QType[qtype.upper()], raw, n, k)
+    y = gpu_ctx.empty((m, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)
+    assert np.array_equal(y.numpy(), oracle.matmul_q(qtype, x, raw, n))
+
+
+@pytest.mark.parametrize("qtype", ["q4_k", "q5_k", "iq4_xs"])
+def test_x16_option_long_k_keeps_working(gpu_ctx, oracle, qtype):
+    # ARFQ_OPT_GEMV_X16 at a 70B-class ffn_down (n = 8192, k = 28672): the 16-bit kernels'
+    # LDS would pass 64 KiB there (Q4_K 66.3 KB, Q5_K / IQ4_XS 68 KB), so these shapes keep
+    # the f32 kernels and must still run
+    import arf_amd
+    _say("case: x16 long k", qtype)
+    gpu_ctx.set_options(arf_amd.arfq.OPT_GEMV_X16)
+    try:
+        got, raw, x = _matmul(gpu_ctx, qtype, 8192, 28672, 1, seed=29)
+    finally:
+        gpu_ctx.set_options(0)
+    e = rel_err(got, oracle.matmul_q(qtype, x, raw, 8192))
+    _say("rel err", e)
+    assert e <= F32_TOL
+
+
+def test_x16_option_long_k_ffn(gpu_ctx, oracle):
+    # the FFN's fused activation-into-down GEMV under ARFQ_OPT_GEMV_X16 with k = 28672
+    import arf_amd
+    from arf_amd import QType, synth
+    _say("case: x16 long k ffn")
+    hidden, inter = 8192, 28672
+    shapes = [(inter, hidden), (inter, hidden), (hidden, inter)]
+    raws = [synth.weight("q4_k", n, k, seed=41 + i) for i, (n, k) in enumerate(shapes)]
+    ws = [gpu_ctx.upload(QType.Q4_K, r, n, k) for r, (n, k) in zip(raws, shapes)]
+    x = (synth.activations(1, hidden, seed=47) * np.float32(0.005)).astype(np.float32)
+    y = gpu_ctx.empty((1, hidden), np.float32)
+    gpu_ctx.set_options(arf_amd.arfq.OPT_GEMV_X16)
+    try:
+        gpu_ctx.ffn(ws[0], ws[1], ws[2], gpu_ctx.to_device(x), 1, y)
+    finally:
+        gpu_ctx.set_options(0)
+    g = oracle.matmul_q("q4_k", x, raws[0], inter)
+    u = oracle.matmul_q("q4_k", x, raws[1], inter)
+    want = oracle.matmul_q("q4_k", oracle.glu(g, u, 0).reshape(g.shape), raws[2], hidden)
+    e = rel_err(y.numpy(), want)
+    _say("rel err", e)
+    assert e <= TOL
+
+
 def test_shape_errors_raise(gpu_ctx):
     from arf_amd import QType, synth
     raw = synth.weight("q4_k", 4, 256, seed=1)

@@ -65,3 +65,43 @@ def test_noalloc_rejects_products_above_its_scratch(gpu_ctx):
     assert st == arfq.ARFQ_E_UNSUPPORTED
     assert b"scratch" in L.arfq_last_error(gpu_ctx.handle)
     w.free()
+
+
+def test_noalloc_allocates_nothing():
+    # a fresh context that has never run arfq_matmul: the allocation-free entry point
+    # must leave the context's scratch at 0 bytes and, after the runtime's own one-time
+    # set-up in the first call, the device's free memory (hipMemGetInfo) unchanged over
+    # further calls -- two products that use scratch (x preparation and split-K
+    # partials), the second smaller; the outputs then match arfq_matmul's bit for bit
+    from arf_amd import QType, synth
+    _say("case: noalloc allocates nothing")
+    ctx = arf_amd.Context(0)
+    try:
+        L = arf_amd.load_library()
+        shapes = [("q6_k", 2048, 8192, 8), ("q6_k", 2048, 8192, 8), ("q6_k", 96, 2048, 5)]
+        ws, xs, ys = [], [], []
+        for i, (qtype, n, k, m) in enumerate(shapes):
+            ws.append(ctx.upload(QType[qtype.upper()], synth.weight(qtype, n, k, seed=77 + i), n, k))
+            xs.append(ctx.to_device(synth.activations(m, k, seed=78 + i)))
+            ys.append(ctx.empty((m, n), np.float32))
+        ctx.sync()
+        free0 = None
+        for i, (qtype, n, k, m) in enumerate(shapes):
+            st = L.arfq_matmul_noalloc(ctx.handle, ws[i].handle, 0, m, xs[i].ptr, int(arf_amd.DType.F32),
+                                       ys[i].ptr)
+            assert st == arfq.ARFQ_OK, L.arfq_last_error(ctx.handle)
+            ctx.sync()
+            scratch, free, _ = ctx.memory()
+            assert scratch == 0
+            if i == 0:
+                free0 = free
+            else:
+                assert free == free0, (free0, free)
+        got = [y.numpy() for y in ys]
+        for i, (qtype, n, k, m) in enumerate(shapes):
+            want = ctx.empty((m, n), np.float32)
+            ctx.matmul(ws[i], xs[i], m, want)
+            assert np.array_equal(got[i].view(np.uint32), want.numpy().view(np.uint32))
+        assert ctx.memory()[0] > 0  # arfq_matmul grew the context's scratch
+    finally:
+        ctx.close()
