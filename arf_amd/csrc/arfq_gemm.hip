@@ -91,9 +91,10 @@ __global__ __launch_bounds__(GM_THREADS, F::WG_PER_CU) void gemm_q(
 // S workgroups to arrive (counted in tick[blockIdx.x], which it resets to 0)
 // sums the S partials in split order into y, so the result does not depend on
 // the arrival order.
-// (held to 256 VGPRs: two workgroups per CU)
+// (held to 256 VGPRs: two workgroups per CU; with four x tiles the LDS leaves
+// room for one, which gets all 512)
 template <class F, int TA, class XT, int PARTS, int GM = 0xFF>
-__global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__restrict__ x,
+__global__ __launch_bounds__(SK_THREADS, TA == 4 ? 1 : 2) void gemm_sk(F fmt, const XT *__restrict__ x,
                                                       const uint16_t *__restrict__ xs,
                                                       const float *__restrict__ rs,
                                                       float *__restrict__ y, float *__restrict__ part,
@@ -106,7 +107,8 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
     const int nb = K / 256, S = gridDim.y, sp = blockIdx.y;
     const int b0 = (int)((int64_t)sp * nb / S), b1 = (int)((int64_t)(sp + 1) * nb / S);
     // PARTS 2 (M <= 16 TA): x row r < M stages hi row r of x, row PO + r its lo
-    // row M + r (PO = 16 in one 32-row tile, 32 = the second tile with two).
+    // row M + r (PO = 16 in one 32-row tile, 32 = the second tile with two, 64 =
+    // tiles 2 and 3 with four).
     // PARTS 3 (M <= 8, one tile): rows r, 8 + r and 16 + r stage the hi, mid and
     // lo rows r, M + r and 2M + r; a lane's accumulator holds rows r, r + 8 and
     // r + 16 of its column as elements i, i + 4 and i + 8.  Rows that stage
@@ -132,8 +134,8 @@ __global__ __launch_bounds__(SK_THREADS, 2) void gemm_sk(F fmt, const XT *__rest
     for (int t = 0; t < TA; t++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-    // PAIR with two tiles: the lo tile's products go into tile 0's accumulators
-    skinny_run<F, TA, 1, SK_THREADS, XT, false, GM, PAIR && TA == 2, true>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
+    // PAIR with two or four tiles: the lo tiles' products go into the hi tiles' accumulators
+    skinny_run<F, TA, 1, SK_THREADS, XT, false, GM, PAIR && TA >= 2, true>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
                                                                     PARTS == 3 ? 16 + M : PAIR ? PO + M : M);
     if constexpr (PAIR && TA == 1) {
         // rows r and r + 16 of a lane's accumulator are elements i and i + 8
@@ -318,7 +320,7 @@ static int64_t bd_stream_bytes(int qtype) {
 
 static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
+GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     GemmPlan p;
     const int cus = w->ctx && w->ctx->cus > 0 ? w->ctx->cus : 256;
     const bool kind2 = w->qtype == ARFQ_Q4_K || w->qtype == ARFQ_Q5_K;  // min term: x sums
@@ -330,19 +332,20 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
     const int64_t bdb = bd_stream_bytes(w->qtype);
     p.bd = !p.skinny && m > 64 && bdb && w->k % 256 == 0 && !(w->qtype == ARFQ_IQ4_XS && x_dtype == ARFQ_F32) &&
            w->n * (w->k / 256) * bdb < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
-    // f32 x: scaled per row by a power of two into f16 range, then rounded to
-    // f16 for the skinny kernel and the direct-operand prefill, or split into
-    // f16 hi + lo for the tile loop (at m <= 64, and IQ4_XS prefill, whose
-    // weights are rounded to f16: this way only one of the two operands is);
-    // the output rows are multiplied back by the scale
+    // f32 x: scaled per row by a power of two into f16 range, then split into
+    // f16 parts for the skinny kernel, rounded to f16 for the direct-operand
+    // prefill, or split into f16 hi + lo for the tile loop (IQ4_XS prefill,
+    // whose weights are rounded to f16: this way only one of the two operands
+    // is); the output rows are multiplied back by the scale
     p.xsplit = !p.skinny && !p.bd && x_dtype == ARFQ_F32;
     p.convert = x_dtype == ARFQ_F32;
-    // skinny kernel, f32 x, m <= 32: x as f16 hi + lo (about 22 bits, as close
-    // to the reference's f32 batched GEMV as the f16 MFMA gets): at m <= 16 the
-    // lo rows fill the other half of the 32-row x tile staged anyway (no extra
-    // MFMAs), at m <= 32 a second tile (twice the MFMAs)
-    // m <= 8 (one 32-row tile holds three row blocks of 8): hi + mid + lo, exact
-    p.parts = p.skinny && x_dtype == ARFQ_F32 ? (m <= 8 ? 3 : m <= 32 ? 2 : 1) : 1;
+    // skinny kernel, f32 x: m <= 8 as three f16 parts (one 32-row x tile holds
+    // three row blocks of 8: hi + mid + lo, exact for every x within 2^15 of its
+    // row's max), m = 9..64 as hi + lo (~22 bits): the lo rows fill the other
+    // half of the 32-row tile at m <= 16 (no extra MFMAs), a second tile at
+    // m <= 32 and two more at m <= 64 (twice the MFMAs).  With x16
+    // (ARFQ_OPT_GEMV_X16): one part, x rounded to f16.
+    p.parts = p.skinny && x_dtype == ARFQ_F32 && !x16 ? (m <= 8 ? 3 : 2) : 1;
     // the exact Q4_K paths read x sub-block sums (min term)
     p.sums = (p.skinny || p.bd) && kind2;
     int64_t S;
@@ -365,9 +368,11 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype) {
             p.bd_full = (int)tiles;
         }
     } else if (p.skinny) {
-        // split K (whole blocks, >= 2 per split) until ~2 workgroups per CU
+        // split K (whole blocks, >= 2 per split) until ~2 workgroups per CU (~1 with
+        // the four x tiles of f32 x at m > 32, whose LDS holds one workgroup per CU)
         const int64_t nt = (w->n + 127) / 128, nb = w->k / 256;
-        S = std::max<int64_t>(1, (2 * (int64_t)cus) / nt);
+        const int per_cu = p.parts == 2 && m > 32 ? 1 : 2;
+        S = std::max<int64_t>(1, (per_cu * (int64_t)cus) / nt);
         S = std::min<int64_t>(S, std::max<int64_t>(1, nb / 2));
     } else {
         const int64_t mt = (m + p.bm - 1) / p.bm, nt = (w->n + GM_BN - 1) / GM_BN;
@@ -421,7 +426,7 @@ static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, con
 
 // S > 1 splits need S <= 16 and one zeroed counter per 128-column tile.  x is
 // f16 (an f32 x arrives prepared and scaled, rs[split * rss + row] its scale
-// over each split's K range); with parts 2 (m <= 32) it is [2m, K]: the hi
+// over each split's K range); with parts 2 (m <= 64) it is [2m, K]: the hi
 // rows, then the lo rows; with parts 3 (m <= 8) [3m, K]: hi, mid, lo rows.
 template <class F>
 static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
@@ -433,9 +438,10 @@ static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const
         return launch_sk_t<F, 1, 3>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
     }
     if (parts == 2) {
-        if (m > 32) return hipErrorInvalidValue;
-        return m <= 16 ? launch_sk_t<F, 1, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
-                       : launch_sk_t<F, 2, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+        if (m > 64) return hipErrorInvalidValue;
+        if (m <= 16) return launch_sk_t<F, 1, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+        if (m <= 32) return launch_sk_t<F, 2, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+        return launch_sk_t<F, 4, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
     }
     return m <= 32 ? launch_sk_t<F, 1, 1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
                    : launch_sk_t<F, 2, 1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);

@@ -320,7 +320,7 @@ static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64
     if (x_dtype == ARFQ_F32 && arfq::gemv_supports(w, m, x16)) {
         e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream, x16);
     } else if (arfq::gemm_supports(w, m)) {
-        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
+        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype, x16);
         if (int rc = ensure_scratch(ctx, plan.scratch_bytes)) return rc;
         e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->scratch, ctx->tickets,
                               ctx->ntickets, plan, ctx->stream);
@@ -351,7 +351,7 @@ int arfq_matmul_noalloc(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t
         // the decode GEMVs use no scratch
         e = arfq::launch_gemv(w, expert, m, (const float *)x, y, ctx->stream, x16);
     } else if (arfq::gemm_supports(w, m)) {
-        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype);
+        const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype, x16);
         if (plan.scratch_bytes > ARFQ_NOALLOC_SCRATCH_BYTES)
             return fail(ctx, ARFQ_E_UNSUPPORTED,
                         "matmul_noalloc: this product needs " + std::to_string(plan.scratch_bytes) +
@@ -598,7 +598,7 @@ int arfq_moe_ids_add(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *
 // Scratch bytes a matmul of w at m rows needs (GEMM plans; the GEMV needs none).
 static size_t matmul_scratch(const arfq_weight *w, int64_t m, bool x16) {
     if (arfq::gemv_supports(w, m, x16)) return 0;
-    return arfq::gemm_supports(w, m) ? arfq::gemm_plan(w, m, ARFQ_F32).scratch_bytes : 0;
+    return arfq::gemm_supports(w, m) ? arfq::gemm_plan(w, m, ARFQ_F32, x16).scratch_bytes : 0;
 }
 
 int arfq_ffn_act(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,

@@ -388,9 +388,10 @@ constexpr size_t sk_lds() {
 // wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
 // The block loop of skinny_run for the first TU (<= TA) x tiles.
 // GM: the 8-row accumulator groups (bit 4 t + g: rows 32 t + 8 g .. + 7) that
-// hold real rows; KIND 4 scales only those (the others stay 0).  MERGE: x tile
-// 1 holds the low halves of tile 0's rows (f32 x as f16 hi + lo), so its
-// products go into tile 0's accumulators (acc[w][1] is left as it is).  PIN:
+// hold real rows; KIND 4 scales only those (the others stay 0).  MERGE: the
+// second half of the x tiles (TU / 2 .. TU - 1) holds the low halves of the
+// first half's rows (f32 x as f16 hi + lo), so tile t's products go into tile
+// t % (TU / 2)'s accumulators (the second half of acc is left as it is).  PIN:
 // with two accumulator tiles, hold the scheduler to one step's operands at a
 // time (left free, it hoists all four steps' operand builds and x reads; the
 // dense skinny GEMM at C3 m = 64 ran 57.6 -> 53.0 us with the step boundary
@@ -406,7 +407,8 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                                             floatx16 (&acc)[NW][TA], _Float16 *lds) {
     constexpr int KIND = F::KIND;
     constexpr int XR = 32 * TA;       // x rows staged
-    constexpr int TO = MERGE ? 1 : TU;  // accumulator tiles written
+    constexpr int TO = MERGE ? TU / 2 : TU;  // accumulator tiles written
+    static_assert(!MERGE || TU % 2 == 0, "merged tiles come in (hi, lo) halves");
     constexpr int XC = SkRows<TA, NT>::XC;
     constexpr int RL = F::RB / 16;          // lanes per weight row in a coalesced load
     constexpr int NI = 32 * F::RB / 1024;   // 16-byte loads per lane per block
@@ -537,8 +539,8 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                         for (int t = 0; t < TU; t++) {
                             const half8 af = *reinterpret_cast<const half8 *>(
                                 xl + (xb * XR + 32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
-                            const int ti = MERGE ? 0 : t;
-                            c[ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], MERGE && t > 0 ? c[0] : z,
+                            const int ti = MERGE ? t % TO : t;
+                            c[ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], MERGE && t >= TO ? c[ti] : z,
                                                                            0, 0, 0);
                         }
                         const float ss = F::sub_scale(wb[w], p, kk);
@@ -552,8 +554,8 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                         for (int t = 0; t < TU; t++) {
                             const half8 af = *reinterpret_cast<const half8 *>(
                                 xl + (xb * XR + 32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
-                            const int ti = MERGE ? 0 : t;
-                            const bool cont = MERGE && t > 0;  // tile 1 adds onto tile 0's chain
+                            const int ti = MERGE ? t % TO : t;
+                            const bool cont = MERGE && t >= TO;  // a lo tile adds onto its hi tile's chain
                             floatx16 z;
 #pragma unroll
                             for (int i = 0; i < 16; i++) z[i] = 0.f;
@@ -593,7 +595,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
                     for (int t = 0; t < TU; t++) {
                         const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sl + (xb * XR + 32 * t + lr) * 16 + 8 * h);
-                        const int ti = MERGE ? 0 : t;
+                        const int ti = MERGE ? t % TO : t;
                         cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][ti], 0, 0, 0);
                         cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][ti], 0, 0, 0);
                     }

@@ -460,7 +460,7 @@ def only_config(ctx, args):
         ms, _ = time_matmul(ctx, "q5_k", 1, 17408, 5120, args.steps, args.warmup, 6, 0xA7F00005)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q5_k", 1, 17408, 5120) / ms / 1e6}
     elif c.startswith("c3"):
-        if c.endswith("x16"):
+        if c.endswith("x16"):  # the 16-bit GEMV (m = 1) or one f16 part of x (skinny)
             ctx.set_options(_arfq.OPT_GEMV_X16)
         mm = int(c[3:].replace("x16", ""))
         ms, _ = time_matmul(ctx, "q6_k", mm, 5120, 17408, args.steps, args.warmup, 6, 0xA7F00003)
@@ -490,7 +490,7 @@ def main():
                     help="time the GGUF reader instead: open a synthetic model file (C5's expert "
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
-    ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c4",
+    ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c3m64x16", "c4",
                                        "c5", "q5km1", "c1n8"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
@@ -561,8 +561,20 @@ def main():
             b3 = algorithmic_bytes("q6_k", mm, 5120, 17408)
             configs[f"c3_q6_k_m{mm}_k17408_n5120"] = {
                 "us_per_launch": round(ms3 * 1e3, 3), "GB/s": round(b3 / ms3 / 1e6, 1),
-                "hbm_frac": round(b3 / ms3 / 1e6 / HBM_PEAK_GBS, 4)}
+                "hbm_frac": round(b3 / ms3 / 1e6 / HBM_PEAK_GBS, 4),
+                "x": "f32" if mm == 1 else "f16 hi + mid + lo" if mm <= 8 else "f16 hi + lo"}
             log(f"[bench] C3 m={mm}: {ms3 * 1e3:.2f} us/launch")
+            if mm in (32, 64):
+                # the same with ARFQ_OPT_GEMV_X16: x rounded to f16 (one part), not the
+                # reference's f32
+                ctx.set_options(_arfq.OPT_GEMV_X16)
+                msx3, _ = time_matmul(ctx, "q6_k", mm, 5120, 17408, steps2, 20, 6, seed=0xA7F00003)
+                ctx.set_options(0)
+                configs[f"c3_q6_k_m{mm}_k17408_n5120_x16_option"] = {
+                    "us_per_launch": round(msx3 * 1e3, 3), "GB/s": round(b3 / msx3 / 1e6, 1),
+                    "hbm_frac": round(b3 / msx3 / 1e6 / HBM_PEAK_GBS, 4), "x": "f16 (one part)",
+                    "note": "ARFQ_OPT_GEMV_X16: x rounded to f16, not the reference's f32 arithmetic"}
+                log(f"[bench] C3 m={mm} x16 option: {msx3 * 1e3:.2f} us/launch")
         # Q5_K and IQ4_XS at C2's shape: the survey's next row (no benchmark config): the
         # decode GEMV (m = 1), the skinny MFMA kernel (m = 8, 64) and, at m = 2048 (f16 x),
         # the rounded-weight prefill tile
@@ -635,15 +647,16 @@ def main():
                 log(f"[bench] MoE T={T}: {msT * 1e3:.1f} us/launch ({len(ids)} experts)")
             except arf_amd.ArfqError as e:
                 configs[f"moe_decode_q4_k_e128_top8_t{T}"] = {"error": str(e)}
-        try:
-            msv, _ = time_matmul(ctx, "q6_k", 1, 151936, 5120, 200, 20, 2, seed=0xA7F0000A)
-            bv = algorithmic_bytes("q6_k", 1, 151936, 5120)
-            configs["lm_head_q6_k_gemv_m1_k5120_n151936"] = {
-                "us_per_launch": round(msv * 1e3, 2), "GB/s": round(bv / msv / 1e6, 1),
-                "hbm_frac": round(bv / msv / 1e6 / HBM_PEAK_GBS, 4)}
-            log(f"[bench] lm_head Q6_K m=1 n=151936: {msv * 1e3:.1f} us/launch")
-        except arf_amd.ArfqError as e:
-            configs["lm_head_q6_k_gemv_m1_k5120_n151936"] = {"error": str(e)}
+        for qv in ("q4_k", "q6_k"):
+            try:
+                msv, _ = time_matmul(ctx, qv, 1, 151936, 5120, 200, 20, 2, seed=0xA7F0000A)
+                bv = algorithmic_bytes(qv, 1, 151936, 5120)
+                configs[f"lm_head_{qv}_gemv_m1_k5120_n151936"] = {
+                    "us_per_launch": round(msv * 1e3, 2), "GB/s": round(bv / msv / 1e6, 1),
+                    "hbm_frac": round(bv / msv / 1e6 / HBM_PEAK_GBS, 4)}
+                log(f"[bench] lm_head {qv} m=1 n=151936: {msv * 1e3:.1f} us/launch")
+            except arf_amd.ArfqError as e:
+                configs[f"lm_head_{qv}_gemv_m1_k5120_n151936"] = {"error": str(e)}
         # the dense FFN (gate / up / SwiGLU / down) of one decode step at C2's shape
         for qts, tag in ((("q4_k", "q4_k", "q4_k"), "q4_k"), (("q4_k", "q4_k", "q6_k"), "q4_k_down_q6_k")):
             try:

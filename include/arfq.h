@@ -90,7 +90,9 @@ int arfq_ctx_sync(arfq_ctx *ctx);
  *   of f32 x to 16-bit fixed point (relative to the block's max |x|) and take
  *   exact integer dots; faster, max relative error ~1e-4 of the output's rms.
  *   Only where those kernels' LDS fits 64 KiB: longer x keeps the default
- *   path.  By default every GEMV multiplies f32 x by the exact weights in f32,
+ *   path.  The skinny MFMA kernel (below) then takes an f32 x as one f16 part
+ *   (11 bits) instead of two or three.
+ *   By default every GEMV multiplies f32 x by the exact weights in f32,
  *   as the reference GEMVs do
  *   (crates/arf-gpu/src/shaders/metal/matmul_vec_q4ks_msl.metal:46-165,
  *   matmul_vec_q4ks_batch_msl.metal:104-288).
@@ -133,9 +135,8 @@ int arfq_weight_info(const arfq_weight *w, int *qtype, int64_t *n_rows, int64_t 
  *     per row (and per K range) by a power of two that puts the row's max |x|
  *     in [2^14, 2^15), so every x within 2^15 of that max is represented
  *     exactly; exact codes, f32 sums, the output scaled back.
- *   - m = 9..32: the same with two parts (hi + lo, ~22 bits).
- *   - m = 33..64: one f16 part.  Above 64 rows: one part (the Q5_K / IQ4_XS
- *     tile loop keeps hi + lo).
+ *   - m = 9..64: the same with two parts (hi + lo, ~22 bits).
+ *   - Above 64 rows: one f16 part (the Q5_K / IQ4_XS tile loop keeps hi + lo).
  * f16 x enters as is.  The weights are exact up to 64 rows; above 64 rows
  * Q6_K, Q8_0, Q5_K and IQ4_XS use the dequant rounded once to f16.
  * Replaces add_matmul_m / add_matmul
