@@ -84,17 +84,22 @@ __global__ __launch_bounds__(GM_THREADS, F::WG_PER_CU) void gemm_q(
     }
 }
 
-// Skinny products (m <= 64): workgroup = 128 weight rows x all m rows, over the
-// 256-element blocks of split blockIdx.y (arfq_skinny.h).  x is f16, or f32
+// threads and weight rows (column tile) of a skinny workgroup with TA x tiles
+__host__ __device__ constexpr int sk_nt(int ta) { return ta == 4 ? 512 : SK_THREADS; }
+__host__ __device__ constexpr int sk_ct(int ta) { return sk_nt(ta) / 2; }
+
+// Skinny products (m <= 64): workgroup = sk_ct(TA) weight rows x all m rows
+// (a wave per 32 weight rows), over the 256-element blocks of split blockIdx.y
+// (arfq_skinny.h).  x is f16, or f32
 // rounded to f16 as it is staged.  With S = gridDim.y > 1 splits each
 // workgroup stores its partial to part[sp][m][n]; the last of a column tile's
 // S workgroups to arrive (counted in tick[blockIdx.x], which it resets to 0)
 // sums the S partials in split order into y, so the result does not depend on
 // the arrival order.
-// (held to 256 VGPRs: two workgroups per CU; with four x tiles the LDS leaves
-// room for one, which gets all 512)
+// (held to 256 VGPRs: two 4-wave workgroups per CU; with four x tiles the LDS
+// leaves room for one workgroup, of 8 waves: two per SIMD again)
 template <class F, int TA, class XT, int PARTS, int GM = 0xFF>
-__global__ __launch_bounds__(SK_THREADS, TA == 4 ? 1 : 2) void gemm_sk(F fmt, const XT *__restrict__ x,
+__global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, const XT *__restrict__ x,
                                                       const uint16_t *__restrict__ xs,
                                                       const float *__restrict__ rs,
                                                       float *__restrict__ y, float *__restrict__ part,
@@ -102,8 +107,9 @@ __global__ __launch_bounds__(SK_THREADS, TA == 4 ? 1 : 2) void gemm_sk(F fmt, co
                                                       int rss) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     __shared__ int last;
+    constexpr int NT = sk_nt(TA), CT = NT / 2;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * 128;
+    const int n0 = blockIdx.x * CT;
     const int nb = K / 256, S = gridDim.y, sp = blockIdx.y;
     const int b0 = (int)((int64_t)sp * nb / S), b1 = (int)((int64_t)(sp + 1) * nb / S);
     // PARTS 2 (M <= 16 TA): x row r < M stages hi row r of x, row PO + r its lo
@@ -116,16 +122,16 @@ __global__ __launch_bounds__(SK_THREADS, TA == 4 ? 1 : 2) void gemm_sk(F fmt, co
     constexpr bool PAIR = PARTS == 2;
     constexpr int PO = PARTS == 3 ? 8 : 16 * TA;
     static_assert(PARTS != 3 || TA == 1, "three parts fit one tile");
-    const SkRows<TA> rows =
-        PARTS == 3 ? sk_rows<TA>(16 + M, K, [M](int r) {
+    const SkRows<TA, NT> rows =
+        PARTS == 3 ? sk_rows<TA, NT>(16 + M, K, [M](int r) {
             return r < M ? r : r < 8 ? 0 : r < 8 + M ? M + r - 8 : r < 16 ? 0 : 2 * M + r - 16;
         })
-        : PAIR ? sk_rows<TA>(PO + M, K, [M](int r) { return r < M ? r : r >= PO ? M + r - PO : 0; })
-               : sk_rows<TA>(M, K, [](int r) { return r; });
+        : PAIR ? sk_rows<TA, NT>(PO + M, K, [M](int r) { return r < M ? r : r >= PO ? M + r - PO : 0; })
+               : sk_rows<TA, NT>(M, K, [](int r) { return r; });
     const int n = n0 + 32 * wave + (lane & 31);
     // the x rows' scales of this K range into LDS past the loop's own, before
     // the loop: the epilogue reads them there instead of loading per output
-    float *lrs = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + sk_lds<F, TA, 1>());
+    float *lrs = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + sk_lds<F, TA, 1, NT>());
     if (rs && tid < 32 * TA) lrs[tid] = tid < M ? rs[(int64_t)sp * rss + tid] : 1.f;
     const F fm[1] = {fmt};
     const int64_t wrow0[1] = {n0 + 32 * wave};
@@ -135,7 +141,7 @@ __global__ __launch_bounds__(SK_THREADS, TA == 4 ? 1 : 2) void gemm_sk(F fmt, co
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // PAIR with two or four tiles: the lo tiles' products go into the hi tiles' accumulators
-    skinny_run<F, TA, 1, SK_THREADS, XT, false, GM, PAIR && TA >= 2, true>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
+    skinny_run<F, TA, 1, NT, XT, false, GM, PAIR && TA >= 2, true>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
                                                                     PARTS == 3 ? 16 + M : PAIR ? PO + M : M);
     if constexpr (PAIR && TA == 1) {
         // rows r and r + 16 of a lane's accumulator are elements i and i + 8
@@ -180,9 +186,9 @@ __global__ __launch_bounds__(SK_THREADS, TA == 4 ? 1 : 2) void gemm_sk(F fmt, co
     // loads the others' partials only after it has seen the count.
     const int GT = (M + 7) >> 3, nt = gridDim.x;
     const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        part, (short)0, (int)((uint32_t)S * nt * GT * 4096u), 0x00020000);
+        part, (short)0, (int)((uint32_t)S * nt * (NT / 64) * GT * 1024u), 0x00020000);
     auto poff = [&](int j, int gi) -> uint32_t {
-        return ((((uint32_t)j * nt + blockIdx.x) * 4 + wave) * GT + gi) * 1024u + lane * 16u;
+        return ((((uint32_t)j * nt + blockIdx.x) * (NT / 64) + wave) * GT + gi) * 1024u + lane * 16u;
     };
     constexpr int SC1 = 16;  // cache-policy operand: device scope
 #pragma unroll
@@ -370,7 +376,7 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     } else if (p.skinny) {
         // split K (whole blocks, >= 2 per split) until ~2 workgroups per CU (~1 with
         // the four x tiles of f32 x at m > 32, whose LDS holds one workgroup per CU)
-        const int64_t nt = (w->n + 127) / 128, nb = w->k / 256;
+        const int64_t ct = sk_ct(p.parts == 2 && m > 32 ? 4 : 1), nt = (w->n + ct - 1) / ct, nb = w->k / 256;
         const int per_cu = p.parts == 2 && m > 32 ? 1 : 2;
         S = std::max<int64_t>(1, (per_cu * (int64_t)cus) / nt);
         S = std::min<int64_t>(S, std::max<int64_t>(1, nb / 2));
@@ -394,9 +400,12 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     p.off_rs = o;  // skinny: one scale per row and split
     o += p.convert ? al256((size_t)(p.skinny ? p.splits : 1) * m * 4) : 0;
     p.off_part = o;
-    if (p.skinny)  // partials in register order: [split][column tile][wave][8-row group][lane] float4
-        o += p.splits > 1 ? al256((size_t)p.splits * ((w->n + 127) / 128) * ((std::min<int64_t>(m, 64) + 7) / 8) * 4096)
+    if (p.skinny) {  // partials in register order: [split][column tile][wave][8-row group][lane] float4
+        const int64_t ct = sk_ct(p.parts == 2 && m > 32 ? 4 : 1);
+        o += p.splits > 1 ? al256((size_t)p.splits * ((w->n + ct - 1) / ct) * (ct / 32) *
+                                  ((std::min<int64_t>(m, 64) + 7) / 8) * 1024)
                           : 0;
+    }
     else
         o += p.splits > 1 ? al256((size_t)p.splits * m * w->n * 4) : al256(bd_part);
     p.scratch_bytes = o;
@@ -414,17 +423,18 @@ static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, con
             return launch_sk_t<F, 1, PARTS, PARTS == 3 ? 0x7 : PARTS == 2 ? 0x5 : 0x1>(fmt, w, m, x, xs, rs, rss, y,
                                                                                       part, tick, S, s);
     }
-    constexpr size_t lds = sk_lds<F, TA, 1>() + 32 * TA * 4;  // + the x rows' scales
+    constexpr int NT = sk_nt(TA), CT = NT / 2;
+    constexpr size_t lds = sk_lds<F, TA, 1, NT>() + 32 * TA * 4;  // + the x rows' scales
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PARTS, GM>, lds, lds_set))
         return err;
-    const dim3 grid((unsigned)((w->n + 127) / 128), (unsigned)S);
-    gemm_sk<F, TA, _Float16, PARTS, GM><<<grid, SK_THREADS, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
+    const dim3 grid((unsigned)((w->n + CT - 1) / CT), (unsigned)S);
+    gemm_sk<F, TA, _Float16, PARTS, GM><<<grid, NT, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
                                                                      (int)w->n, (int)w->k, rss);
     return hipGetLastError();
 }
 
-// S > 1 splits need S <= 16 and one zeroed counter per 128-column tile.  x is
+// S > 1 splits need S <= 16 and one zeroed counter per column tile.  x is
 // f16 (an f32 x arrives prepared and scaled, rs[split * rss + row] its scale
 // over each split's K range); with parts 2 (m <= 64) it is [2m, K]: the hi
 // rows, then the lo rows; with parts 3 (m <= 8) [3m, K]: hi, mid, lo rows.
@@ -432,7 +442,7 @@ template <class F>
 static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                             const uint16_t *xs, const float *rs, int rss, float *y, float *part,
                             uint32_t *tick, int ntick, int S, hipStream_t s, int parts) {
-    if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;
+    if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;  // >= ceil(n / CT)
     if (parts == 3) {
         if (m > 8) return hipErrorInvalidValue;
         return launch_sk_t<F, 1, 3>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
