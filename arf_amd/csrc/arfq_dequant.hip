@@ -9,10 +9,11 @@ namespace arfq {
 // ---- repack ------------------------------------------------------------------
 
 __global__ void repack_q4k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr,
-                           uint8_t *__restrict__ qs, int64_t nblk) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblk) return;
-    const uint8_t *src = raw + b * 144;
+                           uint8_t *__restrict__ qs, int64_t b0, int64_t nblk) {
+    const int64_t lb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (lb >= nblk) return;
+    const int64_t b = b0 + lb;
+    const uint8_t *src = raw + lb * 144;
     uint8_t *h = hdr + b * 16;
     for (int i = 0; i < 16; i++) h[i] = src[i];
     // regroup nibbles per sub-block: element 32j+i lives in ggml byte
@@ -32,20 +33,22 @@ __global__ void repack_q4k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
 }
 
 __global__ void repack_q80(const uint8_t *__restrict__ raw, uint8_t *__restrict__ qs,
-                           uint16_t *__restrict__ d, int64_t nblk) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblk) return;
-    const uint8_t *src = raw + b * 34;
+                           uint16_t *__restrict__ d, int64_t b0, int64_t nblk) {
+    const int64_t lb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (lb >= nblk) return;
+    const int64_t b = b0 + lb;
+    const uint8_t *src = raw + lb * 34;
     d[b] = (uint16_t)(src[0] | (src[1] << 8));
     uint8_t *q = qs + b * 32;
     for (int i = 0; i < 32; i++) q[i] = src[2 + i];
 }
 
 __global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ qb,
-                           uint8_t *__restrict__ sc, uint16_t *__restrict__ d, int64_t nblk) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblk) return;
-    const uint8_t *src = raw + b * 210;
+                           uint8_t *__restrict__ sc, uint16_t *__restrict__ d, int64_t b0, int64_t nblk) {
+    const int64_t lb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (lb >= nblk) return;
+    const int64_t b = b0 + lb;
+    const uint8_t *src = raw + lb * 210;
     const uint8_t *ql = src, *qh = src + 128;
     uint8_t *dst = qb + b * 192;
     for (int c = 0; c < 4; c++) {
@@ -63,43 +66,47 @@ __global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
 
 // Q5_K: the 16-byte header (d, dmin, scales) and ggml's qh[32] + qs[128] as they are.
 __global__ void repack_q5k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr,
-                           uint8_t *__restrict__ q, int64_t nblk) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblk) return;
-    const uint8_t *src = raw + b * 176;
+                           uint8_t *__restrict__ q, int64_t b0, int64_t nblk) {
+    const int64_t lb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (lb >= nblk) return;
+    const int64_t b = b0 + lb;
+    const uint8_t *src = raw + lb * 176;
     for (int i = 0; i < 16; i++) hdr[b * 16 + i] = src[i];
     for (int i = 0; i < 160; i++) q[b * 160 + i] = src[16 + i];
 }
 
 // IQ4_XS: the 8-byte header (d, scales_h, scales_l) and qs[128] as they are.
 __global__ void repack_iq4xs(const uint8_t *__restrict__ raw, uint8_t *__restrict__ hdr,
-                             uint8_t *__restrict__ qs, int64_t nblk) {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblk) return;
-    const uint8_t *src = raw + b * 136;
+                             uint8_t *__restrict__ qs, int64_t b0, int64_t nblk) {
+    const int64_t lb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (lb >= nblk) return;
+    const int64_t b = b0 + lb;
+    const uint8_t *src = raw + lb * 136;
     for (int i = 0; i < 8; i++) hdr[b * 8 + i] = src[i];
     for (int i = 0; i < 128; i++) qs[b * 128 + i] = src[8 + i];
 }
 
-hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s) {
+hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s, int64_t b0, int64_t nb) {
+    if (nb < 0) nb = w->nblk - b0;
+    if (b0 < 0 || nb < 0 || b0 + nb > w->nblk) return hipErrorInvalidValue;
+    if (nb == 0) return hipSuccess;
     const int tpb = 256;
-    const unsigned grid = (unsigned)((w->nblk + tpb - 1) / tpb);
+    const unsigned grid = (unsigned)((nb + tpb - 1) / tpb);
     switch (w->qtype) {
     case ARFQ_Q4_K:
-        repack_q4k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, w->nblk);
+        repack_q4k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, b0, nb);
         break;
     case ARFQ_Q8_0:
-        repack_q80<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint16_t *)w->s1, w->nblk);
+        repack_q80<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint16_t *)w->s1, b0, nb);
         break;
     case ARFQ_Q6_K:
-        repack_q6k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1,
-                                        (uint16_t *)w->s2, w->nblk);
+        repack_q6k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, (uint16_t *)w->s2, b0, nb);
         break;
     case ARFQ_Q5_K:
-        repack_q5k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, w->nblk);
+        repack_q5k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, b0, nb);
         break;
     case ARFQ_IQ4_XS:
-        repack_iq4xs<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, w->nblk);
+        repack_iq4xs<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, b0, nb);
         break;
     default:
         return hipErrorInvalidValue;

@@ -141,8 +141,9 @@ int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
 int arfq_ctx_destroy(arfq_ctx *ctx) {
     if (!ctx) return ARFQ_E_INVALID;
     (void)hipSetDevice(ctx->device);
+    if (ctx->stream && ctx->scratch) (void)hipFreeAsync(ctx->scratch, ctx->stream);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->staging) (void)hipFree(ctx->staging);
     if (ctx->tickets) (void)hipFree(ctx->tickets);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
@@ -245,16 +246,32 @@ int arfq_weight_upload(arfq_ctx *ctx, int qtype, const void *host_blocks, size_t
     if (!ctx || !host_blocks || !out) return fail(ctx, ARFQ_E_INVALID, "weight upload: null argument");
     arfq_weight *w = nullptr;
     if (int rc = weight_create(ctx, qtype, nbytes, n_rows, k_cols, n_experts, &w)) return rc;
-    void *staging = nullptr;
-    hipError_t e = hipMalloc(&staging, nbytes);
-    if (e != hipSuccess) {
-        arfq_weight_free(w);
-        return fail(ctx, ARFQ_E_NOMEM, std::string("weight upload: staging: ") + hipGetErrorString(e));
+    // through the context's staging buffer, UPLOAD_CHUNK bytes of whole blocks at a
+    // time (copy and repack are ordered on the stream); the buffer is allocated
+    // once, on the first upload that needs it
+    const int64_t bb = arfq::block_bytes_of(qtype);
+    const int64_t per = std::max<int64_t>(1, (int64_t)arfq::UPLOAD_CHUNK / bb);
+    const size_t need = (size_t)std::min<int64_t>(w->nblk, per) * (size_t)bb;
+    hipError_t e = hipSuccess;
+    if (ctx->staging_bytes < need) {
+        e = hipStreamSynchronize(ctx->stream);  // an earlier upload's copies are done
+        if (e == hipSuccess && ctx->staging) (void)hipFree(ctx->staging);
+        ctx->staging = nullptr;
+        ctx->staging_bytes = 0;
+        if (e == hipSuccess) e = hipMalloc(&ctx->staging, std::max(need, (size_t)1 << 20));
+        if (e != hipSuccess) {
+            arfq_weight_free(w);
+            return fail(ctx, ARFQ_E_NOMEM, std::string("weight upload: staging: ") + hipGetErrorString(e));
+        }
+        ctx->staging_bytes = std::max(need, (size_t)1 << 20);
     }
-    e = hipMemcpyAsync(staging, host_blocks, nbytes, hipMemcpyHostToDevice, ctx->stream);
-    if (e == hipSuccess) e = arfq::launch_repack(w, (const uint8_t *)staging, ctx->stream);
+    for (int64_t b0 = 0; e == hipSuccess && b0 < w->nblk; b0 += per) {
+        const int64_t nb = std::min(per, w->nblk - b0);
+        e = hipMemcpyAsync(ctx->staging, (const uint8_t *)host_blocks + b0 * bb, (size_t)(nb * bb),
+                           hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess) e = arfq::launch_repack(w, (const uint8_t *)ctx->staging, ctx->stream, b0, nb);
+    }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    (void)hipFree(staging);
     if (e != hipSuccess) {
         arfq_weight_free(w);
         return hip_fail(ctx, e, "weight upload");
@@ -298,16 +315,16 @@ static int check_matmul(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t
     return ARFQ_OK;
 }
 
-// Grow the context scratch to at least `bytes` (synchronises the stream first
-// when it has to reallocate, since enqueued work may still use the old block).
+// Grow the context scratch to at least `bytes`.  Stream-ordered: the old block
+// is freed after the work already enqueued on the stream (which may still use
+// it) and the new one is allocated in stream order, so the host does not wait.
 static int ensure_scratch(arfq_ctx *ctx, size_t bytes) {
     if (ctx->scratch_bytes >= bytes) return ARFQ_OK;
-    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
-    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->scratch) HIP_TRY(ctx, hipFreeAsync(ctx->scratch, ctx->stream));
     ctx->scratch = nullptr;
     ctx->scratch_bytes = 0;
     const size_t sz = (bytes + 0xFFFFF) & ~(size_t)0xFFFFF;
-    hipError_t e = hipMalloc(&ctx->scratch, sz);
+    hipError_t e = hipMallocAsync(&ctx->scratch, sz, ctx->stream);
     if (e != hipSuccess) return fail(ctx, ARFQ_E_NOMEM, std::string("scratch: ") + hipGetErrorString(e));
     ctx->scratch_bytes = sz;
     return ARFQ_OK;

@@ -18,9 +18,13 @@ struct arfq_ctx {
     std::string err;
     hipEvent_t ev_start = nullptr, ev_stop = nullptr;
     unsigned options = 0;  // ARFQ_OPT_* bits
-    // growable scratch for the MoE pipeline (routing, grouping, intermediates)
+    // growable scratch for the GEMM plans, the MoE pipeline and the FFN
+    // (stream-ordered allocations: grown without waiting for the stream)
     void *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // staging of host uploads, reused across calls (at most UPLOAD_CHUNK bytes)
+    void *staging = nullptr;
+    size_t staging_bytes = 0;
     // device address of the allocation-free matmul's fixed scratch on this device
     void *noalloc_scratch = nullptr;
     // split-K arrival counters, one per column tile: zero between launches (the
@@ -47,6 +51,8 @@ namespace arfq {
 // words past the split-K counters (arfq_ctx::tickets) that arfq_stream_read's
 // kernel may store to (one per thread of a 256-thread workgroup)
 constexpr int STREAM_SINK_WORDS = 256;
+// host uploads go through the context's staging buffer in pieces of at most this many bytes
+constexpr size_t UPLOAD_CHUNK = (size_t)64 << 20;
 
 // hipFuncSetAttribute(MaxDynamicSharedMemorySize) for `fn` on the current
 // device, once per device: `done` (one per kernel, zero-initialised static)
@@ -70,8 +76,10 @@ inline int block_bytes_of(int qtype) {
 }
 
 // ---- arfq_dequant.hip ----
-// Split raw ggml blocks (device) into the layout streams of `w`.
-hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s);
+// Split raw ggml blocks (device) into the layout streams of `w`: blocks
+// [b0, b0 + nb) of w (nb < 0: to the end), raw pointing at block b0's bytes.
+hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s, int64_t b0 = 0,
+                         int64_t nb = -1);
 // Dequantize all blocks of `w` to f32.
 hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s);
 

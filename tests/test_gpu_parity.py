@@ -740,3 +740,28 @@ def test_x16_option_skinny_one_part(gpu_ctx, oracle, m):
     e16, e = rel_err(got16, want), rel_err(got, want)
     _say("rel err x16", e16, "default", e)
     assert e16 <= TOL and e <= SMALL_M_TOL and e16 > e
+
+
+@pytest.mark.parametrize("qtype,n,k", [("q8_0", 16384, 4096), ("q6_k", 3000, 27648)])
+def test_upload_in_staging_chunks_bit_exact(gpu_ctx, oracle, qtype, n, k):
+    # host uploads pass through the context's staging buffer 64 MB of whole blocks at a
+    # time: rows on both sides of each chunk boundary (and the first and last rows)
+    # dequantize bit-exactly
+    from arf_amd import QType, synth
+    _say("case: chunked upload", qtype, n, k)
+    raw = synth.weight(qtype, n, k, seed=611)
+    bb, qk = synth.BLOCK_BYTES[qtype], synth.QK[qtype]
+    assert raw.size > (64 << 20)
+    w = gpu_ctx.upload(QType[qtype.upper()], raw, n, k)
+    got = gpu_ctx.dequant(w).numpy().reshape(n, k)
+    per = (64 << 20) // bb  # blocks per chunk
+    bpr = k // qk           # blocks per row
+    rows = {0, n - 1}
+    for c in range(1, raw.size // bb // per + 1):
+        r = c * per // bpr
+        rows.update(range(max(0, r - 2), min(n, r + 3)))
+    rb = raw.reshape(n, -1)
+    for r in sorted(rows):
+        want = oracle.dequant(qtype, rb[r], k)
+        assert np.array_equal(got[r].view(np.uint32), want.view(np.uint32)), r
+    w.free()
