@@ -313,11 +313,15 @@ constexpr int Q4K_GEMV_WG_PER_CU = 2;
 constexpr int Q4K_GEMV_GROUPS = Q4K_GEMV_THREADS / 16;  // 16-lane groups
 constexpr int Q4K_GEMV_PF = 2;                          // steps of loads in flight
 constexpr int Q4K_GEMV_CHUNK = 2;                       // rows per claimed chunk (divides PF)
+constexpr int Q4K_F32_THREADS = 1024;                   // the m = 1 f32 GEMV: one workgroup per CU
 constexpr uint32_t Q4K_OOB = 0x80000000u;               // buffer offset past any stream
 
 // Work split: two 512-thread workgroups per CU (x is quantized once per
 // workgroup; two independent workgroups per CU measured faster than one of
-// 1024 threads); workgroup w owns rows [r0, r1) = [w*n/G, (w+1)*n/G).  Each row is cut into
+// 1024 threads); workgroup w owns rows [r0, r1) = [w*n/G, (w+1)*n/G).  (The
+// single m = 1 f32 GEMV, gemv_q4k_f32, differs: one 1024-thread workgroup per
+// CU owning rows w, w + G, ..., and its x scaled before the first weight load;
+// see gemv_q4k_f32_body.)  Each row is cut into
 // spr = ceil(nblk/4) "columns" of 4 blocks; a "step" is one (row, column)
 // pair.  The steps are handed out in chunks of CHUNK consecutive rows of one
 // column: group g starts with chunk g and then claims chunks from an LDS
@@ -605,11 +609,17 @@ __device__ __forceinline__ float q4k_fdot(const uint4 c, const float *X) {
 
 }  // namespace
 
-template <int XR, int PF, class XSRC>
+// NT threads per workgroup.  XFIRST: x is scaled into LDS before any weight
+// load is issued, and workgroup w owns rows w, w + G, w + 2G, ... (G
+// workgroups) instead of one contiguous range -- the layout of the single
+// m = 1 GEMV, one 1024-thread workgroup per CU.  Otherwise the first weight
+// loads go out ahead of the x scaling and the rows are a contiguous range.
+template <int XR, int PF, int NT, bool XFIRST, class XSRC>
 __device__ __forceinline__ void gemv_q4k_f32_body(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const XSRC &xsrc, float *__restrict__ y, int n, int nblk) {
     constexpr int C = Q4K_GEMV_CHUNK;
+    constexpr int GROUPS = NT / 16;
     static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
     extern __shared__ uint4 smem4[];
     const int nsub = nblk * 8;
@@ -629,9 +639,10 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     const int bq = l16 >> 2, jj = l16 & 3;
 
     const int G = gridDim.x;
-    const int r0 = (int)((int64_t)blockIdx.x * n / G);
-    const int r1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
-    const int R = r1 - r0;
+    // rows of this workgroup: r0 + i * rs for i < R
+    const int r0 = XFIRST ? (int)blockIdx.x : (int)((int64_t)blockIdx.x * n / G);
+    const int rs = XFIRST ? G : 1;
+    const int R = XFIRST ? (n - r0 + G - 1) / G : (int)((int64_t)(blockIdx.x + 1) * n / G) - r0;
     const int cpc = (R + C - 1) / C;  // chunks (of C rows) per column
 
     // Each 16-lane group has a home column (group % spr) and starts on chunk
@@ -666,7 +677,7 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
         }
         const int b = 4 * icol + bq;
         const bool live = icol < spr && irow < R && b < nblk;
-        const uint32_t blk = (uint32_t)(r0 + irow) * (uint32_t)nblk + (uint32_t)b;
+        const uint32_t blk = (uint32_t)(r0 + irow * rs) * (uint32_t)nblk + (uint32_t)b;
         const uint32_t oc = live ? blk * 128u + (uint32_t)jj * 16u : Q4K_OOB;
         const uint32_t oh = live ? blk * 16u + (uint32_t)jj * 4u : Q4K_OOB;
         clo[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oc, 0, 2);
@@ -677,27 +688,36 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     };
 
     // counters start past the chunks the groups begin on
-    for (int c = tid; c < spr; c += Q4K_GEMV_THREADS)
-        cnt[c] = (Q4K_GEMV_GROUPS - c + spr - 1) / spr;
-    // x loads, then (after every wave has issued them) the first chunk of
-    // weights, then x is scaled into LDS; the barrier after it orders LDS only,
-    // so the weight loads stay in flight across it
+    for (int c = tid; c < spr; c += NT)
+        cnt[c] = (GROUPS - c + spr - 1) / spr;
+    // x loads; without XFIRST (after every wave has issued them) the first
+    // chunk of weights, then x is scaled into LDS; the barrier after it orders
+    // LDS only, so the weight loads stay in flight across it.  With XFIRST the
+    // weights go out after the barrier: a wave's loads issue in order and stall
+    // once the CU's memory queue is full, and every CU's weight requests delay
+    // the x requests, so x issued alone arrives 2-3 us earlier at C2's shape.
     const int xitems = nsub * 4;
     XqRound xr[XR];
 #pragma unroll
-    for (int r = 0; r < XR; r++) xr[r] = xsrc.load(xitems, r * Q4K_GEMV_THREADS);
+    for (int r = 0; r < XR; r++) xr[r] = xsrc.load(xitems, r * NT);
     asm volatile("" ::: "memory");  // keep the x loads ahead of the weight loads
-    __builtin_amdgcn_s_barrier();
+    if (!XFIRST) {
+        __builtin_amdgcn_s_barrier();
 #pragma unroll
-    for (int u = 0; u < PF; u++) issue(u, true);
-    asm volatile("" ::: "memory");
+        for (int u = 0; u < PF; u++) issue(u, true);
+        asm volatile("" ::: "memory");
+    }
     // (every round is processed: items past the end load a clamped index and
     // store nothing, and an unconditional use keeps the loads where they are)
 #pragma unroll
-    for (int r = 0; r < XR; r++) xf_process(xr[r], xitems, r * Q4K_GEMV_THREADS, xf, xs);
-    for (int base = XR * Q4K_GEMV_THREADS; base < xitems; base += Q4K_GEMV_THREADS)
+    for (int r = 0; r < XR; r++) xf_process(xr[r], xitems, r * NT, xf, xs);
+    for (int base = XR * NT; base < xitems; base += NT)
         xf_process(xsrc.load(xitems, base), xitems, base, xf, xs);
     lds_barrier();  // scaled x and the counters are visible from here on
+    if (XFIRST) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) issue(u, true);
+    }
 
     // scaled x of the column being consumed (sub-blocks jj, jj + 4)
     int xcol = -1;
@@ -750,19 +770,20 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     }
     lds_barrier();
 
-    for (int t = tid; t < R; t += Q4K_GEMV_THREADS) {
+    for (int t = tid; t < R; t += NT) {
         const float *pr = part + (size_t)t * spr;
         float v = 0.f;
         for (int c = 0; c < spr; c++) v += pr[c];
-        y[r0 + t] = v;
+        y[r0 + t * rs] = v;
     }
 }
 
 template <int XR>
-__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32(
+__global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk) {
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n, nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, true>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n,
+                                                              nblk);
 }
 
 // The FFN's down GEMV at one x row: x = act(g) * u, f32 arithmetic.
@@ -771,7 +792,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_glu(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ g, const float *__restrict__ u,
     float *__restrict__ y, int n, int nblk) {
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y, n, nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y, n, nblk);
 }
 
 // The FFN's gate and up GEMVs in one launch: blockIdx.y = 0 multiplies x by
@@ -783,7 +804,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_dual(
     const uint8_t *__restrict__ qs1, uint32_t hdr_bytes, uint32_t qs_bytes, const float *__restrict__ x,
     float *__restrict__ y0, float *__restrict__ y1, int n, int nblk) {
     const bool second = blockIdx.y != 0;  // uniform over the workgroup
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0, qs_bytes,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0, qs_bytes,
                                        XsF32{x}, second ? y1 : y0, n, nblk);
 }
 
@@ -802,7 +823,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
     const int e = ids[p];
     if (e < 0 || e >= E) return;  // uniform over the workgroup
     xsrc.pair(p);
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
                                        qs + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
                                        y + (int64_t)p * n, n, nblk);
 }
@@ -821,7 +842,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs_dual(
     if (e < 0 || e >= E) return;  // uniform over the workgroup
     const bool second = blockIdx.z != 0;
     xsrc.pair(p);
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF>((second ? hdr1 : hdr0) + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>((second ? hdr1 : hdr0) + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
                                        (second ? qs1 : qs0) + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
                                        (second ? y1 : y0) + (int64_t)p * n, n, nblk);
 }
@@ -1651,7 +1672,7 @@ __global__ __launch_bounds__(64) void gemv_q6k(const uint4 *__restrict__ qb,
 constexpr int GEMV_MAX_M = 4;
 
 static size_t q4k_gemv_lds(const arfq_weight *w, int mx);
-static bool q4k_f32_ok(const arfq_weight *w);
+static bool q4k_f32s_ok(const arfq_weight *w);
 static size_t dot_lds(const arfq_weight *w, int mx);
 static bool dot_f32_ok(const arfq_weight *w);
 // the byte-code dot GEMV: Q6_K at m <= 2, Q5_K at m <= 4, while x fits in LDS and
@@ -1689,7 +1710,7 @@ bool gemv_supports(const arfq_weight *w, int64_t m, bool x16) {
     switch (w->qtype) {
     case ARFQ_Q4_K:
         if (x16 && q4k_x16_ok(w, m)) return true;
-        return m == 1 && q4k_f32_ok(w);
+        return m == 1 && q4k_f32s_ok(w);
     case ARFQ_Q5_K:
     case ARFQ_IQ4_XS:
         if (x16 && dot_ok(w, m)) return true;
@@ -1888,9 +1909,30 @@ static bool q4k_f32_ok(const arfq_weight *w) {
            w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
 }
 // rounds of x loads issued ahead of the weight ring (8 elements per thread and round)
-static int q4k_f32_xr(const arfq_weight *w) {
-    const int64_t rounds = (w->k / 8 + Q4K_GEMV_THREADS - 1) / Q4K_GEMV_THREADS;
+static int q4k_f32_xr(const arfq_weight *w, int threads = Q4K_GEMV_THREADS) {
+    const int64_t rounds = (w->k / 8 + threads - 1) / threads;
     return rounds <= 1 ? 1 : rounds <= 2 ? 2 : 4;
+}
+// The single m = 1 GEMV (gemv_q4k_f32): one 1024-thread workgroup per CU, rows
+// interleaved over the workgroups, x scaled before the first weight load.  At C2
+// (k = 5120, n = 17408) this measured 13.2-13.5 us per launch against 14.6-14.8
+// for two 512-thread workgroups per CU with contiguous row ranges and the
+// weight loads issued ahead of x (same driver loop, rotating weight copies).
+// Small problems get fewer workgroups (>= 2 steps per 16-lane group).
+static int64_t q4k_f32s_grid(const arfq_weight *w) {
+    const int64_t steps = w->n * ((w->k / 256 + 3) / 4);
+    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
+    int64_t grid = std::min<int64_t>(cus, (steps + 2 * (Q4K_F32_THREADS / 16) - 1) / (2 * (Q4K_F32_THREADS / 16)));
+    grid = std::min<int64_t>(grid, w->n);
+    return grid < 1 ? 1 : grid;
+}
+static size_t q4k_f32s_lds(const arfq_weight *w) {
+    const int64_t grid = q4k_f32s_grid(w);
+    return q4k_f32_lds_rows(w, (w->n + grid - 1) / grid);
+}
+static bool q4k_f32s_ok(const arfq_weight *w) {
+    return w->qtype == ARFQ_Q4_K && q4k_f32s_lds(w) <= Q4K_F32_LDS_MAX &&
+           w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
 }
 template <int XR>
 static hipError_t launch_q4k_f32_t(const arfq_weight *w, int e, const float *x, float *y, hipStream_t s) {
@@ -1899,13 +1941,13 @@ static hipError_t launch_q4k_f32_t(const arfq_weight *w, int e, const float *x, 
         return err;
     const int nblk = (int)(w->k / 256);
     const int64_t nb = w->n * nblk, eb = (int64_t)e * nb;
-    gemv_q4k_f32<XR><<<(unsigned)q4k_f32_grid(w), Q4K_GEMV_THREADS, q4k_f32_lds(w), s>>>(
+    gemv_q4k_f32<XR><<<(unsigned)q4k_f32s_grid(w), Q4K_F32_THREADS, q4k_f32s_lds(w), s>>>(
         (const uint8_t *)w->s0 + eb * 16, (uint32_t)(nb * 16), (const uint8_t *)w->s1 + eb * 128,
         (uint32_t)(nb * 128), x, y, (int)w->n, nblk);
     return hipGetLastError();
 }
 static hipError_t launch_q4k_f32(const arfq_weight *w, int e, const float *x, float *y, hipStream_t s) {
-    switch (q4k_f32_xr(w)) {
+    switch (q4k_f32_xr(w, Q4K_F32_THREADS)) {
     case 1: return launch_q4k_f32_t<1>(w, e, x, y, s);
     case 2: return launch_q4k_f32_t<2>(w, e, x, y, s);
     default: return launch_q4k_f32_t<4>(w, e, x, y, s);
@@ -2031,8 +2073,12 @@ static hipError_t launch_gemv_glu_t(const arfq_weight *w, int64_t m, const float
     }
     return launch_q4k_f32_glu<ACT>(w, g, u, y, s);  // m == 1, q4k_f32_ok
 }
+// what launch_gemv_glu_t takes: the 16-bit kernel under x16 where it fits,
+// otherwise the 512-thread f32 kernel at m = 1
 bool gemv_glu_supports(const arfq_weight *w, int64_t m, bool x16) {
-    return w->qtype == ARFQ_Q4_K && w->experts == 1 && gemv_supports(w, m, x16);
+    if (w->qtype != ARFQ_Q4_K || w->experts != 1) return false;
+    if (x16 && q4k_x16_ok(w, m)) return true;
+    return m == 1 && q4k_f32_ok(w);
 }
 hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y, int act,
                            hipStream_t s, bool x16) {
@@ -2100,7 +2146,7 @@ hipError_t launch_gemv(const arfq_weight *w, int e, int64_t m, const float *x, f
             if (m == 2) return launch_gemv_q4k<2>(w, e, 2, x, y, s);
             return launch_gemv_q4k<4>(w, e, (int)m, x, y, s);
         }
-        return launch_q4k_f32(w, e, x, y, s);  // m == 1, q4k_f32_ok
+        return launch_q4k_f32(w, e, x, y, s);  // m == 1, q4k_f32s_ok
     }
     if (w->qtype == ARFQ_Q5_K) {
         const DotQ5K f = dot_q5k(w, e);

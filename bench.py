@@ -449,6 +449,9 @@ def only_config(ctx, args):
         ms, _ = time_matmul(ctx, "q4_k", 1, 17408, 5120, args.steps, args.warmup, args.copies, 0xA7F00002)
         ctx.set_options(0)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q4_k", 1, 17408, 5120) / ms / 1e6}
+    elif c == "lmhead":  # the vocab-wide Q4_K lm_head GEMV (K = 5120, N = 151936)
+        ms, _ = time_matmul(ctx, "q4_k", 1, 151936, 5120, args.steps, args.warmup, 2, 0xA7F0000A)
+        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q4_k", 1, 151936, 5120) / ms / 1e6}
     elif c == "c1n8":
         # one workgroup's worth of C1 (8 rows): the per-launch floor C1 sits on
         ms, _ = time_matmul(ctx, "q8_0", 1, 8, 2048, args.steps, args.warmup, 64, 0xA7F00001)
@@ -491,7 +494,7 @@ def main():
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
     ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c3m64x16", "c4",
-                                       "c5", "q5km1", "c1n8"],
+                                       "c5", "q5km1", "c1n8", "lmhead"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
