@@ -44,7 +44,8 @@ __global__ void repack_q80(const uint8_t *__restrict__ raw, uint8_t *__restrict_
 }
 
 __global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict__ qb,
-                           uint8_t *__restrict__ sc, uint16_t *__restrict__ d, int64_t b0, int64_t nblk) {
+                           uint8_t *__restrict__ sc, uint16_t *__restrict__ d, int64_t b0, int64_t nblk,
+                           uint32_t *__restrict__ wide) {
     const int64_t lb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (lb >= nblk) return;
     const int64_t b = b0 + lb;
@@ -60,8 +61,14 @@ __global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
             o[32 + i] = qh[32 * n2 + l0 + i];
         }
     }
-    for (int i = 0; i < 16; i++) sc[b * 16 + i] = src[192 + i];
+    bool big = false;
+    for (int i = 0; i < 16; i++) {
+        sc[b * 16 + i] = src[192 + i];
+        const int v = (int8_t)src[192 + i];
+        big |= v > 64 || v < -64;
+    }
     d[b] = (uint16_t)(src[208] | (src[209] << 8));
+    if (big && wide) *wide = 1u;  // the prefill GEMM then splits sc * (q - 32) into hi + lo
 }
 
 // Q5_K: the 16-byte header (d, dmin, scales) and ggml's qh[32] + qs[128] as they are.
@@ -86,7 +93,8 @@ __global__ void repack_iq4xs(const uint8_t *__restrict__ raw, uint8_t *__restric
     for (int i = 0; i < 128; i++) qs[b * 128 + i] = src[8 + i];
 }
 
-hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s, int64_t b0, int64_t nb) {
+hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s, int64_t b0, int64_t nb,
+                         uint32_t *wide) {
     if (nb < 0) nb = w->nblk - b0;
     if (b0 < 0 || nb < 0 || b0 + nb > w->nblk) return hipErrorInvalidValue;
     if (nb == 0) return hipSuccess;
@@ -100,7 +108,7 @@ hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s
         repack_q80<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint16_t *)w->s1, b0, nb);
         break;
     case ARFQ_Q6_K:
-        repack_q6k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, (uint16_t *)w->s2, b0, nb);
+        repack_q6k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, (uint16_t *)w->s2, b0, nb, wide);
         break;
     case ARFQ_Q5_K:
         repack_q5k<<<grid, tpb, 0, s>>>(raw, (uint8_t *)w->s0, (uint8_t *)w->s1, b0, nb);

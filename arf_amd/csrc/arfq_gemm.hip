@@ -543,7 +543,11 @@ static hipError_t launch_bd(const arfq_weight *w, int e, int64_t m, const _Float
     case ARFQ_IQ4_XS:
         return launch_bd_t(BdIQ4XS{(const uint2 *)w->s0 + eb, (const uint4 *)w->s1 + eb * 8}, w, m, x, xs, rs,
                            y, part, p, s);
-    case ARFQ_Q6_K:
+    case ARFQ_Q6_K:  // scales beyond +-64 (flagged by the upload): sc * (q - 32) as hi + lo
+        if (w->wide)
+            return launch_bd_t(BdQ6KW{(const uint2 *)w->s0 + eb * 24, (const uint4 *)w->s1 + eb,
+                                      (const uint16_t *)w->s2 + eb},
+                               w, m, x, xs, rs, y, part, p, s);
         return launch_bd_t(BdQ6K{(const uint2 *)w->s0 + eb * 24, (const uint4 *)w->s1 + eb,
                                  (const uint16_t *)w->s2 + eb},
                            w, m, x, xs, rs, y, part, p, s);

@@ -147,7 +147,7 @@ struct BdQ4K {
     static constexpr bool EXTRA = false;
     struct Extra {};
     static constexpr bool XPERM = false, LATE = false;
-    static constexpr bool UNITS = true, MIN = true, STEP_KK = false;
+    static constexpr bool UNITS = true, MIN = true, STEP_KK = false, WLO = false;
     static constexpr int VPM = 3;
     using Code = u32x4;
     using Head = u32x4;
@@ -209,7 +209,7 @@ struct BdQ5K {
     static constexpr int XPARTS = 4;
     static constexpr bool EXTRA = true;  // the qh bytes come separately, late
     static constexpr bool XPERM = true, LATE = true;
-    static constexpr bool UNITS = true, MIN = true, STEP_KK = false;
+    static constexpr bool UNITS = true, MIN = true, STEP_KK = false, WLO = false;
     static constexpr int VPM = 5;
     using Code = u32x4;
     using Head = u32x4;
@@ -300,7 +300,7 @@ struct BdIQ4XS {
     static constexpr bool EXTRA = false;
     struct Extra {};
     static constexpr bool XPERM = false, LATE = false;
-    static constexpr bool UNITS = true, MIN = false, STEP_KK = false;
+    static constexpr bool UNITS = true, MIN = false, STEP_KK = false, WLO = false;
     static constexpr int VPM = 6;
     using Code = u32x4;
     using Head = u32x2;    // d | scales_h << 16, scales_l
@@ -370,16 +370,20 @@ struct BdIQ4XS {
     }
 };
 
-// Q8_0 (weights d * q rounded to f16, true units): step p of block b, lane
-// half h = Q8_0 block 8b + 2p + h (its 32 codes, 32 bytes); group kk =
-// elements 8kk .. 8kk + 7.  The header is the 8 block scales d of the 256
-// elements.  (dequant_q8_0, crates/arf-core/src/model/gguf.rs)
+// Q8_0 (weights d * q exact as two f16 operands, true units): step p of
+// block b, lane half h = Q8_0 block 8b + 2p + h (its 32 codes, 32 bytes);
+// group kk = elements 8kk .. 8kk + 7.  The header is the 8 block scales d of
+// the 256 elements.  d * q has at most 19 significant bits (11 of d, 8 of q):
+// hi = d * q rounded to f16 and lo = fma(q, d, -hi), the exact rounding error
+// (at most 8 significant bits, a multiple of d's last place), are both exact
+// f16 values and hi + lo = d * q, so each group runs its MFMAs twice, once per
+// part (WLO).  (dequant_q8_0, crates/arf-core/src/model/gguf.rs)
 struct BdQ80 {
     static constexpr int XPARTS = 2;
     static constexpr bool EXTRA = false;
     struct Extra {};
     static constexpr bool XPERM = false, LATE = false;
-    static constexpr bool UNITS = false, MIN = false, STEP_KK = false;
+    static constexpr bool UNITS = false, MIN = false, STEP_KK = false, WLO = true;
     static constexpr int VPM = 4;
     struct Code {
         u32x4 a, b;
@@ -421,34 +425,44 @@ struct BdQ80 {
     __device__ static Step step(const Blk &b, int p, int) {
         return as_h2(__builtin_amdgcn_perm(0u, (p >> 1) ? b.y : b.x, (p & 1) ? 0x03020302u : 0x01000100u));
     }
-    __device__ static half8 deq(const Code &c, const Step &d, const Blk &, int, int kk) {
+    __device__ static void deq2(const Code &c, const Step &d, const Blk &, int, int kk, half8 &hi, half8 &lo) {
         const uint32_t w[2] = {kk == 0 ? c.a.x : kk == 1 ? c.a.z : kk == 2 ? c.b.x : c.b.z,
                                kk == 0 ? c.a.y : kk == 1 ? c.a.w : kk == 2 ? c.b.y : c.b.w};
         const half2v m1152 = {-1152.f, -1152.f};
-        uint32_t o[4];
+        uint32_t o[4], l[4];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const uint32_t u = w[j] ^ 0x80808080u;  // q + 128 per byte
-            // (1024 + q + 128) - 1152 = q exactly, then one rounding of d * q
-            o[2 * j] = as_u((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04010400u)) + m1152) * d);
-            o[2 * j + 1] = as_u((as_h2(__builtin_amdgcn_perm(0x64646464u, u, 0x04030402u)) + m1152) * d);
+#pragma unroll
+            for (int pr = 0; pr < 2; pr++) {
+                // (1024 + q + 128) - 1152 = q exactly; hi = d * q rounded once, lo its error
+                const half2v q = as_h2(__builtin_amdgcn_perm(0x64646464u, u, pr ? 0x04030402u : 0x04010400u)) + m1152;
+                const half2v hv = q * d;
+                o[2 * j + pr] = as_u(hv);
+                l[2 * j + pr] = as_u(__builtin_elementwise_fma(q, d, -hv));
+            }
         }
-        return bd_h8(o[0], o[1], o[2], o[3]);
+        hi = bd_h8(o[0], o[1], o[2], o[3]);
+        lo = bd_h8(l[0], l[1], l[2], l[3]);
     }
 };
 
-// Q6_K (weights rounded to f16): step p = 48-byte chunk p of the block
-// (ql_a[16] | ql_b[16] | qh[16]); lane half h takes bytes 8h .. 8h + 7 of
-// each; group kk = quadrant kk: elements 128 (p / 2) + 16 (p % 2) + 32 kk +
-// 8h + 0..7, one 16-element sub-block.  Operands sc * (q - 32) in units of d,
-// rounded once to f16 (exact while |sc| <= 64).
+// Q6_K (exact): step p = 48-byte chunk p of the block (ql_a[16] | ql_b[16] |
+// qh[16]); lane half h takes bytes 8h .. 8h + 7 of each; group kk = quadrant
+// kk: elements 128 (p / 2) + 16 (p % 2) + 32 kk + 8h + 0..7, one 16-element
+// sub-block.  Operands sc * (q - 32) in units of d: an integer of magnitude at
+// most 128 * 32 = 4096, exact in f16 up to 2048 (|sc| <= 64, the synthetic
+// scales and WIDE = false); past 2048 f16 holds only even integers, so with
+// WIDE (a tensor with some |sc| > 64) hi = sc * (q - 32) rounded and lo =
+// fma(q - 32, sc, -hi) in {-1, 0, 1} run as two MFMAs (WLO).
 // (dequant_q6_k, crates/arf-core/src/model/gguf.rs:2092-2131)
-struct BdQ6K {
+template <bool WIDE>
+struct BdQ6KT {
     static constexpr int XPARTS = 2;
     static constexpr bool EXTRA = false;
     struct Extra {};
     static constexpr bool XPERM = false, LATE = true;
-    static constexpr bool UNITS = true, MIN = false, STEP_KK = true;
+    static constexpr bool UNITS = true, MIN = false, STEP_KK = true, WLO = WIDE;
     static constexpr int VPM = 7;
     struct Code {
         u32x2 a, b, qh;
@@ -499,11 +513,13 @@ struct BdQ6K {
         return h2splat((float)(int8_t)(w >> (8 * (si & 3))));
     }
     // q as the f16 1024 + q (v_perm puts 0x64 above each code byte; the two
-    // qh bits go to bits 4-5), minus 1056 (exact), times sc (one rounding)
-    __device__ static half8 deq(const Code &c, const Step &sc, const Blk &, int, int kk) {
+    // qh bits go to bits 4-5), minus 1056 (exact), times sc (one rounding,
+    // none while |sc| <= 64); LO: the rounding error as a second operand
+    template <bool LO>
+    __device__ static void deq_t(const Code &c, const Step &sc, int kk, half8 &hi, half8 &lo) {
         const half2v m1056 = {-1056.f, -1056.f};
         const u32x2 ql = (kk & 1) ? c.b : c.a;
-        uint32_t o[4];
+        uint32_t o[4], e[4];
 #pragma unroll
         for (int hh = 0; hh < 2; hh++) {
             const uint32_t l = (kk & 2) ? ((hh ? ql.y : ql.x) >> 4) : (hh ? ql.y : ql.x);
@@ -514,12 +530,26 @@ struct BdQ6K {
                 const uint32_t hp = __builtin_amdgcn_perm(0u, qw, pr ? 0x0c030c02u : 0x0c010c00u);
                 const uint32_t top = 2 * kk <= 4 ? (hp << (4 - 2 * kk)) : (hp >> (2 * kk - 4));
                 const uint32_t q = (lp & 0x640F640Fu) | (top & 0x00300030u);
-                o[2 * hh + pr] = as_u((as_h2(q) + m1056) * sc);
+                const half2v qm = as_h2(q) + m1056;
+                const half2v hv = qm * sc;
+                o[2 * hh + pr] = as_u(hv);
+                if constexpr (LO) e[2 * hh + pr] = as_u(__builtin_elementwise_fma(qm, sc, -hv));
             }
         }
-        return bd_h8(o[0], o[1], o[2], o[3]);
+        hi = bd_h8(o[0], o[1], o[2], o[3]);
+        if constexpr (LO) lo = bd_h8(e[0], e[1], e[2], e[3]);
+    }
+    __device__ static half8 deq(const Code &c, const Step &sc, const Blk &, int, int kk) {
+        half8 hi, lo;
+        deq_t<false>(c, sc, kk, hi, lo);
+        return hi;
+    }
+    __device__ static void deq2(const Code &c, const Step &sc, const Blk &, int, int kk, half8 &hi, half8 &lo) {
+        deq_t<true>(c, sc, kk, hi, lo);
     }
 };
+using BdQ6K = BdQ6KT<false>;   // every |sc| <= 64: one exact operand
+using BdQ6KW = BdQ6KT<true>;   // some |sc| > 64: hi + lo operands
 
 // Work items: the first `full` items are whole tiles (in XCD order when
 // xcd_order); the remaining tiles are each split into `chunks` K ranges of
@@ -715,7 +745,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         //    read of this block's scales is group 12's b[1]) and issues the
         //    loads of the one after; where every group's operands read the
         //    block data (LATE), group 15 does, after its b[1].
-        half8 a[4], b[2];
+        half8 a[4], b[2], bw[2];  // bw: the weights' lo operands (WLO)
         typename F::Step ks[2];
         bf16x8 bh[2], bl[2], am[4];
         auto xread = [&](int i, int mg) {
@@ -724,7 +754,10 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         auto deq = [&](int i, int g) {
             const int p = i >> 2, kk = i & 3;
             if (F::STEP_KK || kk == 0) ks[g] = F::step(scd[g], p, kk);
-            b[g] = F::deq(cq[p & 1][g], ks[g], scd[g], p, kk);
+            if constexpr (F::WLO)
+                F::deq2(cq[p & 1][g], ks[g], scd[g], p, kk, b[g], bw[g]);
+            else
+                b[g] = F::deq(cq[p & 1][g], ks[g], scd[g], p, kk);
         };
 #pragma unroll
         for (int mg = 0; mg < 4; mg++) xread(0, mg);
@@ -761,6 +794,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
                 acc[mg][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[0], acc[mg][0], 0, 0, 0);
+                if constexpr (F::WLO) acc[mg][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], bw[0], acc[mg][0], 0, 0, 0);
                 if (mgroup) {
 #pragma unroll
                     for (int g = 0; g < 2; g++) {
@@ -774,8 +808,8 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
             if (!mgroup) {
 #pragma unroll
                 for (int mg = 0; mg < 4; mg++) {
-                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
-                    __builtin_amdgcn_sched_group_barrier(0x002, F::VPM, 0);  // VALU
+                    __builtin_amdgcn_sched_group_barrier(0x008, F::WLO ? 2 : 1, 0);  // one MFMA (per part)
+                    __builtin_amdgcn_sched_group_barrier(0x002, F::VPM, 0);           // VALU
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -795,14 +829,15 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
                 acc[mg][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[1], acc[mg][1], 0, 0, 0);
+                if constexpr (F::WLO) acc[mg][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], bw[1], acc[mg][1], 0, 0, 0);
                 if (more) xread(i + 1, mg);
             }
             if (more) deq(i + 1, 0);  // the next group's first B operand, under these MFMAs
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
-                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);        // its x read
-                __builtin_amdgcn_sched_group_barrier(0x002, F::VPM, 0);  // VALU
+                __builtin_amdgcn_sched_group_barrier(0x008, F::WLO ? 2 : 1, 0);  // one MFMA (per part)
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);                // its x read
+                __builtin_amdgcn_sched_group_barrier(0x002, F::VPM, 0);           // VALU
             }
             __builtin_amdgcn_sched_barrier(0);
             if (kk == 3) cload(p & 1, 4 * blk + p + 2);  // the slot is free: step + 2

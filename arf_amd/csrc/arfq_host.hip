@@ -121,12 +121,16 @@ int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_stop);
     if (e == hipSuccess) {
-        // the split-K counters, then STREAM_SINK_WORDS words of arfq_stream_read's sink
+        // the split-K counters, then STREAM_SINK_WORDS words of arfq_stream_read's
+        // sink, then the upload's flag words
         ctx->ntickets = std::max(1024, 2 * ctx->cus);
-        e = hipMalloc(&ctx->tickets, ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS) * sizeof(uint32_t));
+        e = hipMalloc(&ctx->tickets, ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS + arfq::UPLOAD_FLAG_WORDS) *
+                                         sizeof(uint32_t));
     }
     if (e == hipSuccess)
-        e = hipMemsetAsync(ctx->tickets, 0, ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS) * sizeof(uint32_t),
+        e = hipMemsetAsync(ctx->tickets, 0,
+                           ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS + arfq::UPLOAD_FLAG_WORDS) *
+                               sizeof(uint32_t),
                            ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
@@ -226,13 +230,34 @@ static int weight_create(arfq_ctx *ctx, int qtype, size_t nbytes, int64_t n_rows
     return ARFQ_OK;
 }
 
+// Q6_K uploads: the repack flags a sub-block scale outside [-64, 64] in a word
+// of the context's counter allocation (cleared first); read back once the
+// repacks are done, it selects the prefill GEMM's two-operand weights.
+static uint32_t *upload_flag(arfq_ctx *ctx, const arfq_weight *w) {
+    return w->qtype == ARFQ_Q6_K && ctx->tickets ? ctx->tickets + ctx->ntickets + arfq::STREAM_SINK_WORDS : nullptr;
+}
+static hipError_t upload_flag_clear(arfq_ctx *ctx, uint32_t *flag) {
+    return flag ? hipMemsetAsync(flag, 0, sizeof(uint32_t), ctx->stream) : hipSuccess;
+}
+static hipError_t upload_flag_read(arfq_ctx *ctx, uint32_t *flag, arfq_weight *w) {
+    if (!flag) return hipSuccess;
+    uint32_t h = 0;
+    hipError_t e = hipMemcpyAsync(&h, flag, sizeof(h), hipMemcpyDeviceToHost, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    w->wide = h != 0;
+    return e;
+}
+
 int arfq_weight_upload_device(arfq_ctx *ctx, int qtype, const void *dev_blocks, size_t nbytes,
                               int64_t n_rows, int64_t k_cols, int n_experts, arfq_weight **out) {
     if (!dev_blocks) return fail(ctx, ARFQ_E_INVALID, "weight upload: null blocks");
     arfq_weight *w = nullptr;
     if (int rc = weight_create(ctx, qtype, nbytes, n_rows, k_cols, n_experts, &w)) return rc;
-    hipError_t e = arfq::launch_repack(w, (const uint8_t *)dev_blocks, ctx->stream);
+    uint32_t *flag = upload_flag(ctx, w);
+    hipError_t e = upload_flag_clear(ctx, flag);
+    if (e == hipSuccess) e = arfq::launch_repack(w, (const uint8_t *)dev_blocks, ctx->stream, 0, -1, flag);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = upload_flag_read(ctx, flag, w);
     if (e != hipSuccess) {
         arfq_weight_free(w);
         return hip_fail(ctx, e, "weight upload: repack");
@@ -265,13 +290,16 @@ int arfq_weight_upload(arfq_ctx *ctx, int qtype, const void *host_blocks, size_t
         }
         ctx->staging_bytes = std::max(need, (size_t)1 << 20);
     }
+    uint32_t *flag = upload_flag(ctx, w);
+    if (e == hipSuccess) e = upload_flag_clear(ctx, flag);
     for (int64_t b0 = 0; e == hipSuccess && b0 < w->nblk; b0 += per) {
         const int64_t nb = std::min(per, w->nblk - b0);
         e = hipMemcpyAsync(ctx->staging, (const uint8_t *)host_blocks + b0 * bb, (size_t)(nb * bb),
                            hipMemcpyHostToDevice, ctx->stream);
-        if (e == hipSuccess) e = arfq::launch_repack(w, (const uint8_t *)ctx->staging, ctx->stream, b0, nb);
+        if (e == hipSuccess) e = arfq::launch_repack(w, (const uint8_t *)ctx->staging, ctx->stream, b0, nb, flag);
     }
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = upload_flag_read(ctx, flag, w);
     if (e != hipSuccess) {
         arfq_weight_free(w);
         return hip_fail(ctx, e, "weight upload");

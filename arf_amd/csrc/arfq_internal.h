@@ -44,6 +44,7 @@ struct arfq_weight {
     void *s1 = nullptr;  // Q4_K qs  | Q8_0 d  | Q6_K sc | Q5_K qh + qs | IQ4_XS qs
     void *s2 = nullptr;  //                      Q6_K d
     size_t bytes = 0;    // ggml bytes of one expert (what one matmul streams)
+    bool wide = false;   // Q6_K: some sub-block scale outside [-64, 64] (set by the upload)
 };
 
 namespace arfq {
@@ -51,6 +52,8 @@ namespace arfq {
 // words past the split-K counters (arfq_ctx::tickets) that arfq_stream_read's
 // kernel may store to (one per thread of a 256-thread workgroup)
 constexpr int STREAM_SINK_WORDS = 256;
+// words past the sink: the upload's flag (a Q6_K scale outside [-64, 64] seen by the repack)
+constexpr int UPLOAD_FLAG_WORDS = 64;
 // host uploads go through the context's staging buffer in pieces of at most this many bytes
 constexpr size_t UPLOAD_CHUNK = (size_t)64 << 20;
 
@@ -78,8 +81,10 @@ inline int block_bytes_of(int qtype) {
 // ---- arfq_dequant.hip ----
 // Split raw ggml blocks (device) into the layout streams of `w`: blocks
 // [b0, b0 + nb) of w (nb < 0: to the end), raw pointing at block b0's bytes.
+// Q6_K: a repack that meets a sub-block scale outside [-64, 64] stores 1 to
+// *wide (when not null).
 hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s, int64_t b0 = 0,
-                         int64_t nb = -1);
+                         int64_t nb = -1, uint32_t *wide = nullptr);
 // Dequantize all blocks of `w` to f32.
 hipError_t launch_dequant(const arfq_weight *w, float *out, hipStream_t s);
 

@@ -281,10 +281,11 @@ def test_next_formats_skinny_and_prefill(gpu_ctx, oracle, qtype, m, n, k, x16):
 def test_q6_k_full_range_scales(gpu_ctx, oracle, m):
     # quantizers put each block's largest sub-block scale near +-127, where sc * (q - 32)
     # passes 2048 and would round in f16; the skinny kernel (m = 5..64) multiplies the exact
-    # codes q - 32 and scales each sub-block's product by d * sc in f32, the prefill tile
-    # (m = 130) holds d * sc * (q - 32) rounded to f16 (relative error <= 2^-11).  The
-    # synthetic blocks keep scales in [-32, 31], so this test draws them from all of i8;
-    # at m = 8 (x as f16 hi + lo, about 22 bits) the skinny result is held to 2e-5
+    # codes q - 32 and scales each sub-block's product by d * sc in f32, the prefill GEMM
+    # (m = 130) holds sc * (q - 32) as f16 hi + lo (exact; its f32 x is rounded to f16,
+    # which sets the error here).  The synthetic blocks keep scales in [-32, 31], so this
+    # test draws them from all of i8; at m = 8 (x as three f16 parts) the skinny result is
+    # held to 2e-5
     from arf_amd import QType, synth
     _say("case: q6_k full-range scales", m)
     n, k = 384, 4096
@@ -612,6 +613,35 @@ def test_prefill_tile_full(gpu_ctx, oracle, qtype):
     assert rel_err(got[rows], oracle.matmul_q(qtype, x[rows].astype(np.float32), raw, n)) <= TOL
 
 
+@pytest.mark.parametrize("case", ["q6_k_full_range_scales", "q6_k", "q8_0"])
+def test_prefill_exact_weights(gpu_ctx, oracle, case):
+    # the prefill GEMM at 2048 f16 x rows multiplies exact weights: Q8_0's d * q as two f16
+    # operands (hi + lo), Q6_K's sc * (q - 32) in units of d as one operand while every
+    # |sc| <= 64 (the synthetic scales) and as hi + lo once the upload has seen a scale
+    # beyond +-64 (here every scale drawn from all of i8, as quantizers produce them).
+    # x is f16, so the only difference from the oracle's exact dequant + BLAS is the order
+    # of the f32 sums: every output is held to 1e-4
+    from arf_amd import QType, synth
+    qtype = case[:4]
+    _say("case: prefill exact weights", case)
+    m, n, k = 2048, 640, 5120
+    raw = synth.weight(qtype, n, k, seed=0xA7F00020 + len(case)).copy()
+    if case.endswith("full_range_scales"):
+        blk = raw.reshape(-1, 210)
+        rng = np.random.default_rng(0xA7F00021)
+        blk[:, 192:208] = rng.integers(-128, 128, size=(blk.shape[0], 16)).astype(np.int8).view(np.uint8)
+    x = synth.activations(m, k, seed=0xA7F00022).astype(np.float16)
+    w = gpu_ctx.upload(QType[qtype.upper()], raw, n, k)
+    y = gpu_ctx.empty((m, n), np.float32)
+    gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)
+    got = y.numpy()
+    w.free()
+    assert np.all(np.isfinite(got))
+    e = rel_err(got, _dequant_matmul(oracle, qtype, x.astype(np.float32), raw, n))
+    _say("rel err (all rows)", e)
+    assert e <= 1e-4
+
+
 # (bytes per block, offset of the f16 block scale d) of the direct-operand prefill formats,
 # and their elements per block
 _D_FIELD = {"q4_k": (144, 0), "q5_k": (176, 0), "q6_k": (210, 208), "q8_0": (34, 0), "iq4_xs": (136, 0)}
@@ -625,12 +655,11 @@ def test_prefill_direct_operand_block_units(gpu_ctx, oracle, qtype):
     # the generator's, every 5th one dead (d = 0): the accumulators change unit at every
     # block, and the per-block (Q4_K, IQ4_XS, Q8_0) and per-group (Q6_K) scales must belong
     # to the block being multiplied.  Every output against BLAS on the weights the
-    # operands hold, where only the f32 sums differ: the oracle's exact dequant for Q4_K
-    # and Q5_K;
-    # for the formats whose operands are rounded to f16, that dequant rounded the same way
-    # (Q8_0: d * q rounded; Q6_K, IQ4_XS: the dequant at d = 1, sc * (q - 32) and
-    # (ls - 32) * kv, rounded, times d).  (Against the exact dequant their error is the
-    # weights' rounding, 2^-11 each, which the uniform-d prefill test holds to 2e-3.)
+    # operands hold, where only the f32 sums differ: the oracle's exact dequant for Q4_K,
+    # Q5_K and Q8_0 (d * q as f16 hi + lo); for the formats whose operands are in units of
+    # d and rounded to f16 past 2048, that dequant rounded the same way (Q6_K, IQ4_XS: the
+    # dequant at d = 1, sc * (q - 32) and (ls - 32) * kv, rounded, times d; the synthetic
+    # Q6_K scales keep sc * (q - 32) within 2048, so its rounding is none).
     from arf_amd import QType, synth
     m, n, k = 1024, 8704, 1024
     _say("case: direct-operand block units", qtype)
@@ -644,10 +673,8 @@ def test_prefill_direct_operand_block_units(gpu_ctx, oracle, qtype):
     dh = d.astype(np.float16)
     blocks[:, off:off + 2] = dh.reshape(-1, 1).view(np.uint8)
     x = synth.activations(m, k, seed=0xB10E).astype(np.float16)
-    if qtype in ("q4_k", "q5_k"):
+    if qtype in ("q4_k", "q5_k", "q8_0"):
         wref = oracle.dequant(qtype, raw, n * k).reshape(n, k)
-    elif qtype == "q8_0":
-        wref = oracle.dequant(qtype, raw, n * k).reshape(n, k).astype(np.float16).astype(np.float32)
     else:
         one = raw.copy()
         one.reshape(-1, bb)[:, off:off + 2] = np.full((1, 1), 1.0, np.float16).view(np.uint8)
