@@ -197,6 +197,30 @@ struct SkQ6K {
     }
 };
 
+// Q6_K with every sub-block scale in [-64, 64] (the upload's flag; the
+// synthetic and most GGUF tensors): exact integer operands sc * (q - 32)
+// (|.| <= 64 * 32 = 2048, an f16 integer) in units of d, so the whole block
+// accumulates in one set of registers and is scaled by the lane's d at the
+// block end (KIND 1) instead of by d * sc after every MFMA: about 12 fewer
+// VALU per MFMA.  Same slab layout and step map as SkQ6K.
+struct SkQ6KI : SkQ6K {
+    static constexpr int KIND = 1;
+    __host__ __device__ SkQ6KI shifted(int64_t nb) const { return {SkQ6K::shifted(nb)}; }
+    __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
+        half8 q[4];
+        SkQ6K::frag(srow, k, p, h, q);  // q - 32, exact
+        const uint32_t scw[4] = {k.sc.x, k.sc.y, k.sc.z, k.sc.w};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int si = 8 * (p >> 1) + (p & 1) + 2 * t;  // the sub-block of MFMA t
+            const half2v sc = h2splat((float)(int8_t)(scw[si >> 2] >> (8 * (si & 3))));
+            const u32x4 v = __builtin_bit_cast(u32x4, q[t]);
+            f[t] = u4_to_h8(as_u(as_h2(v.x) * sc), as_u(as_h2(v.y) * sc), as_u(as_h2(v.z) * sc),
+                            as_u(as_h2(v.w) * sc));
+        }
+    }
+};
+
 // Q8_0: step p of 256-element block b = Q8_0 blocks 8b + 2p (h = 0) and
 // 8b + 2p + 1 (h = 1); MFMA kk = bytes 8kk .. 8kk + 7 of the lane's block.
 // Weights d * q rounded to f16 (the format's scale is per 32 weights).
