@@ -788,24 +788,25 @@ __global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32(
 
 // The FFN's down GEMV at one x row: x = act(g) * u, f32 arithmetic.
 template <int XR, int ACT>
-__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_glu(
+__global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32_glu(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ g, const float *__restrict__ u,
     float *__restrict__ y, int n, int nblk) {
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y, n, nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, true>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y,
+                                                              n, nblk);
 }
 
 // The FFN's gate and up GEMVs in one launch: blockIdx.y = 0 multiplies x by
 // the first weight into y0, 1 by the second into y1 (same shape), each
 // weight's rows split over gridDim.x workgroups; f32 arithmetic.
 template <int XR>
-__global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_f32_dual(
+__global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32_dual(
     const uint8_t *__restrict__ hdr0, const uint8_t *__restrict__ qs0, const uint8_t *__restrict__ hdr1,
     const uint8_t *__restrict__ qs1, uint32_t hdr_bytes, uint32_t qs_bytes, const float *__restrict__ x,
     float *__restrict__ y0, float *__restrict__ y1, int n, int nblk) {
     const bool second = blockIdx.y != 0;  // uniform over the workgroup
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0, qs_bytes,
-                                       XsF32{x}, second ? y1 : y0, n, nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, true>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0,
+                                                              qs_bytes, XsF32{x}, second ? y1 : y0, n, nblk);
 }
 
 // MoE decode: blockIdx.y = pair p, one x row each, the weight of expert ids[p]
@@ -1884,29 +1885,16 @@ static hipError_t launch_gemv_q4k(const arfq_weight *w, int e, int m, const floa
 
 // ---- the f32-x Q4_K GEMV (one x row) ----
 // LDS: the scaled x (4 B per element), a (sum, factor) pair per sub-block and
-// the column sums of the workgroup's `rows` rows.  Two workgroups per CU share
-// its 160 KB while each needs at most 80 KB; longer x (k above ~19K) runs one
-// workgroup per CU.  (The static LDS of the kernel -- the chunk counter -- sits
-// beside the dynamic part, so the dynamic part stays 1 KB short of 160 KB.)
+// the column sums of the workgroup's `rows` rows.  The single GEMV, the FFN's
+// gate|up pair and its down GEMV run one 1024-thread workgroup per CU (up to
+// 159 KB each); the MoE decode pairs kernels run 512-thread workgroups, two per
+// CU where the LDS allows.  (The static LDS of the kernel -- the chunk counter --
+// sits beside the dynamic part, so the dynamic part stays 1 KB short of 160 KB.)
 constexpr size_t Q4K_F32_LDS_MAX = 159 * 1024;
 static size_t q4k_f32_lds_rows(const arfq_weight *w, int64_t rows) {
     const int64_t nblk = w->k / 256, spr = (nblk + 3) / 4;
     return (size_t)w->k * 4 + (size_t)(w->k / 32) * 8 + (size_t)((spr + 3) & ~3) * 4 +
            (size_t)rows * spr * 4;
-}
-static int64_t q4k_f32_grid(const arfq_weight *w) {
-    const int64_t g2 = q4k_gemv_grid(w);
-    if (q4k_f32_lds_rows(w, (w->n + g2 - 1) / g2) <= Q4K_F32_LDS_MAX / 2) return g2;
-    const int cus = w->ctx->cus > 0 ? w->ctx->cus : 256;
-    return std::max<int64_t>(1, std::min<int64_t>(g2, cus));
-}
-static size_t q4k_f32_lds(const arfq_weight *w) {
-    const int64_t grid = q4k_f32_grid(w);
-    return q4k_f32_lds_rows(w, (w->n + grid - 1) / grid);
-}
-static bool q4k_f32_ok(const arfq_weight *w) {
-    return w->qtype == ARFQ_Q4_K && q4k_f32_lds(w) <= Q4K_F32_LDS_MAX &&
-           w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
 }
 // rounds of x loads issued ahead of the weight ring (8 elements per thread and round)
 static int q4k_f32_xr(const arfq_weight *w, int threads = Q4K_GEMV_THREADS) {
@@ -1960,7 +1948,7 @@ static hipError_t launch_q4k_f32_glu_t(const arfq_weight *w, const float *g, con
     if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_f32_glu<XR, ACT>, Q4K_F32_LDS_MAX, lds_set))
         return err;
     const int64_t nb = w->n * (w->k / 256);
-    gemv_q4k_f32_glu<XR, ACT><<<(unsigned)q4k_f32_grid(w), Q4K_GEMV_THREADS, q4k_f32_lds(w), s>>>(
+    gemv_q4k_f32_glu<XR, ACT><<<(unsigned)q4k_f32s_grid(w), Q4K_F32_THREADS, q4k_f32s_lds(w), s>>>(
         (const uint8_t *)w->s0, (uint32_t)(nb * 16), (const uint8_t *)w->s1, (uint32_t)(nb * 128), g, u, y,
         (int)w->n, (int)(w->k / 256));
     return hipGetLastError();
@@ -1968,7 +1956,7 @@ static hipError_t launch_q4k_f32_glu_t(const arfq_weight *w, const float *g, con
 template <int ACT>
 static hipError_t launch_q4k_f32_glu(const arfq_weight *w, const float *g, const float *u, float *y,
                                      hipStream_t s) {
-    switch (q4k_f32_xr(w)) {
+    switch (q4k_f32_xr(w, Q4K_F32_THREADS)) {
     case 1: return launch_q4k_f32_glu_t<1, ACT>(w, g, u, y, s);
     case 2: return launch_q4k_f32_glu_t<2, ACT>(w, g, u, y, s);
     default: return launch_q4k_f32_glu_t<4, ACT>(w, g, u, y, s);
@@ -1976,10 +1964,10 @@ static hipError_t launch_q4k_f32_glu(const arfq_weight *w, const float *g, const
 }
 
 // gate and up in one launch: half the single GEMV's workgroups per weight
-static int64_t q4k_dual_grid(const arfq_weight *w) { return std::max<int64_t>(1, q4k_f32_grid(w) / 2); }
+static int64_t q4k_dual_grid(const arfq_weight *w) { return std::max<int64_t>(1, q4k_f32s_grid(w) / 2); }
 bool gemv_dual_supports(const arfq_weight *a, const arfq_weight *b, int64_t m) {
     return m == 1 && a->qtype == ARFQ_Q4_K && b->qtype == ARFQ_Q4_K && a->n == b->n && a->k == b->k &&
-           a->experts == 1 && b->experts == 1 && q4k_f32_ok(a) &&
+           a->experts == 1 && b->experts == 1 && q4k_f32s_ok(a) &&
            q4k_f32_lds_rows(a, (a->n + q4k_dual_grid(a) - 1) / q4k_dual_grid(a)) <= Q4K_F32_LDS_MAX;
 }
 template <int XR>
@@ -1989,7 +1977,7 @@ static hipError_t launch_dual_t(const arfq_weight *a, const arfq_weight *b, cons
     if (hipError_t err = set_max_lds_once((const void *)gemv_q4k_f32_dual<XR>, Q4K_F32_LDS_MAX, lds_set))
         return err;
     const int64_t g = q4k_dual_grid(a), nb = a->n * (a->k / 256);
-    gemv_q4k_f32_dual<XR><<<dim3((unsigned)g, 2), Q4K_GEMV_THREADS, q4k_f32_lds_rows(a, (a->n + g - 1) / g), s>>>(
+    gemv_q4k_f32_dual<XR><<<dim3((unsigned)g, 2), Q4K_F32_THREADS, q4k_f32_lds_rows(a, (a->n + g - 1) / g), s>>>(
         (const uint8_t *)a->s0, (const uint8_t *)a->s1, (const uint8_t *)b->s0, (const uint8_t *)b->s1,
         (uint32_t)(nb * 16), (uint32_t)(nb * 128), x, ya, yb, (int)a->n, (int)(a->k / 256));
     return hipGetLastError();
@@ -1997,7 +1985,7 @@ static hipError_t launch_dual_t(const arfq_weight *a, const arfq_weight *b, cons
 hipError_t launch_gemv_dual(const arfq_weight *a, const arfq_weight *b, const float *x, float *ya, float *yb,
                             hipStream_t s) {
     if (!gemv_dual_supports(a, b, 1)) return hipErrorInvalidValue;
-    switch (q4k_f32_xr(a)) {
+    switch (q4k_f32_xr(a, Q4K_F32_THREADS)) {
     case 1: return launch_dual_t<1>(a, b, x, ya, yb, s);
     case 2: return launch_dual_t<2>(a, b, x, ya, yb, s);
     default: return launch_dual_t<4>(a, b, x, ya, yb, s);
@@ -2071,14 +2059,14 @@ static hipError_t launch_gemv_glu_t(const arfq_weight *w, int64_t m, const float
         if (m == 2) return launch_glu_mx<2, ACT>(w, 2, g, u, y, s);
         return launch_glu_mx<4, ACT>(w, (int)m, g, u, y, s);
     }
-    return launch_q4k_f32_glu<ACT>(w, g, u, y, s);  // m == 1, q4k_f32_ok
+    return launch_q4k_f32_glu<ACT>(w, g, u, y, s);  // m == 1, q4k_f32s_ok
 }
 // what launch_gemv_glu_t takes: the 16-bit kernel under x16 where it fits,
-// otherwise the 512-thread f32 kernel at m = 1
+// otherwise the f32 kernel at m = 1
 bool gemv_glu_supports(const arfq_weight *w, int64_t m, bool x16) {
     if (w->qtype != ARFQ_Q4_K || w->experts != 1) return false;
     if (x16 && q4k_x16_ok(w, m)) return true;
-    return m == 1 && q4k_f32_ok(w);
+    return m == 1 && q4k_f32s_ok(w);
 }
 hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y, int act,
                            hipStream_t s, bool x16) {

@@ -473,6 +473,9 @@ def only_config(ctx, args):
         ms, _ = time_matmul(ctx, "q4_k", 2048, 17408, 5120, args.steps, args.warmup, 2, 0xA7F00004,
                             x_dtype=np.float16)
         res = {"us_per_launch": ms * 1e3, "TFLOP/s": 2.0 * 2048 * 17408 * 5120 / ms / 1e9}
+    elif c == "ffn":  # the dense Q4_K FFN of one decode step at C2's shape
+        ms = time_ffn(ctx, ("q4_k", "q4_k", "q4_k"), 5120, 17408, 1, args.steps, args.warmup, 2)
+        res = {"us_per_launch": ms * 1e3}
     elif c == "moe1":  # small-T MoE decode: one token through C5's experts
         ms = time_moe(ctx, args.steps, args.warmup, 3, tokens=1)
         res = {"us_per_launch": ms * 1e3}
@@ -497,7 +500,7 @@ def main():
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
     ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c3m64x16", "c4",
-                                       "c5", "q5km1", "c1n8", "lmhead", "moe1"],
+                                       "c5", "q5km1", "c1n8", "lmhead", "moe1", "ffn"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
