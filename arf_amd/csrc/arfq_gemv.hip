@@ -824,7 +824,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
     const int e = ids[p];
     if (e < 0 || e >= E) return;  // uniform over the workgroup
     xsrc.pair(p);
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, true>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
                                        qs + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
                                        y + (int64_t)p * n, n, nblk);
 }
@@ -843,7 +843,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs_dual(
     if (e < 0 || e >= E) return;  // uniform over the workgroup
     const bool second = blockIdx.z != 0;
     xsrc.pair(p);
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, false>((second ? hdr1 : hdr0) + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, true>((second ? hdr1 : hdr0) + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
                                        (second ? qs1 : qs0) + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
                                        (second ? y1 : y0) + (int64_t)p * n, n, nblk);
 }

@@ -476,8 +476,8 @@ def only_config(ctx, args):
     elif c == "ffn":  # the dense Q4_K FFN of one decode step at C2's shape
         ms = time_ffn(ctx, ("q4_k", "q4_k", "q4_k"), 5120, 17408, 1, args.steps, args.warmup, 2)
         res = {"us_per_launch": ms * 1e3}
-    elif c == "moe1":  # small-T MoE decode: one token through C5's experts
-        ms = time_moe(ctx, args.steps, args.warmup, 3, tokens=1)
+    elif c in ("moe1", "moe4", "moe16"):  # small-T MoE decode: 1, 4 or 16 tokens through C5's experts
+        ms = time_moe(ctx, args.steps, args.warmup, 3, tokens=int(c[3:]))
         res = {"us_per_launch": ms * 1e3}
     else:  # c5
         ms = time_moe(ctx, args.steps, args.warmup, 3)
@@ -500,7 +500,7 @@ def main():
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
     ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c3m64x16", "c4",
-                                       "c5", "q5km1", "c1n8", "lmhead", "moe1", "ffn"],
+                                       "c5", "q5km1", "c1n8", "lmhead", "moe1", "moe4", "moe16", "ffn"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
