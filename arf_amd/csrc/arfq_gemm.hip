@@ -336,13 +336,16 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     // format but IQ4_XS at f32 x (its weights are rounded to f16, so its x
     // keeps the hi + lo split of the tile loop below)
     const int64_t bdb = bd_stream_bytes(w->qtype);
+    // (an f32 x enters it as hi + lo rows unless x16: twice the x bytes)
+    const int64_t bdx = x_dtype == ARFQ_F32 && !x16 ? 2 : 1;
     p.bd = !p.skinny && m > 64 && bdb && w->k % 256 == 0 && !(w->qtype == ARFQ_IQ4_XS && x_dtype == ARFQ_F32) &&
-           w->n * (w->k / 256) * bdb < ((int64_t)1 << 31) && m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
+           w->n * (w->k / 256) * bdb < ((int64_t)1 << 31) && bdx * m * w->k * 2 < ((int64_t)1 << 31);  // buffer loads
     // f32 x: scaled per row by a power of two into f16 range, then split into
-    // f16 parts for the skinny kernel, rounded to f16 for the direct-operand
-    // prefill, or split into f16 hi + lo for the tile loop (IQ4_XS prefill,
-    // whose weights are rounded to f16: this way only one of the two operands
-    // is); the output rows are multiplied back by the scale
+    // f16 parts for the skinny kernel and the direct-operand prefill (hi + lo
+    // rows: its tiles cover 64 rows at twice the MFMAs; one f16 part under x16),
+    // or into f16 hi + lo for the tile loop (IQ4_XS prefill, whose weights are
+    // rounded to f16: this way only one of the two operands is); the output
+    // rows are multiplied back by the scale
     p.xsplit = !p.skinny && !p.bd && x_dtype == ARFQ_F32;
     p.convert = x_dtype == ARFQ_F32;
     // skinny kernel, f32 x: m <= 8 as three f16 parts (one 32-row x tile holds
@@ -351,7 +354,7 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     // half of the 32-row tile at m <= 16 (no extra MFMAs), a second tile at
     // m <= 32 and two more at m <= 64 (twice the MFMAs).  With x16
     // (ARFQ_OPT_GEMV_X16): one part, x rounded to f16.
-    p.parts = p.skinny && x_dtype == ARFQ_F32 && !x16 ? (m <= 8 ? 3 : 2) : 1;
+    p.parts = p.skinny && x_dtype == ARFQ_F32 && !x16 ? (m <= 8 ? 3 : 2) : p.bd && bdx == 2 ? 2 : 1;
     // the exact Q4_K paths read x sub-block sums (min term)
     p.sums = (p.skinny || p.bd) && kind2;
     int64_t S;
@@ -361,7 +364,8 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
         // the tiles past the last whole round of workgroups (one per CU) are
         // split into K ranges that fill that round; with XCD order the whole
         // tiles stay a multiple of the M tiles
-        const int64_t mt = (m + BD_BM - 1) / BD_BM, nt = (w->n + BD_BN - 1) / BD_BN;
+        const int64_t rm = p.parts == 2 ? BD_BM / 2 : BD_BM;  // output rows per tile
+        const int64_t mt = (m + rm - 1) / rm, nt = (w->n + BD_BN - 1) / BD_BN;
         const int64_t tiles = mt * nt, nb = w->k / 256;
         int64_t r = tiles % cus;
         if (mt % 8 == 0 && r % mt) r = std::min(tiles, (r / mt + 1) * mt);
@@ -510,24 +514,33 @@ FmtQ80 fmt_q80(const arfq_weight *w) {
 }
 
 // Prefill: weights straight into the MFMA operands (arfq_gemm_bd.h)
-template <class F>
-static hipError_t launch_bd_t(const F &f, const arfq_weight *w, int64_t m, const _Float16 *x,
-                              const uint16_t *xs, const float *rs, float *y, float *part,
-                              const GemmPlan &p, hipStream_t s) {
-    const int mt = (int)((m + BD_BM - 1) / BD_BM), nt = (int)((w->n + BD_BN - 1) / BD_BN);
+template <class F, bool PX>
+static hipError_t launch_bd_px(const F &f, const arfq_weight *w, int64_t m, const _Float16 *x,
+                               const uint16_t *xs, const float *rs, float *y, float *part,
+                               const GemmPlan &p, hipStream_t s) {
+    constexpr int RM = PX ? BD_BM / 2 : BD_BM;
+    const int mt = (int)((m + RM - 1) / RM), nt = (int)((w->n + BD_BN - 1) / BD_BN);
     const int tiles = mt * nt, nsplit = tiles - p.bd_full;
     const int xcd = (mt % 8 == 0 && p.bd_full % mt == 0) ? 1 : 0;
     if (nsplit && !part) return hipErrorInvalidValue;
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
-    if (hipError_t err = set_max_lds_once((const void *)gemm_bd<F>, bd_lds<F>(), lds_set)) return err;
+    if (hipError_t err = set_max_lds_once((const void *)gemm_bd<F, PX>, bd_lds<F>(), lds_set)) return err;
     const unsigned items = (unsigned)(p.bd_full + nsplit * p.bd_chunks);
-    gemm_bd<F><<<items, BD_THREADS, bd_lds<F>(), s>>>(f, x, xs, rs, y, part, (int)m, (int)w->n, (int)w->k, mt, xcd,
-                                                   p.bd_full, p.bd_chunks);
+    gemm_bd<F, PX><<<items, BD_THREADS, bd_lds<F>(), s>>>(f, x, xs, rs, y, part, (int)m, (int)w->n, (int)w->k, mt,
+                                                       xcd, p.bd_full, p.bd_chunks);
     hipError_t err = hipGetLastError();
     if (err != hipSuccess || !nsplit) return err;
-    bd_reduce_kernel<<<dim3(BD_BM * BD_BN / 1024, (unsigned)nsplit), 256, 0, s>>>(
-        part, rs, y, (int)m, (int)w->n, mt, p.bd_full, p.bd_chunks);
+    bd_reduce_kernel<<<dim3(RM * BD_BN / 1024, (unsigned)nsplit), 256, 0, s>>>(
+        part, rs, y, (int)m, (int)w->n, mt, p.bd_full, p.bd_chunks, RM);
     return hipGetLastError();
+}
+// x as hi + lo rows (an f32 x, plan parts 2) or one f16 part
+template <class F>
+static hipError_t launch_bd_t(const F &f, const arfq_weight *w, int64_t m, const _Float16 *x,
+                              const uint16_t *xs, const float *rs, float *y, float *part,
+                              const GemmPlan &p, hipStream_t s) {
+    return p.parts == 2 ? launch_bd_px<F, true>(f, w, m, x, xs, rs, y, part, p, s)
+                        : launch_bd_px<F, false>(f, w, m, x, xs, rs, y, part, p, s);
 }
 
 static hipError_t launch_bd(const arfq_weight *w, int e, int64_t m, const _Float16 *x, const uint16_t *xs,

@@ -556,11 +556,19 @@ using BdQ6KW = BdQ6KT<true>;   // some |sc| > 64: hi + lo operands
 // whole blocks, one item per range, whose partial tiles go to part[item -
 // full][BD_BM][BD_BN] and are added in chunk order by bd_reduce_kernel.  This
 // fills the last round of workgroups when the tiles do not divide the CUs.
-template <class F>
+// PX (an f32 x as f16 hi + lo): x holds the m hi rows, then the m lo rows
+// (and xs their sub-block sums in the same order).  A tile then covers 64
+// rows: its staged rows 0..63 are the hi rows, 64..127 the same rows' lo
+// parts, and the MFMAs of x row groups 2 and 3 accumulate onto groups 0 and 1
+// (x = hi + lo, ~22 bits), at twice the MFMAs per output.
+template <class F, bool PX = false>
 __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
     F fmt, const _Float16 *__restrict__ x, const uint16_t *__restrict__ xs, const float *__restrict__ rs,
     float *__restrict__ y, float *__restrict__ part, int m, int n, int k, int mt, int xcd_order, int full,
     int chunks) {
+    constexpr int RM = PX ? BD_BM / 2 : BD_BM;  // output rows per tile
+    constexpr int MG = RM / 32;                 // accumulator row groups
+    auto ai = [](int mg) { return PX ? mg & 1 : mg; };  // the accumulators x row group mg adds to
     extern __shared__ __attribute__((aligned(16))) _Float16 sx[];  // [2][BD_BM][BD_LD]
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int nblk = k / 256;
@@ -585,16 +593,16 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         kb1 = (int)((int64_t)(ch + 1) * nblk / chunks);
     }
     const int tm = tile % mt, tn = tile / mt;
-    const int m0 = tm * BD_BM, n0 = tn * BD_BN + wave * BD_WN;
+    const int m0 = tm * RM, n0 = tn * BD_BN + wave * BD_WN;
     const int st0 = 4 * kb0, st1 = 4 * kb1;  // this item's steps
 
     const int col = lane & 31, h = lane >> 5;
     const uint32_t wr0 = min(n0 + col, n - 1), wr1 = min(n0 + 32 + col, n - 1);
     const typename F::Lanes ld = fmt.lanes(n, nblk, wr0, wr1, h);
     const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)x, (short)0, (int)((uint32_t)m * k * 2), 0x00020000);
+        (void *)x, (short)0, (int)((uint32_t)(PX ? 2 : 1) * m * k * 2), 0x00020000);
     const __amdgpu_buffer_rsrc_t srs = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)xs, (short)0, (int)((uint32_t)m * (k / 16) * 2), 0x00020000);
+        (void *)xs, (short)0, (int)((uint32_t)(PX ? 2 : 1) * m * (k / 16) * 2), 0x00020000);
 
     // x tile staging: thread t copies row t / 4.  The next block's x moves in
     // XP parts of 256 / XP halves of the row (two or four; fewer registers
@@ -603,7 +611,9 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
     // per 64 halves.
     constexpr int XP = F::XPARTS, XS = 4 / XP;  // parts, steps per part
     const int xr = tid >> 2, xo = (tid & 3) * 16;
-    const uint32_t xv = (uint32_t)min(m0 + xr, m - 1) * k * 2 + xo * 2;  // bytes
+    // the x row staged as tile row xr (with PX, rows 64.. are lo rows M + r)
+    const uint32_t gxr = PX ? (xr < RM ? min(m0 + xr, m - 1) : m + min(m0 + xr - RM, m - 1)) : min(m0 + xr, m - 1);
+    const uint32_t xv = gxr * k * 2 + xo * 2;  // bytes
     u32x4 xa[2 * XS];
     auto xload = [&](int blk, int part) {
 #pragma unroll
@@ -615,7 +625,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
     };
     // x sub-block sums of the next block (min term): thread t moves 4 of row
     // t / 4's 16
-    const uint32_t sv = (uint32_t)min(m0 + xr, m - 1) * (k / 16) * 2 + (tid & 3) * 8;  // bytes
+    const uint32_t sv = gxr * (k / 16) * 2 + (tid & 3) * 8;  // bytes
     uint16_t *sxs = reinterpret_cast<uint16_t *>(sx + 2 * BD_BM * BD_LD);  // [2][BD_BM][16]
     // EXTRA block data: this wave's [2][4][64] dwords, at this lane
     uint32_t *exl = reinterpret_cast<uint32_t *>(sxs + 2 * BD_BM * 16) + (size_t)wave * 512 + lane;
@@ -679,9 +689,9 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         }
     };
 
-    floatx16 acc[4][2];
+    floatx16 acc[MG][2];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < MG; i++)
 #pragma unroll
         for (int g = 0; g < 2; g++)
 #pragma unroll
@@ -764,7 +774,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
         deq(0, 0);
         if constexpr (F::UNITS) {
 #pragma unroll
-            for (int mg = 0; mg < 4; mg++)
+            for (int mg = 0; mg < MG; mg++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) acc[mg][1][e] *= ratio[1];
         }
@@ -793,13 +803,14 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
             }
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
-                acc[mg][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[0], acc[mg][0], 0, 0, 0);
-                if constexpr (F::WLO) acc[mg][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], bw[0], acc[mg][0], 0, 0, 0);
+                acc[ai(mg)][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[0], acc[ai(mg)][0], 0, 0, 0);
+                if constexpr (F::WLO)
+                    acc[ai(mg)][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], bw[0], acc[ai(mg)][0], 0, 0, 0);
                 if (mgroup) {
 #pragma unroll
                     for (int g = 0; g < 2; g++) {
-                        acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bh[g], acc[mg][g], 0, 0, 0);
-                        acc[mg][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bl[g], acc[mg][g], 0, 0, 0);
+                        acc[ai(mg)][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bh[g], acc[ai(mg)][g], 0, 0, 0);
+                        acc[ai(mg)][g] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[mg], bl[g], acc[ai(mg)][g], 0, 0, 0);
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
@@ -822,14 +833,15 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
                 // block keeps its unit)
                 const float r0 = blk + 1 < kb1 ? ratio[0] : 1.f;
 #pragma unroll
-                for (int mg = 0; mg < 4; mg++)
+                for (int mg = 0; mg < MG; mg++)
 #pragma unroll
                     for (int e = 0; e < 16; e++) acc[mg][0][e] *= r0;
             }
 #pragma unroll
             for (int mg = 0; mg < 4; mg++) {
-                acc[mg][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[1], acc[mg][1], 0, 0, 0);
-                if constexpr (F::WLO) acc[mg][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], bw[1], acc[mg][1], 0, 0, 0);
+                acc[ai(mg)][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], b[1], acc[ai(mg)][1], 0, 0, 0);
+                if constexpr (F::WLO)
+                    acc[ai(mg)][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[mg], bw[1], acc[ai(mg)][1], 0, 0, 0);
                 if (more) xread(i + 1, mg);
             }
             if (more) deq(i + 1, 0);  // the next group's first B operand, under these MFMAs
@@ -853,7 +865,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
 #pragma unroll
         for (int g = 0; g < 2; g++)
 #pragma unroll
-            for (int mg = 0; mg < 4; mg++)
+            for (int mg = 0; mg < MG; mg++)
 #pragma unroll
                 for (int e = 0; e < 16; e++) acc[mg][g][e] *= sprev[g];
     }
@@ -861,7 +873,7 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
     // C layout of a 32x32 tile: lane l, value i -> row 8 (i/4) + 4 (l/32) + i%4, column l % 32
     float *pt = split ? part + (size_t)(item - full) * BD_BM * BD_BN : nullptr;
 #pragma unroll
-    for (int mg = 0; mg < 4; mg++) {
+    for (int mg = 0; mg < MG; mg++) {
 #pragma unroll
         for (int g = 0; g < 2; g++) {
             const int cl = wave * BD_WN + 32 * g + col;  // column within the tile
@@ -881,18 +893,18 @@ __global__ __launch_bounds__(BD_THREADS, 1) void gemm_bd(
 
 // y of the split tiles: the chunks' partial tiles added in chunk order.
 // A thread per 4 consecutive outputs of a tile row (16-byte partial loads,
-// up to 8 chunks' loads in flight at once); grid (BD_BM * BD_BN / 1024, split
-// tiles).
+// up to 8 chunks' loads in flight at once); grid (rm * BD_BN / 1024, split
+// tiles), rm the output rows per tile (BD_BM, or half with an x of two parts).
 __global__ __launch_bounds__(256) void bd_reduce_kernel(const float *__restrict__ part,
                                                         const float *__restrict__ rs,
                                                         float *__restrict__ y, int m, int n,
-                                                        int mt, int full, int chunks) {
+                                                        int mt, int full, int chunks, int rm) {
     const int lt = blockIdx.y;
     const int e = (blockIdx.x * 256 + threadIdx.x) * 4;
     const int rl = e / BD_BN, cl = e - rl * BD_BN;
     const int tile = full + lt;
-    const int r = (tile % mt) * BD_BM + rl, c = (tile / mt) * BD_BN + cl;
-    if (r >= m || c >= n) return;
+    const int r = (tile % mt) * rm + rl, c = (tile / mt) * BD_BN + cl;  // rm rows per tile
+    if (rl >= rm || r >= m || c >= n) return;
     const float4 *pp = reinterpret_cast<const float4 *>(part + (size_t)lt * chunks * BD_BM * BD_BN + e);
     constexpr size_t CS = (size_t)BD_BM * BD_BN / 4;  // one chunk's tile, in float4
     float4 v = make_float4(0.f, 0.f, 0.f, 0.f);

@@ -131,16 +131,16 @@ struct GemmPlan {
     bool sums = false;     // the format needs x sub-block sums (Q4_K)
     bool skinny = false;   // m <= 64: the weight-streaming kernel (arfq_skinny.h)
     bool bd = false;       // Q4_K prefill: weights straight into MFMA operands (arfq_gemm_bd.h)
-    // skinny, f32 x: the f16 parts x enters as (1: x rounded to f16 (f16 x);
-    // 2: hi + lo, ~22 bits, m = 9..64; 3: hi + mid + lo, m <= 8, which represents
-    // every f32 x within 2^15 of its row's max exactly), stored as row blocks
-    // [parts][m][k]
+    // skinny and bd, f32 x: the f16 parts x enters as (1: x rounded to f16 (f16
+    // x, or ARFQ_OPT_GEMV_X16); 2: hi + lo, ~22 bits, skinny m = 9..64 and the bd
+    // prefill; 3: hi + mid + lo, skinny m <= 8, which represents every f32 x
+    // within 2^15 of its row's max exactly), stored as row blocks [parts][m][k]
     int parts = 1;
     int bd_full = 0;       // bd: whole tiles; the rest are split into bd_chunks K ranges
     int bd_chunks = 1;
     size_t off_xh = 0, off_xl = 0, off_xs = 0, off_rs = 0, off_part = 0, scratch_bytes = 0;
 };
-// x16: ARFQ_OPT_GEMV_X16 is set (the skinny kernel takes an f32 x as one f16 part)
+// x16: ARFQ_OPT_GEMV_X16 is set (the skinny and prefill kernels take an f32 x as one f16 part)
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16 = false);
 bool gemm_supports(const arfq_weight *w, int64_t m);
 // y[m, n] = x[m, k] . W_e^T; `scratch` holds plan.scratch_bytes; `tickets`

@@ -90,8 +90,8 @@ int arfq_ctx_sync(arfq_ctx *ctx);
  *   of f32 x to 16-bit fixed point (relative to the block's max |x|) and take
  *   exact integer dots; faster, max relative error ~1e-4 of the output's rms.
  *   Only where those kernels' LDS fits 64 KiB: longer x keeps the default
- *   path.  The skinny MFMA kernel (below) then takes an f32 x as one f16 part
- *   (11 bits) instead of two or three.
+ *   path.  The skinny MFMA kernel and the prefill GEMM (below) then take an
+ *   f32 x as one f16 part (11 bits) instead of two or three.
  *   By default every GEMV multiplies f32 x by the exact weights in f32,
  *   as the reference GEMVs do
  *   (crates/arf-gpu/src/shaders/metal/matmul_vec_q4ks_msl.metal:46-165,
@@ -136,9 +136,14 @@ int arfq_weight_info(const arfq_weight *w, int *qtype, int64_t *n_rows, int64_t 
  *     in [2^14, 2^15), so every x within 2^15 of that max is represented
  *     exactly; exact codes, f32 sums, the output scaled back.
  *   - m = 9..64: the same with two parts (hi + lo, ~22 bits).
- *   - Above 64 rows: one f16 part (the Q5_K / IQ4_XS tile loop keeps hi + lo).
- * f16 x enters as is.  The weights are exact up to 64 rows; above 64 rows
- * Q6_K, Q8_0, Q5_K and IQ4_XS use the dequant rounded once to f16.
+ *   - Above 64 rows: hi + lo of x scaled per row, in the prefill GEMM (twice
+ *     the MFMAs of an f16 x).
+ * f16 x enters as is.  The weights are exact at every m for Q4_K, Q5_K, Q6_K
+ * and Q8_0 (Q6_K scales beyond +-64 and Q8_0's d * q as two f16 operands
+ * above 64 rows), except in the tile loop that takes the shapes the direct
+ * prefill kernel does not (Q8_0 with k not a multiple of 256, streams past
+ * 2 GiB) and IQ4_XS above 64 rows at f32 x: there the dequant is rounded once
+ * to f16.
  * Replaces add_matmul_m / add_matmul
  * (crates/arf-gpu/src/gpu/dispatch.rs:169-202, Q4KS arms :517-630) and the
  * island's gemv_q4ks / gemv_q4ks_batch / matmul_mm_q4ks selection

@@ -268,13 +268,16 @@ def test_next_formats_gemv_c2_shape(gpu_ctx, oracle, qtype):
                                        (100, 130, 1024, False), (130, 64, 512, True)])
 def test_next_formats_skinny_and_prefill(gpu_ctx, oracle, qtype, m, n, k, x16):
     # Q5_K / IQ4_XS beyond the decode GEMV: the skinny MFMA kernel (m <= 64) and the
-    # rounded-weight prefill tile above 64 rows; f16 x is what the oracle sees
+    # prefill above 64 rows; f16 x (the x16 cases) is what the oracle sees.  Exact
+    # weights with x in f16 parts hold 2e-5: Q5_K everywhere at f32 x, IQ4_XS on the skinny
+    # kernel; the IQ4_XS prefill at f32 x runs the tile loop with weights rounded to f16
     _say("case: next-format skinny", qtype, m, n, k, "f16" if x16 else "f32")
     dt = np.float16 if x16 else np.float32
     got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=11 * m + n, x_dtype=dt)
     e = rel_err(got, oracle.matmul_q(qtype, x.astype(np.float32), raw, n))
     _say("rel err", e)
-    assert e <= TOL
+    exact = not x16 and (qtype == "q5_k" or m <= 64)
+    assert e <= (2e-5 if exact else TOL)
 
 
 @pytest.mark.parametrize("m", [1, 8, 64, 130])
@@ -282,9 +285,9 @@ def test_q6_k_full_range_scales(gpu_ctx, oracle, m):
     # quantizers put each block's largest sub-block scale near +-127, where sc * (q - 32)
     # passes 2048 and would round in f16; the skinny kernel (m = 5..64) multiplies the exact
     # codes q - 32 and scales each sub-block's product by d * sc in f32, the prefill GEMM
-    # (m = 130) holds sc * (q - 32) as f16 hi + lo (exact; its f32 x is rounded to f16,
-    # which sets the error here).  The synthetic blocks keep scales in [-32, 31], so this
-    # test draws them from all of i8; at m = 8 (x as three f16 parts) the skinny result is
+    # (m = 130) holds sc * (q - 32) as f16 hi + lo operands (exact) against x as f16
+    # hi + lo.  The synthetic blocks keep scales in [-32, 31], so this test draws them from
+    # all of i8; at m = 8 (three f16 parts of x), 64 and 130 (hi + lo) every output is
     # held to 2e-5
     from arf_amd import QType, synth
     _say("case: q6_k full-range scales", m)
@@ -299,7 +302,7 @@ def test_q6_k_full_range_scales(gpu_ctx, oracle, m):
     gpu_ctx.matmul(w, gpu_ctx.to_device(x), m, y)
     e = rel_err(y.numpy(), oracle.matmul_q("q6_k", x, raw, n))
     _say("rel err", e)
-    assert e <= (2e-5 if m == 8 else TOL)
+    assert e <= (2e-5 if m > 1 else TOL)
 
 
 @pytest.mark.parametrize("qtype", ["q4_k", "q6_k", "q8_0"])
@@ -333,12 +336,13 @@ def test_vocab_wide_lm_head_gemv(gpu_ctx, oracle, qtype):
 SMALL_M_TOL = 2e-5
 
 
-@pytest.mark.parametrize("qtype,n,k", [("q4_k", 200, 2048), ("q5_k", 200, 2048), ("iq4_xs", 200, 2048),
-                                       ("q6_k", 200, 2048), ("q8_0", 200, 2048), ("q4_k", 17408, 5120)])
-@pytest.mark.parametrize("m", [2, 3, 4, 5, 8, 33, 48, 64])
+_SMALL_M_CASES = [(m, q, 200, 2048) for m in (2, 3, 4, 5, 8, 33, 48, 64)
+                  for q in ("q4_k", "q5_k", "iq4_xs", "q6_k", "q8_0")] + \
+                 [(m, "q4_k", 17408, 5120) for m in (2, 4, 64)]  # C2's shape
+
+
+@pytest.mark.parametrize("m,qtype,n,k", _SMALL_M_CASES)
 def test_small_m_f32_x(gpu_ctx, oracle, qtype, n, k, m):
-    if n == 17408 and m not in (2, 4, 64):
-        pytest.skip("C2's shape at m = 2, 4 and 64 only")
     _say("case: small-m f32 x", qtype, n, k, m)
     got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=13 * m + n + k)
     e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
@@ -435,13 +439,14 @@ def test_gemm_q4k_f16_small(gpu_ctx, oracle, m, n, k):
                                        ("q8_0", 100, 2048)])
 def test_gemm_f32_x(gpu_ctx, oracle, qtype, n, k, m):
     # m > 4 goes through the MFMA kernels: f32 x scaled per row into f16 range, then
-    # split into f16 parts on the skinny kernel (m <= 64) and on the tiled kernel (Q8_0
-    # with k not a multiple of 256) at m <= 64, rounded to f16 otherwise
+    # split into f16 parts (three at m <= 8, hi + lo above) on the skinny kernel and the
+    # direct-operand prefill, whose weights are exact: 2e-5.  Q8_0 with k not a multiple
+    # of 256 runs the tile loop (x hi + lo, weights d * q rounded to f16): 2e-3
     _say("case: gemm f32 x", qtype, n, k, m)
     got, raw, x = _matmul(gpu_ctx, qtype, n, k, m, seed=91 + m + n)
     e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
     _say("rel err", e)
-    assert e <= TOL
+    assert e <= (2e-5 if k % 256 == 0 else TOL)
 
 
 @pytest.mark.parametrize("m", [5, 8, 32, 64, 130])
@@ -449,10 +454,10 @@ def test_gemm_f32_x(gpu_ctx, oracle, qtype, n, k, m):
 def test_mfma_paths_f32_x_beyond_f16_range(gpu_ctx, oracle, qtype, m):
     # m >= 5 runs the MFMA kernels on f16 operands: an f32 x is scaled per row by a power
     # of two into f16 range first (and the output rows back), so x blocks up to 1e6 -- far
-    # past f16's 65504 -- stay finite.  At m <= 64 x goes in as f16 hi + mid + lo (m <= 8) or
-    # hi + lo (~22 bits), so even sub-blocks spread over 9 decades stay close to the f32
-    # reference; above 64 rows x is rounded to f16 (11 bits), checked here on N(0,1) x
-    # with 1 block in 8 at 1e6.
+    # past f16's 65504 -- stay finite.  x goes in as f16 hi + mid + lo (m <= 8) or hi + lo
+    # (~22 bits), so even sub-blocks spread over 9 decades stay close to the f32 reference;
+    # above 64 rows (the prefill kernels) checked on N(0,1) x with 1 block in 8 at 1e6.
+    # IQ4_XS above 64 rows at f32 x runs the tile loop, whose weights are rounded to f16.
     _say("case: mfma f32 x range", qtype, m)
     from arf_amd import QType, synth
     n, k = 96, 2048
@@ -476,7 +481,7 @@ def test_mfma_paths_f32_x_beyond_f16_range(gpu_ctx, oracle, qtype, m):
     assert np.all(np.isfinite(got))
     e = rel_err(got, oracle.matmul_q(qtype, x, raw, n))
     _say("rel err", e)
-    assert e <= (1e-4 if m <= 64 else TOL)
+    assert e <= (1e-4 if m <= 64 or qtype != "iq4_xs" else TOL)
 
 
 @pytest.mark.parametrize("qtype,m,n,k", [("q6_k", 33, 64, 4096), ("q8_0", 129, 300, 640),
@@ -730,9 +735,9 @@ def test_x_dynamic_range_and_dead_blocks(gpu_ctx, oracle, qtype, m):
     scale = 10.0 ** rng.uniform(-6, 6, size=(m, k // 32)).astype(np.float32)
     scale[rng.random(size=scale.shape) < 0.1] = 0.0
     x = (x.reshape(m, k // 32, 32) * scale[..., None]).reshape(m, k).astype(np.float32)
-    # the oracle sees x as given (at m = 200 the prefill kernels round x to f16 after
-    # the row's power-of-two scale: blocks 1e12 below the row's largest fall out, and
-    # the gate measures what that costs against the reference's f32 x)
+    # the oracle sees x as given (at m = 200 the prefill kernel splits x into f16 hi + lo
+    # after the row's power-of-two scale: blocks far below the row's largest lose their
+    # low bits or fall out, and the gate measures what that costs against f32 x)
     got = _run(gpu_ctx, qtype, raw, x, n)
     want = oracle.matmul_q(qtype, x, raw, n)
     e = rel_err(got, want)
