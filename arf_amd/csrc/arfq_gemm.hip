@@ -87,6 +87,10 @@ __global__ __launch_bounds__(GM_THREADS, F::WG_PER_CU) void gemm_q(
 // threads and weight rows (column tile) of a skinny workgroup with TA x tiles
 __host__ __device__ constexpr int sk_nt(int ta) { return ta == 4 ? 512 : SK_THREADS; }
 __host__ __device__ constexpr int sk_ct(int ta) { return sk_nt(ta) / 2; }
+// x buffers of the dense skinny loop: two (one barrier per block instead of
+// two) where the second fits beside two workgroups per CU (one x tile: C3 m = 8
+// 31.7 -> 31.2 us), else one
+__host__ __device__ constexpr int SK_XB(int ta) { return ta == 1 ? 2 : 1; }
 
 // Skinny products (m <= 64): workgroup = sk_ct(TA) weight rows x all m rows
 // (a wave per 32 weight rows), over the 256-element blocks of split blockIdx.y
@@ -131,7 +135,7 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
     const int n = n0 + 32 * wave + (lane & 31);
     // the x rows' scales of this K range into LDS past the loop's own, before
     // the loop: the epilogue reads them there instead of loading per output
-    float *lrs = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + sk_lds<F, TA, 1, NT>());
+    float *lrs = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + sk_lds<F, TA, 1, NT, SK_XB(TA)>());
     if (rs && tid < 32 * TA) lrs[tid] = tid < M ? rs[(int64_t)sp * rss + tid] : 1.f;
     const F fm[1] = {fmt};
     const int64_t wrow0[1] = {n0 + 32 * wave};
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // PAIR with two or four tiles: the lo tiles' products go into the hi tiles' accumulators
-    skinny_run<F, TA, 1, NT, XT, false, GM, PAIR && TA >= 2, true>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
+    skinny_run<F, TA, 1, NT, XT, false, GM, PAIR && TA >= 2, true, SK_XB(TA)>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
                                                                     PARTS == 3 ? 16 + M : PAIR ? PO + M : M);
     if constexpr (PAIR && TA == 1) {
         // rows r and r + 16 of a lane's accumulator are elements i and i + 8
@@ -428,7 +432,7 @@ static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, con
                                                                                       part, tick, S, s);
     }
     constexpr int NT = sk_nt(TA), CT = NT / 2;
-    constexpr size_t lds = sk_lds<F, TA, 1, NT>() + 32 * TA * 4;  // + the x rows' scales
+    constexpr size_t lds = sk_lds<F, TA, 1, NT, SK_XB(TA)>() + 32 * TA * 4;  // + the x rows' scales
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PARTS, GM>, lds, lds_set))
         return err;
