@@ -1357,6 +1357,10 @@ __device__ __forceinline__ float codes16_fdot(const uint32_t cw[4], const float 
 
 }  // namespace
 
+// Rows: workgroup w of G owns rows w, w + G, w + 2G, ... (the whole chip reads a
+// narrow window of the weight stream at a time), and x is scaled into LDS
+// before the first weight load is issued (every weight request in flight
+// delays the x requests); as the Q4_K f32 GEMV (gemv_q4k_f32_body).
 template <class F, int XR>
 __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const float *__restrict__ x,
                                                                 float *__restrict__ y, int n, int nblk) {
@@ -1376,9 +1380,8 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
     const int bq = l16 >> 2, c = l16 & 3;
 
     const int G = gridDim.x;
-    const int r0 = (int)((int64_t)blockIdx.x * n / G);
-    const int r1 = (int)((int64_t)(blockIdx.x + 1) * n / G);
-    const int R = r1 - r0;
+    const int r0 = blockIdx.x;             // rows r0 + i * G, i < R
+    const int R = (n - r0 + G - 1) / G;
     const int spr = (nblk + 3) >> 2;
     const int cpc = (R + C - 1) / C;
     const int nchunks = cpc * spr;
@@ -1403,24 +1406,19 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
         }
         const int b = 4 * icol + bq;
         const bool live = icol < spr && irow < R && b < nblk;
-        const uint32_t blk = (uint32_t)(r0 + irow) * (uint32_t)nblk + (uint32_t)b;
+        const uint32_t blk = (uint32_t)(r0 + irow * G) * (uint32_t)nblk + (uint32_t)b;
         F::load(res, ld[u], blk, live, c);
         srow[u] = irow;
         scol[u] = icol;
     };
 
     if (tid == 0) next_chunk = Q6K_GEMV_GROUPS;
-    // x loads, then (after every wave has issued them) the first weights, then
-    // x is scaled into LDS; the barrier after it orders LDS only, so the
-    // weight loads stay in flight across it
+    // x loads, x scaled into LDS, the barrier (which orders LDS only), then the
+    // first weight loads
     const int xitems = k / 8;
     XqRound xr[XR];
 #pragma unroll
     for (int r = 0; r < XR; r++) xr[r] = xq_load(x, xitems, r * Q6K_GEMV_THREADS);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-#pragma unroll
-    for (int u = 0; u < PF; u++) issue(u, u < C);
     asm volatile("" ::: "memory");
 #pragma unroll
     for (int r = 0; r < XR; r++)
@@ -1428,6 +1426,8 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
     for (int base = XR * Q6K_GEMV_THREADS; base < xitems; base += Q6K_GEMV_THREADS)
         xf16_process(xq_load(x, xitems, base), xitems, base, reinterpret_cast<float4 *>(xfl), s16, xe);
     lds_barrier();
+#pragma unroll
+    for (int u = 0; u < PF; u++) issue(u, u < C);
 
     // scaled x of the column being consumed: the lane's 4 quadrants
     int xcol = -1;
@@ -1485,7 +1485,7 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
         const float *pr = part + (size_t)t * spr;
         float v = 0.f;
         for (int cc = 0; cc < spr; cc++) v += pr[cc];
-        y[r0 + t] = v;
+        y[r0 + t * G] = v;
     }
 }
 
