@@ -319,9 +319,10 @@ constexpr uint32_t Q4K_OOB = 0x80000000u;               // buffer offset past an
 // Work split: two 512-thread workgroups per CU (x is quantized once per
 // workgroup; two independent workgroups per CU measured faster than one of
 // 1024 threads); workgroup w owns rows [r0, r1) = [w*n/G, (w+1)*n/G).  (The
-// single m = 1 f32 GEMV, gemv_q4k_f32, differs: one 1024-thread workgroup per
-// CU owning rows w, w + G, ..., and its x scaled before the first weight load;
-// see gemv_q4k_f32_body.)  Each row is cut into
+// f32 GEMVs differ: rows w, w + G, ..., and x scaled before the first weight
+// load; see gemv_q4k_f32_body.  For this kernel, whose x quantization takes
+// longer, that order measured slower: C2 with the x16 option 11.6 -> 12.4 us.)
+// Each row is cut into
 // spr = ceil(nblk/4) "columns" of 4 blocks; a "step" is one (row, column)
 // pair.  The steps are handed out in chunks of CHUNK consecutive rows of one
 // column: group g starts with chunk g and then claims chunks from an LDS
@@ -609,12 +610,10 @@ __device__ __forceinline__ float q4k_fdot(const uint4 c, const float *X) {
 
 }  // namespace
 
-// NT threads per workgroup.  XFIRST: x is scaled into LDS before any weight
-// load is issued, and workgroup w owns rows w, w + G, w + 2G, ... (G
-// workgroups) instead of one contiguous range -- the layout of the single
-// m = 1 GEMV, one 1024-thread workgroup per CU.  Otherwise the first weight
-// loads go out ahead of the x scaling and the rows are a contiguous range.
-template <int XR, int PF, int NT, bool XFIRST, class XSRC>
+// NT threads per workgroup.  x is scaled into LDS before any weight load is
+// issued, and workgroup w owns rows w, w + G, w + 2G, ... (G workgroups): the
+// whole chip reads a narrow window of the weight stream at a time.
+template <int XR, int PF, int NT, class XSRC>
 __device__ __forceinline__ void gemv_q4k_f32_body(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const XSRC &xsrc, float *__restrict__ y, int n, int nblk) {
@@ -639,10 +638,9 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     const int bq = l16 >> 2, jj = l16 & 3;
 
     const int G = gridDim.x;
-    // rows of this workgroup: r0 + i * rs for i < R
-    const int r0 = XFIRST ? (int)blockIdx.x : (int)((int64_t)blockIdx.x * n / G);
-    const int rs = XFIRST ? G : 1;
-    const int R = XFIRST ? (n - r0 + G - 1) / G : (int)((int64_t)(blockIdx.x + 1) * n / G) - r0;
+    // rows of this workgroup: r0 + i * G for i < R
+    const int r0 = blockIdx.x;
+    const int R = (n - r0 + G - 1) / G;
     const int cpc = (R + C - 1) / C;  // chunks (of C rows) per column
 
     // Each 16-lane group has a home column (group % spr) and starts on chunk
@@ -677,7 +675,7 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
         }
         const int b = 4 * icol + bq;
         const bool live = icol < spr && irow < R && b < nblk;
-        const uint32_t blk = (uint32_t)(r0 + irow * rs) * (uint32_t)nblk + (uint32_t)b;
+        const uint32_t blk = (uint32_t)(r0 + irow * G) * (uint32_t)nblk + (uint32_t)b;
         const uint32_t oc = live ? blk * 128u + (uint32_t)jj * 16u : Q4K_OOB;
         const uint32_t oh = live ? blk * 16u + (uint32_t)jj * 4u : Q4K_OOB;
         clo[u] = __builtin_amdgcn_raw_buffer_load_b128(qrs, oc, 0, 2);
@@ -690,23 +688,15 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     // counters start past the chunks the groups begin on
     for (int c = tid; c < spr; c += NT)
         cnt[c] = (GROUPS - c + spr - 1) / spr;
-    // x loads; without XFIRST (after every wave has issued them) the first
-    // chunk of weights, then x is scaled into LDS; the barrier after it orders
-    // LDS only, so the weight loads stay in flight across it.  With XFIRST the
-    // weights go out after the barrier: a wave's loads issue in order and stall
-    // once the CU's memory queue is full, and every CU's weight requests delay
-    // the x requests, so x issued alone arrives 2-3 us earlier at C2's shape.
+    // x loads, x scaled into LDS, the barrier, then the weights: a wave's
+    // loads issue in order and stall once the CU's memory queue is full, and
+    // every CU's weight requests delay the x requests, so x issued alone
+    // arrives 2-3 us earlier at C2's shape than behind the first weights.
     const int xitems = nsub * 4;
     XqRound xr[XR];
 #pragma unroll
     for (int r = 0; r < XR; r++) xr[r] = xsrc.load(xitems, r * NT);
-    asm volatile("" ::: "memory");  // keep the x loads ahead of the weight loads
-    if (!XFIRST) {
-        __builtin_amdgcn_s_barrier();
-#pragma unroll
-        for (int u = 0; u < PF; u++) issue(u, true);
-        asm volatile("" ::: "memory");
-    }
+    asm volatile("" ::: "memory");  // keep the x loads ahead of everything after them
     // (every round is processed: items past the end load a clamped index and
     // store nothing, and an unconditional use keeps the loads where they are)
 #pragma unroll
@@ -714,10 +704,8 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     for (int base = XR * NT; base < xitems; base += NT)
         xf_process(xsrc.load(xitems, base), xitems, base, xf, xs);
     lds_barrier();  // scaled x and the counters are visible from here on
-    if (XFIRST) {
 #pragma unroll
-        for (int u = 0; u < PF; u++) issue(u, true);
-    }
+    for (int u = 0; u < PF; u++) issue(u, true);
 
     // scaled x of the column being consumed (sub-blocks jj, jj + 4)
     int xcol = -1;
@@ -774,7 +762,7 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
         const float *pr = part + (size_t)t * spr;
         float v = 0.f;
         for (int c = 0; c < spr; c++) v += pr[c];
-        y[r0 + t * rs] = v;
+        y[r0 + t * G] = v;
     }
 }
 
@@ -782,8 +770,8 @@ template <int XR>
 __global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk) {
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, true>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n,
-                                                              nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n,
+                                                        nblk);
 }
 
 // The FFN's down GEMV at one x row: x = act(g) * u, f32 arithmetic.
@@ -792,8 +780,8 @@ __global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32_glu(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ g, const float *__restrict__ u,
     float *__restrict__ y, int n, int nblk) {
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, true>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y,
-                                                              n, nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS>(hdr, hdr_bytes, qs, qs_bytes, XsGlu<ACT>{g, u, 0}, y,
+                                                        n, nblk);
 }
 
 // The FFN's gate and up GEMVs in one launch: blockIdx.y = 0 multiplies x by
@@ -805,8 +793,8 @@ __global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32_dual(
     const uint8_t *__restrict__ qs1, uint32_t hdr_bytes, uint32_t qs_bytes, const float *__restrict__ x,
     float *__restrict__ y0, float *__restrict__ y1, int n, int nblk) {
     const bool second = blockIdx.y != 0;  // uniform over the workgroup
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, true>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0,
-                                                              qs_bytes, XsF32{x}, second ? y1 : y0, n, nblk);
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0,
+                                                        qs_bytes, XsF32{x}, second ? y1 : y0, n, nblk);
 }
 
 // MoE decode: blockIdx.y = pair p, one x row each, the weight of expert ids[p]
@@ -824,7 +812,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs(
     const int e = ids[p];
     if (e < 0 || e >= E) return;  // uniform over the workgroup
     xsrc.pair(p);
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, true>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS>(hdr + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
                                        qs + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
                                        y + (int64_t)p * n, n, nblk);
 }
@@ -843,7 +831,7 @@ __global__ __launch_bounds__(Q4K_GEMV_THREADS) void gemv_q4k_pairs_dual(
     if (e < 0 || e >= E) return;  // uniform over the workgroup
     const bool second = blockIdx.z != 0;
     xsrc.pair(p);
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS, true>((second ? hdr1 : hdr0) + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_GEMV_THREADS>((second ? hdr1 : hdr0) + (int64_t)e * e_hdr_bytes, e_hdr_bytes,
                                        (second ? qs1 : qs0) + (int64_t)e * e_qs_bytes, e_qs_bytes, xsrc,
                                        (second ? y1 : y0) + (int64_t)p * n, n, nblk);
 }
