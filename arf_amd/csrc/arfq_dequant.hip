@@ -61,14 +61,17 @@ __global__ void repack_q6k(const uint8_t *__restrict__ raw, uint8_t *__restrict_
             o[32 + i] = qh[32 * n2 + l0 + i];
         }
     }
-    bool big = false;
+    int amax = 0;
     for (int i = 0; i < 16; i++) {
         sc[b * 16 + i] = src[192 + i];
         const int v = (int8_t)src[192 + i];
-        big |= v > 64 || v < -64;
+        amax = max(amax, v < 0 ? -v : v);
     }
     d[b] = (uint16_t)(src[208] | (src[209] << 8));
-    if (big && wide) *wide = 1u;  // the prefill GEMM then splits sc * (q - 32) into hi + lo
+    // the prefill GEMM splits sc * (q - 32) into hi + lo past 64, the skinny
+    // kernel scales each sub-block in f32 past 62
+    if (wide && amax > 64) wide[0] = 1u;
+    if (wide && amax > 62) wide[1] = 1u;
 }
 
 // Q5_K: the 16-byte header (d, dmin, scales) and ggml's qh[32] + qs[128] as they are.

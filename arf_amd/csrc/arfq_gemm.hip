@@ -600,8 +600,8 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         case ARFQ_Q4_K:
             return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
                              p.splits, s, p.parts);
-        case ARFQ_Q6_K:  // scales within +-64 (the upload's flag): integer operands sc * (q - 32)
-            if (!w->wide)
+        case ARFQ_Q6_K:  // scales within +-62 (the upload's flag): integer operands sc * (q - 32) / 2
+            if (!w->over62)
                 return launch_sk(SkQ6KI{sk_q6k(w)}.shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets,
                                  ntickets, p.splits, s, p.parts);
             return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,

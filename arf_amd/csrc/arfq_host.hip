@@ -230,21 +230,23 @@ static int weight_create(arfq_ctx *ctx, int qtype, size_t nbytes, int64_t n_rows
     return ARFQ_OK;
 }
 
-// Q6_K uploads: the repack flags a sub-block scale outside [-64, 64] in a word
-// of the context's counter allocation (cleared first); read back once the
-// repacks are done, it selects the prefill GEMM's two-operand weights.
+// Q6_K uploads: the repack flags a sub-block scale outside [-64, 64] and one
+// outside [-62, 62] in two words of the context's counter allocation (cleared
+// first); read back once the repacks are done, they select the prefill GEMM's
+// two-operand weights and the skinny kernel's operand form.
 static uint32_t *upload_flag(arfq_ctx *ctx, const arfq_weight *w) {
     return w->qtype == ARFQ_Q6_K && ctx->tickets ? ctx->tickets + ctx->ntickets + arfq::STREAM_SINK_WORDS : nullptr;
 }
 static hipError_t upload_flag_clear(arfq_ctx *ctx, uint32_t *flag) {
-    return flag ? hipMemsetAsync(flag, 0, sizeof(uint32_t), ctx->stream) : hipSuccess;
+    return flag ? hipMemsetAsync(flag, 0, 2 * sizeof(uint32_t), ctx->stream) : hipSuccess;
 }
 static hipError_t upload_flag_read(arfq_ctx *ctx, uint32_t *flag, arfq_weight *w) {
     if (!flag) return hipSuccess;
-    uint32_t h = 0;
-    hipError_t e = hipMemcpyAsync(&h, flag, sizeof(h), hipMemcpyDeviceToHost, ctx->stream);
+    uint32_t h[2] = {0, 0};
+    hipError_t e = hipMemcpyAsync(h, flag, sizeof(h), hipMemcpyDeviceToHost, ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-    w->wide = h != 0;
+    w->wide = h[0] != 0;
+    w->over62 = h[1] != 0;
     return e;
 }
 

@@ -45,6 +45,7 @@ struct arfq_weight {
     void *s2 = nullptr;  //                      Q6_K d
     size_t bytes = 0;    // ggml bytes of one expert (what one matmul streams)
     bool wide = false;   // Q6_K: some sub-block scale outside [-64, 64] (set by the upload)
+    bool over62 = false; // Q6_K: some sub-block scale outside [-62, 62] (set by the upload)
 };
 
 namespace arfq {
@@ -82,7 +83,7 @@ inline int block_bytes_of(int qtype) {
 // Split raw ggml blocks (device) into the layout streams of `w`: blocks
 // [b0, b0 + nb) of w (nb < 0: to the end), raw pointing at block b0's bytes.
 // Q6_K: a repack that meets a sub-block scale outside [-64, 64] stores 1 to
-// *wide (when not null).
+// wide[0], one outside [-62, 62] stores 1 to wide[1] (when wide is not null).
 hipError_t launch_repack(const arfq_weight *w, const uint8_t *raw, hipStream_t s, int64_t b0 = 0,
                          int64_t nb = -1, uint32_t *wide = nullptr);
 // Dequantize all blocks of `w` to f32.

@@ -158,35 +158,32 @@ struct SkQ6K {
         const uint32_t scw[4] = {k.sc.x, k.sc.y, k.sc.z, k.sc.w};
         return h2f(k.d) * (float)(int8_t)(scw[si >> 2] >> (8 * (si & 3)));
     }
-    // q - 32: q as the f16 1024 + q (v_perm inserts 0x64 above each code
-    // byte; the 2 qh bits go to bits 4-5), minus 1056, exact
+    // The codes q (0..63) of positions 4j .. 4j + 3 of quadrant t, one per byte:
+    // the ql nibble (ql_b for odd t, the high nibble for t >= 2) and qh bits
+    // 2t, 2t + 1 as bits 4, 5.  Bits a shift carries into a neighbouring byte
+    // land outside that byte's mask.
+    __device__ static uint32_t codes(const u32x2 &qa, const u32x2 &qb, const u32x2 &qh, int t, int j) {
+        const uint32_t l = (t & 1) ? qb[j] : qa[j];
+        const uint32_t lo = (t & 2) ? l >> 4 : l;
+        const uint32_t hi = t == 0 ? qh[j] << 4 : t == 1 ? qh[j] << 2 : t == 2 ? qh[j] : qh[j] >> 2;
+        return (lo & 0x0F0F0F0Fu) | (hi & 0x30303030u);
+    }
+    // q - 32: v_perm puts two code bytes under 0x64 (the f16 1024 + q), less
+    // 1056, exact
     __device__ static void frag(const uint8_t *srow, const Blk &, int p, int h, half8 f[4]) {
         const uint8_t *ch = srow + 48 * p;  // ql_a[16] | ql_b[16] | qh[16]
         const u32x2 qa = *reinterpret_cast<const u32x2 *>(ch + 8 * h);
         const u32x2 qb = *reinterpret_cast<const u32x2 *>(ch + 16 + 8 * h);
         const u32x2 qh = *reinterpret_cast<const u32x2 *>(ch + 32 + 8 * h);
         const half2v m1056 = h2splat(-1056.f);
-        // qh bytes of positions (4hh + 2pr, +1) spread into the two halves
-        uint32_t hp[2][2];
-#pragma unroll
-        for (int hh = 0; hh < 2; hh++)
-#pragma unroll
-            for (int pr = 0; pr < 2; pr++)
-                hp[hh][pr] = __builtin_amdgcn_perm(0u, hh ? qh.y : qh.x, pr ? 0x0c030c02u : 0x0c010c00u);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const u32x2 ql = (t & 1) ? qb : qa;
             uint32_t o[4];
 #pragma unroll
-            for (int hh = 0; hh < 2; hh++) {
-                const uint32_t l = (t & 2) ? ((hh ? ql.y : ql.x) >> 4) : (hh ? ql.y : ql.x);
-#pragma unroll
-                for (int pr = 0; pr < 2; pr++) {
-                    const uint32_t lp = __builtin_amdgcn_perm(0x64646464u, l, pr ? 0x04030402u : 0x04010400u);
-                    const uint32_t top = 2 * t <= 4 ? (hp[hh][pr] << (4 - 2 * t)) : (hp[hh][pr] >> (2 * t - 4));
-                    const uint32_t q = (lp & 0x640F640Fu) | (top & 0x00300030u);
-                    o[2 * hh + pr] = as_u(as_h2(q) + m1056);
-                }
+            for (int j = 0; j < 2; j++) {
+                const uint32_t q = codes(qa, qb, qh, t, j);
+                o[2 * j] = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04010400u)) + m1056);
+                o[2 * j + 1] = as_u(as_h2(__builtin_amdgcn_perm(0x64646464u, q, 0x04030402u)) + m1056);
             }
             f[t] = u4_to_h8(o[0], o[1], o[2], o[3]);
         }
@@ -197,26 +194,41 @@ struct SkQ6K {
     }
 };
 
-// Q6_K with every sub-block scale in [-64, 64] (the upload's flag; the
-// synthetic and most GGUF tensors): exact integer operands sc * (q - 32)
-// (|.| <= 64 * 32 = 2048, an f16 integer) in units of d, so the whole block
-// accumulates in one set of registers and is scaled by the lane's d at the
-// block end (KIND 1) instead of by d * sc after every MFMA: about 12 fewer
-// VALU per MFMA.  Same slab layout and step map as SkQ6K.
+// Q6_K with every sub-block scale in [-62, 62] (the upload's flag; the
+// synthetic and many GGUF tensors): exact integer operands sc * (q - 32) / 2
+// (|.| <= 992, a multiple of 1/2: exact in f16) in units of d, so the whole
+// block accumulates in one set of registers and is scaled by 2d at the block
+// end (KIND 1) instead of by d * sc after every MFMA.  One packed FMA per two
+// weights: (1024 + q) * (sc / 2) - 528 sc, whose constant is an f16 value while
+// |sc| <= 62 (33 * 63 needs 12 bits).  Same slab layout and step map as SkQ6K.
 struct SkQ6KI : SkQ6K {
     static constexpr int KIND = 1;
     __host__ __device__ SkQ6KI shifted(int64_t nb) const { return {SkQ6K::shifted(nb)}; }
+    __device__ static float2 scale(const Blk &k) { return make_float2(2.f * h2f(k.d), 0.f); }
     __device__ static void frag(const uint8_t *srow, const Blk &k, int p, int h, half8 f[4]) {
-        half8 q[4];
-        SkQ6K::frag(srow, k, p, h, q);  // q - 32, exact
-        const uint32_t scw[4] = {k.sc.x, k.sc.y, k.sc.z, k.sc.w};
+        const uint8_t *ch = srow + 48 * p;
+        const u32x2 qa = *reinterpret_cast<const u32x2 *>(ch + 8 * h);
+        const u32x2 qb = *reinterpret_cast<const u32x2 *>(ch + 16 + 8 * h);
+        const u32x2 qh = *reinterpret_cast<const u32x2 *>(ch + 32 + 8 * h);
+        // scale bytes as sc + 128 (unsigned)
+        const uint32_t scw[4] = {k.sc.x ^ 0x80808080u, k.sc.y ^ 0x80808080u, k.sc.z ^ 0x80808080u,
+                                 k.sc.w ^ 0x80808080u};
+        const half2v half = h2splat(0.5f), m576 = h2splat(-576.f), m1056 = h2splat(-1056.f);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int si = 8 * (p >> 1) + (p & 1) + 2 * t;  // the sub-block of MFMA t
-            const half2v sc = h2splat((float)(int8_t)(scw[si >> 2] >> (8 * (si & 3))));
-            const u32x4 v = __builtin_bit_cast(u32x4, q[t]);
-            f[t] = u4_to_h8(as_u(as_h2(v.x) * sc), as_u(as_h2(v.y) * sc), as_u(as_h2(v.z) * sc),
-                            as_u(as_h2(v.w) * sc));
+            // the f16 1152 + sc in both halves; * 1/2 - 576 = sc / 2, exact
+            const uint32_t sel = 0x04000400u | (uint32_t)(si & 3) * 0x00010001u;
+            const half2v s = as_h2(pk_fma(__builtin_amdgcn_perm(0x64646464u, scw[si >> 2], sel), half, m576));
+            const half2v c = s * m1056;  // -528 sc
+            uint32_t o[4];
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const uint32_t q = codes(qa, qb, qh, t, j);
+                o[2 * j] = pk_fma(__builtin_amdgcn_perm(0x64646464u, q, 0x04010400u), s, c);
+                o[2 * j + 1] = pk_fma(__builtin_amdgcn_perm(0x64646464u, q, 0x04030402u), s, c);
+            }
+            f[t] = u4_to_h8(o[0], o[1], o[2], o[3]);
         }
     }
 };

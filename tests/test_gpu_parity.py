@@ -280,22 +280,31 @@ def test_next_formats_skinny_and_prefill(gpu_ctx, oracle, qtype, m, n, k, x16):
     assert e <= (2e-5 if exact else TOL)
 
 
-@pytest.mark.parametrize("m", [1, 8, 64, 130])
-def test_q6_k_full_range_scales(gpu_ctx, oracle, m):
+@pytest.mark.parametrize("m,lim", [(1, 128), (8, 128), (64, 128), (130, 128), (8, 64), (64, 64),
+                                   (130, 64), (8, 62), (64, 62)])
+def test_q6_k_full_range_scales(gpu_ctx, oracle, m, lim):
     # quantizers put each block's largest sub-block scale near +-127, where sc * (q - 32)
     # passes 2048 and would round in f16; the skinny kernel (m = 5..64) multiplies the exact
     # codes q - 32 and scales each sub-block's product by d * sc in f32, the prefill GEMM
     # (m = 130) holds sc * (q - 32) as f16 hi + lo operands (exact) against x as f16
     # hi + lo.  The synthetic blocks keep scales in [-32, 31], so this test draws them from
-    # all of i8; at m = 8 (three f16 parts of x), 64 and 130 (hi + lo) every output is
-    # held to 2e-5
+    # all of i8 (lim 128).  Scales within +-64 keep the prefill's one operand; within +-62
+    # the skinny kernel's integer operands sc * (q - 32) / 2, whose FMA constant -528 sc is
+    # an f16 value only up to |sc| = 62: lim 64 and 62 put +-lim and +-(lim - 1) into every
+    # block, so both sides of each threshold run.  At m = 8 (three f16 parts of x), 64 and
+    # 130 (hi + lo) every output is held to 2e-5
     from arf_amd import QType, synth
-    _say("case: q6_k full-range scales", m)
+    _say("case: q6_k full-range scales", m, lim)
     n, k = 384, 4096
     raw = synth.weight("q6_k", n, k, seed=0xA7F0000C)
     blk = raw.reshape(-1, 210)
     rng = np.random.default_rng(0xA7F0000D)
-    blk[:, 192:208] = rng.integers(-128, 128, size=(blk.shape[0], 16)).astype(np.int8).view(np.uint8)
+    if lim == 128:
+        blk[:, 192:208] = rng.integers(-128, 128, size=(blk.shape[0], 16)).astype(np.int8).view(np.uint8)
+    else:
+        sc = rng.integers(-lim, lim + 1, size=(blk.shape[0], 16))
+        sc[:, :4] = [lim, -lim, lim - 1, 1 - lim]
+        blk[:, 192:208] = rng.permuted(sc, axis=1).astype(np.int8).view(np.uint8)
     x = synth.activations(m, k, seed=0xA7F0000E)
     w = gpu_ctx.upload(QType.Q6_K, raw, n, k)
     y = gpu_ctx.empty((m, n), np.float32)
