@@ -99,7 +99,9 @@ __host__ __device__ constexpr int SK_XB(int ta) { return ta == 1 ? 2 : 1; }
 // workgroup stores its partial to part[sp][m][n]; the last of a column tile's
 // S workgroups to arrive (counted in tick[blockIdx.x], which it resets to 0)
 // sums the S partials in split order into y, so the result does not depend on
-// the arrival order.
+// the arrival order.  An f32 x (XT = float, PARTS 3, formats without the min
+// term) is split into its three f16 parts as it is staged, the scales of its
+// K range worked out here (no separate preparation launch).
 // (held to 256 VGPRs: two 4-wave workgroups per CU; with four x tiles the LDS
 // leaves room for one workgroup, of 8 waves: two per SIMD again)
 template <class F, int TA, class XT, int PARTS, int GM = 0xFF>
@@ -126,8 +128,11 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
     constexpr bool PAIR = PARTS == 2;
     constexpr int PO = PARTS == 3 ? 8 : 16 * TA;
     static_assert(PARTS != 3 || TA == 1, "three parts fit one tile");
+    constexpr bool FX = sizeof(XT) == 4;  // f32 x, split here
+    static_assert(!FX || PARTS == 3, "an f32 x is split here into three parts only");
     const SkRows<TA, NT> rows =
-        PARTS == 3 ? sk_rows<TA, NT>(16 + M, K, [M](int r) {
+        FX ? sk_rows<TA, NT>(M, K, [](int r) { return r; })
+        : PARTS == 3 ? sk_rows<TA, NT>(16 + M, K, [M](int r) {
             return r < M ? r : r < 8 ? 0 : r < 8 + M ? M + r - 8 : r < 16 ? 0 : 2 * M + r - 16;
         })
         : PAIR ? sk_rows<TA, NT>(PO + M, K, [M](int r) { return r < M ? r : r >= PO ? M + r - PO : 0; })
@@ -145,8 +150,15 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // PAIR with two or four tiles: the lo tiles' products go into the hi tiles' accumulators
-    skinny_run<F, TA, 1, NT, XT, false, GM, PAIR && TA >= 2, true, SK_XB(TA)>(fm, wrow0, N, rows, x, xs, b0, b1, acc, lds,
-                                                                    PARTS == 3 ? 16 + M : PAIR ? PO + M : M);
+    int xsh = 0;
+    skinny_run<F, TA, 1, NT, XT, false, GM, PAIR && TA >= 2, true, SK_XB(TA), FX ? 3 : 0>(
+        fm, wrow0, N, rows, x, xs, b0, b1, acc, lds, PARTS == 3 ? 16 + M : PAIR ? PO + M : M, xsh);
+    if constexpr (FX) {
+        // the rows' scales over this K range (row tid / 32 from its lanes' xsh)
+        if ((tid & 31) == 0) lrs[tid >> 5] = tid >> 5 < M ? ldexpf(1.f, -xsh) : 1.f;
+        if (tid >= 8 && tid < 32) lrs[tid] = 1.f;
+        __syncthreads();
+    }
     if constexpr (PAIR && TA == 1) {
         // rows r and r + 16 of a lane's accumulator are elements i and i + 8
 #pragma unroll
@@ -165,12 +177,13 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
                 // (m & 3 == i & 3: one 16-byte LDS read serves four rows)
                 if (m < M && n < N)
                     y[(int64_t)m * N + n] =
-                        rs ? acc[0][t][i] * reinterpret_cast<const float4 *>(lrs)[m >> 2][i & 3] : acc[0][t][i];
+                        FX || rs ? acc[0][t][i] * reinterpret_cast<const float4 *>(lrs)[m >> 2][i & 3]
+                                 : acc[0][t][i];
             }
         return;
     }
     // x scaled per K range (rs[sp * rss + row]): the partial back to true units
-    if (rs) {
+    if (FX || rs) {
 #pragma unroll
         for (int t = 0; t < TA; t++)
 #pragma unroll
@@ -359,6 +372,10 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     // m <= 32 and two more at m <= 64 (twice the MFMAs).  With x16
     // (ARFQ_OPT_GEMV_X16): one part, x rounded to f16.
     p.parts = p.skinny && x_dtype == ARFQ_F32 && !x16 ? (m <= 8 ? 3 : 2) : p.bd && bdx == 2 ? 2 : 1;
+    // three parts without sub-block sums: formed by the skinny kernel as it
+    // stages x (no preparation launch, no scratch for x)
+    p.fx = p.skinny && p.parts == 3 && !kind2;
+    if (p.fx) p.convert = false;
     // the exact Q4_K paths read x sub-block sums (min term)
     p.sums = (p.skinny || p.bd) && kind2;
     int64_t S;
@@ -420,40 +437,48 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     return p;
 }
 
-template <class F, int TA, int PARTS, int GM = 0xFF>
-static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
+template <class F, int TA, int PARTS, int GM = 0xFF, class XT = _Float16>
+static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const XT *x,
                               const uint16_t *xs, const float *rs, int rss, float *y, float *part,
                               uint32_t *tick, int S, hipStream_t s) {
     if constexpr (F::KIND == 4 && TA == 1 && GM == 0xFF) {
         // at most 8 rows (8 hi + 8 lo with two parts, + 8 mid with three): the
         // per-sub-block scaling touches only the accumulator groups that hold them
         if (m <= 8)
-            return launch_sk_t<F, 1, PARTS, PARTS == 3 ? 0x7 : PARTS == 2 ? 0x5 : 0x1>(fmt, w, m, x, xs, rs, rss, y,
-                                                                                      part, tick, S, s);
+            return launch_sk_t<F, 1, PARTS, PARTS == 3 ? 0x7 : PARTS == 2 ? 0x5 : 0x1, XT>(fmt, w, m, x, xs, rs, rss,
+                                                                                          y, part, tick, S, s);
     }
     constexpr int NT = sk_nt(TA), CT = NT / 2;
     constexpr size_t lds = sk_lds<F, TA, 1, NT, SK_XB(TA)>() + 32 * TA * 4;  // + the x rows' scales
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
-    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, _Float16, PARTS, GM>, lds, lds_set))
+    if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, XT, PARTS, GM>, lds, lds_set))
         return err;
     const dim3 grid((unsigned)((w->n + CT - 1) / CT), (unsigned)S);
-    gemm_sk<F, TA, _Float16, PARTS, GM><<<grid, NT, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m,
-                                                                     (int)w->n, (int)w->k, rss);
+    gemm_sk<F, TA, XT, PARTS, GM><<<grid, NT, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m, (int)w->n,
+                                                           (int)w->k, rss);
     return hipGetLastError();
 }
 
 // S > 1 splits need S <= 16 and one zeroed counter per column tile.  x is
 // f16 (an f32 x arrives prepared and scaled, rs[split * rss + row] its scale
 // over each split's K range); with parts 2 (m <= 64) it is [2m, K]: the hi
-// rows, then the lo rows; with parts 3 (m <= 8) [3m, K]: hi, mid, lo rows.
+// rows, then the lo rows; with parts 3 (m <= 8) [3m, K]: hi, mid, lo rows,
+// or, given xf (formats without the min term), the caller's f32 x [m, K],
+// split into those parts by the kernel itself.
 template <class F>
 static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                             const uint16_t *xs, const float *rs, int rss, float *y, float *part,
-                            uint32_t *tick, int ntick, int S, hipStream_t s, int parts) {
+                            uint32_t *tick, int ntick, int S, hipStream_t s, int parts,
+                            const float *xf = nullptr) {
     if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;  // >= ceil(n / CT)
     if (parts == 3) {
         if (m > 8) return hipErrorInvalidValue;
-        return launch_sk_t<F, 1, 3>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+        if constexpr (F::KIND != 2) {
+            if (!xf) return hipErrorInvalidValue;
+            return launch_sk_t<F, 1, 3, 0xFF, float>(fmt, w, m, xf, nullptr, nullptr, 0, y, part, tick, S, s);
+        } else {
+            return launch_sk_t<F, 1, 3>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+        }
     }
     if (parts == 2) {
         if (m > 64) return hipErrorInvalidValue;
@@ -595,6 +620,7 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
     if (p.skinny) {
         // the split-K sum happens inside the kernel
         const _Float16 *xk = p.convert ? xh : (const _Float16 *)x;
+        const float *xf = p.fx ? (const float *)x : nullptr;  // split by the kernel itself
         const int64_t eb = (int64_t)e * w->n * (w->k / 256);
         switch (w->qtype) {
         case ARFQ_Q4_K:
@@ -603,18 +629,18 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         case ARFQ_Q6_K:  // scales within +-62 (the upload's flag): integer operands sc * (q - 32) / 2
             if (!w->over62)
                 return launch_sk(SkQ6KI{sk_q6k(w)}.shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets,
-                                 ntickets, p.splits, s, p.parts);
+                                 ntickets, p.splits, s, p.parts, xf);
             return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.parts);
+                             p.splits, s, p.parts, xf);
         case ARFQ_Q8_0:
             return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xs, rs,
-                             (int)m, y, out, tickets, ntickets, p.splits, s, p.parts);
+                             (int)m, y, out, tickets, ntickets, p.splits, s, p.parts, xf);
         case ARFQ_Q5_K:
             return launch_sk(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
                              p.splits, s, p.parts);
         case ARFQ_IQ4_XS:
             return launch_sk(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.parts);
+                             p.splits, s, p.parts, xf);
         default:
             return hipErrorInvalidValue;
         }

@@ -433,14 +433,22 @@ constexpr size_t sk_lds() {
 // dense skinny GEMM at C3 m = 64 ran 57.6 -> 53.0 us with the step boundary
 // held, the MoE tiles 1 % slower).  XB = 2: two x buffers; the next block's x
 // goes into the one not being read, which leaves one barrier per block
-// instead of two, for a second x buffer of LDS.
+// instead of two, for a second x buffer of LDS.  XP = 3: x is the caller's f32
+// [m <= 8, K] and is split here (one 32-row tile, 256 threads): thread tid
+// stages elements 8 (tid % 32) .. + 7 of row rows.x[0] (row tid / 32,
+// clamped to m - 1) as the f16 parts of x * 2^xsh -- hi, mid = the rounded
+// remainder, lo = the rounded remainder of that -- into tile rows r, 8 + r and
+// 16 + r (r = tid / 32), where xsh (returned) puts the largest |x| of the
+// row over blocks [b0, b1) in [2^14, 2^15): the arithmetic of xprep_kernel
+// with three parts, without its launch.  Rows 24..31 of the tile stage
+// nothing (their products land in rows never stored).
 template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF, bool MERGE = false,
-          bool PIN = false, int XB = 1>
+          bool PIN = false, int XB = 1, int XP = 0>
 __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                             int64_t nrows, const SkRows<TA, NT> &rows,
                                             const XT *__restrict__ x,
                                             const uint16_t *__restrict__ xs, int b0, int b1,
-                                            floatx16 (&acc)[NW][TA], _Float16 *lds) {
+                                            floatx16 (&acc)[NW][TA], _Float16 *lds, int &xsh) {
     constexpr int KIND = F::KIND;
     constexpr int XR = 32 * TA;       // x rows staged
     constexpr int TO = MERGE ? TU / 2 : TU;  // accumulator tiles written
@@ -461,7 +469,9 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
     // f16 when stored to LDS)
     constexpr int XW = sizeof(XT) / 2;
     static_assert(XW == 1 || XW == 2, "x is f16 or f32");
-    constexpr int XU = XC * TU / TA;  // chunks of the x rows in use
+    static_assert(XP == 0 || (XP == 3 && XW == 2 && TA == 1 && TU == 1 && NT == 256 && KIND != 2),
+                  "three parts formed here: f32 x, one tile of 256 threads, no sub-block sums");
+    constexpr int XU = XP == 3 ? 1 : XC * TU / TA;  // chunks of the x rows in use
     u32x4 xv[XU * XW], sv;
     auto xload = [&](int b) {
 #pragma unroll
@@ -478,6 +488,21 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
         }
     };
     auto xstore = [&](int to) {
+        if constexpr (XP == 3) {
+            half8 hp[3];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float u = ldexpf(__uint_as_float(xv[i >> 2][i & 3]), xsh);
+                hp[0][i] = (_Float16)u;
+                const float r1 = u - (float)hp[0][i];  // exact
+                hp[1][i] = (_Float16)r1;
+                hp[2][i] = (_Float16)(r1 - (float)hp[1][i]);  // exact difference
+            }
+#pragma unroll
+            for (int q = 0; q < 3; q++)
+                *reinterpret_cast<half8 *>(xl + (to * XR + 8 * q + (tid >> 5)) * SK_XLD + 8 * (tid & 31)) = hp[q];
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < XU; i++) {
             u32x4 v;
@@ -528,6 +553,31 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
     for (int w = 0; w < NW; w++) wb[w] = fmt[w].load_blk(myrow[w], b0);
     wload(b0);
+    if constexpr (XP == 3) {
+        // the row's largest |x| over the K range, four blocks' loads in flight
+        // (issued behind the first weights, whose arrival the prologue waits
+        // for anyway)
+        const XT *xr = x + rows.x[0] + 8 * (tid & 31);
+        float amax = 0.f;
+        for (int b = b0; b < b1; b += 4) {
+            float4 t[4][2];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int bb = min(b + u, b1 - 1);
+                t[u][0] = *reinterpret_cast<const float4 *>(xr + 256 * bb);
+                t[u][1] = *reinterpret_cast<const float4 *>(xr + 256 * bb + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(t[u][j].x), fabsf(t[u][j].y)),
+                                             fmaxf(fabsf(t[u][j].z), fabsf(t[u][j].w))));
+        }
+#pragma unroll
+        for (int o = 16; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));  // the row's 32 lanes
+        xsh = amax > 0.f && amax < INFINITY ? 15 - __builtin_amdgcn_frexp_expf(amax) : 0;
+    }
     xload(b0);
     xstore(0);
     __syncthreads();
@@ -669,20 +719,34 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 // second x tile is neither staged nor multiplied (acc[w][1] is left as it
 // is).  All threads of the workgroup call it with the same block range and
 // xrows.
+// (xsh: the x scale exponent of XP = 3)
 template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF,
-          bool MERGE = false, bool PIN = false, int XB = 1>
+          bool MERGE = false, bool PIN = false, int XB = 1, int XP = 0>
+__device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
+                                           int64_t nrows, const SkRows<TA, NT> &rows,
+                                           const XT *__restrict__ x,
+                                           const uint16_t *__restrict__ xs, int b0, int b1,
+                                           floatx16 (&acc)[NW][TA], _Float16 *lds, int xrows, int &xsh) {
+    if constexpr (TA == 2 && SHORT) {
+        if (xrows <= 32) {
+            skinny_loop<F, TA, 1, NW, NT, XT, GM, false, false, XB>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds,
+                                                                   xsh);
+            return;
+        }
+    }
+    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE, PIN, XB, XP>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds,
+                                                              xsh);
+}
+template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF,
+          bool MERGE = false, bool PIN = false, int XB = 1, int XP = 0>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
                                            const XT *__restrict__ x,
                                            const uint16_t *__restrict__ xs, int b0, int b1,
                                            floatx16 (&acc)[NW][TA], _Float16 *lds, int xrows) {
-    if constexpr (TA == 2 && SHORT) {
-        if (xrows <= 32) {
-            skinny_loop<F, TA, 1, NW, NT, XT, GM, false, false, XB>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
-            return;
-        }
-    }
-    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE, PIN, XB>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds);
+    int xsh = 0;
+    skinny_run<F, TA, NW, NT, XT, SHORT, GM, MERGE, PIN, XB, XP>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds,
+                                                                  xrows, xsh);
 }
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.
