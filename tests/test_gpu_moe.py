@@ -217,6 +217,23 @@ def test_moe_ids_matches_moe_and_drops_invalid(gpu_ctx, oracle):
     keep[[3, 7]] = False
     assert rel_err(got[keep], ref[keep]) <= 1e-6
     assert np.all(np.isfinite(got))
+    # a dropped pair adds nothing: the same bits as a valid id with weight 0
+    # (acc + 0 * o = acc), so tokens 3 and 7 hold their other slot alone
+    fix, w0 = bad.copy(), w.copy()
+    fix[3, 1], fix[7, 0] = 0, 0
+    w0[3, 1], w0[7, 0] = 0.0, 0.0
+    z = gpu_ctx.empty((T, hidden), np.float32)
+    gpu_ctx.moe_ids(ws[0], ws[1], ws[2], gpu_ctx.to_device(fix), gpu_ctx.to_device(w0), T, k,
+                    gpu_ctx.to_device(x), z)
+    assert np.array_equal(got.view(np.uint32), z.numpy().view(np.uint32))
+    # (T * k = 40 pairs: the decode path, whose down GEMV combines through counters)
+    # the counters are left at zero: a repeat of the first call gives its bits
+    gpu_ctx.moe_ids(ws[0], ws[1], ws[2], gpu_ctx.to_device(ids), gpu_ctx.to_device(w), T, k,
+                    gpu_ctx.to_device(x), y)
+    first = y.numpy().copy()
+    gpu_ctx.moe_ids(ws[0], ws[1], ws[2], gpu_ctx.to_device(ids), gpu_ctx.to_device(w), T, k,
+                    gpu_ctx.to_device(x), y)
+    assert np.array_equal(first.view(np.uint32), y.numpy().view(np.uint32))
 
 
 def test_moe_deterministic(gpu_ctx):
