@@ -99,9 +99,9 @@ __host__ __device__ constexpr int SK_XB(int ta) { return ta == 1 ? 2 : 1; }
 // workgroup stores its partial to part[sp][m][n]; the last of a column tile's
 // S workgroups to arrive (counted in tick[blockIdx.x], which it resets to 0)
 // sums the S partials in split order into y, so the result does not depend on
-// the arrival order.  An f32 x (XT = float, PARTS 3, formats without the min
-// term) is split into its three f16 parts as it is staged, the scales of its
-// K range worked out here (no separate preparation launch).
+// the arrival order.  An f32 x (XT = float, PARTS 3) is split into its three
+// f16 parts (and their sub-block sums) as it is staged, the scales of its K
+// range worked out here (no separate preparation launch).
 // (held to 256 VGPRs: two 4-wave workgroups per CU; with four x tiles the LDS
 // leaves room for one workgroup, of 8 waves: two per SIMD again)
 template <class F, int TA, class XT, int PARTS, int GM = 0xFF>
@@ -372,12 +372,13 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
     // m <= 32 and two more at m <= 64 (twice the MFMAs).  With x16
     // (ARFQ_OPT_GEMV_X16): one part, x rounded to f16.
     p.parts = p.skinny && x_dtype == ARFQ_F32 && !x16 ? (m <= 8 ? 3 : 2) : p.bd && bdx == 2 ? 2 : 1;
-    // three parts without sub-block sums: formed by the skinny kernel as it
+    // three parts (and their sub-block sums): formed by the skinny kernel as it
     // stages x (no preparation launch, no scratch for x)
-    p.fx = p.skinny && p.parts == 3 && !kind2;
+    p.fx = p.skinny && p.parts == 3;
     if (p.fx) p.convert = false;
-    // the exact Q4_K paths read x sub-block sums (min term)
-    p.sums = (p.skinny || p.bd) && kind2;
+    // the exact Q4_K paths read x sub-block sums (min term; with fx the skinny
+    // kernel forms them)
+    p.sums = (p.skinny || p.bd) && kind2 && !p.fx;
     int64_t S;
     size_t bd_part = 0;
     if (p.bd) {
@@ -462,9 +463,9 @@ static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, con
 // S > 1 splits need S <= 16 and one zeroed counter per column tile.  x is
 // f16 (an f32 x arrives prepared and scaled, rs[split * rss + row] its scale
 // over each split's K range); with parts 2 (m <= 64) it is [2m, K]: the hi
-// rows, then the lo rows; with parts 3 (m <= 8) [3m, K]: hi, mid, lo rows,
-// or, given xf (formats without the min term), the caller's f32 x [m, K],
-// split into those parts by the kernel itself.
+// rows, then the lo rows; with parts 3 (m <= 8) the caller's f32 x [m, K] as
+// xf, split into hi, mid and lo parts (and their sub-block sums) by the kernel
+// itself.
 template <class F>
 static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                             const uint16_t *xs, const float *rs, int rss, float *y, float *part,
@@ -473,12 +474,8 @@ static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const
     if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;  // >= ceil(n / CT)
     if (parts == 3) {
         if (m > 8) return hipErrorInvalidValue;
-        if constexpr (F::KIND != 2) {
-            if (!xf) return hipErrorInvalidValue;
-            return launch_sk_t<F, 1, 3, 0xFF, float>(fmt, w, m, xf, nullptr, nullptr, 0, y, part, tick, S, s);
-        } else {
-            return launch_sk_t<F, 1, 3>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
-        }
+        if (!xf) return hipErrorInvalidValue;
+        return launch_sk_t<F, 1, 3, 0xFF, float>(fmt, w, m, xf, nullptr, nullptr, 0, y, part, tick, S, s);
     }
     if (parts == 2) {
         if (m > 64) return hipErrorInvalidValue;
@@ -625,7 +622,7 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         switch (w->qtype) {
         case ARFQ_Q4_K:
             return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.parts);
+                             p.splits, s, p.parts, xf);
         case ARFQ_Q6_K:  // scales within +-62 (the upload's flag): integer operands sc * (q - 32) / 2
             if (!w->over62)
                 return launch_sk(SkQ6KI{sk_q6k(w)}.shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets,
@@ -637,7 +634,7 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
                              (int)m, y, out, tickets, ntickets, p.splits, s, p.parts, xf);
         case ARFQ_Q5_K:
             return launch_sk(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
-                             p.splits, s, p.parts);
+                             p.splits, s, p.parts, xf);
         case ARFQ_IQ4_XS:
             return launch_sk(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
                              p.splits, s, p.parts, xf);

@@ -137,7 +137,7 @@ struct GemmPlan {
     // prefill; 3: hi + mid + lo, skinny m <= 8, which represents every f32 x
     // within 2^15 of its row's max exactly), stored as row blocks [parts][m][k]
     int parts = 1;
-    bool fx = false;       // skinny, parts 3, no x sums: the kernel splits the f32 x itself
+    bool fx = false;       // skinny, parts 3: the kernel splits the f32 x (and sums its parts) itself
     int bd_full = 0;       // bd: whole tiles; the rest are split into bd_chunks K ranges
     int bd_chunks = 1;
     size_t off_xh = 0, off_xl = 0, off_xs = 0, off_rs = 0, off_part = 0, scratch_bytes = 0;

@@ -439,9 +439,11 @@ constexpr size_t sk_lds() {
 // clamped to m - 1) as the f16 parts of x * 2^xsh -- hi, mid = the rounded
 // remainder, lo = the rounded remainder of that -- into tile rows r, 8 + r and
 // 16 + r (r = tid / 32), where xsh (returned) puts the largest |x| of the
-// row over blocks [b0, b1) in [2^14, 2^15): the arithmetic of xprep_kernel
-// with three parts, without its launch.  Rows 24..31 of the tile stage
-// nothing (their products land in rows never stored).
+// row over blocks [b0, b1) in [2^14, 2^15), and for KIND 2 each part's
+// sub-block sums (its lanes' 8 in order, then the quad's (s0 + s1) + (s2 + s3))
+// as bf16 hi + lo: the arithmetic of xprep_kernel with three parts, without
+// its launch.  Rows 24..31 of the tile stage nothing (their products land in
+// rows never stored).
 template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF, bool MERGE = false,
           bool PIN = false, int XB = 1, int XP = 0>
 __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
@@ -469,8 +471,8 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
     // f16 when stored to LDS)
     constexpr int XW = sizeof(XT) / 2;
     static_assert(XW == 1 || XW == 2, "x is f16 or f32");
-    static_assert(XP == 0 || (XP == 3 && XW == 2 && TA == 1 && TU == 1 && NT == 256 && KIND != 2),
-                  "three parts formed here: f32 x, one tile of 256 threads, no sub-block sums");
+    static_assert(XP == 0 || (XP == 3 && XW == 2 && TA == 1 && TU == 1 && NT == 256),
+                  "three parts formed here: f32 x, one tile of 256 threads");
     constexpr int XU = XP == 3 ? 1 : XC * TU / TA;  // chunks of the x rows in use
     u32x4 xv[XU * XW], sv;
     auto xload = [&](int b) {
@@ -483,7 +485,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
         // the sums' load sits in the same branch as their store: loaded
         // unconditionally, it was sunk next to the store, where its wait
         // covered every load in flight
-        if constexpr (KIND == 2) {
+        if constexpr (KIND == 2 && XP == 0) {
             if (tid < 64 * TU) sv = *reinterpret_cast<const u32x4 *>(xs + rows.s + 16 * b + 8 * (tid & 1));
         }
     };
@@ -501,6 +503,23 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 #pragma unroll
             for (int q = 0; q < 3; q++)
                 *reinterpret_cast<half8 *>(xl + (to * XR + 8 * q + (tid >> 5)) * SK_XLD + 8 * (tid & 31)) = hp[q];
+            if constexpr (KIND == 2) {
+#pragma unroll
+                for (int q = 0; q < 3; q++) {
+                    float t = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; i++) t += (float)hp[q][i];
+                    // the quad of lanes holding the sub-block: (s0 + s1) + (s2 + s3) on each
+                    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xf, 0xf, true));
+                    t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xf, 0xf, true));
+                    if ((tid & 3) == 0) {
+                        const uint32_t hi = bf16_bits(t);
+                        uint16_t *d = sl + (to * XR + 8 * q + (tid >> 5)) * 16 + ((tid & 31) >> 2);
+                        d[0] = (uint16_t)hi;
+                        d[8] = (uint16_t)bf16_bits(t - bf16_to_f32(hi));
+                    }
+                }
+            }
             return;
         }
 #pragma unroll
