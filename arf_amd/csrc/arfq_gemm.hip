@@ -96,10 +96,11 @@ __host__ __device__ constexpr int SK_XB(int ta) { return ta == 1 ? 2 : 1; }
 // (a wave per 32 weight rows), over the 256-element blocks of split blockIdx.y
 // (arfq_skinny.h).  x is f16, or f32
 // rounded to f16 as it is staged.  With S = gridDim.y > 1 splits each
-// workgroup stores its partial to part[sp][m][n]; the last of a column tile's
-// S workgroups to arrive (counted in tick[blockIdx.x], which it resets to 0)
-// sums the S partials in split order into y, so the result does not depend on
-// the arrival order.  An f32 x (XT = float, PARTS 3) is split into its three
+// workgroup stores its partial and sk_reduce_kernel, launched next, adds the S
+// partials of every output in split order into y (deterministic: spread over
+// every CU, where the last of a column tile's workgroups to arrive, summing
+// them alone, left the chip idle for 4 / 9 / 18 us at C3 m = 8 / 32 / 64).
+// An f32 x (XT = float, PARTS 3) is split into its three
 // f16 parts (and their sub-block sums) as it is staged, the scales of its K
 // range worked out here (no separate preparation launch).
 // (held to 256 VGPRs: two 4-wave workgroups per CU; with four x tiles the LDS
@@ -109,10 +110,9 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
                                                       const uint16_t *__restrict__ xs,
                                                       const float *__restrict__ rs,
                                                       float *__restrict__ y, float *__restrict__ part,
-                                                      uint32_t *__restrict__ tick, int M, int N, int K,
+                                                      int M, int N, int K,
                                                       int rss) {
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
-    __shared__ int last;
     constexpr int NT = sk_nt(TA), CT = NT / 2;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * CT;
@@ -195,72 +195,54 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
     // Split K.  Each wave stores its accumulators as they sit in registers:
     // float4 (row group gi = 4 t + g, lane) holds acc[t][4 g .. 4 g + 3], rows
     // 32 t + 8 g + 4 (lane / 32) + 0..3 of column n, for the GT 8-row groups
-    // that hold rows < M.  The partials move with the device-scope cache
-    // policy (sc1: written through to, and read from, the level coherent
-    // across the XCDs' L2s, as the compiler encodes agent-scope atomic
-    // accesses) rather than by writing back and invalidating whole L2s; every
-    // store has completed before the counter moves, and the last arriver
-    // loads the others' partials only after it has seen the count.
+    // that hold rows < M; sk_reduce_kernel adds the splits (in split order)
+    // after this launch.
     const int GT = (M + 7) >> 3, nt = gridDim.x;
-    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-        part, (short)0, (int)((uint32_t)S * nt * (NT / 64) * GT * 1024u), 0x00020000);
-    auto poff = [&](int j, int gi) -> uint32_t {
-        return ((((uint32_t)j * nt + blockIdx.x) * (NT / 64) + wave) * GT + gi) * 1024u + lane * 16u;
-    };
-    constexpr int SC1 = 16;  // cache-policy operand: device scope
+    float4 *pw = reinterpret_cast<float4 *>(part) + ((((int64_t)sp * nt + blockIdx.x) * (NT / 64) + wave) * GT) * 64 + lane;
 #pragma unroll
     for (int t = 0; t < TA; t++)
 #pragma unroll
         for (int g = 0; g < 4; g++)
-            if (4 * t + g < GT) {
-                const u32x4 v = {__float_as_uint(acc[0][t][4 * g]), __float_as_uint(acc[0][t][4 * g + 1]),
-                                 __float_as_uint(acc[0][t][4 * g + 2]), __float_as_uint(acc[0][t][4 * g + 3])};
-                __builtin_amdgcn_raw_buffer_store_b128(v, prs, poff(sp, 4 * t + g), 0, SC1);
-            }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are done
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t before =
-            __hip_atomic_fetch_add(tick + blockIdx.x, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        last = before == (uint32_t)(S - 1);
-        if (last) __hip_atomic_store(tick + blockIdx.x, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (!last) return;
-    // Sum in split order, this workgroup's own partial from its registers;
-    // the next row group's loads are in flight while one group is summed.
-    // Straight-line code (branches around loads cost waits on every load in
-    // flight): loads of splits past S, of this workgroup's own split and of
-    // row groups past GT read past the end of the buffer, which returns 0
-    // and moves no data.
-    u32x4 v[2][16];
-    auto load = [&](u32x4(&d)[16], int gi) {
+            if (4 * t + g < GT)
+                pw[(4 * t + g) * 64] = make_float4(acc[0][t][4 * g], acc[0][t][4 * g + 1], acc[0][t][4 * g + 2],
+                                                   acc[0][t][4 * g + 3]);
+}
+
+// y of the skinny split-K: a thread per float4 of one split's partials, in the
+// register order gemm_sk stores them ([split][column tile][wave][row group][lane]),
+// its S splits added in split order; rows 32 t + 8 g + 4 (lane / 32) + 0..3 of
+// column tile * ct + 32 wave + lane % 32 (row group gi = 4 t + g).  All S loads
+// are in flight at once: straight-line code, the loads of splits past S reading
+// past the end of the buffer, which returns 0 and moves no data (adding that 0
+// changes nothing but a -0 sum into +0).
+__global__ __launch_bounds__(256) void sk_reduce_kernel(const float *__restrict__ part, float *__restrict__ y,
+                                                        int S, int nt, int nw, int GT, int ct, int M, int N) {
+    const int64_t units = (int64_t)nt * nw * GT;  // float4 columns of one split, / 64
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= units * 64) return;
+    const int lane = (int)(q & 63);
+    const int64_t u = q >> 6;
+    const int gi = (int)(u % GT), wave = (int)((u / GT) % nw), tile = (int)(u / ((int64_t)GT * nw));
+    const uint32_t split_bytes = (uint32_t)(units * 1024);
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(part), (short)0, (int)(split_bytes * (uint32_t)S), 0x00020000);
+    u32x4 d[16];
 #pragma unroll
-        for (int j = 0; j < 16; j++)
-            d[j] = __builtin_amdgcn_raw_buffer_load_b128(
-                prs, poff(j, gi) | (uint32_t)(j >= S || j == sp || gi >= GT) << 31, 0, SC1);
-    };
-    load(v[0], 0);
+    for (int j = 0; j < 16; j++)
+        d[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, ((uint32_t)j * split_bytes + (uint32_t)q * 16u) |
+                                                              (uint32_t)(j >= S) << 31, 0, 0);
+    float r[4];
 #pragma unroll
-    for (int gi = 0; gi < 4 * TA; gi++) {
-        if (gi + 1 < 4 * TA) load(v[(gi + 1) & 1], gi + 1);
-        const int t = gi >> 2, g = gi & 3;
-        const u32x4(&d)[16] = v[gi & 1];
-        float r[4];
+    for (int c = 0; c < 4; c++) r[c] = __uint_as_float(d[0][c]);
 #pragma unroll
-        for (int c = 0; c < 4; c++) r[c] = sp == 0 ? acc[0][t][4 * g + c] : __uint_as_float(d[0][c]);
-        // splits past S add the 0 their loads returned (exact but for a -0
-        // sum turning +0)
+    for (int j = 1; j < 16; j++)
 #pragma unroll
-        for (int j = 1; j < 16; j++)
+        for (int c = 0; c < 4; c++) r[c] += __uint_as_float(d[j][c]);
+    const int row = 32 * (gi >> 2) + 8 * (gi & 3) + 4 * (lane >> 5);
+    const int n = tile * ct + 32 * wave + (lane & 31);
 #pragma unroll
-            for (int c = 0; c < 4; c++) r[c] += j == sp ? acc[0][t][4 * g + c] : __uint_as_float(d[j][c]);
-        const int row = 32 * t + 8 * g + 4 * (lane >> 5);
-#pragma unroll
-        for (int c = 0; c < 4; c++)
-            if (row + c < M && n < N) y[(int64_t)(row + c) * N + n] = r[c];
-    }
+    for (int c = 0; c < 4; c++)
+        if (row + c < M && n < N) y[(int64_t)(row + c) * N + n] = r[c];
 }
 
 // y[i] = part[0][i] + part[1][i] + ... in split order, times the row's x
@@ -441,23 +423,32 @@ GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16) {
 template <class F, int TA, int PARTS, int GM = 0xFF, class XT = _Float16>
 static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, const XT *x,
                               const uint16_t *xs, const float *rs, int rss, float *y, float *part,
-                              uint32_t *tick, int S, hipStream_t s) {
+                              int S, hipStream_t s) {
     if constexpr (F::KIND == 4 && TA == 1 && GM == 0xFF) {
         // at most 8 rows (8 hi + 8 lo with two parts, + 8 mid with three): the
         // per-sub-block scaling touches only the accumulator groups that hold them
         if (m <= 8)
             return launch_sk_t<F, 1, PARTS, PARTS == 3 ? 0x7 : PARTS == 2 ? 0x5 : 0x1, XT>(fmt, w, m, x, xs, rs, rss,
-                                                                                          y, part, tick, S, s);
+                                                                                          y, part, S, s);
     }
     constexpr int NT = sk_nt(TA), CT = NT / 2;
     constexpr size_t lds = sk_lds<F, TA, 1, NT, SK_XB(TA)>() + 32 * TA * 4;  // + the x rows' scales
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)gemm_sk<F, TA, XT, PARTS, GM>, lds, lds_set))
         return err;
-    const dim3 grid((unsigned)((w->n + CT - 1) / CT), (unsigned)S);
-    gemm_sk<F, TA, XT, PARTS, GM><<<grid, NT, lds, s>>>(fmt, x, xs, rs, y, part, tick, (int)m, (int)w->n,
-                                                           (int)w->k, rss);
-    return hipGetLastError();
+    const int nt = (int)((w->n + CT - 1) / CT);
+    const dim3 grid((unsigned)nt, (unsigned)S);
+    gemm_sk<F, TA, XT, PARTS, GM><<<grid, NT, lds, s>>>(fmt, x, xs, rs, y, part, (int)m, (int)w->n, (int)w->k,
+                                                           rss);
+    if (hipError_t err = hipGetLastError()) return err;
+    if (S > 1) {
+        const int gt = (int)((m + 7) / 8);
+        const int64_t threads = (int64_t)nt * (NT / 64) * gt * 64;
+        sk_reduce_kernel<<<(unsigned)((threads + 255) / 256), 256, 0, s>>>(part, y, S, nt, NT / 64, gt, CT, (int)m,
+                                                                           (int)w->n);
+        return hipGetLastError();
+    }
+    return hipSuccess;
 }
 
 // S > 1 splits need S <= 16 and one zeroed counter per column tile.  x is
@@ -469,22 +460,21 @@ static hipError_t launch_sk_t(const F &fmt, const arfq_weight *w, int64_t m, con
 template <class F>
 static hipError_t launch_sk(const F &fmt, const arfq_weight *w, int64_t m, const _Float16 *x,
                             const uint16_t *xs, const float *rs, int rss, float *y, float *part,
-                            uint32_t *tick, int ntick, int S, hipStream_t s, int parts,
-                            const float *xf = nullptr) {
-    if (S > 1 && (S > 16 || !part || !tick || (w->n + 127) / 128 > ntick)) return hipErrorInvalidValue;  // >= ceil(n / CT)
+                            int S, hipStream_t s, int parts, const float *xf = nullptr) {
+    if (S > 1 && (S > 16 || !part)) return hipErrorInvalidValue;
     if (parts == 3) {
         if (m > 8) return hipErrorInvalidValue;
         if (!xf) return hipErrorInvalidValue;
-        return launch_sk_t<F, 1, 3, 0xFF, float>(fmt, w, m, xf, nullptr, nullptr, 0, y, part, tick, S, s);
+        return launch_sk_t<F, 1, 3, 0xFF, float>(fmt, w, m, xf, nullptr, nullptr, 0, y, part, S, s);
     }
     if (parts == 2) {
         if (m > 64) return hipErrorInvalidValue;
-        if (m <= 16) return launch_sk_t<F, 1, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
-        if (m <= 32) return launch_sk_t<F, 2, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
-        return launch_sk_t<F, 4, 2>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+        if (m <= 16) return launch_sk_t<F, 1, 2>(fmt, w, m, x, xs, rs, rss, y, part, S, s);
+        if (m <= 32) return launch_sk_t<F, 2, 2>(fmt, w, m, x, xs, rs, rss, y, part, S, s);
+        return launch_sk_t<F, 4, 2>(fmt, w, m, x, xs, rs, rss, y, part, S, s);
     }
-    return m <= 32 ? launch_sk_t<F, 1, 1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s)
-                   : launch_sk_t<F, 2, 1>(fmt, w, m, x, xs, rs, rss, y, part, tick, S, s);
+    return m <= 32 ? launch_sk_t<F, 1, 1>(fmt, w, m, x, xs, rs, rss, y, part, S, s)
+                   : launch_sk_t<F, 2, 1>(fmt, w, m, x, xs, rs, rss, y, part, S, s);
 }
 
 SkQ4K sk_q4k(const arfq_weight *w) {
@@ -599,7 +589,7 @@ static hipError_t launch_bd(const arfq_weight *w, int e, int64_t m, const _Float
 }
 
 hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
-                       float *y, void *scratch, uint32_t *tickets, int ntickets,
+                       float *y, void *scratch,
                        const GemmPlan &p, hipStream_t s) {
     char *sc = (char *)scratch;
     if (p.scratch_bytes && !sc) return hipErrorInvalidValue;
@@ -621,22 +611,22 @@ hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, in
         const int64_t eb = (int64_t)e * w->n * (w->k / 256);
         switch (w->qtype) {
         case ARFQ_Q4_K:
-            return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
+            return launch_sk(sk_q4k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out,
                              p.splits, s, p.parts, xf);
         case ARFQ_Q6_K:  // scales within +-62 (the upload's flag): integer operands sc * (q - 32) / 2
             if (!w->over62)
-                return launch_sk(SkQ6KI{sk_q6k(w)}.shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets,
-                                 ntickets, p.splits, s, p.parts, xf);
-            return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
+                return launch_sk(SkQ6KI{sk_q6k(w)}.shifted(eb), w, m, xk, xs, rs, (int)m, y, out, p.splits, s,
+                                 p.parts, xf);
+            return launch_sk(sk_q6k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out,
                              p.splits, s, p.parts, xf);
         case ARFQ_Q8_0:
             return launch_sk(sk_q80(w).shifted((int64_t)e * w->n * (w->k / 32)), w, m, xk, xs, rs,
-                             (int)m, y, out, tickets, ntickets, p.splits, s, p.parts, xf);
+                             (int)m, y, out, p.splits, s, p.parts, xf);
         case ARFQ_Q5_K:
-            return launch_sk(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
+            return launch_sk(sk_q5k(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out,
                              p.splits, s, p.parts, xf);
         case ARFQ_IQ4_XS:
-            return launch_sk(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out, tickets, ntickets,
+            return launch_sk(sk_iq4xs(w).shifted(eb), w, m, xk, xs, rs, (int)m, y, out,
                              p.splits, s, p.parts, xf);
         default:
             return hipErrorInvalidValue;

@@ -121,16 +121,12 @@ int arfq_ctx_create(int device, void *stream, arfq_ctx **out) {
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_start);
     if (e == hipSuccess) e = hipEventCreate(&ctx->ev_stop);
     if (e == hipSuccess) {
-        // the split-K counters, then STREAM_SINK_WORDS words of arfq_stream_read's
-        // sink, then the upload's flag words
-        ctx->ntickets = std::max(1024, 2 * ctx->cus);
-        e = hipMalloc(&ctx->tickets, ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS + arfq::UPLOAD_FLAG_WORDS) *
-                                         sizeof(uint32_t));
+        // STREAM_SINK_WORDS words of arfq_stream_read's sink, then the upload's
+        // flag words
+        e = hipMalloc(&ctx->aux, ((size_t)arfq::STREAM_SINK_WORDS + arfq::UPLOAD_FLAG_WORDS) * sizeof(uint32_t));
     }
     if (e == hipSuccess)
-        e = hipMemsetAsync(ctx->tickets, 0,
-                           ((size_t)ctx->ntickets + arfq::STREAM_SINK_WORDS + arfq::UPLOAD_FLAG_WORDS) *
-                               sizeof(uint32_t),
+        e = hipMemsetAsync(ctx->aux, 0, ((size_t)arfq::STREAM_SINK_WORDS + arfq::UPLOAD_FLAG_WORDS) * sizeof(uint32_t),
                            ctx->stream);
     if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
     if (e != hipSuccess) {
@@ -148,7 +144,7 @@ int arfq_ctx_destroy(arfq_ctx *ctx) {
     if (ctx->stream && ctx->scratch) (void)hipFreeAsync(ctx->scratch, ctx->stream);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->staging) (void)hipFree(ctx->staging);
-    if (ctx->tickets) (void)hipFree(ctx->tickets);
+    if (ctx->aux) (void)hipFree(ctx->aux);
     if (ctx->ev_start) (void)hipEventDestroy(ctx->ev_start);
     if (ctx->ev_stop) (void)hipEventDestroy(ctx->ev_stop);
     if (ctx->own_stream && ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -235,7 +231,7 @@ static int weight_create(arfq_ctx *ctx, int qtype, size_t nbytes, int64_t n_rows
 // first); read back once the repacks are done, they select the prefill GEMM's
 // two-operand weights and the skinny kernel's operand form.
 static uint32_t *upload_flag(arfq_ctx *ctx, const arfq_weight *w) {
-    return w->qtype == ARFQ_Q6_K && ctx->tickets ? ctx->tickets + ctx->ntickets + arfq::STREAM_SINK_WORDS : nullptr;
+    return w->qtype == ARFQ_Q6_K && ctx->aux ? ctx->aux + arfq::STREAM_SINK_WORDS : nullptr;
 }
 static hipError_t upload_flag_clear(arfq_ctx *ctx, uint32_t *flag) {
     return flag ? hipMemsetAsync(flag, 0, 2 * sizeof(uint32_t), ctx->stream) : hipSuccess;
@@ -369,8 +365,7 @@ static int matmul_enqueue(arfq_ctx *ctx, const arfq_weight *w, int expert, int64
     } else if (arfq::gemm_supports(w, m)) {
         const arfq::GemmPlan plan = arfq::gemm_plan(w, m, x_dtype, x16);
         if (int rc = ensure_scratch(ctx, plan.scratch_bytes)) return rc;
-        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->scratch, ctx->tickets,
-                              ctx->ntickets, plan, ctx->stream);
+        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->scratch, plan, ctx->stream);
     } else {
         return fail(ctx, ARFQ_E_UNSUPPORTED,
                     "matmul: no kernel for qtype " + std::to_string(w->qtype) + " at m=" +
@@ -405,10 +400,8 @@ int arfq_matmul_noalloc(arfq_ctx *ctx, const arfq_weight *w, int expert, int64_t
                             " bytes of scratch, above the " + std::to_string(ARFQ_NOALLOC_SCRATCH_BYTES) +
                             "-byte limit (use arfq_matmul)");
         // every scratch byte a plan reads is written earlier in the same call
-        // (x preparation, then split-K partials before their counter moves); the
-        // split-K counters are the context's, zero between calls
-        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->noalloc_scratch, ctx->tickets,
-                              ctx->ntickets, plan, ctx->stream);
+        // (x preparation, then the split-K partials before the launch that adds them)
+        e = arfq::launch_gemm(w, expert, m, x, x_dtype, y, ctx->noalloc_scratch, plan, ctx->stream);
     } else {
         return fail(ctx, ARFQ_E_UNSUPPORTED,
                     "matmul_noalloc: no kernel for qtype " + std::to_string(w->qtype) + " at m=" +
@@ -794,14 +787,13 @@ int arfq_stream_read(arfq_ctx *ctx, const void *src, size_t bytes, uint64_t *sta
     if (nstamps < 0 || (nstamps > 0 && !stamps)) return fail(ctx, ARFQ_E_INVALID, "stream_read: bad stamps");
     if (int rc = use_device(ctx)) return rc;
     if (bytes == 0) return ARFQ_OK;
-    // the sink (a word per thread of a workgroup) sits past the split-K counters
-    // in the same allocation; nothing reads it
-    if (!ctx->tickets) return fail(ctx, ARFQ_E_DEVICE, "stream_read: no sink");
+    // the sink (a word per thread of a workgroup) is the start of the context's
+    // aux words; nothing reads it
+    if (!ctx->aux) return fail(ctx, ARFQ_E_DEVICE, "stream_read: no sink");
     const int64_t n = (int64_t)(bytes / 16);
     // eight 256-thread workgroups per CU (fewer for a short stream: a load per lane at least)
     const unsigned grid = (unsigned)std::min<int64_t>((n + 255) / 256, (int64_t)std::max(ctx->cus, 1) * 8);
-    read_stream_kernel<<<grid, 256, 0, ctx->stream>>>((const uint4 *)src, n, ctx->tickets + ctx->ntickets,
-                                                       stamps, nstamps);
+    read_stream_kernel<<<grid, 256, 0, ctx->stream>>>((const uint4 *)src, n, ctx->aux, stamps, nstamps);
     HIP_TRY(ctx, hipGetLastError());
     return ARFQ_OK;
 }

@@ -27,10 +27,9 @@ struct arfq_ctx {
     size_t staging_bytes = 0;
     // device address of the allocation-free matmul's fixed scratch on this device
     void *noalloc_scratch = nullptr;
-    // split-K arrival counters, one per column tile: zero between launches (the
-    // last workgroup of a tile to arrive resets its counter)
-    uint32_t *tickets = nullptr;
-    int ntickets = 0;
+    // device words: arfq_stream_read's sink (STREAM_SINK_WORDS), then the
+    // upload's flag words (UPLOAD_FLAG_WORDS)
+    uint32_t *aux = nullptr;
 };
 
 struct arfq_weight {
@@ -50,8 +49,8 @@ struct arfq_weight {
 
 namespace arfq {
 
-// words past the split-K counters (arfq_ctx::tickets) that arfq_stream_read's
-// kernel may store to (one per thread of a 256-thread workgroup)
+// words of arfq_ctx::aux that arfq_stream_read's kernel may store to (one per
+// thread of a 256-thread workgroup)
 constexpr int STREAM_SINK_WORDS = 256;
 // words past the sink: the upload's flag (a Q6_K scale outside [-64, 64] seen by the repack)
 constexpr int UPLOAD_FLAG_WORDS = 64;
@@ -145,10 +144,9 @@ struct GemmPlan {
 // x16: ARFQ_OPT_GEMV_X16 is set (the skinny and prefill kernels take an f32 x as one f16 part)
 GemmPlan gemm_plan(const arfq_weight *w, int64_t m, int x_dtype, bool x16 = false);
 bool gemm_supports(const arfq_weight *w, int64_t m);
-// y[m, n] = x[m, k] . W_e^T; `scratch` holds plan.scratch_bytes; `tickets`
-// holds ntickets zeroed split-K counters (left zeroed).
+// y[m, n] = x[m, k] . W_e^T; `scratch` holds plan.scratch_bytes.
 hipError_t launch_gemm(const arfq_weight *w, int e, int64_t m, const void *x, int x_dtype,
-                       float *y, void *scratch, uint32_t *tickets, int ntickets,
+                       float *y, void *scratch,
                        const GemmPlan &p, hipStream_t s);
 // Activation preparation: x (f32 or f16, [m, k]) -> f16 copy (xh), f16
 // remainder (xl), bf16 sub-block sums (xs, [m][k / 256][16]); null outputs are

@@ -548,11 +548,11 @@ def test_gemm_q4k_prefill_split_tail(gpu_ctx, oracle, m, n, k, xdt):
     assert rel_err(outs[0][rows], oracle.matmul_q("q4_k", x[rows].astype(np.float32), raw, n)) <= TOL
 
 
-def test_skinny_split_counters_reset(gpu_ctx, oracle):
-    # skinny products split over K sum their partials in the kernel, the last
-    # workgroup of each column tile resetting that tile's arrival counter:
-    # interleaved shapes (split counts 16, 3 and 8; column counts a multiple of
-    # 4 and not) give the oracle's result, and the same bits, on every repeat
+def test_skinny_split_k_repeats(gpu_ctx, oracle):
+    # skinny products split over K store their partials and a second launch adds
+    # each output's splits in split order: interleaved shapes (split counts 16, 3
+    # and 8; column counts a multiple of 4 and not) give the oracle's result, and
+    # the same bits, on every repeat
     from arf_amd import QType, synth
     cases = [("q6_k", 512, 8192, 8), ("q6_k", 130, 1792, 16), ("q8_0", 1000, 4096, 24)]
     runs = []
