@@ -455,6 +455,151 @@ __global__ __launch_bounds__(SK_THREADS, 2) void moe_down_kernel(
         }
 }
 
+// down, x-stationary, where a tile's h16 rows over all of K fit in LDS beside
+// eight weight slabs (C5: K = 768, 142 KB): workgroup = one tile x DXS_COLS
+// columns of hidden, 8 waves.  The tile's rows and their sub-block sums are
+// staged once; then each wave streams its own weight rows -- passes of
+// 8 x 32 rows, each over every K block, the next block's weights in flight --
+// with no barrier in the loop (the slabs are wave-private and x does not
+// change).  Per pass the wave stores its 32 columns of the tile's rows to
+// o[pair index], times the row's h scale.  Against the tile x 128-column
+// workgroups above: one x staging and one pipeline start per 1024 columns
+// instead of per 128, and no per-block barrier.
+constexpr int DXS_THREADS = 512;
+constexpr size_t MOE_DXS_LDS_MAX = 160 * 1024;
+constexpr int DXS_COLS = 1024;  // columns per workgroup: passes of 8 waves x 32 rows
+template <class F>
+__host__ __device__ constexpr size_t dxs_lds(int K) {
+    return (size_t)MOE_BM * (K + 8) * 2                          // h16 rows [64][K + 8]
+           + (size_t)MOE_BM * (K / 256) * 32                     // their sums [64][K / 256][16]
+           + (size_t)MOE_BM * 8                                  // pair index, h scale per row
+           + (size_t)(DXS_THREADS / 64) * 32 * (F::RB + 16);     // one weight slab per wave
+}
+template <class F>
+__global__ __launch_bounds__(DXS_THREADS, 1) void moe_down_xs_kernel(
+    F down, int64_t expert_blocks, const _Float16 *__restrict__ h, const uint16_t *__restrict__ hs,
+    const float *__restrict__ rs, int K, int hidden, const int32_t *__restrict__ off,
+    const int32_t *__restrict__ sorted, const int2 *__restrict__ tiles, const int32_t *__restrict__ ntiles,
+    float *__restrict__ o) {
+    constexpr int KIND = F::KIND;
+    constexpr int RL = F::RB / 16, NI = 32 * F::RB / 1024, SL = F::RB + 16;
+    extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+    const int ncb = (hidden + DXS_COLS - 1) / DXS_COLS;
+    const int ti = (int)blockIdx.x / ncb;
+    if (ti >= *ntiles) return;  // uniform over the workgroup
+    const int tid = sk_tid(), lane = tid & 63, wave = tid >> 6, lr = lane & 31;
+    const int2 tile = tiles[ti];
+    const int e = tile.x, row0 = tile.y;
+    const int rows = min(MOE_BM, off[e + 1] - row0);
+    const int c0 = ((int)blockIdx.x - ti * ncb) * DXS_COLS;
+    const int nb = K / 256, xld = K + 8;
+    _Float16 *xs_l = lds;                                                        // [64][xld]
+    uint16_t *ss_l = reinterpret_cast<uint16_t *>(lds + MOE_BM * xld);           // [64][nb][16]
+    int *lrow = reinterpret_cast<int *>(ss_l + MOE_BM * nb * 16);               // [64]
+    float *lrs = reinterpret_cast<float *>(lrow + MOE_BM);                       // [64]
+    uint8_t *slab = reinterpret_cast<uint8_t *>(lrs + MOE_BM) + (size_t)wave * 32 * SL;
+    // the tile's rows (rows past the tile repeat its last: their products land
+    // in rows never stored), 16 bytes a thread at a time
+    const int kc8 = K / 8;
+    for (int c = tid; c < MOE_BM * kc8; c += DXS_THREADS) {
+        const int r = c / kc8, kc = c - r * kc8;
+        *reinterpret_cast<u32x4 *>(xs_l + r * xld + 8 * kc) =
+            *reinterpret_cast<const u32x4 *>(h + (int64_t)(row0 + min(r, rows - 1)) * K + 8 * kc);
+    }
+    if constexpr (KIND == 2) {
+        const int sc8 = nb * 2;  // 16-byte pieces of a row's sums
+        for (int c = tid; c < MOE_BM * sc8; c += DXS_THREADS) {
+            const int r = c / sc8, j = c - r * sc8;
+            *reinterpret_cast<u32x4 *>(ss_l + r * nb * 16 + 8 * j) =
+                *reinterpret_cast<const u32x4 *>(hs + (int64_t)(row0 + min(r, rows - 1)) * (K / 16) + 8 * j);
+        }
+    }
+    if (tid < MOE_BM) {
+        lrow[tid] = tid < rows ? sorted[row0 + tid] : 0;
+        lrs[tid] = tid < rows ? rs[row0 + tid] : 0.f;
+    }
+    __syncthreads();
+
+    const F fm = down.shifted((int64_t)e * expert_blocks);
+    const int npass = min(DXS_COLS, hidden - c0 + 255) / 256;  // passes with a column < hidden
+    const int S = npass * nb;  // steps (pass, block)
+    auto wrow_of = [&](int st) { return c0 + 256 * (st / nb) + 32 * wave; };
+    // two steps of weights in flight: register set j holds the steps st with
+    // st % 2 == j, wbs[j] their scales
+    u32x4 rv[2][NI];
+    typename F::Blk wbs[2][1], wbn[1];
+    auto wload = [&](u32x4 (&r)[NI], int st) {
+        const int wr = wrow_of(st), b = st % nb;
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int c = 64 * i + lane;
+            const int64_t row = min(wr + c / RL, hidden - 1);
+            r[i] = *reinterpret_cast<const u32x4 *>(fm.raw(row, b) + 16 * (c % RL));
+        }
+    };
+    auto wstore = [&](const u32x4 (&r)[NI]) {
+#pragma unroll
+        for (int i = 0; i < NI; i++) {
+            const int c = 64 * i + lane;
+            *reinterpret_cast<u32x4 *>(slab + (c / RL) * SL + 16 * (c % RL)) = r[i];
+        }
+    };
+    auto loop = [&](auto tu) {
+        constexpr int TU = decltype(tu)::value;
+        floatx16 acc[1][2], cb[1][2], cmin[1][KIND == 2 ? 2 : 1], cq[1][KIND == 3 ? 2 : 1];
+        auto zero = [&]() {
+#pragma unroll
+            for (int t = 0; t < 2; t++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) {
+                    acc[0][t][i] = 0.f;
+                    if constexpr (KIND == 2) cmin[0][t][i] = 0.f;
+                }
+        };
+        zero();
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int sj = min(j, S - 1);
+            wbs[j][0] = fm.load_blk(min(wrow_of(sj) + lr, hidden - 1), sj % nb);
+            wload(rv[j], sj);
+        }
+        auto step = [&](u32x4 (&r)[NI], typename F::Blk (&wb)[1], int st) {
+            const int b = st % nb, sn = min(st + 2, S - 1);  // past the end: a re-read of the last step
+            wstore(r);
+            wbn[0] = fm.load_blk(min(wrow_of(sn) + lr, hidden - 1), sn % nb);
+            __builtin_amdgcn_sched_barrier(0);
+            wload(r, sn);
+            __builtin_amdgcn_sched_barrier(0);
+            sk_block<F, 2, TU, 1, 0xFF, false, false>(
+                slab, wb, [&](int t) { return xs_l + (32 * t + lr) * xld + 256 * b; },
+                [&](int t) { return ss_l + ((32 * t + lr) * nb + b) * 16; }, lr, lane >> 5, acc, cb, cmin, cq);
+            wb[0] = wbn[0];
+            if (b == nb - 1) {
+                // the pass's 32 columns of every tile row
+                const int n = wrow_of(st) + lr;
+#pragma unroll
+                for (int t = 0; t < TU; t++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) {
+                        const int r = sk_out_row(t, i);
+                        float v = acc[0][t][i];
+                        if constexpr (KIND == 2) v += cmin[0][t][i];
+                        if (r < rows && n < hidden) o[(int64_t)lrow[r] * hidden + n] = v * lrs[r];
+                    }
+                zero();
+            }
+        };
+        for (int st = 0; st < S; st += 2) {
+            step(rv[0], wbs[0], st);
+            if (st + 1 < S) step(rv[1], wbs[1], st + 1);
+        }
+    };
+    if (rows <= 32)
+        loop(std::integral_constant<int, 1>{});
+    else
+        loop(std::integral_constant<int, 2>{});
+}
+
 // ---- combine -------------------------------------------------------------------
 // y[t, c] = ((0 + w0*o0) + w1*o1) + ... over the token's slots in order, each
 // product and sum rounded separately (the reference's out[t] += w_j * y_j).
@@ -574,6 +719,17 @@ static hipError_t down_t(const F &d, const arfq_weight *dw, const _Float16 *h, c
                          const float *rs, const int32_t *off, const int32_t *sorted,
                          const void *tiles, const int32_t *ntiles, int64_t max_tiles, float *o,
                          hipStream_t s) {
+    const size_t xlds = dxs_lds<F>((int)dw->k);
+    if (xlds <= MOE_DXS_LDS_MAX) {  // the tile's rows fit beside the slabs: x-stationary
+        static std::atomic<uint64_t> lds_set{0};
+        if (hipError_t err = set_max_lds_once((const void *)moe_down_xs_kernel<F>, MOE_DXS_LDS_MAX, lds_set))
+            return err;
+        const int64_t eb = dw->n * d.nblk;
+        const unsigned grid = (unsigned)(max_tiles * ((dw->n + DXS_COLS - 1) / DXS_COLS));
+        moe_down_xs_kernel<F><<<grid, DXS_THREADS, xlds, s>>>(d, eb, h, hs, rs, (int)dw->k, (int)dw->n, off,
+                                                             sorted, (const int2 *)tiles, ntiles, o);
+        return hipGetLastError();
+    }
     constexpr size_t lds = sk_lds<F, 2, 1>();
     static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
     if (hipError_t err = set_max_lds_once((const void *)moe_down_kernel<F>, lds, lds_set)) return err;

@@ -419,6 +419,107 @@ constexpr size_t sk_lds() {
     return (size_t)XB * (32 * TA * SK_XLD * 2 + 32 * TA * 32) + (size_t)(NT / 64) * NW * 32 * (F::RB + 16);
 }
 
+// The MFMAs of one 256-element block: the wave's NW x 32 weight rows (slab
+// rows 32 w + lr, scales wbk; lr = lane % 32, h = lane / 32, as the caller
+// has them) against the x tiles t < TU, whose row 32 t + lr of this block
+// starts at xrow(t) (LDS, the k order of
+// F::a_off) and, for KIND 2, whose sub-block sums (bf16 hi[8] | lo[8]) start
+// at srow(t); then the block end of KIND 1 / 2 (acc += d * cb, the min term
+// into cmin).  cb and cq are the block's own accumulators.  (GM, MERGE, PIN:
+// as skinny_loop.)
+template <class F, int TA, int TU, int NW, int GM, bool MERGE, bool PIN, class XRow, class SRow>
+__device__ __forceinline__ void sk_block(const uint8_t *slab, const typename F::Blk (&wbk)[NW], XRow xrow,
+                                         SRow srow, int lr, int h, floatx16 (&acc)[NW][TA], floatx16 (&cb)[NW][TA],
+                                         floatx16 (&cmin)[NW][F::KIND == 2 ? TA : 1],
+                                         floatx16 (&cq)[NW][F::KIND == 3 ? TA : 1]) {
+    constexpr int KIND = F::KIND;
+    constexpr int TO = MERGE ? TU / 2 : TU;  // accumulator tiles written
+    constexpr int SL = F::RB + 16;           // slab row stride (bytes)
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        if constexpr (PIN && TO == 2) __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            half8 bf[4];
+            F::frag(slab + (w * 32 + lr) * SL, wbk[w], p, h, bf);
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                if constexpr (KIND == 4) {
+                    // one sub-block per MFMA (both x tiles with MERGE), times its d * sc
+                    floatx16 c[TO], z;
+#pragma unroll
+                    for (int i = 0; i < 16; i++) z[i] = 0.f;
+#pragma unroll
+                    for (int t = 0; t < TU; t++) {
+                        const half8 af = *reinterpret_cast<const half8 *>(xrow(t) + F::a_off(p, kk, h));
+                        const int ti = MERGE ? t % TO : t;
+                        c[ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], MERGE && t >= TO ? c[ti] : z,
+                                                                       0, 0, 0);
+                    }
+                    const float ss = F::sub_scale(wbk[w], p, kk);
+#pragma unroll
+                    for (int ti = 0; ti < TO; ti++)
+#pragma unroll
+                        for (int i = 0; i < 16; i++)
+                            if ((GM >> (4 * ti + (i >> 2))) & 1) acc[w][ti][i] = fmaf(ss, c[ti][i], acc[w][ti][i]);
+                } else {
+#pragma unroll
+                    for (int t = 0; t < TU; t++) {
+                        const half8 af = *reinterpret_cast<const half8 *>(xrow(t) + F::a_off(p, kk, h));
+                        const int ti = MERGE ? t % TO : t;
+                        const bool cont = MERGE && t >= TO;  // a lo tile adds onto its hi tile's chain
+                        floatx16 z;
+#pragma unroll
+                        for (int i = 0; i < 16; i++) z[i] = 0.f;
+                        if constexpr (KIND == 3) {
+                            floatx16 &c = kk < 2 ? cb[w][ti] : cq[w][ti];
+                            c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], kk % 2 == 0 && !cont ? z : c,
+                                                                       0, 0, 0);
+                        } else if constexpr (KIND != 0) {
+                            cb[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                                af, bf[kk], p == 0 && kk == 0 && !cont ? z : cb[w][ti], 0, 0, 0);
+                        } else {
+                            acc[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], acc[w][ti], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+            if constexpr (KIND == 3) {
+                // the step's two sub-blocks, each times its own d * (ls - 32)
+                const float2 ss = F::sub_scales(wbk[w], p);
+#pragma unroll
+                for (int ti = 0; ti < TO; ti++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++)
+                        acc[w][ti][i] = fmaf(ss.y, cq[w][ti][i], fmaf(ss.x, cb[w][ti][i], acc[w][ti][i]));
+            }
+        }
+    }
+    if constexpr (KIND == 1 || KIND == 2) {
+        // block end: acc += d * C_block; the min term (two bf16 MFMAs)
+        // accumulates across blocks in its own registers
+#pragma unroll
+        for (int w = 0; w < NW; w++) {
+            const float2 dd = F::scale(wbk[w]);
+            if constexpr (KIND == 2) {
+                bf16x8 bh, bl;
+                F::minsb(wbk[w], bh, bl);
+#pragma unroll
+                for (int t = 0; t < TU; t++) {
+                    const bf16x8 am = *reinterpret_cast<const bf16x8 *>(srow(t) + 8 * h);
+                    const int ti = MERGE ? t % TO : t;
+                    cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][ti], 0, 0, 0);
+                    cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][ti], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int ti = 0; ti < TO; ti++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[w][ti][i] = fmaf(dd.x, cb[w][ti][i], acc[w][ti][i]);
+        }
+    }
+}
+
 // Accumulates acc[w][t] (w < NW weights, t < TA 32-row x tiles) over the
 // 256-element blocks [b0, b1) for the wave's 32 weight rows wrow0[w] ..
 // wrow0[w] + 31 (rows past nrows are clamped: computed, never to be stored).
@@ -626,91 +727,9 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
         // keep the scheduler from sinking the loads: they must be in flight
         // during this block, not issued at its end
         __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            if constexpr (PIN && TO == 2) __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int w = 0; w < NW; w++) {
-                half8 bf[4];
-                F::frag(slab + (w * 32 + lr) * SL, wb[w], p, h, bf);
-#pragma unroll
-                for (int kk = 0; kk < 4; kk++) {
-                    if constexpr (KIND == 4) {
-                        // one sub-block per MFMA (both x tiles with MERGE), times its d * sc
-                        floatx16 c[TO], z;
-#pragma unroll
-                        for (int i = 0; i < 16; i++) z[i] = 0.f;
-#pragma unroll
-                        for (int t = 0; t < TU; t++) {
-                            const half8 af = *reinterpret_cast<const half8 *>(
-                                xl + (xb * XR + 32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
-                            const int ti = MERGE ? t % TO : t;
-                            c[ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], MERGE && t >= TO ? c[ti] : z,
-                                                                           0, 0, 0);
-                        }
-                        const float ss = F::sub_scale(wb[w], p, kk);
-#pragma unroll
-                        for (int ti = 0; ti < TO; ti++)
-#pragma unroll
-                            for (int i = 0; i < 16; i++)
-                                if ((GM >> (4 * ti + (i >> 2))) & 1) acc[w][ti][i] = fmaf(ss, c[ti][i], acc[w][ti][i]);
-                    } else {
-#pragma unroll
-                        for (int t = 0; t < TU; t++) {
-                            const half8 af = *reinterpret_cast<const half8 *>(
-                                xl + (xb * XR + 32 * t + lr) * SK_XLD + F::a_off(p, kk, h));
-                            const int ti = MERGE ? t % TO : t;
-                            const bool cont = MERGE && t >= TO;  // a lo tile adds onto its hi tile's chain
-                            floatx16 z;
-#pragma unroll
-                            for (int i = 0; i < 16; i++) z[i] = 0.f;
-                            if constexpr (KIND == 3) {
-                                floatx16 &c = kk < 2 ? cb[w][ti] : cq[w][ti];
-                                c = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], kk % 2 == 0 && !cont ? z : c,
-                                                                           0, 0, 0);
-                            } else if constexpr (KIND != 0) {
-                                cb[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                                    af, bf[kk], p == 0 && kk == 0 && !cont ? z : cb[w][ti], 0, 0, 0);
-                            } else {
-                                acc[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af, bf[kk], acc[w][ti], 0, 0, 0);
-                            }
-                        }
-                    }
-                }
-                if constexpr (KIND == 3) {
-                    // the step's two sub-blocks, each times its own d * (ls - 32)
-                    const float2 ss = F::sub_scales(wb[w], p);
-#pragma unroll
-                    for (int ti = 0; ti < TO; ti++)
-#pragma unroll
-                        for (int i = 0; i < 16; i++)
-                            acc[w][ti][i] = fmaf(ss.y, cq[w][ti][i], fmaf(ss.x, cb[w][ti][i], acc[w][ti][i]));
-                }
-            }
-        }
-        if constexpr (KIND == 1 || KIND == 2) {
-            // block end: acc += d * C_block; the min term (two bf16 MFMAs)
-            // accumulates across blocks in its own registers
-#pragma unroll
-            for (int w = 0; w < NW; w++) {
-                const float2 dd = F::scale(wb[w]);
-                if constexpr (KIND == 2) {
-                    bf16x8 bh, bl;
-                    F::minsb(wb[w], bh, bl);
-#pragma unroll
-                    for (int t = 0; t < TU; t++) {
-                        const bf16x8 am = *reinterpret_cast<const bf16x8 *>(sl + (xb * XR + 32 * t + lr) * 16 + 8 * h);
-                        const int ti = MERGE ? t % TO : t;
-                        cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][ti], 0, 0, 0);
-                        cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][ti], 0, 0, 0);
-                    }
-                }
-#pragma unroll
-                for (int ti = 0; ti < TO; ti++)
-#pragma unroll
-                    for (int i = 0; i < 16; i++) acc[w][ti][i] = fmaf(dd.x, cb[w][ti][i], acc[w][ti][i]);
-            }
-        }
+        sk_block<F, TA, TU, NW, GM, MERGE, PIN>(
+            slab, wb, [&](int t) { return xl + (xb * XR + 32 * t + lr) * SK_XLD; },
+            [&](int t) { return sl + (xb * XR + 32 * t + lr) * 16; }, lr, h, acc, cb, cmin, cq);
 #pragma unroll
         for (int w = 0; w < NW; w++) wb[w] = wbn[w];
         if constexpr (XB == 2) {
