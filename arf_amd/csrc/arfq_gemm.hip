@@ -115,8 +115,19 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     constexpr int NT = sk_nt(TA), CT = NT / 2;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * CT;
-    const int nb = K / 256, S = gridDim.y, sp = blockIdx.y;
+    // (column tile, split) of this workgroup.  With four x tiles the
+    // dispatcher's placement of workgroup L (x fastest) on XCD L % 8 is used:
+    // XCD x takes items [x per, (x + 1) per) of the split-major order, a
+    // contiguous run of splits whose x ranges then stay in its L2 (C3 m = 64:
+    // x as 128 f16 rows is 4.5 MB, more than an L2; 52.1 -> 50.3 us); the last
+    // total % 8 items go in order.  With one or two tiles (x within an L2)
+    // that order measured slower (C3 m = 8: 27.7 -> 28.4 us).
+    const int nt = gridDim.x, total = nt * gridDim.y, per = total >> 3;
+    const int L = blockIdx.y * nt + blockIdx.x;
+    const int q = TA == 4 && L < 8 * per ? (L & 7) * per + (L >> 3) : L;
+    const int tile = q % nt;
+    const int n0 = tile * CT;
+    const int nb = K / 256, S = gridDim.y, sp = q / nt;
     const int b0 = (int)((int64_t)sp * nb / S), b1 = (int)((int64_t)(sp + 1) * nb / S);
     // PARTS 2 (M <= 16 TA): x row r < M stages hi row r of x, row PO + r its lo
     // row M + r (PO = 16 in one 32-row tile, 32 = the second tile with two, 64 =
@@ -197,8 +208,8 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
     // 32 t + 8 g + 4 (lane / 32) + 0..3 of column n, for the GT 8-row groups
     // that hold rows < M; sk_reduce_kernel adds the splits (in split order)
     // after this launch.
-    const int GT = (M + 7) >> 3, nt = gridDim.x;
-    float4 *pw = reinterpret_cast<float4 *>(part) + ((((int64_t)sp * nt + blockIdx.x) * (NT / 64) + wave) * GT) * 64 + lane;
+    const int GT = (M + 7) >> 3;
+    float4 *pw = reinterpret_cast<float4 *>(part) + ((((int64_t)sp * nt + tile) * (NT / 64) + wave) * GT) * 64 + lane;
 #pragma unroll
     for (int t = 0; t < TA; t++)
 #pragma unroll
