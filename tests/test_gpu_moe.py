@@ -125,10 +125,11 @@ def test_moe_decode_small_T_at_c5_experts(gpu_ctx, oracle, T):
 
 @pytest.mark.parametrize("T,E,k,hidden,inter", [(5, 8, 2, 256, 256), (70, 16, 4, 512, 768),
                                                 (1, 4, 4, 256, 512), (129, 6, 2, 768, 256),
-                                                (70, 16, 4, 512, 256)])
+                                                (70, 16, 4, 512, 256), (70, 8, 4, 256, 1024)])
 def test_moe_block_small(gpu_ctx, oracle, T, E, k, hidden, inter):
     # synthetic Q4_K experts give |silu(g) * u| up to ~1e5 at hidden >= 512: the
-    # intermediate must not overflow f16 on the way to the down projection
+    # intermediate must not overflow f16 on the way to the down projection.  inter = 1024
+    # is past the x-stationary down kernel's LDS (the tile x 128-column kernel runs)
     from arf_amd import synth
     _say("case: moe block", T, E, k, hidden, inter)
     raw, ws = _weights(gpu_ctx, E, hidden, inter, seed=T + E + k)
