@@ -162,7 +162,7 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // PAIR with two or four tiles: the lo tiles' products go into the hi tiles' accumulators
     int xsh = 0;
-    skinny_run<F, TA, 1, NT, XT, false, GM, PAIR && TA >= 2, true, SK_XB(TA), FX ? 3 : 0>(
+    skinny_run<F, TA, 1, NT, XT, false, GM, PAIR && TA >= 2, true, SK_XB(TA), FX ? 3 : 0, FX>(
         fm, wrow0, N, rows, x, xs, b0, b1, acc, lds, PARTS == 3 ? 16 + M : PAIR ? PO + M : M, xsh);
     if constexpr (FX) {
         // the rows' scales over this K range (row tid / 32 from its lanes' xsh)

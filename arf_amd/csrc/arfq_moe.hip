@@ -274,7 +274,7 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
         for (int t = 0; t < 2; t++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
-        skinny_run<F, 2, 1, MOE_GU_THREADS, _Float16, true, 0xFF, false, false, MOE_GU_XB>(
+        skinny_run<F, 2, 1, MOE_GU_THREADS, _Float16, true, 0xFF, false, false, MOE_GU_XB, 0, true>(
             fm, wrow0, inter, xr, x, xs, 0, K / 256, acc, lds, rows);
         // the loop ends with a barrier after its last LDS use: hand up to gate
         float *ex = reinterpret_cast<float *>(lds);  // [4 waves][2 tiles][16][64 lanes]
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(SK_THREADS, 2) void moe_down_kernel(
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
     // (Q6_K: the second loop copy would not fit the registers)
-    skinny_run<F, 2, 1, SK_THREADS, _Float16, F::KIND != 4>(fm, wrow0, hidden, xr, h, hs, 0, K / 256,
+    skinny_run<F, 2, 1, SK_THREADS, _Float16, F::KIND != 4, 0xFF, false, false, 1, 0, true>(fm, wrow0, hidden, xr, h, hs, 0, K / 256,
                                                            acc, lds, rows);
     // the loop ends with a barrier after its last LDS use
     int *lrow = reinterpret_cast<int *>(lds);                // [64]
@@ -525,7 +525,9 @@ __global__ __launch_bounds__(DXS_THREADS, 1) void moe_down_xs_kernel(
     const int S = npass * nb;  // steps (pass, block)
     auto wrow_of = [&](int st) { return c0 + 256 * (st / nb) + 32 * wave; };
     // two steps of weights in flight: register set j holds the steps st with
-    // st % 2 == j, wbs[j] their scales
+    // st % 2 == j, wbs[j] their scales.  The weight loads are non-temporal
+    // (each byte is used once): the L2 keeps the staged rows' sources and
+    // the gate|up outputs instead
     u32x4 rv[2][NI];
     typename F::Blk wbs[2][1], wbn[1];
     auto wload = [&](u32x4 (&r)[NI], int st) {
@@ -534,7 +536,7 @@ __global__ __launch_bounds__(DXS_THREADS, 1) void moe_down_xs_kernel(
         for (int i = 0; i < NI; i++) {
             const int c = 64 * i + lane;
             const int64_t row = min(wr + c / RL, hidden - 1);
-            r[i] = *reinterpret_cast<const u32x4 *>(fm.raw(row, b) + 16 * (c % RL));
+            r[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(fm.raw(row, b) + 16 * (c % RL)));
         }
     };
     auto wstore = [&](const u32x4 (&r)[NI]) {

@@ -544,9 +544,9 @@ __device__ __forceinline__ void sk_block(const uint8_t *slab, const typename F::
 // sub-block sums (its lanes' 8 in order, then the quad's (s0 + s1) + (s2 + s3))
 // as bf16 hi + lo: the arithmetic of xprep_kernel with three parts, without
 // its launch.  Rows 24..31 of the tile stage nothing (their products land in
-// rows never stored).
+// rows never stored).  WNT: the weights are loaded non-temporal.
 template <class F, int TA, int TU, int NW, int NT, class XT, int GM = 0xFF, bool MERGE = false,
-          bool PIN = false, int XB = 1, int XP = 0>
+          bool PIN = false, int XB = 1, int XP = 0, bool WNT = false>
 __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                             int64_t nrows, const SkRows<TA, NT> &rows,
                                             const XT *__restrict__ x,
@@ -644,7 +644,11 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 
     // weights: each wave loads its 32 rows x RB bytes of a block with NI
     // coalesced 16-byte loads per lane (flat chunk c = 64 i + lane: row c / RL,
-    // bytes 16 (c % RL)), one block ahead of use
+    // bytes 16 (c % RL)), one block ahead of use.  With WNT the loads are
+    // non-temporal: each weight byte is used once, so the L2 keeps the x rows
+    // that every column tile re-reads instead (C3 m = 8 27.9 -> 27.2 us, C5
+    // 160.8 -> 156.9 us with the MoE kernels; at m = 9..64 slower, m = 32
+    // 36.2 -> 38.4 us, same box)
     u32x4 rv[NW][NI];
     typename F::Blk wb[NW], wbn[NW];
     auto wload = [&](int b) {
@@ -654,7 +658,11 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
             for (int i = 0; i < NI; i++) {
                 const int c = 64 * i + lane;
                 const int64_t row = min(wrow0[w] + c / RL, nrows - 1);
-                rv[w][i] = *reinterpret_cast<const u32x4 *>(fmt[w].raw(row, b) + 16 * (c % RL));
+                const u32x4 *p = reinterpret_cast<const u32x4 *>(fmt[w].raw(row, b) + 16 * (c % RL));
+                if constexpr (WNT)
+                    rv[w][i] = __builtin_nontemporal_load(p);
+                else
+                    rv[w][i] = *p;
             }
     };
     auto wstore = [&]() {
@@ -757,9 +765,9 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
 // second x tile is neither staged nor multiplied (acc[w][1] is left as it
 // is).  All threads of the workgroup call it with the same block range and
 // xrows.
-// (xsh: the x scale exponent of XP = 3)
+// (xsh: the x scale exponent of XP = 3; WNT: non-temporal weight loads)
 template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF,
-          bool MERGE = false, bool PIN = false, int XB = 1, int XP = 0>
+          bool MERGE = false, bool PIN = false, int XB = 1, int XP = 0, bool WNT = false>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
                                            const XT *__restrict__ x,
@@ -767,24 +775,24 @@ __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&w
                                            floatx16 (&acc)[NW][TA], _Float16 *lds, int xrows, int &xsh) {
     if constexpr (TA == 2 && SHORT) {
         if (xrows <= 32) {
-            skinny_loop<F, TA, 1, NW, NT, XT, GM, false, false, XB>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds,
-                                                                   xsh);
+            skinny_loop<F, TA, 1, NW, NT, XT, GM, false, false, XB, 0, WNT>(fmt, wrow0, nrows, rows, x, xs, b0, b1,
+                                                                           acc, lds, xsh);
             return;
         }
     }
-    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE, PIN, XB, XP>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds,
-                                                              xsh);
+    skinny_loop<F, TA, TA, NW, NT, XT, GM, MERGE, PIN, XB, XP, WNT>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc,
+                                                                   lds, xsh);
 }
 template <class F, int TA, int NW, int NT = SK_THREADS, class XT = _Float16, bool SHORT = false, int GM = 0xFF,
-          bool MERGE = false, bool PIN = false, int XB = 1, int XP = 0>
+          bool MERGE = false, bool PIN = false, int XB = 1, int XP = 0, bool WNT = false>
 __device__ __forceinline__ void skinny_run(const F (&fmt)[NW], const int64_t (&wrow0)[NW],
                                            int64_t nrows, const SkRows<TA, NT> &rows,
                                            const XT *__restrict__ x,
                                            const uint16_t *__restrict__ xs, int b0, int b1,
                                            floatx16 (&acc)[NW][TA], _Float16 *lds, int xrows) {
     int xsh = 0;
-    skinny_run<F, TA, NW, NT, XT, SHORT, GM, MERGE, PIN, XB, XP>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc, lds,
-                                                                  xrows, xsh);
+    skinny_run<F, TA, NW, NT, XT, SHORT, GM, MERGE, PIN, XB, XP, WNT>(fmt, wrow0, nrows, rows, x, xs, b0, b1, acc,
+                                                                       lds, xrows, xsh);
 }
 // The rows of `rows` for a tile whose x row r (r < n) is row_of(r) of an
 // [*, K] matrix.
