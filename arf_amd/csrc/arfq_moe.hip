@@ -548,15 +548,12 @@ __global__ __launch_bounds__(DXS_THREADS, 1) void moe_down_xs_kernel(
     };
     auto loop = [&](auto tu) {
         constexpr int TU = decltype(tu)::value;
-        floatx16 acc[1][2], cb[1][2], cmin[1][KIND == 2 ? 2 : 1], cq[1][KIND == 3 ? 2 : 1];
+        floatx16 acc[1][2], cb[1][2], cq[1][KIND == 3 ? 2 : 1];
         auto zero = [&]() {
 #pragma unroll
             for (int t = 0; t < 2; t++)
 #pragma unroll
-                for (int i = 0; i < 16; i++) {
-                    acc[0][t][i] = 0.f;
-                    if constexpr (KIND == 2) cmin[0][t][i] = 0.f;
-                }
+                for (int i = 0; i < 16; i++) acc[0][t][i] = 0.f;
         };
         zero();
 #pragma unroll
@@ -574,7 +571,7 @@ __global__ __launch_bounds__(DXS_THREADS, 1) void moe_down_xs_kernel(
             __builtin_amdgcn_sched_barrier(0);
             sk_block<F, 2, TU, 1, 0xFF, false, false>(
                 slab, wb, [&](int t) { return xs_l + (32 * t + lr) * xld + 256 * b; },
-                [&](int t) { return ss_l + ((32 * t + lr) * nb + b) * 16; }, lr, lane >> 5, acc, cb, cmin, cq);
+                [&](int t) { return ss_l + ((32 * t + lr) * nb + b) * 16; }, lr, lane >> 5, acc, cb, cq);
             wb[0] = wbn[0];
             if (b == nb - 1) {
                 // the pass's 32 columns of every tile row
@@ -584,9 +581,7 @@ __global__ __launch_bounds__(DXS_THREADS, 1) void moe_down_xs_kernel(
 #pragma unroll
                     for (int i = 0; i < 16; i++) {
                         const int r = sk_out_row(t, i);
-                        float v = acc[0][t][i];
-                        if constexpr (KIND == 2) v += cmin[0][t][i];
-                        if (r < rows && n < hidden) o[(int64_t)lrow[r] * hidden + n] = v * lrs[r];
+                        if (r < rows && n < hidden) o[(int64_t)lrow[r] * hidden + n] = acc[0][t][i] * lrs[r];
                     }
                 zero();
             }

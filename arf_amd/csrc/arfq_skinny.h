@@ -424,13 +424,13 @@ constexpr size_t sk_lds() {
 // has them) against the x tiles t < TU, whose row 32 t + lr of this block
 // starts at xrow(t) (LDS, the k order of
 // F::a_off) and, for KIND 2, whose sub-block sums (bf16 hi[8] | lo[8]) start
-// at srow(t); then the block end of KIND 1 / 2 (acc += d * cb, the min term
-// into cmin).  cb and cq are the block's own accumulators.  (GM, MERGE, PIN:
+// at srow(t); then the block end of KIND 1 / 2 (the min term's two MFMAs
+// into acc, then acc += d * cb).  cb and cq are the block's own accumulators.
+// (GM, MERGE, PIN:
 // as skinny_loop.)
 template <class F, int TA, int TU, int NW, int GM, bool MERGE, bool PIN, class XRow, class SRow>
 __device__ __forceinline__ void sk_block(const uint8_t *slab, const typename F::Blk (&wbk)[NW], XRow xrow,
                                          SRow srow, int lr, int h, floatx16 (&acc)[NW][TA], floatx16 (&cb)[NW][TA],
-                                         floatx16 (&cmin)[NW][F::KIND == 2 ? TA : 1],
                                          floatx16 (&cq)[NW][F::KIND == 3 ? TA : 1]) {
     constexpr int KIND = F::KIND;
     constexpr int TO = MERGE ? TU / 2 : TU;  // accumulator tiles written
@@ -496,8 +496,11 @@ __device__ __forceinline__ void sk_block(const uint8_t *slab, const typename F::
         }
     }
     if constexpr (KIND == 1 || KIND == 2) {
-        // block end: acc += d * C_block; the min term (two bf16 MFMAs)
-        // accumulates across blocks in its own registers
+        // block end: the min term (two bf16 MFMAs, in true units) onto acc,
+        // then acc += d * C_block.  (Kept in registers of its own, the min
+        // term took 24-32 more VGPRs: the MoE gate|up 250 -> 226, the x-
+        // stationary down 198 -> 166, and no spill in Q5_K's down; the times
+        // did not move.)
 #pragma unroll
         for (int w = 0; w < NW; w++) {
             const float2 dd = F::scale(wbk[w]);
@@ -508,8 +511,8 @@ __device__ __forceinline__ void sk_block(const uint8_t *slab, const typename F::
                 for (int t = 0; t < TU; t++) {
                     const bf16x8 am = *reinterpret_cast<const bf16x8 *>(srow(t) + 8 * h);
                     const int ti = MERGE ? t % TO : t;
-                    cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, cmin[w][ti], 0, 0, 0);
-                    cmin[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, cmin[w][ti], 0, 0, 0);
+                    acc[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bh, acc[w][ti], 0, 0, 0);
+                    acc[w][ti] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am, bl, acc[w][ti], 0, 0, 0);
                 }
             }
 #pragma unroll
@@ -554,7 +557,6 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
                                             floatx16 (&acc)[NW][TA], _Float16 *lds, int &xsh) {
     constexpr int KIND = F::KIND;
     constexpr int XR = 32 * TA;       // x rows staged
-    constexpr int TO = MERGE ? TU / 2 : TU;  // accumulator tiles written
     static_assert(!MERGE || TU % 2 == 0, "merged tiles come in (hi, lo) halves");
     constexpr int XC = SkRows<TA, NT>::XC;
     constexpr int RL = F::RB / 16;          // lanes per weight row in a coalesced load
@@ -711,15 +713,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
     __syncthreads();
 
     // KIND 3: cb holds the step's first sub-block (MFMAs 0, 1), cq its second
-    floatx16 cb[NW][TA], cmin[NW][KIND == 2 ? TA : 1], cq[NW][KIND == 3 ? TA : 1];
-    if constexpr (KIND == 2) {
-#pragma unroll
-        for (int w = 0; w < NW; w++)
-#pragma unroll
-            for (int t = 0; t < TO; t++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) cmin[w][t][i] = 0.f;
-    }
+    floatx16 cb[NW][TA], cq[NW][KIND == 3 ? TA : 1];
     for (int b = b0; b < b1; b++) {
         const int bn = min(b + 1, b1 - 1);  // past the end: a re-read of the last block
         wstore();                            // block b's weights (loaded one block ago)
@@ -737,7 +731,7 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
         __builtin_amdgcn_sched_barrier(0);
         sk_block<F, TA, TU, NW, GM, MERGE, PIN>(
             slab, wb, [&](int t) { return xl + (xb * XR + 32 * t + lr) * SK_XLD; },
-            [&](int t) { return sl + (xb * XR + 32 * t + lr) * 16; }, lr, h, acc, cb, cmin, cq);
+            [&](int t) { return sl + (xb * XR + 32 * t + lr) * 16; }, lr, h, acc, cb, cq);
 #pragma unroll
         for (int w = 0; w < NW; w++) wb[w] = wbn[w];
         if constexpr (XB == 2) {
@@ -749,14 +743,6 @@ __device__ __forceinline__ void skinny_loop(const F (&fmt)[NW], const int64_t (&
             xstore(0);
             __syncthreads();
         }
-    }
-    if constexpr (KIND == 2) {
-#pragma unroll
-        for (int w = 0; w < NW; w++)
-#pragma unroll
-            for (int ti = 0; ti < TO; ti++)
-#pragma unroll
-                for (int i = 0; i < 16; i++) acc[w][ti][i] += cmin[w][ti][i];
     }
 }
 
