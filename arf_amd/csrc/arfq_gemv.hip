@@ -1887,7 +1887,7 @@ static size_t q4k_f32_lds_rows(const arfq_weight *w, int64_t rows) {
 // rounds of x loads issued ahead of the weight ring (8 elements per thread and round)
 static int q4k_f32_xr(const arfq_weight *w, int threads = Q4K_GEMV_THREADS) {
     const int64_t rounds = (w->k / 8 + threads - 1) / threads;
-    return rounds <= 1 ? 1 : rounds <= 2 ? 2 : 4;
+    return rounds <= 1 ? 1 : rounds <= 2 ? 2 : rounds <= 3 ? 3 : 4;
 }
 // The single m = 1 GEMV (gemv_q4k_f32): one 1024-thread workgroup per CU, rows
 // interleaved over the workgroups, x scaled before the first weight load.  At C2
@@ -1926,6 +1926,7 @@ static hipError_t launch_q4k_f32(const arfq_weight *w, int e, const float *x, fl
     switch (q4k_f32_xr(w, Q4K_F32_THREADS)) {
     case 1: return launch_q4k_f32_t<1>(w, e, x, y, s);
     case 2: return launch_q4k_f32_t<2>(w, e, x, y, s);
+    case 3: return launch_q4k_f32_t<3>(w, e, x, y, s);
     default: return launch_q4k_f32_t<4>(w, e, x, y, s);
     }
 }
@@ -1947,7 +1948,10 @@ static hipError_t launch_q4k_f32_glu(const arfq_weight *w, const float *g, const
     switch (q4k_f32_xr(w, Q4K_F32_THREADS)) {
     case 1: return launch_q4k_f32_glu_t<1, ACT>(w, g, u, y, s);
     case 2: return launch_q4k_f32_glu_t<2, ACT>(w, g, u, y, s);
-    default: return launch_q4k_f32_glu_t<4, ACT>(w, g, u, y, s);
+    case 3: return launch_q4k_f32_glu_t<3, ACT>(w, g, u, y, s);
+    // GeGLU's activation over four rounds of x spills; three rounds ahead and
+    // the rest in turn do not
+    default: return launch_q4k_f32_glu_t<ACT == ACT_GELU_TANH ? 3 : 4, ACT>(w, g, u, y, s);
     }
 }
 
@@ -1976,6 +1980,7 @@ hipError_t launch_gemv_dual(const arfq_weight *a, const arfq_weight *b, const fl
     switch (q4k_f32_xr(a, Q4K_F32_THREADS)) {
     case 1: return launch_dual_t<1>(a, b, x, ya, yb, s);
     case 2: return launch_dual_t<2>(a, b, x, ya, yb, s);
+    case 3: return launch_dual_t<3>(a, b, x, ya, yb, s);
     default: return launch_dual_t<4>(a, b, x, ya, yb, s);
     }
 }
