@@ -250,7 +250,14 @@ __global__ __launch_bounds__(MOE_GU_THREADS) void moe_gateup_kernel(
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int ncol = (inter + 127) / 128;
     const int items = *ntiles * ncol;
-    for (int it = blockIdx.x; it < items; it += gridDim.x) {  // uniform over the workgroup
+    // workgroup b runs on XCD b % 8: XCD x walks items [x per, (x + 1) per), so
+    // the column items of a tile share its x rows in one L2 (C5 142.2 -> 140.8
+    // us with the same order in down; a stride of the grid over all items
+    // put a tile's six column items on six XCDs)
+    const int G = gridDim.x, nx = G % 8 == 0 ? 8 : 1, GX = G / nx;
+    const int per = (items + nx - 1) / nx, xbase = ((int)blockIdx.x % nx) * per;
+    const int xend = min(items, xbase + per);
+    for (int it = xbase + (int)blockIdx.x / nx; it < xend; it += GX) {  // uniform over the workgroup
         const int tid = sk_tid(), lane = tid & 63;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform
         const int wq = wave & 3;
@@ -485,13 +492,18 @@ __global__ __launch_bounds__(DXS_THREADS, 1) void moe_down_xs_kernel(
     constexpr int RL = F::RB / 16, NI = 32 * F::RB / 1024, SL = F::RB + 16;
     extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
     const int ncb = (hidden + DXS_COLS - 1) / DXS_COLS;
-    const int ti = (int)blockIdx.x / ncb;
-    if (ti >= *ntiles) return;  // uniform over the workgroup
+    // workgroup L runs on XCD L % 8: XCD x takes items [x per, (x + 1) per) of
+    // the real ones, so the column items of a tile share its rows in one L2
+    const int total = *ntiles * ncb, L = (int)blockIdx.x;
+    if (L >= total) return;  // uniform over the workgroup
+    const int per = total >> 3;
+    const int q = L < 8 * per ? (L & 7) * per + (L >> 3) : L;
+    const int ti = q / ncb;
     const int tid = sk_tid(), lane = tid & 63, wave = tid >> 6, lr = lane & 31;
     const int2 tile = tiles[ti];
     const int e = tile.x, row0 = tile.y;
     const int rows = min(MOE_BM, off[e + 1] - row0);
-    const int c0 = ((int)blockIdx.x - ti * ncb) * DXS_COLS;
+    const int c0 = (q - ti * ncb) * DXS_COLS;
     const int nb = K / 256, xld = K + 8;
     _Float16 *xs_l = lds;                                                        // [64][xld]
     uint16_t *ss_l = reinterpret_cast<uint16_t *>(lds + MOE_BM * xld);           // [64][nb][16]
