@@ -121,7 +121,7 @@ __global__ __launch_bounds__(sk_nt(TA), TA == 4 ? 1 : 2) void gemm_sk(F fmt, con
     // contiguous run of splits whose x ranges then stay in its L2 (C3 m = 64:
     // x as 128 f16 rows is 4.5 MB, more than an L2; 52.1 -> 50.3 us); the last
     // total % 8 items go in order.  With one or two tiles (x within an L2)
-    // that order measured slower (C3 m = 8: 27.7 -> 28.4 us).
+    // that order measured slower (C3 m = 8: 27.7 -> 28.4 us, m = 32: 36.6 -> 37.9).
     const int nt = gridDim.x, total = nt * gridDim.y, per = total >> 3;
     const int L = blockIdx.y * nt + blockIdx.x;
     const int q = TA == 4 && L < 8 * per ? (L & 7) * per + (L >> 3) : L;
