@@ -1949,9 +1949,7 @@ static hipError_t launch_q4k_f32_glu(const arfq_weight *w, const float *g, const
     case 1: return launch_q4k_f32_glu_t<1, ACT>(w, g, u, y, s);
     case 2: return launch_q4k_f32_glu_t<2, ACT>(w, g, u, y, s);
     case 3: return launch_q4k_f32_glu_t<3, ACT>(w, g, u, y, s);
-    // GeGLU's activation over four rounds of x spills; three rounds ahead and
-    // the rest in turn do not
-    default: return launch_q4k_f32_glu_t<ACT == ACT_GELU_TANH ? 3 : 4, ACT>(w, g, u, y, s);
+    default: return launch_q4k_f32_glu_t<4, ACT>(w, g, u, y, s);
     }
 }
 
@@ -2054,12 +2052,19 @@ static hipError_t launch_gemv_glu_t(const arfq_weight *w, int64_t m, const float
     }
     return launch_q4k_f32_glu<ACT>(w, g, u, y, s);  // m == 1, q4k_f32s_ok
 }
+// The activation applied as the down GEMV reads its x: every workgroup then
+// evaluates it over all of x (exp / tanh and an IEEE divide per element), which
+// at the decode FFN's inter 17408 cost more than a launch of its own (the
+// separate activation kernel, then the plain GEMV: 40.9 -> 38.9 and 41.1 ->
+// 40.4 us per FFN on two boxes), so only up to GLU_FUSE_MAX_K elements of x (8192 for the
+// 1024-thread f32 kernel, half that for the 512-thread 16-bit one).
+constexpr int64_t GLU_FUSE_MAX_K = 8192;
 // what launch_gemv_glu_t takes: the 16-bit kernel under x16 where it fits,
-// otherwise the f32 kernel at m = 1
+// otherwise the f32 kernel at m = 1, both up to those k
 bool gemv_glu_supports(const arfq_weight *w, int64_t m, bool x16) {
     if (w->qtype != ARFQ_Q4_K || w->experts != 1) return false;
-    if (x16 && q4k_x16_ok(w, m)) return true;
-    return m == 1 && q4k_f32s_ok(w);
+    if (x16 && q4k_x16_ok(w, m)) return w->k <= GLU_FUSE_MAX_K / 2;
+    return m == 1 && q4k_f32s_ok(w) && w->k <= GLU_FUSE_MAX_K;
 }
 hipError_t launch_gemv_glu(const arfq_weight *w, int64_t m, const float *g, const float *u, float *y, int act,
                            hipStream_t s, bool x16) {

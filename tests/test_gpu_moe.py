@@ -346,7 +346,7 @@ def _glu_oracle(oracle, x, raws, qts, inter, hidden, act):
     # m = 1, Q4_K: gate and up in one launch, GeGLU applied as the down GEMV reads its x
     (("q4_k", "q4_k", "q4_k"), 512, 768, 1, 0.02, False),
     (("q4_k", "q4_k", "q4_k"), 5120, 17408, 1, 0.005, False),
-    # inter 28672: the down GEMV's x takes four rounds, three loaded ahead
+    # inter 28672: the activation as a launch of its own, the down GEMV's x in four rounds
     (("q4_k", "q4_k", "q4_k"), 512, 28672, 1, 0.02, False),
     # the 16-bit-x GEMV option (gate and up as two launches)
     (("q4_k", "q4_k", "q4_k"), 512, 768, 1, 0.02, True),
