@@ -280,8 +280,10 @@ typedef enum { ARFQ_ACT_SILU = 0, ARFQ_ACT_GELU_TANH = 1 } arfq_act;
  * in the decode and batch paths (crates/arf-gpu/src/gpu/decode.rs:123,
  * batch.rs:6953) and Mlp::forward (crates/arf-core/src/model/mlp.rs:20-24).
  * At m = 1 with Q4_K gate and up of one shape, gate and up run as one launch;
- * with Q4_K down weights at m <= 4 the activation is applied as the down GEMV
- * reads its x (no intermediate). */
+ * with Q4_K down weights at m = 1 and inter <= 8192 (m <= 4 and inter <= 4096
+ * under ARFQ_OPT_GEMV_X16) the activation is applied as the down GEMV reads
+ * its x (no intermediate), otherwise it runs as a kernel of its own between
+ * them.  Either way h = act(g) * u is the same f32 value. */
 int arfq_ffn_act(arfq_ctx *ctx, const arfq_weight *gate, const arfq_weight *up, const arfq_weight *down,
                  int64_t m, const float *x, float *y, int act);
 /* arfq_ffn_act with ARFQ_ACT_SILU (Mlp::forward). */
