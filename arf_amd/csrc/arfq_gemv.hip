@@ -1943,14 +1943,11 @@ static hipError_t launch_q4k_f32_glu_t(const arfq_weight *w, const float *g, con
     return hipGetLastError();
 }
 template <int ACT>
+// (taken for k <= 8192 only, gemv_glu_supports: x is one round of loads)
 static hipError_t launch_q4k_f32_glu(const arfq_weight *w, const float *g, const float *u, float *y,
                                      hipStream_t s) {
-    switch (q4k_f32_xr(w, Q4K_F32_THREADS)) {
-    case 1: return launch_q4k_f32_glu_t<1, ACT>(w, g, u, y, s);
-    case 2: return launch_q4k_f32_glu_t<2, ACT>(w, g, u, y, s);
-    case 3: return launch_q4k_f32_glu_t<3, ACT>(w, g, u, y, s);
-    default: return launch_q4k_f32_glu_t<4, ACT>(w, g, u, y, s);
-    }
+    if (q4k_f32_xr(w, Q4K_F32_THREADS) != 1) return hipErrorInvalidValue;
+    return launch_q4k_f32_glu_t<1, ACT>(w, g, u, y, s);
 }
 
 // gate and up in one launch: half the single GEMV's workgroups per weight
