@@ -1349,13 +1349,14 @@ __device__ __forceinline__ float codes16_fdot(const uint32_t cw[4], const float 
 // narrow window of the weight stream at a time), and x is scaled into LDS
 // before the first weight load is issued (every weight request in flight
 // delays the x requests); as the Q4_K f32 GEMV (gemv_q4k_f32_body).
-template <class F, int XR, bool COL>
+template <class F, int XR>
 __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const float *__restrict__ x,
                                                                 float *__restrict__ y, int n, int nblk) {
     constexpr int C = Q6K_GEMV_CHUNK, PF = F::PF;
     static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
     extern __shared__ uint4 smem4[];
-    __shared__ int cnt[COL ? 64 : 1];  // the chunk counters: per column (spr <= 64), or one
+    __shared__ int cnt[64];             // chunk counters per column (spr <= 64)
+    __shared__ unsigned long long exm;  // columns seen exhausted
     const int k = nblk * 256;
     float *xfl = reinterpret_cast<float *>(smem4);  // [k], scaled
     float *s16 = xfl + k;                           // [k / 16]
@@ -1372,51 +1373,58 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
     const int R = (n - r0 + G - 1) / G;
     const int spr = (nblk + 3) >> 2;
     const int cpc = (R + C - 1) / C;
-    const int nchunks = cpc * spr;
 
-    // COL: a home column per group (group % spr), its chunks claimed from that
-    // column's counter and only then from the next columns', so a group keeps
-    // the x of one column in registers for most of its work.  Otherwise chunk kc
-    // of one counter is column kc / cpc: a workgroup's groups work through the
-    // columns together (a narrow window of the stream), reloading x per chunk.
-    int icol = COL ? grp % spr : 0, irow = COL ? (grp / spr) * C : 0;
+    // A home column per group (group % spr), its chunks claimed from that
+    // column's counter, so a group keeps the x of one column in registers for
+    // most of its work; when it runs out, the next column not yet seen
+    // exhausted (a bit mask of them).  Lane 0 of the group decides and claims,
+    // the group takes column and chunk by broadcast, so its lanes stay in step.
+    // (One counter over all chunks, column by column, had a group's chunks ~32
+    // apart, in another column each time, its x reloaded from LDS per chunk:
+    // Q5_K at C2's shape 24.1 -> 19.5 us, C3 m = 1 21.9 -> 20.7 us with home
+    // columns and the mask; home columns that tried the next columns one by
+    // one were slower at C3's 17 columns, 24.2 us: every failed try is an LDS
+    // atomic round trip.)
+    int icol = grp % spr, irow = (grp / spr) * C;
     auto claim = [&]() {
         int col = icol;
         for (int t = 0; t < spr; t++) {
             int kk = 0;
-            if (l16 == 0) kk = atomicAdd(&cnt[col], 1);
-            kk = __builtin_amdgcn_ds_swizzle(kk, 0x10);  // lane 0 of each 16-lane group
+            if (l16 == 0) {
+                if (t > 0) {
+                    const uint64_t all = spr == 64 ? ~0ull : ((1ull << spr) - 1);
+                    const uint64_t av = ~__hip_atomic_load(&exm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & all;
+                    const uint64_t r = col == 0 ? av : ((av >> col) | (av << (spr - col))) & all;
+                    if (r == 0) {
+                        col = -1;  // none left
+                    } else {
+                        col += __builtin_ctzll(r);
+                        if (col >= spr) col -= spr;
+                    }
+                }
+                if (col >= 0) {
+                    kk = atomicAdd(&cnt[col], 1);
+                    if (kk >= cpc) atomicOr(&exm, 1ull << col);
+                }
+            }
+            col = __builtin_amdgcn_ds_swizzle(col, 0x10);  // lane 0 of each 16-lane group
+            kk = __builtin_amdgcn_ds_swizzle(kk, 0x10);
+            if (col < 0) break;
             if (kk < cpc) {
                 icol = col;
                 irow = kk * C;
                 return;
             }
-            col = col + 1 == spr ? 0 : col + 1;
         }
         icol = spr;  // no work left
-    };
-    auto start_chunk = [&](int kc) {
-        icol = kc < nchunks ? kc / cpc : spr;
-        irow = (kc - icol * cpc) * C;
     };
     typename F::Lane ld[PF];
     int srow[PF], scol[PF];
     auto issue = [&](int u, bool first) {
-        if constexpr (COL) {
-            if (!first) {
-                if (u % C == 0) claim();
-                else irow++;
-            } else if (u > 0) {
-                irow++;
-            }
-        } else if (u % C == 0) {
-            int kc = grp;
-            if (!first) {
-                if (l16 == 0) kc = atomicAdd(&cnt[0], 1);
-                kc = __builtin_amdgcn_ds_swizzle(kc, 0x10);  // lane 0 of each 16-lane group
-            }
-            start_chunk(kc);
-        } else {
+        if (!first) {
+            if (u % C == 0) claim();
+            else irow++;
+        } else if (u > 0) {
             irow++;
         }
         const int b = 4 * icol + bq;
@@ -1428,11 +1436,8 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
     };
 
     // counters start past the chunks the groups begin on
-    if constexpr (COL) {
-        for (int cc = tid; cc < spr; cc += Q6K_GEMV_THREADS) cnt[cc] = (Q6K_GEMV_GROUPS - cc + spr - 1) / spr;
-    } else if (tid == 0) {
-        cnt[0] = Q6K_GEMV_GROUPS;
-    }
+    for (int cc = tid; cc < spr; cc += Q6K_GEMV_THREADS) cnt[cc] = (Q6K_GEMV_GROUPS - cc + spr - 1) / spr;
+    if (tid == 0) exm = 0;
     // x loads, x scaled into LDS, the barrier (which orders LDS only), then the
     // first weight loads
     const int xitems = k / 8;
@@ -1849,20 +1854,12 @@ static bool dot_f32_ok(const arfq_weight *w) {
 }
 template <class F, int XR>
 static hipError_t launch_dot_f32_t(const F &fmt, const arfq_weight *w, const float *x, float *y, hipStream_t s) {
-    // home columns while there are at least four groups per column (k <= 8192:
-    // Q5_K at C2's shape 24.1 -> 19.4 us); with more columns than that (C3, k =
-    // 17408: 17 columns, two groups each) one counter for all of them is faster
-    // (22.0 against 24.2 us with home columns, same box)
-    const bool col = (w->k / 256 + 3) / 4 * 4 <= Q6K_GEMV_GROUPS;
-    auto go = [&](auto kern) {
-        static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device (one per go)
-        if (hipError_t err = set_max_lds_once((const void *)kern, DOT_F32_LDS_MAX, lds_set))
-            return err;
-        kern<<<(unsigned)dot_f32_grid(w), Q6K_GEMV_THREADS, dot_f32_lds(w), s>>>(fmt, x, y, (int)w->n,
-                                                                                (int)(w->k / 256));
-        return hipGetLastError();
-    };
-    return col ? go(gemv_dot_f32<F, XR, true>) : go(gemv_dot_f32<F, XR, false>);
+    static std::atomic<uint64_t> lds_set{0};  // the attribute belongs to the kernel, per device
+    if (hipError_t err = set_max_lds_once((const void *)gemv_dot_f32<F, XR>, DOT_F32_LDS_MAX, lds_set))
+        return err;
+    gemv_dot_f32<F, XR><<<(unsigned)dot_f32_grid(w), Q6K_GEMV_THREADS, dot_f32_lds(w), s>>>(
+        fmt, x, y, (int)w->n, (int)(w->k / 256));
+    return hipGetLastError();
 }
 template <class F>
 static hipError_t launch_dot_f32(const F &fmt, const arfq_weight *w, const float *x, float *y, hipStream_t s) {
