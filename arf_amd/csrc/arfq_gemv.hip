@@ -613,7 +613,7 @@ __device__ __forceinline__ float q4k_fdot(const uint4 c, const float *X) {
 // NT threads per workgroup.  x is scaled into LDS before any weight load is
 // issued, and workgroup w owns rows w, w + G, w + 2G, ... (G workgroups): the
 // whole chip reads a narrow window of the weight stream at a time.
-template <int XR, int PF, int NT, class XSRC>
+template <int XR, int PF, int NT, class XSRC, bool MASKED = false>
 __device__ __forceinline__ void gemv_q4k_f32_body(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const XSRC &xsrc, float *__restrict__ y, int n, int nblk) {
@@ -621,6 +621,7 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     constexpr int GROUPS = NT / 16;
     static_assert(PF % C == 0, "claims must sit at fixed slots of the unrolled loop");
     extern __shared__ uint4 smem4[];
+    __shared__ unsigned long long exm;  // columns seen exhausted (spr <= 64)
     const int nsub = nblk * 8;
     const int spr = (nblk + 3) >> 2;
     float4 *xf = reinterpret_cast<float4 *>(smem4);                 // [k / 4]
@@ -648,18 +649,49 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     // and only when it runs out from the next columns, so a group keeps the x
     // of one column in registers for most of its work.
     int icol = grp % spr, irow = (grp / spr) * C;
+    // MASKED (taken past 8 columns, i.e. with more than one round of x at
+    // 1024 threads): a group whose column ran out takes the
+    // next column not yet seen exhausted (a bit mask; lane 0 decides and
+    // claims, the group follows by broadcast).  Trying the next columns one by
+    // one costs an LDS atomic round trip per exhausted column: at the FFN's
+    // down GEMV (17 columns) 40.2 -> 37.2 us per FFN with the mask (same box);
+    // at C2's 5 columns the scan stays (the mask's code there cost 0.3 us).
     auto claim = [&]() {
         int col = icol;
         for (int t = 0; t < spr; t++) {
             int k = 0;
-            if (l16 == 0) k = atomicAdd(&cnt[col], 1);
-            k = __builtin_amdgcn_ds_swizzle(k, 0x10);  // lane 0 of each 16-lane group
+            if constexpr (MASKED) {
+                if (l16 == 0) {
+                    if (t > 0) {
+                        const uint64_t all = spr == 64 ? ~0ull : ((1ull << spr) - 1);
+                        const uint64_t av =
+                            ~__hip_atomic_load(&exm, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) & all;
+                        const uint64_t r = col == 0 ? av : ((av >> col) | (av << (spr - col))) & all;
+                        if (r == 0) {
+                            col = -1;  // none left
+                        } else {
+                            col += __builtin_ctzll(r);
+                            if (col >= spr) col -= spr;
+                        }
+                    }
+                    if (col >= 0) {
+                        k = atomicAdd(&cnt[col], 1);
+                        if (k >= cpc) atomicOr(&exm, 1ull << col);
+                    }
+                }
+                col = __builtin_amdgcn_ds_swizzle(col, 0x10);  // lane 0 of each 16-lane group
+                k = __builtin_amdgcn_ds_swizzle(k, 0x10);
+                if (col < 0) break;
+            } else {
+                if (l16 == 0) k = atomicAdd(&cnt[col], 1);
+                k = __builtin_amdgcn_ds_swizzle(k, 0x10);  // lane 0 of each 16-lane group
+            }
             if (k < cpc) {
                 icol = col;
                 irow = k * C;
                 return;
             }
-            col = col + 1 == spr ? 0 : col + 1;
+            if constexpr (!MASKED) col = col + 1 == spr ? 0 : col + 1;
         }
         icol = spr;  // no work left
     };
@@ -688,6 +720,7 @@ __device__ __forceinline__ void gemv_q4k_f32_body(
     // counters start past the chunks the groups begin on
     for (int c = tid; c < spr; c += NT)
         cnt[c] = (GROUPS - c + spr - 1) / spr;
+    if (MASKED && tid == 0) exm = 0;
     // x loads, x scaled into LDS, the barrier, then the weights: a wave's
     // loads issue in order and stall once the CU's memory queue is full, and
     // every CU's weight requests delay the x requests, so x issued alone
@@ -770,7 +803,7 @@ template <int XR>
 __global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32(
     const uint8_t *__restrict__ hdr, uint32_t hdr_bytes, const uint8_t *__restrict__ qs,
     uint32_t qs_bytes, const float *__restrict__ x, float *__restrict__ y, int n, int nblk) {
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, XsF32, (XR > 1)>(hdr, hdr_bytes, qs, qs_bytes, XsF32{x}, y, n,
                                                         nblk);
 }
 
@@ -793,7 +826,7 @@ __global__ __launch_bounds__(Q4K_F32_THREADS) void gemv_q4k_f32_dual(
     const uint8_t *__restrict__ qs1, uint32_t hdr_bytes, uint32_t qs_bytes, const float *__restrict__ x,
     float *__restrict__ y0, float *__restrict__ y1, int n, int nblk) {
     const bool second = blockIdx.y != 0;  // uniform over the workgroup
-    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0,
+    gemv_q4k_f32_body<XR, Q4K_GEMV_PF, Q4K_F32_THREADS, XsF32, (XR > 1)>(second ? hdr1 : hdr0, hdr_bytes, second ? qs1 : qs0,
                                                         qs_bytes, XsF32{x}, second ? y1 : y0, n, nblk);
 }
 
@@ -1946,7 +1979,7 @@ static size_t q4k_f32s_lds(const arfq_weight *w) {
 }
 static bool q4k_f32s_ok(const arfq_weight *w) {
     return w->qtype == ARFQ_Q4_K && q4k_f32s_lds(w) <= Q4K_F32_LDS_MAX &&
-           w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB;
+           w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB && (w->k / 256 + 3) / 4 <= 64;
 }
 template <int XR>
 static hipError_t launch_q4k_f32_t(const arfq_weight *w, int e, const float *x, float *y, hipStream_t s) {
@@ -2023,7 +2056,7 @@ static size_t q4k_pairs_lds(const arfq_weight *w, int64_t g) { return q4k_f32_ld
 
 bool gemv_pairs_supports(const arfq_weight *w) {
     return w->qtype == ARFQ_Q4_K && w->k % 256 == 0 && w->n * (w->k / 256) * 128 < (int64_t)Q4K_OOB &&
-           q4k_pairs_lds(w, 1) <= Q4K_F32_LDS_MAX;
+           q4k_pairs_lds(w, 1) <= Q4K_F32_LDS_MAX && (w->k / 256 + 3) / 4 <= 64;
 }
 
 // Workgroups per CU of the decode-pair GEMVs: two, or one for up to 8 pairs (one token's
