@@ -95,6 +95,18 @@ def test_gemv_small_shapes(gpu_ctx, oracle, qtype, n, k, m):
     assert rel_err(got, want) <= TOL
 
 
+@pytest.mark.parametrize("qtype", ["q4_k", "q6_k", "q5_k", "iq4_xs"])
+@pytest.mark.parametrize("n,k", [(300, 32768), (5000, 12288)])
+def test_gemv_f32_many_columns(gpu_ctx, oracle, qtype, n, k):
+    # the m = 1 f32 GEMVs at 32 and 12 four-block columns: a group whose home column runs
+    # out takes the next one not yet exhausted from the workgroup's mask; at n = 300 most
+    # workgroups hold 1-2 rows, fewer chunks per column than groups
+    _say("case: gemv f32 many columns", qtype, n, k)
+    got, raw, x = _matmul(gpu_ctx, qtype, n, k, 1, seed=11 * n + k)
+    want = oracle.matmul_q(qtype, x, raw, n)
+    assert rel_err(got, want) <= 1e-5
+
+
 @pytest.mark.parametrize("qtype,m", [("q4_k", 1), ("q6_k", 1), ("q6_k", 2), ("q5_k", 1), ("q5_k", 3),
                                      ("iq4_xs", 1), ("iq4_xs", 4)])
 def test_gemv_expert_offset(gpu_ctx, oracle, qtype, m):
