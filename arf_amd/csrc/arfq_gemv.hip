@@ -1367,7 +1367,9 @@ __device__ __forceinline__ float codes16_fdot(const uint32_t cw[4], const float 
     float acc = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-        const uint32_t A = cw[j] & 0x00FF00FFu, B = (cw[j] >> 8) & 0x00FF00FFu;
+        // bytes 0, 2 and bytes 1, 3 into 16-bit halves (v_perm_b32, selector 0x0C = 0)
+        const uint32_t A = __builtin_amdgcn_perm(cw[j], cw[j], 0x0C020C00u),
+                       B = __builtin_amdgcn_perm(cw[j], cw[j], 0x0C030C01u);
         acc = fmix<0>(X[4 * j], A, acc);
         acc = fmix<1>(X[4 * j + 2], A, acc);
         acc = fmix<0>(X[4 * j + 1], B, acc);
