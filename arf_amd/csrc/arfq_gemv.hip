@@ -977,16 +977,15 @@ struct DotQ6K {
     // scales 8 n2 + isub + 2t: bytes isub, isub + 2 of dwords 2 n2 and 2 n2 + 1 of
     // the quad's scale dwords (all lanes take part in the DPP broadcasts)
     __device__ static void scales(const Lane &l, int c, float A[4], float B[4]) {
-        const uint32_t s0 = quad_bcast<0>(l.sw), s1 = quad_bcast<1>(l.sw);
-        const uint32_t s2 = quad_bcast<2>(l.sw), s3 = quad_bcast<3>(l.sw);
-        const int n2 = c >> 1;
-        const uint32_t sa = n2 ? s2 : s0, sb = n2 ? s3 : s1;
+        // lanes 0, 1 of the quad take its scale dwords 0, 1 and lanes 2, 3
+        // dwords 2, 3 (DPP quad_perm [0,0,2,2] and [1,1,3,3]); v_perm then
+        // gathers bytes isub, isub + 2 of both into one dword
+        const uint32_t sa = (uint32_t)__builtin_amdgcn_mov_dpp((int)l.sw, 0xA0, 0xf, 0xf, true);
+        const uint32_t sb = (uint32_t)__builtin_amdgcn_mov_dpp((int)l.sw, 0xF5, 0xf, 0xf, true);
+        const uint32_t sc = __builtin_amdgcn_perm(sb, sa, (c & 1) ? 0x07050301u : 0x06040200u);
         const float d = h2f(l.dw);
-        const uint32_t sh = 8u * (uint32_t)(c & 1);
-        A[0] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh, 8);
-        A[1] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sa, sh + 16u, 8);
-        A[2] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh, 8);
-        A[3] = d * (float)(int8_t)__builtin_amdgcn_ubfe(sb, sh + 16u, 8);
+#pragma unroll
+        for (int t = 0; t < 4; t++) A[t] = d * (float)(int8_t)(sc >> (8 * t));
         (void)B;
     }
     // quadrant t: ql_a / ql_b (t odd), low / high nibble (t >= 2), qh bits 2t..2t+1
@@ -1006,11 +1005,13 @@ struct DotQ6K {
         (void)B;
         return A * (xsc * (float)sdot - 32.f * xsum);
     }
-    // the f32-x kernel's codes are the bytes xor FXOR (unsigned), its quadrant term
+    // the f32-x kernel's codes are the bytes xor FXOR (unsigned), its quadrant
+    // term; its xsum arrives as XSUM_MUL * sum(x), scaled where x is read from LDS
     static constexpr uint32_t FXOR = 0u;
+    static constexpr float XSUM_MUL = -32.f;
     __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
         (void)B;
-        return A * (xsc * dot - 32.f * xsum);
+        return A * __builtin_fmaf(xsc, dot, xsum);
     }
 };
 
@@ -1085,6 +1086,7 @@ struct DotQ5K {
         return A * (xsc * (float)sdot) - B * xsum;
     }
     static constexpr uint32_t FXOR = 0u;
+    static constexpr float XSUM_MUL = 1.f;
     __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
         return A * (xsc * dot) - B * xsum;
     }
@@ -1172,9 +1174,10 @@ struct DotIQ4XS {
     }
     // f32 x: the unsigned codes kv + 128 (kv xor 0x80), less 128 * sum(x)
     static constexpr uint32_t FXOR = 0x80808080u;
+    static constexpr float XSUM_MUL = -128.f;
     __device__ static float fterm(float A, float B, float xsc, float dot, float xsum) {
         (void)B;
-        return A * (xsc * dot - 128.f * xsum);
+        return A * __builtin_fmaf(xsc, dot, xsum);
     }
 };
 
@@ -1337,7 +1340,7 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot(F fmt, const float 
 // 2^(24 - s) per 32.  A quadrant's 16 codes (unsigned bytes: Q6_K q < 64,
 // Q5_K q < 32, IQ4_XS kv + 128) go into v_fma_mix_f32 as the f16 subnormals
 // q * 2^-24, so each product x * 2^s * q * 2^-24 is exact in f32 and the
-// quadrant adds F::fterm(A, B, 2^(24 - s), sum(x * q), sum(x)): for Q6_K
+// quadrant adds F::fterm(A, B, 2^(24 - s), sum(x * q), XSUM_MUL * sum(x)): for Q6_K
 // (d * sc) * (sum(x * q) - 32 * sum(x)), the oracle's (d * sc) * (q - 32) per
 // weight (gguf.rs:2120-2123) times f32 x, factorised.
 namespace {
@@ -1507,7 +1510,7 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
                 X[t][4 * i + 2] = v.z;
                 X[t][4 * i + 3] = v.w;
             }
-            XS[t] = s16[eo >> 4];
+            XS[t] = F::XSUM_MUL * s16[eo >> 4];
             XE[t] = xe[eo >> 5];
         }
     };
