@@ -989,14 +989,15 @@ struct DotQ6K {
         (void)B;
     }
     // quadrant t: ql_a / ql_b (t odd), low / high nibble (t >= 2), qh bits 2t..2t+1
+    template <uint32_t X = 0u>
     __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
         (void)c;
         const uint32_t w[12] = {l.q0.x, l.q0.y, l.q0.z, l.q0.w, l.q1.x, l.q1.y,
                                 l.q1.z, l.q1.w, l.q2.x, l.q2.y, l.q2.z, l.q2.w};
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            cw[j] = ((w[4 * (t & 1) + j] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) |
-                    (((w[8 + j] >> (2 * t)) << 4) & 0x30303030u);
+            cw[j] = (((w[4 * (t & 1) + j] >> (4 * (t >> 1))) & 0x0F0F0F0Fu) |
+                     (((w[8 + j] >> (2 * t)) << 4) & 0x30303030u)) ^ X;
     }
     __device__ static int subdot(const uint32_t cw[4], const u32x4 lo, const u32x4 hi) {
         return q6k_subdot(cw, lo, hi);
@@ -1071,13 +1072,14 @@ struct DotQ5K {
         }
     }
     // quadrant t: qs bytes 16 (t % 2) + 4j ..+3 and qh dword 4 (t % 2) + j
+    template <uint32_t X = 0u>
     __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
         const int nib = t >> 1;
         const u32x4 qs = (t & 1) ? l.qs1 : l.qs0;
         const uint32_t hs = (uint32_t)(2 * c + nib);
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            cw[j] = ((qs[j] >> (4 * nib)) & 0x0F0F0F0Fu) | (((l.qhd[4 * (t & 1) + j] >> hs) & 0x01010101u) << 4);
+            cw[j] = (((qs[j] >> (4 * nib)) & 0x0F0F0F0Fu) | (((l.qhd[4 * (t & 1) + j] >> hs) & 0x01010101u) << 4)) ^ X;
     }
     __device__ static int subdot(const uint32_t cw[4], const u32x4 lo, const u32x4 hi) {
         return q6k_subdot(cw, lo, hi);
@@ -1137,11 +1139,13 @@ struct DotIQ4XS {
             B[2 * u] = B[2 * u + 1] = 0.f;
         }
     }
+    template <uint32_t X = 0u>
     __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
         (void)c;
         // kvalues_iq4nl as bytes: entries 0..7 and 8..15, little-endian
-        constexpr uint32_t T0lo = 0xBFAD9881u, T0hi = 0xF6EADDCFu;
-        constexpr uint32_t T1lo = 0x26190D01u, T1hi = 0x71594535u;
+        // (xor X: the table of kv ^ X)
+        constexpr uint32_t T0lo = 0xBFAD9881u ^ X, T0hi = 0xF6EADDCFu ^ X;
+        constexpr uint32_t T1lo = 0x26190D01u ^ X, T1hi = 0x71594535u ^ X;
         const u32x4 q = (t >> 1) ? l.q1 : l.q0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -1149,9 +1153,9 @@ struct DotIQ4XS {
             const uint32_t s7 = sel & 0x07070707u;
             const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
             const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
-            const uint32_t hi = (sel >> 3) & 0x01010101u;
-            const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
-            cw[j] = (v1 & mask) | (v0 & ~mask);
+            // byte i from v0 (selector i) or, where the code is >= 8, from v1 (i + 4)
+            const uint32_t pick = ((sel >> 1) & 0x04040404u) | 0x03020100u;
+            cw[j] = __builtin_amdgcn_perm(v1, v0, pick);
         }
     }
     // sum(kv * X) with signed kv: the high plane by sdot4; the low (unsigned)
@@ -1526,9 +1530,7 @@ __global__ __launch_bounds__(Q6K_GEMV_THREADS) void gemv_dot_f32(F fmt, const fl
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             uint32_t cw[4];
-            F::codes(ld[u], c, t, cw);
-#pragma unroll
-            for (int j = 0; j < 4; j++) cw[j] ^= F::FXOR;
+            F::template codes<F::FXOR>(ld[u], c, t, cw);
             v += F::fterm(A[t], B[t], XE[t], codes16_fdot(cw, X[t]), XS[t]);
         }
         v = row16_sum(v);

@@ -459,9 +459,10 @@ def only_config(ctx, args):
     elif c == "c1":
         ms, _ = time_matmul(ctx, "q8_0", 1, 2048, 2048, args.steps, args.warmup, 64, 0xA7F00001)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q8_0", 1, 2048, 2048) / ms / 1e6}
-    elif c == "q5km1":
-        ms, _ = time_matmul(ctx, "q5_k", 1, 17408, 5120, args.steps, args.warmup, 6, 0xA7F00005)
-        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q5_k", 1, 17408, 5120) / ms / 1e6}
+    elif c in ("q5km1", "iq4m1"):
+        qt, seed = ("q5_k", 0xA7F00005) if c == "q5km1" else ("iq4_xs", 0xA7F00006)
+        ms, _ = time_matmul(ctx, qt, 1, 17408, 5120, args.steps, args.warmup, 6, seed)
+        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes(qt, 1, 17408, 5120) / ms / 1e6}
     elif c.startswith("c3"):
         if c.endswith("x16"):  # the 16-bit GEMV (m = 1) or one f16 part of x (skinny)
             ctx.set_options(_arfq.OPT_GEMV_X16)
@@ -500,7 +501,7 @@ def main():
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
     ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c3m64x16", "c4",
-                                       "c5", "q5km1", "c1n8", "lmhead", "moe1", "moe4", "moe16", "ffn"],
+                                       "c5", "q5km1", "iq4m1", "c1n8", "lmhead", "moe1", "moe4", "moe16", "ffn"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
