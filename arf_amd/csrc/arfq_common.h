@@ -71,6 +71,20 @@ __host__ __device__ constexpr int q4k_sigma_inv(int t) { return t < 4 ? 2 * t : 
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 
+// The IQ4_NL codebook value (ggml's kvalues_iq4nl, gguf.rs:1908-1914) xor X of
+// four 4-bit codes, one per byte of sel: two v_perm over the table's 8-entry
+// halves (entries 0..7 and 8..15 as little-endian bytes), and a third that
+// takes each byte from the half its code's bit 3 names (selector i or i + 4).
+template <uint32_t X>
+__device__ __forceinline__ uint32_t iq4nl_lookup(uint32_t sel) {
+    constexpr uint32_t T0lo = 0xBFAD9881u ^ X, T0hi = 0xF6EADDCFu ^ X;
+    constexpr uint32_t T1lo = 0x26190D01u ^ X, T1hi = 0x71594535u ^ X;
+    const uint32_t s7 = sel & 0x07070707u;
+    const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
+    const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
+    return __builtin_amdgcn_perm(v1, v0, ((sel >> 1) & 0x04040404u) | 0x03020100u);
+}
+
 // 6-bit scale / min of Q4_K sub-block j (0..7) from the header dwords
 // s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11]  (ggml
 // get_scale_min_k4; crates/arf-ml/src/weight.rs:1353-1365).

@@ -348,20 +348,12 @@ struct BdIQ4XS {
         return {s, s * (half2v){-1152.f, -1152.f}};  // 1152 |ls - 32| <= 36864: exact
     }
     __device__ static half8 deq(const Code &c, const Step &k, Blk, int, int kk) {
-        // kvalues_iq4nl + 128 as bytes: entries 0..7 and 8..15, little-endian
-        constexpr uint32_t T0lo = 0xBFAD9881u ^ 0x80808080u, T0hi = 0xF6EADDCFu ^ 0x80808080u;
-        constexpr uint32_t T1lo = 0x26190D01u ^ 0x80808080u, T1hi = 0x71594535u ^ 0x80808080u;
         const uint32_t w[2] = {(kk & 1) ? c.z : c.x, (kk & 1) ? c.w : c.y};
         uint32_t o[4];
 #pragma unroll
         for (int j = 0; j < 2; j++) {
             const uint32_t sel = (kk >> 1) ? (w[j] >> 4) & 0x0F0F0F0Fu : w[j] & 0x0F0F0F0Fu;
-            const uint32_t s7 = sel & 0x07070707u;
-            const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
-            const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
-            const uint32_t hi = (sel >> 3) & 0x01010101u;
-            const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
-            const uint32_t v = (v1 & mask) | (v0 & ~mask);
+            const uint32_t v = iq4nl_lookup<0x80808080u>(sel);  // kv + 128 per byte
             // (1024 + kv + 128) * s - 1152 s = s * kv, one rounding
             o[2 * j] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), k.s, k.c);
             o[2 * j + 1] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u), k.s, k.c);

@@ -377,9 +377,6 @@ struct FmtIQ4XSR {
         const int ls = (int)(((r.h.y >> (4 * s)) & 0xFu) | (((r.h.x >> (16 + 2 * s)) & 3u) << 4));
         const float dl = h2f(r.h.x) * (float)(ls - 32);
         const float m128 = -128.f * dl;  // exact
-        // kvalues_iq4nl + 128 as bytes: entries 0..7 and 8..15, little-endian
-        constexpr uint32_t T0lo = 0xBFAD9881u ^ 0x80808080u, T0hi = 0xF6EADDCFu ^ 0x80808080u;
-        constexpr uint32_t T1lo = 0x26190D01u ^ 0x80808080u, T1hi = 0x71594535u ^ 0x80808080u;
         const uint32_t cw[4] = {r.c.x, r.c.y, r.c.z, r.c.w};
 #pragma unroll
         for (int nib = 0; nib < 2; nib++)
@@ -387,12 +384,7 @@ struct FmtIQ4XSR {
             for (int w = 0; w < 4; w++) {
                 // elements 16 nib + 4w .. + 3: kv + 128 per byte
                 const uint32_t sel = (cw[w] >> (4 * nib)) & 0x0F0F0F0Fu;
-                const uint32_t s7 = sel & 0x07070707u;
-                const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
-                const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
-                const uint32_t hi = (sel >> 3) & 0x01010101u;
-                const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
-                const uint32_t v = (v1 & mask) | (v0 & ~mask);
+                const uint32_t v = iq4nl_lookup<0x80808080u>(sel);  // kv + 128 per byte
                 // (kv + 128) * dl - 128 dl = kv * dl, one rounding
                 o[8 * nib + 2 * w] = pack2h(fmaf(dl, (float)(v & 0xffu), m128), fmaf(dl, (float)((v >> 8) & 0xffu), m128));
                 o[8 * nib + 2 * w + 1] = pack2h(fmaf(dl, (float)((v >> 16) & 0xffu), m128), fmaf(dl, (float)(v >> 24), m128));

@@ -1142,21 +1142,9 @@ struct DotIQ4XS {
     template <uint32_t X = 0u>
     __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
         (void)c;
-        // kvalues_iq4nl as bytes: entries 0..7 and 8..15, little-endian
-        // (xor X: the table of kv ^ X)
-        constexpr uint32_t T0lo = 0xBFAD9881u ^ X, T0hi = 0xF6EADDCFu ^ X;
-        constexpr uint32_t T1lo = 0x26190D01u ^ X, T1hi = 0x71594535u ^ X;
         const u32x4 q = (t >> 1) ? l.q1 : l.q0;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t sel = (q[j] >> (4 * (t & 1))) & 0x0F0F0F0Fu;
-            const uint32_t s7 = sel & 0x07070707u;
-            const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
-            const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
-            // byte i from v0 (selector i) or, where the code is >= 8, from v1 (i + 4)
-            const uint32_t pick = ((sel >> 1) & 0x04040404u) | 0x03020100u;
-            cw[j] = __builtin_amdgcn_perm(v1, v0, pick);
-        }
+        for (int j = 0; j < 4; j++) cw[j] = iq4nl_lookup<X>((q[j] >> (4 * (t & 1))) & 0x0F0F0F0Fu);
     }
     // sum(kv * X) with signed kv: the high plane by sdot4; the low (unsigned)
     // plane by udot4 of kv + 128 (kv xor 0x80), less 128 * sum(X_lo)

@@ -382,6 +382,8 @@ struct SkIQ4XS {
                     const uint32_t s7 = sel & 0x07070707u;
                     const uint32_t v0 = __builtin_amdgcn_perm(T0hi, T0lo, s7);
                     const uint32_t v1 = __builtin_amdgcn_perm(T1hi, T1lo, s7);
+                    // a byte-mask blend: iq4nl_lookup's third v_perm measured 25.5 -> 25.9 us
+                    // at m = 8 here
                     const uint32_t hi = (sel >> 3) & 0x01010101u;
                     const uint32_t mask = (hi << 8) - hi;  // 0xFF in the bytes whose code is >= 8
                     const uint32_t v = (v1 & mask) | (v0 & ~mask);

@@ -459,10 +459,14 @@ def only_config(ctx, args):
     elif c == "c1":
         ms, _ = time_matmul(ctx, "q8_0", 1, 2048, 2048, args.steps, args.warmup, 64, 0xA7F00001)
         res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes("q8_0", 1, 2048, 2048) / ms / 1e6}
-    elif c in ("q5km1", "iq4m1"):
-        qt, seed = ("q5_k", 0xA7F00005) if c == "q5km1" else ("iq4_xs", 0xA7F00006)
-        ms, _ = time_matmul(ctx, qt, 1, 17408, 5120, args.steps, args.warmup, 6, seed)
-        res = {"us_per_launch": ms * 1e3, "GB/s": algorithmic_bytes(qt, 1, 17408, 5120) / ms / 1e6}
+    elif c.startswith(("q5km", "iq4m")):  # Q5_K / IQ4_XS at C2's shape, m = 1, 8, 64 or 2048
+        qt, seed = ("q5_k", 0xA7F00005) if c.startswith("q5k") else ("iq4_xs", 0xA7F00006)
+        mm = int(c[4:])
+        xd = np.float16 if mm == 2048 else np.float32
+        ms, _ = time_matmul(ctx, qt, mm, 17408, 5120, args.steps, args.warmup, 6 if mm < 2048 else 2, seed,
+                            x_dtype=xd)
+        res = {"us_per_launch": ms * 1e3,
+               "GB/s": algorithmic_bytes(qt, mm, 17408, 5120, x_bytes=2 if mm == 2048 else 4) / ms / 1e6}
     elif c.startswith("c3"):
         if c.endswith("x16"):  # the 16-bit GEMV (m = 1) or one f16 part of x (skinny)
             ctx.set_options(_arfq.OPT_GEMV_X16)
@@ -501,7 +505,8 @@ def main():
                          "tensors, C2's matrix, a 152K-token vocabulary) and upload its tensors; "
                          "prints its own JSON line")
     ap.add_argument("--only", choices=["c1", "c2", "c2x16", "c3m1", "c3m1x16", "c3m8", "c3m32", "c3m64", "c3m64x16", "c4",
-                                       "c5", "q5km1", "iq4m1", "c1n8", "lmhead", "moe1", "moe4", "moe16", "ffn"],
+                                       "c5", "q5km1", "q5km8", "q5km64", "q5km2048", "iq4m1", "iq4m8", "iq4m64",
+                                       "iq4m2048", "c1n8", "lmhead", "moe1", "moe4", "moe16", "ffn"],
                     help="time one config (for per-kernel rocprofv3 passes); prints its own JSON line")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="for rocprofv3 --pmc passes: COPY_PROBE_BYTES device copies (counter "
