@@ -71,6 +71,12 @@ __host__ __device__ constexpr int q4k_sigma_inv(int t) { return t < 4 ? 2 * t : 
 
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 
+// Bit s (0..7) of every byte of w, moved to bit 4 of its byte (the fifth bit of
+// a Q5_K code): one rotate (v_alignbit_b32) and a mask.
+__device__ __forceinline__ uint32_t bit_to4(uint32_t w, int s) {
+    return __builtin_amdgcn_alignbit(w, w, (uint32_t)(s - 4) & 31u) & 0x10101010u;
+}
+
 // The IQ4_NL codebook value (ggml's kvalues_iq4nl, gguf.rs:1908-1914) xor X of
 // four 4-bit codes, one per byte of sel: two v_perm over the table's 8-entry
 // halves (entries 0..7 and 8..15 as little-endian bytes), and a third that

@@ -337,7 +337,7 @@ struct FmtQ5KR {
 #pragma unroll
         for (int w = 0; w < 8; w++) {
             // elements 4w .. 4w + 3, one per byte
-            const uint32_t v = ((qw[w] >> (4 * ws)) & 0x0F0F0F0Fu) | (((hw[w] >> s) & 0x01010101u) << 4);
+            const uint32_t v = ((qw[w] >> (4 * ws)) & 0x0F0F0F0Fu) | bit_to4(hw[w], s);
             o[2 * w] = pack2h(fmaf(d1, (float)(v & 0xffu), -m1), fmaf(d1, (float)((v >> 8) & 0xffu), -m1));
             o[2 * w + 1] = pack2h(fmaf(d1, (float)((v >> 16) & 0xffu), -m1), fmaf(d1, (float)(v >> 24), -m1));
         }

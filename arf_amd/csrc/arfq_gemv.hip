@@ -1076,10 +1076,9 @@ struct DotQ5K {
     __device__ static void codes(const Lane &l, int c, int t, uint32_t cw[4]) {
         const int nib = t >> 1;
         const u32x4 qs = (t & 1) ? l.qs1 : l.qs0;
-        const uint32_t hs = (uint32_t)(2 * c + nib);
 #pragma unroll
         for (int j = 0; j < 4; j++)
-            cw[j] = (((qs[j] >> (4 * nib)) & 0x0F0F0F0Fu) | (((l.qhd[4 * (t & 1) + j] >> hs) & 0x01010101u) << 4)) ^ X;
+            cw[j] = (((qs[j] >> (4 * nib)) & 0x0F0F0F0Fu) | bit_to4(l.qhd[4 * (t & 1) + j], 2 * c + nib)) ^ X;
     }
     __device__ static int subdot(const uint32_t cw[4], const u32x4 lo, const u32x4 hi) {
         return q6k_subdot(cw, lo, hi);

@@ -319,8 +319,7 @@ struct SkQ5K {
 #pragma unroll
             for (int u = 0; u < 2; u++) {
                 // elements 8kk + 4u + 0..3 of the sub-block, one per byte
-                const uint32_t v = ((qw[2 * kk + u] >> (4 * h)) & 0x0F0F0F0Fu) |
-                                   (((hw[2 * kk + u] >> s) & 0x01010101u) << 4);
+                const uint32_t v = ((qw[2 * kk + u] >> (4 * h)) & 0x0F0F0F0Fu) | bit_to4(hw[2 * kk + u], s);
                 o[2 * u] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04010400u), s1, c1);
                 o[2 * u + 1] = pk_fma(__builtin_amdgcn_perm(0x64646464u, v, 0x04030402u), s1, c1);
             }
